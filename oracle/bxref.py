@@ -1,0 +1,531 @@
+"""CPU restatement of the reference's integer rules for the exact / int8 linear and attention path.
+
+TEST INFRASTRUCTURE ONLY. This module is the checker: only tests/, __graft_entry__.smoke() and bench.py's
+cpu_baseline leg import it. The product (bitexact-llm_amd/) never imports it and has no CPU path.
+
+Everything is numpy int64 (two's complement, wrapping like torch's CPU int64) or Python int. Shifts follow
+torch's CPU rules where the reference could produce counts >= 64: `<<` by >= 64 gives 0, `>>` by >= 64
+gives the sign (the helpers _shl / _sar); every other shift stays in [0, 63] by the reference's own clamps.
+Each function cites the reference function it restates (paths under the reference checkout).
+
+How each function is pinned (tests/test_oracle.py):
+  rshc / rsh / fdiv / rdiv / isqrt / bitlen / div_round / combine / shift_round_hl / quant
+      against Fraction / math.isqrt / int.bit_length closed forms, and the self-check fixture hash
+  split/stack/join_limbs             round-trip invariants and an integer matmul
+  decompose + wmm_f64 + residual + epilogue
+                                     the closed form round(sum_k q w_bf16 2^(sh+FR)) as an exact Fraction,
+                                     the self-check fixture `bf16_linear_with_sparse_residual`, and the
+                                     reconstruction invariant W 2^g + R 2^gf == w
+  epilogue(checked) flag             the big-integer rule |y| >= 2^62 (reference tests/test_model_bounds.py)
+  quant_rows / rdiv32 / bitlen32     closed forms and rdiv equality near ties
+  imm / bmm / int8 GEMM              brute-force Python-int matmul
+  exp2neg_lut / softmax_w / rms      golden vectors written from the reference (tests/golden/) plus
+                                     the precision bounds of the reference's own tests
+  paged attention                    softmax_w + exact matmuls (the reference's own test formulation,
+                                     tests/test_vllm_exact_attn.py:38-41)
+"""
+
+import math
+
+import numpy as np
+
+I64 = np.int64
+
+# ---- constants (src/bitexact/exact/consts.py:23-30, src/bitexact/exact/ops.py:14-23, segs.py:21) ----
+LIM = {1: 127, 2: 32639, 3: 8355711}            # src/bitexact/intops.py:11
+FR = 24
+FT = 30
+EXP2_BITS = 14
+EXP2_ONE = 60
+LIM3 = LIM[3]
+QB = 22
+FN = 40
+FT2 = 26
+FZ = 26
+L2E28 = 387270501
+L2E30 = 1549082005
+L2E28_HD = {64: L2E28, 128: 273841598}
+EPS60 = 11529215046068
+NEG_BIG = -(1 << 20)
+FK, FV, FP = 17, 19, 22
+NEG = -(1 << 62)
+
+
+def _a(x):
+    return np.asarray(x, dtype=I64)
+
+
+def _shl(x, s):
+    """torch CPU `x << s` for int64 (s >= 0): 0 when s >= 64, else the wrapped product."""
+    x, s = np.broadcast_arrays(_a(x), _a(s))
+    out = np.left_shift(x, np.minimum(s, 63))
+    return np.where(s >= 64, I64(0), out)
+
+
+def _sar(x, s):
+    """torch CPU `x >> s` for int64 (s >= 0): arithmetic shift with the count clamped to 63."""
+    return np.right_shift(_a(x), np.minimum(_a(s), 63))
+
+
+# ---- src/bitexact/intops.py ----
+def bitlen(x):
+    """Bit length of int64 x >= 0 (intops.bitlen, src/bitexact/intops.py:14-21); exact by integer compare."""
+    x = _a(x)
+    b = np.frexp(x.astype(np.float64))[1].astype(I64)
+    up = _shl(np.ones_like(b), np.maximum(b - 1, 0)) > x
+    return np.where(x > 0, b - up.astype(I64), I64(0))
+
+
+def rsh(x, s):
+    """round(x / 2^s) ties up for s > 0, x * 2^-s for s <= 0 (src/bitexact/intops.py:24-33)."""
+    x = _a(x)
+    if np.isscalar(s) or np.ndim(s) == 0:
+        s = int(s)
+        if s > 0:
+            return (x + I64(1 << (s - 1))) >> I64(s)
+        return _shl(x, -s)
+    s = _a(s)
+    pos = np.maximum(s, 0)
+    neg = np.maximum(-s, 0)
+    half = np.where(pos > 0, _shl(np.ones_like(pos), np.maximum(pos - 1, 0)), I64(0))
+    return _shl(_sar(x + half, pos), neg)
+
+
+def fdiv(a, b):
+    """floor(a / b), b > 0 (src/bitexact/intops.py:36-38)."""
+    return np.floor_divide(_a(a), _a(b))
+
+
+def rdiv(a, b):
+    """round(a / b) ties up (src/bitexact/intops.py:41-43)."""
+    a, b = _a(a), _a(b)
+    return fdiv(2 * a + b, 2 * b)
+
+
+def isqrt(x):
+    """floor(sqrt(x)), x >= 0 (src/bitexact/intops.py:46-52): float64 estimate + integer correction."""
+    x = _a(x)
+    s = np.floor(np.sqrt(x.astype(np.float64))).astype(I64)
+    for _ in range(2):
+        s = np.where(s * s > x, s - 1, s)
+        s = np.where((s + 1) * (s + 1) <= x, s + 1, s)
+    return s
+
+
+def first_argmax(v):
+    """First maximum index per row (src/bitexact/intops.py:55-59)."""
+    return np.argmax(_a(v), axis=-1)      # numpy argmax returns the first maximum
+
+
+def split_limbs(x, n):
+    """Signed base-256 digits, least significant first (src/bitexact/intops.py:62-70)."""
+    out, r = [], _a(x)
+    for _ in range(n):
+        lo = ((r + 128) & 255) - 128
+        out.append(lo)
+        r = (r - lo) >> 8
+    return out, r
+
+
+def stack_limbs(q, n):
+    """[n M padded to >= 24 rows and a multiple of 8, K] int8 (src/bitexact/intops.py:73-79)."""
+    a = np.concatenate([lo.astype(np.int8) for lo in split_limbs(q, n)[0]])
+    rows = a.shape[0]
+    pad = max(24, (rows + 7) // 8 * 8) - rows
+    return np.concatenate([a, np.zeros((pad, a.shape[1]), np.int8)]) if pad else a
+
+
+def join_limbs(c, M, n):
+    """sum_i c[iM:(i+1)M] 2^(8i) (src/bitexact/intops.py:82-87)."""
+    c = _a(c)
+    acc = c[:M].copy()
+    for i in range(1, n):
+        acc = acc + (c[i * M:(i + 1) * M] << I64(8 * i))
+    return acc
+
+
+# ---- src/bitexact/exact/ops.py ----
+def rshc(x, s):
+    """round(x / 2^s) with s clamped to [-62, 62] (src/bitexact/exact/ops.py:25-34)."""
+    x = _a(x)
+    if np.isscalar(s) or np.ndim(s) == 0:
+        s = max(-62, min(62, int(s)))
+        return ((x + I64(1 << (s - 1))) >> I64(s)) if s > 0 else (x << I64(-s))
+    s = np.clip(_a(s), -62, 62)
+    pos = np.maximum(s, 0)
+    half = np.where(pos > 0, I64(1) << np.maximum(pos - 1, 0), I64(0))
+    return ((x + half) >> pos) << np.maximum(-s, 0)
+
+
+def div_round(a, p, r, chunk=28):
+    """round(a 2^p / r) by 28-bit long division (src/bitexact/exact/ops.py:37-57)."""
+    a, r = np.broadcast_arrays(_a(a), _a(r))
+    p = np.broadcast_to(_a(p), a.shape)
+    Q = np.floor_divide(a, r)
+    R = a - Q * r
+    left = np.maximum(p, 0)
+    for _ in range(3):
+        c = np.minimum(left, chunk)
+        X = R << c
+        q1 = np.floor_divide(X, r)
+        Q = (Q << c) + q1
+        R = X - q1 * r
+        left = left - c
+    up = Q + (2 * R >= r).astype(I64)
+    k = np.clip(-p, 1, 62)
+    down = (Q + (I64(1) << (k - 1))) >> k
+    return np.where(p >= 0, up, down)
+
+
+def combine(T, d, B):
+    """(H, L): H 2^32 + L = T 2^d + B, 0 <= L < 2^32 (src/bitexact/exact/ops.py:60-66)."""
+    T, d, B = np.broadcast_arrays(_a(T), _a(d), _a(B))
+    s = 32 - d
+    H = T >> s
+    L = (T & ((I64(1) << s) - 1)) << d
+    L = L + B
+    return H + (L >> 32), L & I64(0xFFFFFFFF)
+
+
+def shift_round_hl(H, L, p):
+    """round((H 2^32 + L) 2^p) (src/bitexact/exact/ops.py:69-79)."""
+    H, L, p = np.broadcast_arrays(_a(H), _a(L), _a(p))
+    k = np.maximum(-p, 0)
+    pp = np.clip(p, 0, 30)
+    up = (H << (32 + pp)) + (L << pp)
+    k1 = np.clip(k, 1, 31)
+    small = (H << (32 - k1)) + ((L + (I64(1) << (k1 - 1))) >> k1)
+    k2 = np.clip(k, 32, 94)
+    carry = np.where(k2 == 32, (L + I64(1 << 31)) >> 32, _shl(np.ones_like(L), np.maximum(k2 - 33, 0)))
+    big = (H + carry) >> np.minimum(k2 - 32, 62)
+    return np.where(p >= 0, up, np.where(k < 32, small, big))
+
+
+def quant(P, eps):
+    """Per-row power-of-two quantization, |q| <= 2^22 (src/bitexact/exact/ops.py:82-89). Returns (q, sh)."""
+    P = _a(P)
+    eps = np.broadcast_to(_a(eps), P.shape) if np.ndim(eps) else np.full(P.shape, int(eps), I64)
+    e = np.where(P != 0, bitlen(np.abs(P)) + eps, I64(NEG_BIG))
+    sh = np.maximum(e.max(-1) - QB, NEG_BIG)
+    return rshc(P, sh[..., None] - eps), sh
+
+
+def rms(x):
+    """(r, er): rms = r 2^er, 2^30 <= r < 2^31 (src/bitexact/exact/ops.py:92-105)."""
+    x = _a(x)
+    D = x.shape[-1]
+    lg = D.bit_length() - 1
+    assert D == 1 << lg and lg <= 12, "row length a power of two <= 4096"
+    amax = np.maximum(np.abs(x).max(-1), 1)
+    shx = np.maximum(bitlen(amax) - 25, -6)
+    xs = rshc(x, shx[:, None])
+    S = (xs * xs).sum(-1)
+    T = S + rshc(np.full(S.shape, EPS60 * D, I64), 60 - 2 * (FR - shx))
+    m = (62 + lg - bitlen(T)) // 2
+    s = 2 * m - lg
+    V = np.where(s >= 0, T << np.maximum(s, 0), T >> np.maximum(-s, 0))
+    return isqrt(V), shx - FR - m
+
+
+def ndiv(x, gm, ge, r, er):
+    """x gamma / rms at FN (src/bitexact/exact/segs.py:49-51)."""
+    return div_round(_a(x) * _a(gm), _a(ge) - FR - _a(er)[:, None] + FN, _a(r)[:, None])
+
+
+def norm_quant(x, gm, ge):
+    """rms + ndiv + quant(-FN) (src/bitexact/exact/segs.py:59-63). Returns (q int32, sh, flag)."""
+    x = _a(x)
+    r, er = rms(x)
+    q, sh = quant(ndiv(x, gm, ge, r, er), -FN)
+    return q.astype(np.int32), sh, bool(np.abs(x).max() >= 1 << 40)
+
+
+def exp2_table():
+    """2^-f at 2^60 for f = i / 2^14, i = 0 .. 2^14 (src/bitexact/exact/consts.py:110-115)."""
+    f = np.arange((1 << EXP2_BITS) + 1, dtype=np.float64) / (1 << EXP2_BITS)
+    return np.round(np.power(2.0, -f) * 2.0 ** EXP2_ONE).astype(I64)
+
+
+def exp2neg_lut(t, lut, out_bits):
+    """2^-t at out_bits, t >= 0 at FT2 bits (src/bitexact/exact/ops.py:108-116)."""
+    t = _a(t)
+    lut = _a(lut)
+    n = t >> FT2
+    f = t & ((1 << FT2) - 1)
+    idx = f >> (FT2 - EXP2_BITS)
+    rr = f & ((1 << (FT2 - EXP2_BITS)) - 1)
+    a = lut[idx]
+    v = a + rshc((lut[idx + 1] - a) * rr, FT2 - EXP2_BITS)
+    return rshc(v, EXP2_ONE - out_bits + n)
+
+
+def softmax_w(raw, ok, sh, kbits, lut, fp, l2e=None):
+    """Attention weights at fp bits and row sums (src/bitexact/exact/ops.py:133-143)."""
+    raw = np.where(ok, _a(raw), I64(NEG))
+    z = raw.max(-1, keepdims=True) - raw
+    zf = np.minimum(rshc(z, kbits + 3 - _a(sh) - FZ), I64(48 << FZ))
+    t = rshc(zf * I64(L2E28 if l2e is None else l2e), FZ + 28 - FT2)
+    p = np.where(ok, exp2neg_lut(t, lut, fp), I64(0))
+    return p, p.sum(-1, keepdims=True)
+
+
+def attn_div(num, den):
+    """o = round(num 2^(FR-FV) / den) (src/bitexact/exact/segs.py:108-113, before the regroup)."""
+    return div_round(_a(num), FR - FV, _a(den))
+
+
+# ---- src/bitexact/exact/consts.py ----
+def bf16_parts(bits):
+    """bf16 raw bits (uint16 / int16 array) -> (signed significand, exponent): w = sm 2^ex
+    (src/bitexact/exact/consts.py:33-42)."""
+    b = _a(np.asarray(bits).view(np.uint16)) & 0xFFFF
+    e = (b >> 7) & 0xFF
+    assert not bool((e == 255).any()), "inf/nan weight"
+    m = b & 0x7F
+    mag = np.where(e > 0, m | 0x80, m)
+    ex = np.where(e > 0, e, 1) - 134
+    sm = np.where((b >> 15) == 1, -mag, mag)
+    return sm, ex
+
+
+def _bitlen9(x):
+    out = np.zeros_like(x)
+    for i in range(9):
+        out = np.where(x >> i != 0, i + 1, out)
+    return out
+
+
+def _lowbit9(x):
+    out = np.full_like(x, 99)
+    for i in range(8, -1, -1):
+        out = np.where(((x >> i) & 1) == 1, i, out)
+    return out
+
+
+def bf16_to_f64(bits):
+    sm, ex = bf16_parts(bits)
+    return sm.astype(np.float64) * np.power(2.0, ex.astype(np.float64))
+
+
+def decompose(bits):
+    """bf16 [N, K] (raw bits) -> dict(limbs int8 [3, N, K], g, d, rr, rc, rv)
+    (src/bitexact/exact/consts.py:67-107). Residual COO in row-major (rr, rc) order."""
+    sm, ex = bf16_parts(bits)
+    mag = np.abs(sm)
+    nz = mag > 0
+    top = np.where(nz, ex + _bitlen9(mag), -10 ** 6).max(1)
+    g = top - 23
+    while True:
+        sh = np.minimum(ex - g[:, None], 40)
+        big = nz & (sh >= 0) & ((mag << np.maximum(sh, 0)) > LIM3)
+        bad = big.any(1)
+        if not bool(bad.any()):
+            break
+        g = np.where(bad, g + 1, g)
+    g = np.where(top < -10 ** 5, 0, g)
+    sh = ex - g[:, None]
+    up = sh >= 0
+    dmag = np.where(up, mag << np.clip(sh, 0, 40), mag >> np.clip(-sh, 0, 40))
+    rmag = mag - np.where(up, mag, dmag << np.clip(-sh, 0, 40))
+    rmag = np.where(up, 0, rmag)
+    W = np.where(sm < 0, -dmag, dmag)
+    has = rmag > 0
+    low = np.where(has, ex + _lowbit9(rmag), 10 ** 6)
+    gf = np.minimum(low.min(1), g)
+    d = g - gf
+    assert int(d.max()) <= 30, "residual grid too fine"
+    rr, rc = np.nonzero(has)
+    rsh_ = ex[rr, rc] - gf[rr]
+    rm_ = rmag[rr, rc]
+    rv = np.where(rsh_ >= 0, rm_ << np.maximum(rsh_, 0), rm_ >> np.maximum(-rsh_, 0))
+    rv = np.where(sm[rr, rc] < 0, -rv, rv)
+    lo, rem = split_limbs(W, 3)
+    assert not bool(rem.any())
+    return {"limbs": np.stack([x.astype(np.int8) for x in lo]), "W": W, "g": g.astype(I64),
+            "d": d.astype(I64), "rr": rr.astype(I64), "rc": rc.astype(I64), "rv": rv.astype(I64)}
+
+
+def to_ell(rr, rc, rv, N):
+    """Padded per-row residual lists (src/bitexact/vllm_plugin/exact_gemm.py:264-282): cnt, ec, ev."""
+    cnt = np.bincount(rr, minlength=N).astype(I64) if len(rr) else np.zeros(N, I64)
+    R = int(cnt.max()) if len(rr) else 0
+    start = np.cumsum(cnt) - cnt
+    j = np.arange(len(rr)) - start[rr] if len(rr) else np.zeros(0, I64)
+    ec = np.zeros((N, max(R, 1)), I64)
+    ev = np.zeros((N, max(R, 1)), I64)
+    if len(rr):
+        ec[rr, j] = rc
+        ev[rr, j] = rv
+    return cnt, ec, ev, R
+
+
+# ---- src/bitexact/exact/wmm.py ----
+def wmm_f64(q, W):
+    """T = q W^T exactly: q's 3 limbs as float64 [3M, K] times W^T (|W| <= 2^23) -- every partial sum
+    < 2^43 < 2^53, so float64 BLAS is exact in any order (src/bitexact/exact/wmm.py:117-121)."""
+    q = _a(q)
+    M = q.shape[0]
+    A = np.concatenate(split_limbs(q, 3)[0]).astype(np.float64)
+    C = (A @ _a(W).astype(np.float64).T).astype(I64)
+    return C[:M] + (C[M:2 * M] << 8) + (C[2 * M:] << 16)
+
+
+def residual(q, rr, rc, rv, N):
+    """B [M, N] = sum over residual entries of q[:, k] v (src/bitexact/exact/wmm.py:124-129)."""
+    q = _a(q)
+    B = np.zeros((q.shape[0], N), I64)
+    if len(rr):
+        np.add.at(B.T, _a(rr), (q[:, _a(rc)] * _a(rv)).T)
+    return B
+
+
+def epilogue(T, B, d, g, sh, FR_=FR, checked=False):
+    """round((T 2^d + B) 2^p), p = sh + g - d + FR, and the checked flag
+    (src/bitexact/exact/wmm.py:132-150). With checked=True returns (y, flag_any, flag_per_element)."""
+    d, g, sh = _a(d), _a(g), _a(sh)
+    H, L = combine(T, d[None, :], B)
+    p = sh[:, None] + (g - d)[None, :] + FR_
+    y = shift_round_hl(H, L, p)
+    if not checked:
+        return y
+    up_limit = I64(1) << (31 - np.clip(p, 0, 30))
+    small_limit = I64(1) << (31 + np.clip(-p, 1, 31))
+    up_lost = (H >= up_limit) | (H < -up_limit) | ((p > 30) & ((H != 0) | (L != 0)))
+    small_lost = (H >= small_limit) | (H < -small_limit)
+    lost = np.where(p >= 0, up_lost, (p > -32) & small_lost)
+    bad = lost | (y <= -(1 << 62)) | (y >= 1 << 62)
+    return y, bool(bad.any()), bad
+
+
+def exact_linear(q, dec, sh, checked=True):
+    """The whole exact linear (segs.lin_y over Lin on CPU, src/bitexact/exact/segs.py:25-32):
+    y int64 [M, N] at FR and the checked flag."""
+    T = wmm_f64(q, dec["W"])
+    B = residual(q, dec["rr"], dec["rc"], dec["rv"], dec["W"].shape[0])
+    if checked:
+        y, flag, _ = epilogue(T, B, dec["d"], dec["g"], sh, FR, True)
+        return y, flag
+    return epilogue(T, B, dec["d"], dec["g"], sh, FR), False
+
+
+# ---- src/bitexact/int8/ops.py ----
+def qmax(nl):
+    return 127 << (8 * (nl - 1))
+
+
+def bitlen32(x):
+    """Same integers as bitlen (src/bitexact/int8/ops.py:38-44); restated through bitlen."""
+    return bitlen(x)
+
+
+def rdiv32(a, b):
+    """Same integers as rdiv in its range (src/bitexact/int8/ops.py:47-55)."""
+    return rdiv(a, b)
+
+
+def quant_rows(z, nl):
+    """(q, as_, sh): q = round(rsh(z, sh) qmax / as_) (src/bitexact/int8/ops.py:24-35)."""
+    z = _a(z)
+    amax = np.maximum(np.abs(z).max(-1), 1)
+    sh = bitlen(amax) - 30
+    as_ = rsh(amax, sh)
+    zs = rsh(z, sh[:, None])
+    return rdiv(zs * qmax(nl), as_[:, None]), as_, sh
+
+
+def imm(q, W):
+    """Exact q @ W^T (src/bitexact/int8/ops.py:87-90): float64, |partial sums| < 2^53."""
+    return (_a(q).astype(np.float64) @ _a(W).astype(np.float64).T).astype(I64)
+
+
+def int_mm(a, w):
+    """int8 [R, K] x int8 [N, K]^T -> exact int (int32 contract of gemm_skinny.int_mm,
+    src/bitexact/int8/gemm_skinny.py:80-97)."""
+    return imm(a, w)
+
+
+# ---- src/bitexact/bmm.py ----
+def bmm(a, b):
+    """Exact [Z, M, K] x [Z, K, N] -> int64, by 3x3 limbs in float64 (each partial < 2^53 for K < 2^21)
+    (src/bitexact/bmm.py:78-102 computes the same integers)."""
+    a, b = _a(a), _a(b)
+    la, ra = split_limbs(a, 3)
+    lb, rb = split_limbs(b, 3)
+    assert not ra.any() and not rb.any(), "operands within 3 limbs"
+    out = np.zeros((a.shape[0], a.shape[1], b.shape[2]), I64)
+    for i in range(3):
+        for j in range(3):
+            out += (la[i].astype(np.float64) @ lb[j].astype(np.float64)).astype(I64) << I64(8 * (i + j))
+    return out
+
+
+def brute_matmul(a, b):
+    """Python-int matmul [M, K] x [K, N] (tiny shapes only)."""
+    a = [[int(v) for v in r] for r in np.asarray(a).tolist()]
+    bt = [[int(v) for v in c] for c in np.asarray(b).T.tolist()]
+    return [[sum(x * y for x, y in zip(r, c)) for c in bt] for r in a]
+
+
+# ---- paged limb-plane cache (src/bitexact/vllm_plugin/tri_paged.py:22-26, 311-348) ----
+def to_limbs(c):
+    """int32 cache [nb, HKV, bs, 2 HD] (K | V) -> int8 limb planes [nb, HKV, bs, 8 HD]."""
+    c = _a(c)
+    HD = c.shape[-1] // 2
+    out = np.zeros(c.shape[:3] + (8 * HD,), np.int8)
+    for part, o in ((c[..., :HD], 0), (c[..., HD:], 3)):
+        lo, _ = split_limbs(part, 3)
+        for i in range(3):
+            out[..., (o + i) * HD:(o + i + 1) * HD] = lo[i].astype(np.int8)
+    return out
+
+
+def paged_attend(q, sh, qpos, c32, bt, rmap, lut, l2e):
+    """Exact paged attention as the reference's test states it (tests/test_vllm_exact_attn.py:38-41 over
+    src/bitexact/vllm_plugin/tri_exact_attn.py:1-15): q [R, HKV, M, HD], sh [R, HKV, M], qpos [R, M],
+    c32 int32 cache [nb, HKV, bs, 2 HD], bt [*, nblk], rmap [R] -> num [R, HKV, M, HD], den [R, HKV, M, 1]."""
+    q, sh, qpos, c32, bt, rmap = (_a(x) for x in (q, sh, qpos, c32, bt, rmap))
+    R, HKV, M, HD = q.shape
+    bs = c32.shape[2]
+    num = np.zeros((R, HKV, M, HD), I64)
+    den = np.zeros((R, HKV, M, 1), I64)
+    for r in range(R):
+        S = int(qpos[r].max()) + 1
+        if S <= 0:
+            continue
+        s = np.arange(S)
+        kv = c32[bt[rmap[r], s // bs], :, s % bs]                      # [S, HKV, 2 HD]
+        for h in range(HKV):
+            K, V = kv[:, h, :HD], kv[:, h, HD:]
+            raw = bmm(q[r, h][None], K.T[None])[0]                    # [M, S]
+            ok = s[None, :] <= qpos[r][:, None]
+            p, dn = softmax_w(raw, ok, sh[r, h][:, None], FK, lut, FP, l2e)
+            num[r, h] = bmm(p[None], V[None])[0]
+            den[r, h] = dn
+    return num, den
+
+
+def attention_prefill(qg, shg, K, V, qpos, lut, l2e):
+    """The unfused exact/model.py attention (src/bitexact/exact/model.py:114-120): qg int32 [Z, gT, HD],
+    shg [Z, gT, 1], K / V [Z, S, HD] int32, qpos [Z, gT, 1] -> num [Z, gT, HD], den [Z, gT, 1]."""
+    raw = bmm(qg, np.swapaxes(_a(K), 1, 2))
+    ok = np.arange(raw.shape[-1])[None, None, :] <= _a(qpos)
+    p, den = softmax_w(raw, ok, shg, FK, lut, FP, l2e)
+    return bmm(p, V), den
+
+
+# ---- RoPE tables (src/bitexact/llama.py:52-68): llama3 inverse frequencies in closed form ----
+def llama3_inv_freq(hd=64, theta=500000.0, factor=32.0, low=1.0, high=4.0, orig=8192):
+    """transformers' llama3 rope rule (the function src/bitexact/llama.py:57-60 calls), float64."""
+    inv = 1.0 / theta ** (np.arange(0, hd, 2, dtype=np.float64) / hd)
+    low_wl, high_wl = orig / low, orig / high
+    wl = 2 * math.pi / inv
+    out = np.where(wl > low_wl, inv / factor, inv)
+    smooth = (orig / wl - low) / (high - low)
+    mid = (1 - smooth) * out / factor + smooth * out
+    is_mid = (wl >= high_wl) & (wl <= low_wl)
+    return np.where(is_mid, mid, out)
+
+
+def rope_tables(n_pos, bits, inv_freq):
+    ang = np.arange(n_pos, dtype=np.float64)[:, None] * inv_freq[None, :]
+    return np.round(np.cos(ang) * 2.0 ** bits).astype(I64), np.round(np.sin(ang) * 2.0 ** bits).astype(I64)
