@@ -1,0 +1,251 @@
+"""bench.py -- the hot path on one MI355X: int8-mode decode GEMMs (HBM GB/s) and exact-mode prefill limb GEMMs
+(effective limb-op TOPS against the dense int8 MFMA peak).
+
+One step = one pass over BASELINE config 2's decode GEMMs: batch M in {1, 8, 64} x {gate K=2048 N=8192,
+up K=2048 N=8192, down K=8192 N=2048}, int8 weights uniform in [-127, 127], activations N(0,1) quantized per
+row into 2 int8 limbs, int64 joined output (bitexact.int8.gemm_skinny.int_mm_join). Weights rotate over
+>= 1 GiB of copies per shape (4x the 256 MB MALL) so every launch reads them from HBM. The steps are captured
+in a HIP graph and timed with HIP events on the launch stream.
+value = sum of algorithmic bytes (N K + 2 M K + 8 M N per GEMM) / time, in GB/s.
+
+Also measured (config 3): exact-mode prefill, M = 2048 over every Llama-3.2-1B linear, reported as effective
+TOPS = 9 x 2 M N K / time and as a fraction of the 5.0 POP/s dense int8 peak. And a CPU baseline: the oracle's
+float64 restatement of the same GEMMs (oracle/bxref.py imm, the reference's CPU path) on a bounded sample.
+
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-prefill] [--no-cpu]
+"""
+
+import argparse
+import json
+import os
+import sys
+import time
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, os.path.join(HERE, "bitexact-llm_amd"))
+
+HBM_PEAK_GBS = 8000.0
+INT8_PEAK_TOPS = 5000.0
+DECODE_SHAPES = [("gate", 8192, 2048), ("up", 8192, 2048), ("down", 2048, 8192)]
+DECODE_M = (1, 8, 64)
+PREFILL_SHAPES = [("q_o", 2048, 2048), ("k_v", 512, 2048), ("gate_up_each", 8192, 2048), ("down", 2048, 8192),
+                  ("qkv_fused", 3072, 2048), ("gate_up_fused", 16384, 2048), ("lm_head", 128256, 2048)]
+
+
+def log(*a):
+    print(*a, file=sys.stderr, flush=True)
+
+
+def quant_rows2(z):
+    """int8.ops.quant_rows(z, 2) on the device with torch int64 ops (input preparation, not timed):
+    sh = bitlen(amax) - 30, as_ = rsh(amax, sh), q = rdiv(rsh(z, sh) * 32512, as_)."""
+    import torch
+    amax = z.abs().amax(-1).clamp(min=1)
+    b = torch.frexp(amax.double()).exponent.long()
+    b = b - ((torch.ones_like(b) << (b - 1).clamp(min=0)) > amax).long()
+    sh = b - 30
+
+    def rsh(x, s):
+        pos, neg = s.clamp(min=0), (-s).clamp(min=0)
+        half = torch.where(pos > 0, torch.ones_like(pos) << (pos - 1).clamp(min=0), torch.zeros_like(pos))
+        return ((x + half) >> pos) << neg
+    as_ = rsh(amax, sh)
+    zs = rsh(z, sh[:, None])
+    n = 2 * zs * 32512 + as_[:, None]
+    return torch.div(n, 2 * as_[:, None], rounding_mode="floor")
+
+
+def stack2(q):
+    import torch
+    lo = ((q + 128) & 255) - 128
+    hi = (q - lo) >> 8
+    return torch.cat([lo, hi]).to(torch.int8).contiguous()
+
+
+def quant40(x):
+    """exact.ops.quant(P, -40) of P = round(x 2^40) on the device (input preparation, not timed)."""
+    import torch
+    P = torch.floor(x * 2.0 ** 40 + 0.5).long()
+    amax = P.abs().amax(-1).clamp(min=1)
+    b = torch.frexp(amax.double()).exponent.long()
+    b = b - ((torch.ones_like(b) << (b - 1).clamp(min=0)) > amax).long()
+    sh = b - 40 - 22
+    s = (sh + 40).clamp(-62, 62)[:, None]
+    pos = s.clamp(min=0)
+    half = torch.where(pos > 0, torch.ones_like(pos) << (pos - 1).clamp(min=0), torch.zeros_like(pos))
+    q = ((P + half) >> pos) << (-s).clamp(min=0)
+    return q.to(torch.int32).contiguous(), sh
+
+
+def time_graph(fn_steps, warmup, steps, stream):
+    """Capture `steps` calls of fn_steps(i) in one graph (and `warmup` in another); return seconds for the
+    timed replay, measured with HIP events recorded on the capture/launch stream."""
+    import torch
+    gw, gt = torch.cuda.CUDAGraph(), torch.cuda.CUDAGraph()
+    with torch.cuda.stream(stream):
+        fn_steps(0)                      # allocations (outputs, workspaces) before capture
+        torch.cuda.synchronize()
+        if warmup:
+            with torch.cuda.graph(gw, stream=stream):
+                for i in range(warmup):
+                    fn_steps(i)
+        with torch.cuda.graph(gt, stream=stream):
+            for i in range(steps):
+                fn_steps(warmup + i)
+        torch.cuda.synchronize()
+        if warmup:
+            gw.replay()
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record(stream)
+        gt.replay()
+        e1.record(stream)
+        torch.cuda.synchronize()
+    return e0.elapsed_time(e1) / 1e3
+
+
+def bench_decode(dev, steps, warmup):
+    import torch
+    from bitexact.int8.gemm_skinny import int_mm_join
+    g = torch.Generator(device=dev).manual_seed(1234)
+    copies = {}
+    for name, N, K in DECODE_SHAPES:
+        if (N, K) not in copies:
+            n = max(4, -(-(1 << 30) // (N * K)))
+            copies[(N, K)] = [torch.randint(-127, 128, (N, K), dtype=torch.int8, device=dev, generator=g)
+                              for _ in range(n)]
+    gc = torch.Generator().manual_seed(99)
+    acts = {}
+    for M in DECODE_M:
+        for K in (2048, 8192):
+            x = torch.randn(M, K, generator=gc, dtype=torch.float64).to(dev)
+            acts[(M, K)] = stack2(quant_rows2(torch.floor(x * 2.0 ** 16 + 0.5).long()))
+    outs = {}
+    plan = [(M, name, N, K) for M in DECODE_M for name, N, K in DECODE_SHAPES]
+    step_bytes = sum(N * K + 2 * M * K + 8 * M * N for M, _, N, K in plan)
+
+    def step(i):
+        for j, (M, name, N, K) in enumerate(plan):
+            cs = copies[(N, K)]
+            outs[j] = int_mm_join(acts[(M, K)], cs[(i * 3 + j) % len(cs)], M, 2)
+
+    stream = torch.cuda.Stream(dev)
+    sec = time_graph(step, warmup, steps, stream)
+    per = []
+    for M, name, N, K in plan:          # per-GEMM figures, each on its own graph (rotation as above)
+        cs = copies[(N, K)]
+        reps = 64
+        s = time_graph(lambda i: int_mm_join(acts[(M, K)], cs[i % len(cs)], M, 2), 8, reps, stream)
+        b = N * K + 2 * M * K + 8 * M * N
+        per.append({"M": M, "gemm": name, "N": N, "K": K, "us": round(s / reps * 1e6, 3),
+                    "GBps": round(b / (s / reps) / 1e9, 1)})
+    del copies
+    torch.cuda.empty_cache()
+    return sec, step_bytes, len(plan), per
+
+
+def bench_prefill(dev, reps=10):
+    import torch
+    from bitexact.exact.consts import decompose
+    from bitexact.vllm_plugin.exact_gemm import exact_linear
+    M = 2048
+    gc = torch.Generator().manual_seed(5)
+    stream = torch.cuda.Stream(dev)
+    res, tot_ops, tot_s = [], 0, 0.0
+    for name, N, K in PREFILL_SHAPES:
+        gw = torch.Generator(device=dev).manual_seed(N + K)
+        w = (torch.randn(N, K, generator=gw, device=dev) * 0.02).to(torch.bfloat16)
+        dec = decompose(w)
+        del w
+        q, sh = quant40(torch.randn(M, K, generator=gc, dtype=torch.float64).to(dev))
+        flag = torch.zeros(1, dtype=torch.int32, device=dev)
+
+        def run(i):
+            exact_linear(q, sh, dec["limbs"], dec["d"], dec["g"], dec["ell_cnt"], dec["ell_col"], dec["ell_val"],
+                         dec["R"], flag, True)
+        s = time_graph(run, 2, reps, stream) / reps
+        ops = 9 * 2 * M * N * K
+        tops = ops / s / 1e12
+        res.append({"gemm": name, "M": M, "N": N, "K": K, "us": round(s * 1e6, 1), "TOPS": round(tops, 1),
+                    "frac": round(tops / INT8_PEAK_TOPS, 4)})
+        if name not in ("qkv_fused", "gate_up_fused"):
+            mult = {"q_o": 2, "k_v": 2, "gate_up_each": 2}.get(name, 1)
+            tot_ops += mult * ops
+            tot_s += mult * s
+        del dec, q
+        torch.cuda.empty_cache()
+    return res, tot_ops / tot_s / 1e12
+
+
+def cpu_baseline(budget_s=20.0):
+    """oracle/bxref.py's float64 restatement of the int8 GEMM (the reference's CPU path imm,
+    src/bitexact/int8/ops.py:87-90) on the config-2 shapes at M = 8, on the host cores; GB/s of the same
+    algorithmic bytes as the GPU figure."""
+    import numpy as np
+    from threadpoolctl import threadpool_info
+    sys.path.insert(0, HERE)
+    from oracle import bxref as R
+    rng = np.random.default_rng(0)
+    M, t_tot, b_tot, runs = 8, 0.0, 0, 0
+    t_start = time.perf_counter()
+    ws = {(N, K): rng.integers(-127, 128, (N, K)).astype(np.int8) for _, N, K in DECODE_SHAPES}
+    while time.perf_counter() - t_start < budget_s:
+        for name, N, K in DECODE_SHAPES:
+            q = rng.integers(-32512, 32513, (M, K))
+            t0 = time.perf_counter()
+            R.imm(q, ws[(N, K)])
+            t_tot += time.perf_counter() - t0
+            b_tot += N * K + 2 * M * K + 8 * M * N
+        runs += 1
+    threads = max([i.get("num_threads", 1) for i in threadpool_info()] or [1])
+    return {"value": round(b_tot / t_tot / 1e9, 3), "unit": "GB/s", "cores": threads, "kind": "port",
+            "sample": f"oracle float64 imm (numpy BLAS) on config-2 gate/up/down at M={M}, {runs} passes, "
+                      f"{t_tot:.1f} s of GEMM time"}
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=60)
+    ap.add_argument("--warmup", type=int, default=6)
+    ap.add_argument("--no-prefill", action="store_true")
+    ap.add_argument("--no-cpu", action="store_true")
+    args = ap.parse_args()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
+        print("bench.py: this build runs on one GPU only (the hot path has no collectives); use --gpus 1",
+              file=sys.stderr)
+        sys.exit(2)
+    import torch
+    if not torch.cuda.is_available():
+        print("bench.py: no GPU visible", file=sys.stderr)
+        sys.exit(1)
+    dev = torch.device("cuda:0")
+    log("decode GEMMs ...")
+    sec, step_bytes, launches, per = bench_decode(dev, args.steps, args.warmup)
+    value = step_bytes * args.steps / sec / 1e9
+    out = {"metric": "int8 decode GEMM HBM GB/s (config 2); exact prefill limb-GEMM TOPS and % int8 MFMA peak "
+                     "(config 3); 1 GPU",
+           "value": round(value, 1), "unit": "GB/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+           "ms_per_step": round(sec / args.steps * 1e3, 4), "higher_is_better": True, "scaling": "weak",
+           "vs_baseline": None, "dtype": "int8 (int32 accumulate, int64 join)", "data": "synthetic",
+           "config": {"workload": "config 2: int8-mode decode GEMMs, M in {1,8,64} x gate/up (K=2048, N=8192), "
+                                  "down (K=8192, N=2048), 2 activation limbs, int64 joined output",
+                      "gemms_per_step": launches, "bytes_per_step": step_bytes, "weight_rotation": ">=1 GiB/shape"},
+           "roofline": {"bound": "hbm", "achieved": round(value, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                        "frac": round(value / HBM_PEAK_GBS, 4), "traffic": None},
+           "per_gemm": per}
+    if not args.no_prefill:
+        log("exact prefill GEMMs ...")
+        res, tops = bench_prefill(dev)
+        out["exact_prefill"] = {"workload": "config 3: exact limb GEMM, M=2048, Llama-3.2-1B linears (bf16 N(0,0.02) "
+                                            "weights, 3-limb N(0,1) activations), fused epilogue",
+                                "TOPS": round(tops, 1), "frac_int8_peak": round(tops / INT8_PEAK_TOPS, 4),
+                                "peak_TOPS": INT8_PEAK_TOPS, "per_gemm": res}
+    if not args.no_cpu:
+        log("cpu baseline ...")
+        out["cpu_baseline"] = cpu_baseline()
+    print(json.dumps(out), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,90 @@
+"""ctypes binding of libbitexact_hip.so (the C ABI declared in include/bitexact_hip.h).
+
+Every kernel call goes through `call`: launches happen on torch's current stream of the tensors' device, a
+BX_EINVAL return is re-raised as AssertionError (the reference's shape/contract asserts) and BX_EHIP as
+RuntimeError. There is no fallback: without the built library or a GPU the import of a kernel module fails.
+"""
+
+import ctypes
+import os
+import threading
+
+import torch
+
+_LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "_lib", "libbitexact_hip.so")
+_lib = None
+_lock = threading.Lock()
+
+P, I32, I64 = ctypes.c_void_p, ctypes.c_int32, ctypes.c_int64
+
+# name -> (restype, argtypes); the order and meaning follow include/bitexact_hip.h
+SIGNATURES = {
+    "bx_version": (ctypes.c_int, []),
+    "bx_last_error": (ctypes.c_char_p, []),
+    "bx_exact_linear": (ctypes.c_int, [P, I64, P, P, I64, I64, P, P, P, P, P, I32, P, I32, I32, I32, I32, I32, P,
+                                       P, I64, P]),
+    "bx_exact_linear_workspace": (I64, [I32, I32, I32]),
+    "bx_exact_wmm": (ctypes.c_int, [P, I64, P, I64, I64, P, I32, I32, I32, P, I64, P]),
+    "bx_decompose_rows": (ctypes.c_int, [P, I32, I32, P, P, P, P, P, P]),
+    "bx_decompose_residual": (ctypes.c_int, [P, I32, I32, P, P, P, P, I32, P]),
+    "bx_int8_gemm": (ctypes.c_int, [P, P, P, I32, I32, I32, P, I64, P]),
+    "bx_int8_gemm_join": (ctypes.c_int, [P, P, P, I32, I32, I32, I32, P, I64, P]),
+    "bx_int8_gemm_workspace": (I64, [I32, I32, I32]),
+}
+
+
+def lib():
+    """The loaded library; raises if it was not built (python bitexact-llm_amd/build.py)."""
+    global _lib
+    if _lib is None:
+        with _lock:
+            if _lib is None:
+                if not os.path.exists(_LIB_PATH):
+                    raise ImportError(f"{_LIB_PATH} is missing: build it with `python bitexact-llm_amd/build.py`")
+                L = ctypes.CDLL(_LIB_PATH)
+                for name, (res, args) in SIGNATURES.items():
+                    f = getattr(L, name)
+                    f.restype = res
+                    f.argtypes = args
+                _lib = L
+    return _lib
+
+
+def ptr(t):
+    return None if t is None else ctypes.c_void_p(t.data_ptr())
+
+
+def stream_of(t):
+    return ctypes.c_void_p(torch.cuda.current_stream(t.device).cuda_stream)
+
+
+def call(name, *args):
+    rc = getattr(lib(), name)(*args)
+    if rc == 0:
+        return
+    msg = lib().bx_last_error().decode(errors="replace")
+    if rc == -1:
+        raise AssertionError(f"{name}: {msg}")
+    raise RuntimeError(f"{name} failed ({rc}): {msg}")
+
+
+def require_cuda(*ts):
+    for t in ts:
+        if t is not None and not t.is_cuda:
+            raise AssertionError("bitexact HIP kernels take device tensors only (no CPU path)")
+
+
+# ---- split-K workspaces: one zero-filled buffer per (device, stream); every call leaves it zeroed ----
+_ws = {}
+
+
+def workspace(dev, nbytes):
+    if nbytes <= 0:
+        return None, 0
+    s = torch.cuda.current_stream(dev)
+    key = (dev.index, s.cuda_stream)
+    buf = _ws.get(key)
+    if buf is None or buf.numel() < nbytes:
+        buf = torch.zeros(max(nbytes, 1 << 20), dtype=torch.uint8, device=dev)
+        _ws[key] = buf
+    return buf, buf.numel()

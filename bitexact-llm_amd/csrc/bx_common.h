@@ -1,0 +1,119 @@
+// Shared device code for the bitexact HIP library (gfx950 / MI355X).
+//
+// Integer rules follow the reference's torch int64 semantics exactly: two's complement wrap (the library is
+// built with -fwrapv and wrapping sums are done in uint64), `<<` by >= 64 gives 0, `>>` by >= 64 gives the
+// sign. Every helper cites the reference rule it restates.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "bitexact_hip.h"
+
+typedef int32_t v4i __attribute__((ext_vector_type(4)));
+typedef int32_t v16i __attribute__((ext_vector_type(16)));
+
+namespace bx {
+
+constexpr int64_t kLim3 = 8355711;     // 3 signed base-256 digits (src/bitexact/intops.py:11)
+constexpr int64_t kNeg = -(1LL << 62);  // masked score (src/bitexact/exact/ops.py:138)
+
+// ---- host-side error plumbing ----
+void set_error(const char* fmt, ...);
+int check_launch(const char* what);
+int device_cus();   // compute units of the current device (cached per device)
+
+// ---- shifts with torch's CPU semantics ----
+__device__ __forceinline__ int64_t shl(int64_t x, int64_t s) {   // s >= 0
+  return s >= 64 ? 0 : (int64_t)((uint64_t)x << s);
+}
+__device__ __forceinline__ int64_t sar(int64_t x, int64_t s) {   // s >= 0
+  return x >> (s > 63 ? 63 : s);
+}
+__device__ __forceinline__ int64_t add_wrap(int64_t a, int64_t b) {
+  return (int64_t)((uint64_t)a + (uint64_t)b);
+}
+__device__ __forceinline__ int64_t mul_wrap(int64_t a, int64_t b) {
+  return (int64_t)((uint64_t)a * (uint64_t)b);
+}
+__device__ __forceinline__ int64_t imin(int64_t a, int64_t b) { return a < b ? a : b; }
+__device__ __forceinline__ int64_t imax(int64_t a, int64_t b) { return a > b ? a : b; }
+
+// ops.rshc (src/bitexact/exact/ops.py:25-34): round(x / 2^s), s clamped to [-62, 62].
+__device__ __forceinline__ int64_t rshc(int64_t x, int64_t s) {
+  s = imin(imax(s, -62), 62);
+  if (s > 0) return add_wrap(x, 1LL << (s - 1)) >> s;
+  return shl(x, -s);
+}
+
+// intops.bitlen (src/bitexact/intops.py:14-21) for x >= 0: 64 - clz.
+__device__ __forceinline__ int64_t bitlen(int64_t x) {
+  return x > 0 ? 64 - __clzll((unsigned long long)x) : 0;
+}
+
+// floor(a / b) for b > 0 (intops.fdiv, src/bitexact/intops.py:36-38).
+__device__ __forceinline__ int64_t fdiv(int64_t a, int64_t b) {
+  int64_t q = a / b;
+  return (a - q * b < 0) ? q - 1 : q;
+}
+
+// Signed base-256 digit and remainder (intops.split_limbs, src/bitexact/intops.py:62-70).
+__device__ __forceinline__ int32_t limb_lo(int32_t r) { return ((r + 128) & 255) - 128; }
+__device__ __forceinline__ int64_t limb_lo64(int64_t r) { return ((r + 128) & 255) - 128; }
+
+// wmm.epilogue (src/bitexact/exact/wmm.py:132-150) over ops.combine + ops.shift_round_hl
+// (src/bitexact/exact/ops.py:60-79): y = round((T 2^d + B) 2^p), and the `checked` loss / range test.
+__device__ __forceinline__ int64_t exact_round(int64_t T, int64_t B, int64_t d, int64_t p, bool& bad) {
+  const int64_t s = 32 - d;
+  int64_t H = T >> s;
+  int64_t L = (int64_t)((uint64_t)(T & ((1LL << s) - 1)) << d);
+  L = add_wrap(L, B);
+  H = add_wrap(H, L >> 32);
+  L = L & 0xFFFFFFFFLL;
+  const int64_t k = p < 0 ? -p : 0;
+  int64_t y;
+  if (p >= 0) {
+    const int64_t pp = p > 30 ? 30 : p;
+    y = (int64_t)(((uint64_t)H << (32 + pp)) + ((uint64_t)L << pp));
+  } else if (k < 32) {
+    y = add_wrap((int64_t)((uint64_t)H << (32 - k)), (L + (1LL << (k - 1))) >> k);
+  } else {
+    const int64_t k2 = k > 94 ? 94 : k;
+    const int64_t carry = (k2 == 32) ? ((L + (1LL << 31)) >> 32) : (1LL << (k2 - 33));
+    y = add_wrap(H, carry) >> imin(k2 - 32, 62);
+  }
+  const int64_t up_limit = 1LL << (31 - imin(imax(p, 0), 30));
+  const int64_t small_limit = 1LL << (31 + imin(imax(-p, 1), 31));
+  const bool up_lost = (H >= up_limit) | (H < -up_limit) | ((p > 30) & ((H != 0) | (L != 0)));
+  const bool small_lost = (H >= small_limit) | (H < -small_limit);
+  const bool lost = (p >= 0) ? up_lost : ((p > -32) & small_lost);
+  bad = lost | (y <= -(1LL << 62)) | (y >= (1LL << 62));
+  return y;
+}
+
+// ---- wavefront reductions (wave64) ----
+__device__ __forceinline__ int64_t wave_max64(int64_t v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v = imax(v, __shfl_xor(v, o, 64));
+  return v;
+}
+__device__ __forceinline__ int64_t wave_sum64(int64_t v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+  return v;
+}
+__device__ __forceinline__ int wave_or(int v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v |= __shfl_xor(v, o, 64);
+  return v;
+}
+
+}  // namespace bx
+
+#define BX_REQUIRE(cond, ...)          \
+  do {                                 \
+    if (!(cond)) {                     \
+      bx::set_error(__VA_ARGS__);      \
+      return BX_EINVAL;                \
+    }                                  \
+  } while (0)

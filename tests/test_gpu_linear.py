@@ -1,0 +1,181 @@
+"""HIP exact / int8 linear kernels against the CPU oracle, bit for bit (reference tests/test_exact_ops.py:137-152,
+tests/test_gemm_skinny.py, tests/test_vllm_exact_gemm.py: shapes, row counts, extremes, magnitude ranges)."""
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import bxref as R
+
+pytestmark = pytest.mark.gpu
+
+
+def _bf16(N, K, seed, force=True):
+    g = torch.Generator().manual_seed(seed)
+    w = (torch.randn(N, K, generator=g) * 0.02).to(torch.bfloat16)
+    if force:
+        w[0, :5] = torch.tensor([1e-9, -3e-8, 0.0, 2.0, -0.5]).to(torch.bfloat16)
+        w[min(3, N - 1), K - 3:] = torch.tensor([3e-7, -1e-6, 1e-10]).to(torch.bfloat16)
+    return w
+
+
+def _dec(w):
+    return R.decompose(w.view(torch.int16).numpy())
+
+
+def _ell(dec, N, dev):
+    cnt, ec, ev, Rr = R.to_ell(dec["rr"], dec["rc"], dec["rv"], N)
+    return (torch.from_numpy(cnt).to(torch.int32).to(dev), torch.from_numpy(ec).to(torch.int32).to(dev),
+            torch.from_numpy(ev).to(dev), Rr)
+
+
+def test_decompose_matches_oracle(dev):
+    from bitexact.exact.consts import decompose
+    for N, K, seed in [(48, 256, 2), (3072, 2048, 5), (7, 64, 9)]:
+        w = _bf16(N, K, seed)
+        ref = _dec(w)
+        got = decompose(w.to(dev))
+        assert np.array_equal(got["limbs"].cpu().numpy(), ref["limbs"])
+        assert np.array_equal(got["g"].cpu().numpy(), ref["g"]) and np.array_equal(got["d"].cpu().numpy(), ref["d"])
+        assert np.array_equal(got["rr"].cpu().numpy(), ref["rr"])
+        assert np.array_equal(got["rc"].cpu().numpy(), ref["rc"])
+        assert np.array_equal(got["rv"].cpu().numpy(), ref["rv"])
+    # an all-zero row and a row of tiny values (residual grid at its limit)
+    w = torch.zeros(4, 128, dtype=torch.bfloat16)
+    w[1, 0], w[1, 5] = 1.0, 2.0 ** -20
+    w[2] = (torch.randn(128) * 1e-30).to(torch.bfloat16)
+    ref = _dec(w)
+    got = decompose(w.to(dev))
+    for k in ("g", "d", "rr", "rc", "rv"):
+        assert np.array_equal(got[k].cpu().numpy(), ref[k]), k
+
+
+@pytest.mark.parametrize("M,N,K", [(1, 256, 2048), (7, 3072, 2048), (37, 512, 8192), (300, 1024, 2048),
+                                   (21, 200, 320), (22, 130, 64)])
+def test_wmm_exact_extremes(dev, M, N, K):
+    from bitexact.exact.wmm import wmm_hip
+    g = np.random.default_rng(M * 1000 + N)
+    q = g.integers(-(1 << 22), (1 << 22) + 1, (M, K))
+    q[0, :] = 1 << 22
+    if M > 1:
+        q[1, :] = -(1 << 22)
+    W = g.integers(-R.LIM3, R.LIM3 + 1, (N, K))
+    W[0, :] = R.LIM3
+    W[-1, :] = -R.LIM3
+    L = np.stack([x.astype(np.int8) for x in R.split_limbs(W, 3)[0]])
+    ref = R.wmm_f64(q, W)
+    T = wmm_hip(torch.from_numpy(q).to(torch.int32).to(dev), torch.from_numpy(L).to(dev))
+    assert T.shape == (1, M, N)
+    assert np.array_equal(T[0].cpu().numpy(), ref)
+
+
+@pytest.mark.parametrize("M", [1, 3, 8, 9, 16, 17, 21, 22, 33, 64, 65, 100, 129, 200])
+def test_exact_linear_matches_oracle(dev, M):
+    from bitexact.vllm_plugin.exact_gemm import exact_linear
+    N, K = 160, 512
+    w = _bf16(N, K, 11)
+    dec = _dec(w)
+    limbs = torch.from_numpy(dec["limbs"]).to(dev)
+    d, gg = torch.from_numpy(dec["d"]).to(dev), torch.from_numpy(dec["g"]).to(dev)
+    cnt, ec, ev, Rr = _ell(dec, N, dev)
+    assert Rr > 0
+    g = np.random.default_rng(M)
+    for lim, shr in ((1 << 22, (-30, -20)), (1 << 12, (-45, -8)), (3, (-70, 10))):
+        q = g.integers(-lim, lim + 1, (M, K))
+        sh = g.integers(shr[0], shr[1], M)
+        ref, rflag, _ = R.epilogue(R.wmm_f64(q, dec["W"]), R.residual(q, dec["rr"], dec["rc"], dec["rv"], N),
+                                   dec["d"], dec["g"], sh, R.FR, True)
+        flag = torch.zeros(1, dtype=torch.int32, device=dev)
+        y = exact_linear(torch.from_numpy(q).to(torch.int32).to(dev), torch.from_numpy(sh).to(dev), limbs, d, gg,
+                         cnt, ec, ev, Rr, flag, True)
+        assert np.array_equal(y.cpu().numpy(), ref), (M, lim)
+        assert bool(flag.item()) == rflag, (M, lim)
+
+
+def test_exact_linear_flag_cases(dev):
+    """The checked epilogue's loss / range flag, per element (reference tests/test_model_bounds.py)."""
+    from bitexact.vllm_plugin.exact_gemm import exact_linear
+    N, K = 64, 64
+    W = np.zeros((N, K), np.int64)
+    W[:, 0] = 1
+    L = torch.from_numpy(np.stack([x.astype(np.int8) for x in R.split_limbs(W, 3)[0]])).to(dev)
+    zeros = torch.zeros(N, dtype=torch.long, device=dev)
+    for value, shift in [(1 << 21, 22), (-(1 << 21), 22), (1 << 20, 30), (5, 31), (-5, 31), (1 << 21, -90),
+                         (12345, -33), (1, 0)]:
+        q = np.zeros((1, K), np.int64)
+        q[0, 0] = value
+        ref, rflag, _ = R.epilogue(R.wmm_f64(q, W), np.zeros((1, N), np.int64), np.zeros(N, np.int64),
+                                   np.zeros(N, np.int64), np.array([shift - R.FR]), R.FR, True)
+        flag = torch.zeros(1, dtype=torch.int32, device=dev)
+        y = exact_linear(torch.from_numpy(q).to(torch.int32).to(dev), torch.tensor([shift - R.FR], device=dev), L,
+                         zeros, zeros, None, None, None, 0, flag, True)
+        assert np.array_equal(y.cpu().numpy(), ref), (value, shift)
+        assert bool(flag.item()) == rflag, (value, shift)
+
+
+def test_config1_exact_linear(dev):
+    """Config 1: M=8, K=N=2048, bf16 N(0, 0.02) weights with forced residuals, FN=40 activations."""
+    from bitexact.exact.consts import decompose
+    from bitexact.vllm_plugin.exact_gemm import exact_linear
+    M, N, K = 8, 2048, 2048
+    w = _bf16(N, K, 1)
+    dec = _dec(w)
+    gd = decompose(w.to(dev))
+    x = torch.randn(M, K, generator=torch.Generator().manual_seed(2), dtype=torch.float64)
+    P = torch.floor(x * 2.0 ** 40 + 0.5).long().numpy()
+    q, sh = R.quant(P, -40)
+    ref, rflag = R.exact_linear(q, dec, sh)
+    flag = torch.zeros(1, dtype=torch.int32, device=dev)
+    y = exact_linear(torch.from_numpy(q).to(torch.int32).to(dev), torch.from_numpy(sh).to(dev), gd["limbs"], gd["d"],
+                     gd["g"], gd["ell_cnt"], gd["ell_col"], gd["ell_val"], gd["R"], flag, True)
+    assert np.array_equal(y.cpu().numpy(), ref) and bool(flag.item()) == rflag
+
+
+@pytest.mark.parametrize("N,K", [(3072, 2048), (2048, 2048), (2048, 8192), (8192, 2048), (512, 256)])
+def test_int_mm_rows(dev, N, K):
+    from bitexact.int8.gemm_skinny import int_mm
+    g = torch.Generator().manual_seed(N + K)
+    w = torch.randint(-128, 128, (N, K), dtype=torch.int8, generator=g)
+    for Rr in (2, 16, 24, 56, 64, 72, 128, 200, 264):
+        for kind in ("rand", "max", "min"):
+            a = torch.randint(-128, 128, (Rr, K), dtype=torch.int8, generator=g)
+            w2 = w
+            if kind == "max":
+                a.fill_(-128)
+                w2 = torch.full_like(w, -128)
+            elif kind == "min":
+                a.fill_(127)
+                w2 = torch.full_like(w, -128)
+            ref = R.imm(a.numpy(), w2.numpy())
+            c = int_mm(a.to(dev), w2.to(dev))
+            assert c.dtype == torch.int32 and np.array_equal(c.cpu().numpy().astype(np.int64), ref), (N, K, Rr, kind)
+
+
+@pytest.mark.parametrize("M", [1, 8, 64, 100])
+@pytest.mark.parametrize("nl", [1, 2, 3])
+def test_int_mm_join(dev, M, nl):
+    from bitexact.int8.gemm_skinny import int_mm_join
+    N, K = 1024, 2048
+    g = np.random.default_rng(M * 10 + nl)
+    z = g.integers(-(1 << 44), 1 << 44, (M, K))
+    q, _, _ = R.quant_rows(z, nl)
+    a = R.stack_limbs(q, nl)
+    w = g.integers(-127, 128, (N, K)).astype(np.int8)
+    ref = R.imm(q, w)
+    y = int_mm_join(torch.from_numpy(a).to(dev), torch.from_numpy(w).to(dev), M, nl)
+    assert np.array_equal(y.cpu().numpy(), ref)
+
+
+@pytest.mark.parametrize("M", [1, 8, 64])
+@pytest.mark.parametrize("N,K", [(8192, 2048), (2048, 8192)])
+def test_config2_int8_decode(dev, M, N, K):
+    """Config 2 shapes at full size: int8 uniform weights, N(0,1) activations in 2 limbs."""
+    from bitexact.int8.gemm_skinny import int_mm_join
+    g = torch.Generator().manual_seed(7)
+    w = torch.randint(-127, 128, (N, K), dtype=torch.int8, generator=g)
+    x = torch.randn(M, K, generator=g, dtype=torch.float64)
+    z = torch.floor(x * 2.0 ** 16 + 0.5).long().numpy()
+    q, _, _ = R.quant_rows(z, 2)
+    a = R.stack_limbs(q, 2)
+    y = int_mm_join(torch.from_numpy(a).to(dev), w.to(dev), M, 2)
+    assert np.array_equal(y.cpu().numpy(), R.imm(q, w.numpy()))
