@@ -22,14 +22,15 @@ SIGNATURES = {
     "bx_version": (ctypes.c_int, []),
     "bx_last_error": (ctypes.c_char_p, []),
     "bx_exact_linear": (ctypes.c_int, [P, I64, P, P, I64, I64, P, P, P, P, P, I32, P, I32, I32, I32, I32, I32, P,
-                                       P, I64, P]),
+                                       P, I64, P, I64, P]),
     "bx_exact_linear_workspace": (I64, [I32, I32, I32]),
-    "bx_exact_wmm": (ctypes.c_int, [P, I64, P, I64, I64, P, I32, I32, I32, P, I64, P]),
+    "bx_exact_linear_scratch": (I64, [I32, I32, I32]),
+    "bx_exact_wmm": (ctypes.c_int, [P, I64, P, I64, I64, P, I32, I32, I32, P, I64, P, I64, P]),
     "bx_decompose_rows": (ctypes.c_int, [P, I32, I32, P, P, P, P, P, P]),
     "bx_decompose_residual": (ctypes.c_int, [P, I32, I32, P, P, P, P, I32, P]),
     "bx_int8_gemm": (ctypes.c_int, [P, P, P, I32, I32, I32, P, I64, P]),
     "bx_int8_gemm_join": (ctypes.c_int, [P, P, P, I32, I32, I32, I32, P, I64, P]),
-    "bx_int8_gemm_workspace": (I64, [I32, I32, I32]),
+    "bx_int8_gemm_workspace": (I64, [I32, I32, I32, I32]),
 }
 
 
@@ -74,17 +75,25 @@ def require_cuda(*ts):
             raise AssertionError("bitexact HIP kernels take device tensors only (no CPU path)")
 
 
-# ---- split-K workspaces: one zero-filled buffer per (device, stream); every call leaves it zeroed ----
+# ---- per (device, stream) buffers: the split-K workspace (zero-filled; every call leaves it zeroed) and a
+# scratch buffer (no contents kept between calls) ----
 _ws = {}
 
 
-def workspace(dev, nbytes):
+def _buffer(kind, dev, nbytes):
     if nbytes <= 0:
         return None, 0
-    s = torch.cuda.current_stream(dev)
-    key = (dev.index, s.cuda_stream)
+    key = (kind, dev.index, torch.cuda.current_stream(dev).cuda_stream)
     buf = _ws.get(key)
     if buf is None or buf.numel() < nbytes:
-        buf = torch.zeros(max(nbytes, 1 << 20), dtype=torch.uint8, device=dev)
+        buf = (torch.zeros if kind == "ws" else torch.empty)(max(nbytes, 1 << 20), dtype=torch.uint8, device=dev)
         _ws[key] = buf
     return buf, buf.numel()
+
+
+def workspace(dev, nbytes):
+    return _buffer("ws", dev, nbytes)
+
+
+def scratch(dev, nbytes):
+    return _buffer("tmp", dev, nbytes)

@@ -19,6 +19,7 @@ def wmm_hip(q, limbs):
     assert limbs.shape[2] == K
     T = torch.empty(1, M, N, dtype=torch.long, device=q.device)
     ws, wsb = _hip.workspace(q.device, _hip.lib().bx_exact_linear_workspace(M, N, K))
+    tmp, tmpb = _hip.scratch(q.device, _hip.lib().bx_exact_linear_scratch(M, N, K))
     _hip.call("bx_exact_wmm", _hip.ptr(q), q.stride(0), _hip.ptr(limbs), limbs.stride(0), limbs.stride(1),
-              _hip.ptr(T), M, N, K, _hip.ptr(ws), wsb, _hip.stream_of(q))
+              _hip.ptr(T), M, N, K, _hip.ptr(ws), wsb, _hip.ptr(tmp), tmpb, _hip.stream_of(q))
     return T

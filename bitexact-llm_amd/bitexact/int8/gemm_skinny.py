@@ -21,7 +21,7 @@ def int_mm(a, w):
     R, K = a.shape
     N = w.shape[0]
     c = torch.empty(R, N, dtype=torch.int32, device=a.device)
-    ws, wsb = _hip.workspace(a.device, _hip.lib().bx_int8_gemm_workspace(R, N, K))
+    ws, wsb = _hip.workspace(a.device, _hip.lib().bx_int8_gemm_workspace(R, N, K, 1))
     _hip.call("bx_int8_gemm", _hip.ptr(a), _hip.ptr(w), _hip.ptr(c), R, N, K, _hip.ptr(ws), wsb, _hip.stream_of(a))
     return c
 
@@ -33,7 +33,7 @@ def int_mm_join(a, w, M, nl):
     N = w.shape[0]
     assert a.shape[0] >= nl * M
     y = torch.empty(M, N, dtype=torch.long, device=a.device)
-    ws, wsb = _hip.workspace(a.device, _hip.lib().bx_int8_gemm_workspace(nl * M, N, K))
+    ws, wsb = _hip.workspace(a.device, _hip.lib().bx_int8_gemm_workspace(M, N, K, nl))
     _hip.call("bx_int8_gemm_join", _hip.ptr(a), _hip.ptr(w), _hip.ptr(y), M, N, K, nl, _hip.ptr(ws), wsb,
               _hip.stream_of(a))
     return y

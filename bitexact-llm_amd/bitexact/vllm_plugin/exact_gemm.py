@@ -22,11 +22,12 @@ def exact_linear(q, sh, limbs, d, g, cnt, ec, ev, R, flag=None, checked=True, fr
         assert flag is not None and flag.dtype == torch.int32
     y = torch.empty(M, N, dtype=torch.long, device=q.device)
     ws, wsb = _hip.workspace(q.device, _hip.lib().bx_exact_linear_workspace(M, N, K))
+    tmp, tmpb = _hip.scratch(q.device, _hip.lib().bx_exact_linear_scratch(M, N, K))
     sh = sh.contiguous()
     _hip.call("bx_exact_linear", _hip.ptr(q), q.stride(0), _hip.ptr(sh), _hip.ptr(limbs), limbs.stride(0),
               limbs.stride(1), _hip.ptr(d), _hip.ptr(g), _hip.ptr(cnt) if R else None,
               _hip.ptr(ec) if R else None, _hip.ptr(ev) if R else None, R, _hip.ptr(y), M, N, K, fr, int(checked),
-              _hip.ptr(flag), _hip.ptr(ws), wsb, _hip.stream_of(q))
+              _hip.ptr(flag), _hip.ptr(ws), wsb, _hip.ptr(tmp), tmpb, _hip.stream_of(q))
     return y
 
 

@@ -91,6 +91,21 @@ __device__ __forceinline__ int64_t exact_round(int64_t T, int64_t B, int64_t d, 
   return y;
 }
 
+// exact_round with a short path for the common case. With k = -p >= d, k <= 62, |T| < 2^59 and |B| < 2^60:
+// floor((T 2^d + B + 2^(k-1)) / 2^k) = floor((T + floor((B + 2^(k-1)) / 2^d)) / 2^(k-d)) (nested floors of
+// power-of-two divisions), every intermediate fits int64, |y| < 2^59, and wmm.epilogue's checked conditions
+// are all false there, so the value and the flag equal the full rule's. Anything else takes the full rule.
+__device__ __forceinline__ int64_t exact_round_fast(int64_t T, int64_t B, int64_t d, int64_t p, bool& bad) {
+  const int64_t k = -p;
+  const bool fast = (k >= d) & (k >= 1) & (k <= 62) & (T < (1LL << 59)) & (T > -(1LL << 59)) & (B < (1LL << 60)) &
+                    (B > -(1LL << 60));
+  if (fast) {
+    bad = false;
+    return (T + ((B + (1LL << (k - 1))) >> d)) >> (k - d);
+  }
+  return exact_round(T, B, d, p, bad);
+}
+
 // ---- wavefront reductions (wave64) ----
 __device__ __forceinline__ int64_t wave_max64(int64_t v) {
 #pragma unroll

@@ -1,18 +1,22 @@
 // Exact-mode limb GEMM and int8-mode GEMM for gfx950.
 //
 // Two kernel families share one epilogue:
-//  * skinny_kernel (decode, <= 64 stacked activation rows): the limb rows of the activations (exact mode:
-//    limb i of q[m] is row i*M+m; int8 mode: the caller's stacked rows) sit in LDS for the block's K slice;
-//    every wave streams 16 weight rows straight from HBM into MFMA B operands (16-byte loads, no LDS), one
-//    v_mfma_i32_16x16x64_i8 per (16-row block, weight plane). Int32 products go through LDS once and are
-//    joined in int64 (sum C_j[i M + m] 2^(8(i+j))). Split-K partials meet in an int64 workspace with atomics;
-//    the last block of a column tile (a device-scope counter) applies the epilogue and re-zeroes workspace
-//    and counter, so one launch does everything.
-//  * wide_kernel (prefill): 32x64 wave tiles of v_mfma_i32_32x32x32_i8 over LDS-staged, double-buffered
-//    64-deep K tiles. Exact mode splits int32 q into 3 int8 limb planes on the way into LDS and runs the
-//    9 limb products into 5 int32 accumulators by limb weight i + j (|acc| <= 3 K 2^14 < 2^31 for
-//    K < 43690), joined in int64 in registers and rounded in the fused epilogue with the sparse residual.
-// Integer sums are exact in any order, so tiles, splits and schedules never change a bit.
+//  * gemv_kernel (decode, <= 64 stacked activation rows). The limb rows of the activations (exact mode: limb i
+//    of q[m] is row i*M+m, split from int32 q while staging; int8 mode: the caller's stacked rows) sit in LDS
+//    for the block's K range. A block is CG column groups x KS k-slices of waves; every wave streams its 16
+//    weight rows straight from HBM into MFMA B operands (unconditional 16-byte loads, U k-steps per group,
+//    two groups in flight), one v_mfma_i32_16x16x64_i8 per (16-row block, weight plane). The first group is
+//    requested before the activations are staged. The k-slices meet in LDS with ds_add (int32 sums are exact:
+//    |sum| <= K 2^14 < 2^31), then the int32 limb products are joined in int64 (sum C_j[i M+m] 2^(8(i+j))).
+//  * tile_kernel (prefill and the 128-row int8 case). A 3-stage LDS ring is filled by asynchronous
+//    global_load_lds_dwordx4 (1 KiB per wave instruction, XOR-swizzled 16-byte chunks so the MFMA operand
+//    reads are bank-conflict free); 32x64 wave tiles of v_mfma_i32_32x32x32_i8 run the NA x NB limb products
+//    into NA + NB - 1 int32 accumulators by limb weight i + j (|acc| <= 3 K 2^14 < 2^31 for K < 43690), joined
+//    in int64 in registers. Exact mode reads int8 limb planes of q written by split_q_kernel.
+// Both split K over blocks when the tile grid is small: partials meet in an int64 workspace with atomics and
+// the last block of a tile (device-scope counter) applies the epilogue and re-zeroes workspace and counter,
+// so one launch does everything. Integer sums are exact in any order, so tiles, splits and schedules never
+// change a bit.
 #include "bx_common.h"
 
 namespace bx {
@@ -22,7 +26,7 @@ enum Mode { RAW32 = 0, JOIN = 1, WMM_T = 2, EXACT = 3 };
 struct LinArgs {
   const int32_t* q;      // exact: q int32 [M, ldq]
   int64_t ldq;
-  const int8_t* a;       // int8 mode: stacked limb rows [rows_a, K]
+  const int8_t* a;       // int8 limb rows: stacked [rows_a, K] (gemv) or planes [NA][M][K] (tile)
   const int8_t* w;       // weight planes
   int64_t ld_plane, ld_row;
   const int64_t* sh;
@@ -39,8 +43,9 @@ struct LinArgs {
   int rows_a;            // stacked activation rows (exact: 3M, JOIN: nl M, RAW32: M)
   int nl;                // JOIN limbs
   int64_t* ws;           // split-K int64 [M, N]
-  int32_t* sem;          // split-K counters, one per column tile
-  int ks;                // K per split (multiple of 64)
+  int32_t* sem;          // split-K counters, one per output tile
+  int ks;                // K bytes per block (multiple of 64)
+  int spw;               // gemv: k steps per wave
 };
 
 // ---- epilogue shared by both kernels: one output element from its exact int64 dense value ----
@@ -64,16 +69,91 @@ __device__ __forceinline__ void finalize(const LinArgs& p, int m, int n, int64_t
     const int64_t dn = p.d[n];
     const int64_t pe = p.sh[m] + p.g[n] - dn + p.FR;
     bool b;
-    ((int64_t*)p.out)[o] = exact_round(v, B, dn, pe, b);
+    ((int64_t*)p.out)[o] = exact_round_fast(v, B, dn, pe, b);
     bad |= b;
   }
+}
+
+// Per-column epilogue context, loaded once per thread when a thread keeps one output column: d, g, and the
+// first kRes residual entries of the column in registers (more entries, rare, are read from memory).
+constexpr int kRes = 4;
+struct ColCtx {
+  int64_t d, gdr;        // d[n] and g[n] - d[n] + FR
+  int cnt;
+  int32_t ec[kRes];
+  int64_t ev[kRes];
+  const int32_t* ecp;
+  const int64_t* evp;
+};
+
+__device__ __forceinline__ ColCtx col_ctx(const LinArgs& p, int n) {
+  ColCtx c;
+  const int nn = min(n, p.N - 1);
+  c.d = p.d[nn];
+  c.gdr = p.g[nn] - c.d + p.FR;
+  c.cnt = p.R > 0 ? p.cnt[nn] : 0;
+  c.ecp = p.ecol + (int64_t)nn * p.R;
+  c.evp = p.eval + (int64_t)nn * p.R;
+#pragma unroll
+  for (int j = 0; j < kRes; ++j) {
+    const bool has = j < c.cnt;
+    c.ec[j] = has ? c.ecp[j] : 0;
+    c.ev[j] = has ? c.evp[j] : 0;
+  }
+  return c;
+}
+
+// The sparse residual B of row m in column cc (segs.lin_y's ELL gather, src/bitexact/exact/segs.py:31).
+__device__ __forceinline__ int64_t residual_col(const LinArgs& p, const ColCtx& cc, int m) {
+  int64_t B = 0;
+  if (cc.cnt > 0) {
+    const int32_t* qr = p.q + (int64_t)m * p.ldq;
+#pragma unroll
+    for (int j = 0; j < kRes; ++j) B = add_wrap(B, mul_wrap((int64_t)qr[cc.ec[j]], cc.ev[j]));   // padded: ev = 0
+    for (int j = kRes; j < cc.cnt; ++j) B = add_wrap(B, mul_wrap((int64_t)qr[cc.ecp[j]], cc.evp[j]));
+  }
+  return B;
+}
+
+__device__ __forceinline__ void finalize_col(const LinArgs& p, const ColCtx& cc, int m, int n, int64_t shm, int64_t v,
+                                             int64_t B, bool& bad) {
+  bool b;
+  ((int64_t*)p.out)[(int64_t)m * p.N + n] = exact_round_fast(v, B, cc.d, shm + cc.gdr, b);
+  bad |= b;
+}
+
+// Split-K handshake: after every thread has added its partials to the workspace, returns true in the last
+// block of tile `tile` (all threads), which then owns the sums; that block also resets the tile counter.
+// The workspace and the counters are only ever accessed with agent-scope read-modify-write atomics, which are
+// performed at the device's coherence point, so no cache flush is needed (an agent-scope fence here would
+// write back and invalidate the XCD's whole L2 in every block): each wave waits until its atomics are
+// acknowledged (s_waitcnt) before the barrier, so every partial is in memory before the counter moves, and the
+// last block reads the sums back with atomic exchanges.
+__device__ __forceinline__ bool splitk_last(const LinArgs& p, int tile, int nsplit, int* s_last) {
+  __builtin_amdgcn_s_waitcnt(0);
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    const bool last = atomicAdd(&p.sem[tile], 1) == nsplit - 1;
+    if (last) atomicExch(&p.sem[tile], 0);
+    *s_last = last;
+  }
+  __syncthreads();
+  return *s_last;
+}
+
+__device__ __forceinline__ int64_t ws_take(const LinArgs& p, int m, int n) {
+  return (int64_t)atomicExch((unsigned long long*)&p.ws[(int64_t)m * p.N + n], 0ull);
+}
+
+__device__ __forceinline__ void ws_add(const LinArgs& p, int m, int n, int64_t v) {
+  atomicAdd((unsigned long long*)&p.ws[(int64_t)m * p.N + n], (unsigned long long)v);
 }
 
 __device__ __forceinline__ uint32_t pack4(int32_t a, int32_t b, int32_t c, int32_t d) {
   return (uint32_t)(a & 255) | ((uint32_t)(b & 255) << 8) | ((uint32_t)(c & 255) << 16) | ((uint32_t)(d & 255) << 24);
 }
 
-// Three int8 limb words (4 values each) of 4 int32 values.
+// Three int8 limb words (4 values each) of 4 int32 values (intops.split_limbs, src/bitexact/intops.py:62-70).
 __device__ __forceinline__ void split3(v4i v, uint32_t& l0, uint32_t& l1, uint32_t& l2) {
   int32_t a0[4], a1[4], a2[4];
 #pragma unroll
@@ -90,344 +170,571 @@ __device__ __forceinline__ void split3(v4i v, uint32_t& l0, uint32_t& l1, uint32
   l2 = pack4(a2[0], a2[1], a2[2], a2[3]);
 }
 
-// =====================================================================================================
-// skinny kernel: 256 threads, 4 waves x 16 weight rows = 64 output columns per block, grid (N/64, splits)
-// =====================================================================================================
-constexpr int kSkU = 4;   // k steps of 64 in flight per wave
+// Ring-stage barrier: wait until at most n of this wave's vector memory operations (the asynchronous LDS
+// loads of later stages) are outstanding and all its LDS reads are done (gfx9 s_waitcnt encoding: vmcnt <= n,
+// lgkmcnt = 0), then a bare s_barrier. __syncthreads() would add a release fence, i.e. vmcnt(0), and drain
+// the whole ring every iteration; the memory clobber keeps the compiler from moving LDS accesses across.
+template <int n>
+__device__ __forceinline__ void ring_barrier() {
+  static_assert(n >= 0 && n < 64, "vmcnt range");
+  __builtin_amdgcn_s_waitcnt((n & 15) | ((n >> 4) << 14) | (7 << 4));
+  asm volatile("s_barrier" ::: "memory");
+}
 
-template <int NB, int RB, int MODE>
-__global__ __launch_bounds__(256) void skinny_kernel(LinArgs p) {
-  extern __shared__ __align__(16) char smem[];
-  __shared__ int s_last;
-  constexpr int RA = 16 * RB;
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int n0 = blockIdx.x * 64;
-  const int k0 = blockIdx.y * p.ks;
-  const int kend = min(p.K, k0 + p.ks);
-  const int kpad = ((kend - k0) + 63) & ~63;
-  const int LDA = kpad + 16;
-  int8_t* As = (int8_t*)smem;
-
-  // ---- stage the activation limb rows of this K slice in LDS ----
+// =====================================================================================================
+// gemv kernel (decode)
+// =====================================================================================================
+template <int RA, int MODE, int NT>
+__device__ __forceinline__ void stage_a(const LinArgs& p, int8_t* As, int k0, int kend, int kpad, int LDA) {
+  const int tid = threadIdx.x;
   if (MODE == EXACT || MODE == WMM_T) {
-    const int nq = kpad >> 2;
-    for (int c = tid; c < p.M * nq; c += 256) {
-      const int m = c / nq, kq = c - m * nq, k = k0 + kq * 4;
-      v4i v = {0, 0, 0, 0};
-      if (k < kend) v = *(const v4i*)(p.q + (int64_t)m * p.ldq + k);
-      uint32_t l0, l1, l2;
-      split3(v, l0, l1, l2);
-      *(uint32_t*)(As + (0 * p.M + m) * LDA + kq * 4) = l0;
-      *(uint32_t*)(As + (1 * p.M + m) * LDA + kq * 4) = l1;
-      *(uint32_t*)(As + (2 * p.M + m) * LDA + kq * 4) = l2;
+    const int nq = kpad >> 2, total = p.M * nq;
+    for (int c0 = tid; c0 < total; c0 += NT * 4) {
+      v4i v[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {   // unconditional (clamped) loads, then select: no per-lane branches
+        const int c = min(c0 + i * NT, total - 1), m = c / nq, k = k0 + (c - m * nq) * 4;
+        v[i] = *(const v4i*)(p.q + (int64_t)m * p.ldq + min(k, p.K - 4));
+      }
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int c = c0 + i * NT;
+        if (c < total) {
+          const int m = c / nq, kq = c - m * nq;
+          uint32_t l0 = 0, l1 = 0, l2 = 0;
+          if (k0 + kq * 4 < kend) split3(v[i], l0, l1, l2);
+          *(uint32_t*)(As + (0 * p.M + m) * LDA + kq * 4) = l0;
+          *(uint32_t*)(As + (1 * p.M + m) * LDA + kq * 4) = l1;
+          *(uint32_t*)(As + (2 * p.M + m) * LDA + kq * 4) = l2;
+        }
+      }
     }
     const int nc = kpad >> 4;
-    for (int c = tid; c < (RA - 3 * p.M) * nc; c += 256) {
+    for (int c = tid; c < (RA - 3 * p.M) * nc; c += NT) {
       const int r = 3 * p.M + c / nc, kc = c % nc;
       *(v4i*)(As + r * LDA + kc * 16) = v4i{0, 0, 0, 0};
     }
   } else {
-    const int nc = kpad >> 4;
-    for (int c = tid; c < RA * nc; c += 256) {
-      const int r = c / nc, kc = c - r * nc, k = k0 + kc * 16;
-      v4i v = {0, 0, 0, 0};
-      if (r < p.rows_a && k < kend) v = *(const v4i*)(p.a + (int64_t)r * p.K + k);
-      *(v4i*)(As + r * LDA + kc * 16) = v;
+    const int nc = kpad >> 4, total = RA * nc;
+    for (int c0 = tid; c0 < total; c0 += NT * 4) {
+      v4i v[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int c = min(c0 + i * NT, total - 1), r = min(c / nc, p.rows_a - 1), k = k0 + (c % nc) * 16;
+        v[i] = *(const v4i*)(p.a + (int64_t)r * p.K + min(k, p.K - 16));
+      }
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int c = c0 + i * NT;
+        if (c < total) {
+          const int r = c / nc, kc = c - r * nc;
+          const bool ok = r < p.rows_a && k0 + kc * 16 < kend;
+          *(v4i*)(As + r * LDA + kc * 16) = ok ? v[i] : v4i{0, 0, 0, 0};
+        }
+      }
     }
   }
-  __syncthreads();
+}
 
-  // ---- stream weights: lane -> weight row n (= MFMA B column), 16 bytes at k = 16 (lane / 16) ----
-  const int nrow = n0 + wave * 16 + (lane & 15);
-  const bool nok = nrow < p.N;
+template <int NB, int RB, int CG, int KS, int U, int MODE>
+__global__ __launch_bounds__(64 * CG * KS) void gemv_kernel(LinArgs p) {
+  constexpr int NT = 64 * CG * KS, RA = 16 * RB, BNC = 16 * CG;
+  extern __shared__ __align__(16) char smem[];
+  __shared__ int s_last;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int cg = wave % CG, kslice = wave / CG;
+  const int n0 = blockIdx.x * BNC;
+  const int k0 = blockIdx.y * p.ks;
+  const int kend = min(p.K, k0 + p.ks);
+  const int nst = (kend - k0 + 63) >> 6;           // k steps of 64 in this block
+  const int kpad = nst * 64;
+  const int LDA = kpad + 16;
+  int8_t* As = (int8_t*)smem;
+  int32_t* Cs = (int32_t*)(smem + ((RA * LDA + 15) & ~15));   // [NB][RA][BNC]
+
+  // this wave's weight row and k steps [s0, s1)
   const int kl = (lane >> 4) * 16;
-  const int8_t* wrow = p.w + (int64_t)(nok ? nrow : 0) * p.ld_row;
-  const int8_t* arow = As + (lane & 15) * LDA + kl;
+  const int8_t* wrow = p.w + (int64_t)min(n0 + cg * 16 + (lane & 15), p.N - 1) * p.ld_row;
+  const int s0 = kslice * p.spw, s1 = min(nst, s0 + p.spw);
+  const int ngroups = s1 > s0 ? (s1 - s0 + U - 1) / U : 0;
+  const int kmax = p.K - 16;
+  auto issue = [&](v4i(&b)[U][NB], int s) {
+#pragma unroll
+    for (int u = 0; u < U; ++u)
+#pragma unroll
+      for (int j = 0; j < NB; ++j)
+        b[u][j] = *(const v4i*)(wrow + j * p.ld_plane + min(k0 + (s + u) * 64 + kl, kmax));
+  };
   v4i acc[RB][NB];
 #pragma unroll
   for (int r = 0; r < RB; ++r)
 #pragma unroll
     for (int j = 0; j < NB; ++j) acc[r][j] = v4i{0, 0, 0, 0};
-
-  for (int kk = 0; kk < kpad; kk += 64 * kSkU) {
-    v4i b[kSkU][NB];
+  const int8_t* arow = As + (lane & 15) * LDA + kl;
+  auto compute = [&](v4i(&b)[U][NB], int s) {
 #pragma unroll
-    for (int u = 0; u < kSkU; ++u) {
-      const int k = k0 + kk + u * 64 + kl;
-#pragma unroll
-      for (int j = 0; j < NB; ++j)
-        b[u][j] = (nok && k < kend) ? *(const v4i*)(wrow + j * p.ld_plane + k) : v4i{0, 0, 0, 0};
-    }
-#pragma unroll
-    for (int u = 0; u < kSkU; ++u) {
-      if (kk + u * 64 < kpad) {
+    for (int u = 0; u < U; ++u) {
+      if (s + u < s1) {
 #pragma unroll
         for (int r = 0; r < RB; ++r) {
-          const v4i av = *(const v4i*)(arow + r * 16 * LDA + kk + u * 64);
+          const v4i av = *(const v4i*)(arow + r * 16 * LDA + (s + u) * 64);
 #pragma unroll
           for (int j = 0; j < NB; ++j) acc[r][j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(av, b[u][j], acc[r][j], 0, 0, 0);
         }
       }
     }
-  }
+  };
+
+  v4i b0[U][NB], b1[U][NB];
+  if (ngroups > 0) issue(b0, s0);                   // weights in flight while the activations are staged
+  stage_a<RA, MODE, NT>(p, As, k0, kend, kpad, LDA);
+  for (int i = tid; i < NB * RA * BNC; i += NT) Cs[i] = 0;
   __syncthreads();
 
-  // ---- int32 products to LDS: Cs[j][row][col], row = MFMA row (stacked limb row), col in [0, 64) ----
-  int32_t* Cs = (int32_t*)smem;
+  for (int gi = 0; gi < ngroups; gi += 2) {
+    const int sa = s0 + gi * U, sb = sa + U;
+    if (gi + 1 < ngroups) issue(b1, sb);
+    compute(b0, sa);
+    if (gi + 2 < ngroups) issue(b0, sb + U);
+    if (gi + 1 < ngroups) compute(b1, sb);
+  }
+
+  // ---- reduce the k-slices in LDS: Cs[j][row][col] += acc (row = stacked limb row, col in [0, BNC)) ----
 #pragma unroll
   for (int r = 0; r < RB; ++r)
 #pragma unroll
     for (int j = 0; j < NB; ++j)
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
-        const int row = r * 16 + (lane >> 4) * 4 + e, col = wave * 16 + (lane & 15);
-        Cs[(j * RA + row) * 64 + col] = acc[r][j][e];
+        const int row = r * 16 + (lane >> 4) * 4 + e, col = cg * 16 + (lane & 15);
+        if (KS == 1)
+          Cs[(j * RA + row) * BNC + col] = acc[r][j][e];
+        else
+          atomicAdd(&Cs[(j * RA + row) * BNC + col], acc[r][j][e]);
       }
   __syncthreads();
 
   bool bad = false;
-  const bool split = gridDim.y > 1;
-  for (int e = tid; e < p.M * 64; e += 256) {
-    const int m = e >> 6, c = e & 63, n = n0 + c;
+  const int nsplit = gridDim.y;
+  for (int e = tid; e < p.M * BNC; e += NT) {
+    const int m = e / BNC, c = e - m * BNC, n = n0 + c;
     if (n >= p.N) continue;
     int64_t v;
     if (MODE == RAW32) {
-      v = Cs[m * 64 + c];
+      v = Cs[m * BNC + c];
     } else if (MODE == JOIN) {
       v = 0;
-      for (int i = 0; i < p.nl; ++i) v += (int64_t)Cs[(i * p.M + m) * 64 + c] << (8 * i);
+      for (int i = 0; i < p.nl; ++i) v += (int64_t)Cs[(i * p.M + m) * BNC + c] << (8 * i);
     } else {
       v = 0;
 #pragma unroll
       for (int i = 0; i < 3; ++i)
 #pragma unroll
-        for (int j = 0; j < NB; ++j) v += (int64_t)Cs[(j * RA + i * p.M + m) * 64 + c] << (8 * (i + j));
+        for (int j = 0; j < NB; ++j) v += (int64_t)Cs[(j * RA + i * p.M + m) * BNC + c] << (8 * (i + j));
     }
-    if (split)
-      atomicAdd((unsigned long long*)&p.ws[(int64_t)m * p.N + n], (unsigned long long)v);
+    if (nsplit > 1)
+      ws_add(p, m, n, v);
     else
       finalize<MODE>(p, m, n, v, bad);
   }
-  if (split) {
-    __threadfence();
-    __syncthreads();
-    if (tid == 0) s_last = atomicAdd(&p.sem[blockIdx.x], 1) == (int)gridDim.y - 1;
-    __syncthreads();
-    if (s_last) {
-      __threadfence();
-      for (int e = tid; e < p.M * 64; e += 256) {
-        const int m = e >> 6, n = n0 + (e & 63);
-        if (n >= p.N) continue;
-        const int64_t v = (int64_t)atomicExch((unsigned long long*)&p.ws[(int64_t)m * p.N + n], 0ull);
-        finalize<MODE>(p, m, n, v, bad);
-      }
-      if (tid == 0) atomicExch(&p.sem[blockIdx.x], 0);
+  if (nsplit > 1 && splitk_last(p, blockIdx.x, nsplit, &s_last)) {
+    for (int e = tid; e < p.M * BNC; e += NT) {
+      const int m = e / BNC, n = n0 + (e - m * BNC);
+      if (n < p.N) finalize<MODE>(p, m, n, ws_take(p, m, n), bad);
     }
   }
   if (MODE == EXACT && p.checked && bad) p.flag[0] = 1;
 }
 
 // =====================================================================================================
-// wide kernel: WM x WN waves, wave tile 32 x 64 (two 32x32 MFMA column blocks), BK = 64, 2 LDS stages
+// split q into int8 limb planes (tile-kernel input): planes [3][M][K]
 // =====================================================================================================
-constexpr int kRow = 80;   // LDS bytes per 64-byte operand row (16 bytes of padding: conflict-free b128 reads)
+__global__ __launch_bounds__(256) void split_q_kernel(const int32_t* q, int64_t ldq, int M, int K, int8_t* planes) {
+  const int nk = K >> 4;
+  const int64_t total = (int64_t)M * nk, plane = (int64_t)M * K;
+  for (int64_t c = blockIdx.x * 256LL + threadIdx.x; c < total; c += (int64_t)gridDim.x * 256) {
+    const int m = (int)(c / nk), k = (int)(c - (int64_t)m * nk) * 16;
+    const int32_t* src = q + (int64_t)m * ldq + k;
+    v4i o0, o1, o2;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      uint32_t l0, l1, l2;
+      split3(*(const v4i*)(src + 4 * i), l0, l1, l2);
+      o0[i] = (int32_t)l0;
+      o1[i] = (int32_t)l1;
+      o2[i] = (int32_t)l2;
+    }
+    int8_t* dst = planes + (int64_t)m * K + k;
+    *(v4i*)dst = o0;
+    *(v4i*)(dst + plane) = o1;
+    *(v4i*)(dst + 2 * plane) = o2;
+  }
+}
 
-template <int NA, int NB, int MODE, int WM, int WN>
-__global__ __launch_bounds__(WM * WN * 64) void wide_kernel(LinArgs p) {
-  constexpr int NT = WM * WN * 64;
-  constexpr int BM = 32 * WM, BN = 64 * WN;
+// =====================================================================================================
+// tile kernel (prefill): WM x WN waves, wave tile (32 TM) x (32 TN), BK = 64, S-stage async LDS ring,
+// grid (N / BN, M / BM, splits)
+// =====================================================================================================
+// 16-byte chunk swizzle of a BK-byte LDS row (CH = BK / 16 chunks): rows that share LDS banks get different
+// chunk slots, so the 16 lanes of each MFMA operand read phase hit 16 distinct bank groups.
+template <int BK>
+__device__ __forceinline__ int swz(int row) {
+  return BK == 64 ? (row >> 2) & 3 : (row >> 3) & 1;
+}
+
+__device__ __forceinline__ void async16(const void* g, void* lds_base) {
+  __builtin_amdgcn_global_load_lds((const void __attribute__((address_space(1)))*)g,
+                                   (void __attribute__((address_space(3)))*)lds_base, 16, 0, 0);
+}
+
+template <int NA, int NB, int MODE, int WM, int WN, int TM, int TN, int BK, int S>
+__global__ __launch_bounds__(WM * WN * 64) void tile_kernel(LinArgs p) {
+  static_assert(BK == 32 || BK == 64, "k tile");
+  constexpr int NW = WM * WN;
+  constexpr int BM = 32 * TM * WM, BN = 32 * TN * WN;
   constexpr int NS = NA + NB - 1;
-  constexpr bool AQ = (MODE == EXACT || MODE == WMM_T);
-  constexpr int A_BYTES = NA * BM * kRow, STAGE = (NA * BM + NB * BN) * kRow;
-  constexpr int CA = AQ ? (BM * 16) / NT : (NA * BM * 4) / NT;   // 16-byte A source chunks per thread
-  constexpr int CB = (NB * BN * 4) / NT;                          // 16-byte B chunks per thread
-  static_assert(CA * NT == (AQ ? BM * 16 : NA * BM * 4) && CB * NT == NB * BN * 4, "tile/thread mismatch");
+  constexpr int CH = BK / 16, RPI = 1024 / BK;                 // chunks per row, rows per 1 KiB instruction
+  constexpr int SA = NA * BM * BK, STAGE = SA + NB * BN * BK;
+  constexpr int LA = NA * BM / RPI, LT = LA + NB * BN / RPI;   // 1 KiB load instructions per stage
+  constexpr int LWL = LT / NW, LWX = LT % NW;                 // per wave: LWL + 1 for the first LWX waves
+  static_assert((LWL + (LWX > 0)) * (S - 2) < 64, "vmcnt range");
   extern __shared__ __align__(16) char smem[];
+  __shared__ int s_last;
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int wm = wave % WM, wn = wave / WM;
   const int m0 = blockIdx.y * BM, n0 = blockIdx.x * BN;
-  const int nk = (p.K + 63) >> 6;
+  const int kt0 = blockIdx.z * (p.ks / BK);
+  const int nk = min((p.K + BK - 1) / BK, kt0 + p.ks / BK) - kt0;
+  const int ktail = p.K / BK;                 // first k tile that reaches past K (only when K % BK != 0)
 
-  v4i ra[CA], rb[CB];
-  auto load = [&](int kt) {
+  // Each 1 KiB load instruction covers RPI rows x BK bytes: lane L -> row L / CH of the group, LDS slot L % CH,
+  // global chunk (L % CH) ^ swz(row); swz only sees row bits that are the same for every instruction, so the
+  // lane's chunk is fixed. Rows past M / N are clamped (discarded in the epilogue); k chunks past K are clamped
+  // and zeroed in the A operand so they contribute nothing. Addresses are recomputed per issue (few VALU ops)
+  // rather than held in registers next to the accumulators.
+  const int lrow = lane / CH;
+  const int lch = ((lane % CH) ^ swz<BK>(lrow)) << 4;
+  const int64_t aplane = (int64_t)p.M * p.K;
+  const bool xwave = wave < LWX;
+  const int inst0 = xwave ? wave * (LWL + 1) : LWX * (LWL + 1) + (wave - LWX) * LWL;
+  auto issue = [&](int kt, int stage) {
+    char* sbase = smem + stage * STAGE + inst0 * 1024;
+    const int kk = min(kt * BK + lch, p.K - 16);
 #pragma unroll
-    for (int i = 0; i < CA; ++i) {
-      const int c = tid + i * NT;
-      if (AQ) {
-        const int row = c >> 4, kq = c & 15, m = m0 + row, k = kt * 64 + kq * 4;
-        ra[i] = (m < p.M && k < p.K) ? *(const v4i*)(p.q + (int64_t)m * p.ldq + k) : v4i{0, 0, 0, 0};
+    for (int i = 0; i < LWL + (LWX > 0); ++i) {
+      if (i == LWL && !xwave) break;
+      const int inst = inst0 + i;
+      const int8_t* src;
+      if (inst < LA) {
+        const int pl = inst / (BM / RPI), row = (inst % (BM / RPI)) * RPI + lrow;
+        src = p.a + pl * aplane + (int64_t)min(m0 + row, p.M - 1) * p.K + kk;
       } else {
-        const int pl = c / (BM * 4), rem = c - pl * (BM * 4), row = rem >> 2, kc = rem & 3;
-        const int m = m0 + row, k = kt * 64 + kc * 16;
-        ra[i] = (m < p.M && k < p.K) ? *(const v4i*)(p.a + ((int64_t)pl * p.M + m) * p.K + k) : v4i{0, 0, 0, 0};
+        const int ib = inst - LA, pl = ib / (BN / RPI), row = (ib % (BN / RPI)) * RPI + lrow;
+        src = p.w + pl * p.ld_plane + (int64_t)min(n0 + row, p.N - 1) * p.ld_row + kk;
       }
-    }
-#pragma unroll
-    for (int i = 0; i < CB; ++i) {
-      const int c = tid + i * NT;
-      const int pl = c / (BN * 4), rem = c - pl * (BN * 4), row = rem >> 2, kc = rem & 3;
-      const int n = n0 + row, k = kt * 64 + kc * 16;
-      rb[i] = (n < p.N && k < p.K) ? *(const v4i*)(p.w + pl * p.ld_plane + (int64_t)n * p.ld_row + k)
-                                   : v4i{0, 0, 0, 0};
-    }
-  };
-  auto store = [&](int s) {
-    char* base = smem + s * STAGE;
-#pragma unroll
-    for (int i = 0; i < CA; ++i) {
-      const int c = tid + i * NT;
-      if (AQ) {
-        const int row = c >> 4, kq = c & 15;
-        uint32_t l0, l1, l2;
-        split3(ra[i], l0, l1, l2);
-        *(uint32_t*)(base + 0 * BM * kRow + row * kRow + kq * 4) = l0;
-        *(uint32_t*)(base + 1 * BM * kRow + row * kRow + kq * 4) = l1;
-        *(uint32_t*)(base + 2 * BM * kRow + row * kRow + kq * 4) = l2;
-      } else {
-        const int pl = c / (BM * 4), rem = c - pl * (BM * 4), row = rem >> 2, kc = rem & 3;
-        *(v4i*)(base + pl * BM * kRow + row * kRow + kc * 16) = ra[i];
-      }
-    }
-#pragma unroll
-    for (int i = 0; i < CB; ++i) {
-      const int c = tid + i * NT;
-      const int pl = c / (BN * 4), rem = c - pl * (BN * 4), row = rem >> 2, kc = rem & 3;
-      *(v4i*)(base + A_BYTES + pl * BN * kRow + row * kRow + kc * 16) = rb[i];
+      async16(src, sbase + i * 1024);
     }
   };
 
-  v16i acc[NS][2];
+  v16i acc[NS][TM][TN];
 #pragma unroll
   for (int s = 0; s < NS; ++s)
 #pragma unroll
-    for (int t = 0; t < 2; ++t)
+    for (int a = 0; a < TM; ++a)
 #pragma unroll
-      for (int e = 0; e < 16; ++e) acc[s][t][e] = 0;
+      for (int t = 0; t < TN; ++t)
+#pragma unroll
+        for (int e = 0; e < 16; ++e) acc[s][a][t][e] = 0;
 
-  load(0);
-  store(0);
-  __syncthreads();
-  for (int kt = 0; kt < nk; ++kt) {
-    if (kt + 1 < nk) load(kt + 1);
-    const char* base = smem + (kt & 1) * STAGE;
 #pragma unroll
-    for (int h = 0; h < 2; ++h) {
-      const int koff = h * 32 + (lane >> 5) * 16;
-      v4i av[NA], bv[NB][2];
+  for (int t = 0; t < S - 1; ++t)
+    if (t < nk) issue(kt0 + t, t);
+
+  for (int it = 0; it < nk; ++it) {
+    if (it + S - 2 >= nk) {
+      ring_barrier<0>();
+    } else if constexpr (LWX == 0) {
+      ring_barrier<LWL * (S - 2)>();
+    } else {
+      if (xwave)
+        ring_barrier<(LWL + 1) * (S - 2)>();
+      else
+        ring_barrier<LWL * (S - 2)>();
+    }
+    if (it + S - 1 < nk) issue(kt0 + it + S - 1, (it + S - 1) % S);
+    const char* base = smem + (it % S) * STAGE;
+    const int kt = kt0 + it;
 #pragma unroll
-      for (int i = 0; i < NA; ++i) av[i] = *(const v4i*)(base + i * BM * kRow + (wm * 32 + (lane & 31)) * kRow + koff);
+    for (int h = 0; h < BK / 32; ++h) {
+      const int c = 2 * h + (lane >> 5);
+      const bool kok = kt < ktail || kt * BK + c * 16 < p.K;
+      v4i av[NA][TM], bv[NB][TN];
+#pragma unroll
+      for (int i = 0; i < NA; ++i)
+#pragma unroll
+        for (int a = 0; a < TM; ++a) {
+          const int arow = (wm * TM + a) * 32 + (lane & 31);
+          av[i][a] = *(const v4i*)(base + i * BM * BK + arow * BK + ((c ^ swz<BK>(arow)) << 4));
+          if (!kok) av[i][a] = v4i{0, 0, 0, 0};
+        }
 #pragma unroll
       for (int j = 0; j < NB; ++j)
 #pragma unroll
-        for (int t = 0; t < 2; ++t)
-          bv[j][t] = *(const v4i*)(base + A_BYTES + j * BN * kRow + (wn * 64 + t * 32 + (lane & 31)) * kRow + koff);
+        for (int t = 0; t < TN; ++t) {
+          const int brow = (wn * TN + t) * 32 + (lane & 31);
+          bv[j][t] = *(const v4i*)(base + SA + j * BN * BK + brow * BK + ((c ^ swz<BK>(brow)) << 4));
+        }
 #pragma unroll
       for (int i = 0; i < NA; ++i)
 #pragma unroll
         for (int j = 0; j < NB; ++j)
 #pragma unroll
-          for (int t = 0; t < 2; ++t)
-            acc[i + j][t] = __builtin_amdgcn_mfma_i32_32x32x32_i8(av[i], bv[j][t], acc[i + j][t], 0, 0, 0);
+          for (int a = 0; a < TM; ++a)
+#pragma unroll
+            for (int t = 0; t < TN; ++t)
+              acc[i + j][a][t] = __builtin_amdgcn_mfma_i32_32x32x32_i8(av[i][a], bv[j][t], acc[i + j][a][t], 0, 0, 0);
     }
-    if (kt + 1 < nk) store((kt + 1) & 1);
-    __syncthreads();
   }
 
+  // ---- epilogue straight from the accumulators: lane (l % 32) owns column (wn TN + t) 32 + l % 32 of each
+  // 32-column block t, so the column contexts (d, g, residual list) stay in registers; the row exponents are
+  // read from LDS. Stores of 32 lanes cover 256 contiguous bytes of a row. ----
+  __shared__ int64_t s_sh[MODE == EXACT ? BM : 1];
+  if (MODE == EXACT)
+    for (int r = tid; r < BM; r += NW * 64) s_sh[r] = p.sh[min(m0 + r, p.M - 1)];
+  __syncthreads();
   bool bad = false;
+  const int nsplit = gridDim.z;
+  ColCtx cc[TN];
+  if (MODE == EXACT)
 #pragma unroll
-  for (int t = 0; t < 2; ++t)
+    for (int t = 0; t < TN; ++t) cc[t] = col_ctx(p, n0 + (wn * TN + t) * 32 + (lane & 31));
 #pragma unroll
-    for (int e = 0; e < 16; ++e) {
-      const int m = m0 + wm * 32 + (e >> 2) * 8 + (lane >> 5) * 4 + (e & 3);
-      const int n = n0 + wn * 64 + t * 32 + (lane & 31);
-      if (m < p.M && n < p.N) {
-        int64_t v = 0;
+  for (int a = 0; a < TM; ++a)
 #pragma unroll
-        for (int s = 0; s < NS; ++s) v += (int64_t)acc[s][t][e] << (8 * s);
-        finalize<MODE>(p, m, n, v, bad);
+    for (int t = 0; t < TN; ++t) {
+      const int n = n0 + (wn * TN + t) * 32 + (lane & 31);
+#pragma unroll
+      for (int e0 = 0; e0 < 16; e0 += 4) {
+        int64_t v[4], B[4];
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+          const int e = e0 + u, r = (wm * TM + a) * 32 + (e >> 2) * 8 + (lane >> 5) * 4 + (e & 3);
+          v[u] = 0;
+#pragma unroll
+          for (int s2 = 0; s2 < NS; ++s2) v[u] += (int64_t)acc[s2][a][t][e] << (8 * s2);
+          B[u] = (MODE == EXACT && nsplit == 1 && n < p.N && m0 + r < p.M) ? residual_col(p, cc[t], m0 + r) : 0;
+        }
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+          const int e = e0 + u, r = (wm * TM + a) * 32 + (e >> 2) * 8 + (lane >> 5) * 4 + (e & 3), m = m0 + r;
+          if (m < p.M && n < p.N) {
+            if (nsplit > 1)
+              ws_add(p, m, n, v[u]);
+            else if (MODE == EXACT)
+              finalize_col(p, cc[t], m, n, s_sh[r], v[u], B[u], bad);
+            else
+              finalize<MODE>(p, m, n, v[u], bad);
+          }
+        }
       }
     }
+  if (nsplit > 1 && splitk_last(p, blockIdx.y * gridDim.x + blockIdx.x, nsplit, &s_last)) {
+#pragma unroll
+    for (int a = 0; a < TM; ++a)
+#pragma unroll
+      for (int t = 0; t < TN; ++t) {
+        const int n = n0 + (wn * TN + t) * 32 + (lane & 31);
+#pragma unroll
+        for (int e = 0; e < 16; ++e) {
+          const int r = (wm * TM + a) * 32 + (e >> 2) * 8 + (lane >> 5) * 4 + (e & 3), m = m0 + r;
+          if (m < p.M && n < p.N) {
+            const int64_t v = ws_take(p, m, n);
+            if (MODE == EXACT)
+              finalize_col(p, cc[t], m, n, s_sh[r], v, residual_col(p, cc[t], m), bad);
+            else
+              finalize<MODE>(p, m, n, v, bad);
+          }
+        }
+      }
+  }
   if (MODE == EXACT && p.checked && bad) p.flag[0] = 1;
 }
 
 // =====================================================================================================
-// host dispatch
+// host planning and dispatch
 // =====================================================================================================
-struct SkinnyPlan {
-  int rb, split, ks, tiles;
+// tile configurations: (WM, WN, TM, TN, S)
+enum TileCfg { T_BIG = 0, T_MID = 1, T_NARROW = 2 };
+struct TileShape {
+  int wm, wn, tm, tn, bk, stages;
+};
+static const TileShape kTiles[3] = {{2, 2, 2, 2, 64, 3},    // 128 x 128, 64x64 wave tiles (prefill)
+                                    {2, 2, 1, 2, 64, 3},    // 64 x 128 (few tiles)
+                                    {2, 1, 1, 1, 64, 8}};   // 64 x 32, deep ring (<= 64 output rows, decode)
+static const TileShape kTileExact = {4, 2, 1, 2, 64, 3};   // 5 accumulator sets: 32x64 wave tiles
+
+struct Plan {
+  bool gemv;
+  int rb, cg, ks_waves, u, spw;   // gemv
+  int tile;                       // tile config
+  int tiles_x, tiles_y, split, kbytes;
   size_t lds;
-  int64_t ws_bytes;
+  int64_t ws_bytes;               // zero-invariant split-K region
+  int64_t tmp_bytes;              // scratch (exact tile path: q limb planes)
 };
 
-static SkinnyPlan plan_skinny(int rows_a, int M_out, int N, int K, int nb) {
-  SkinnyPlan s;
-  s.rb = rows_a <= 16 ? 1 : rows_a <= 32 ? 2 : 4;
-  const int RA = 16 * s.rb;
-  s.tiles = (N + 63) / 64;
-  const int nk = (K + 63) / 64;
-  const int target = 2 * device_cus();
-  int split = (target + s.tiles - 1) / s.tiles;
-  split = split < 1 ? 1 : split > nk ? nk : split;
-  int kstep = (nk + split - 1) / split;
-  const int kmax = ((65536 / RA) - 16) / 64;   // A slice in LDS <= 64 KiB
-  if (kstep > kmax) kstep = kmax;
-  s.ks = kstep * 64;
-  s.split = (K + s.ks - 1) / s.ks;
-  const size_t a_lds = (size_t)RA * (s.ks + 16), c_lds = (size_t)nb * RA * 64 * 4;
-  s.lds = a_lds > c_lds ? a_lds : c_lds;
-  s.ws_bytes = s.split > 1 ? (int64_t)M_out * N * 8 + 256 + (int64_t)s.tiles * 4 : 0;
+static int64_t ws_size(int M_out, int N, int tiles) {
+  return (((int64_t)M_out * N * 8 + 255) & ~255LL) + (int64_t)tiles * 4;
+}
+
+// rows_a: stacked activation rows; nb: weight planes (exact 3, int8 1); na: activation planes on the tile path
+static Plan make_plan(int rows_a, int M_out, int N, int K, int nb, int na, bool exact) {
+  Plan s = {};
+  const int cus = device_cus();
+  const int nst = (K + 63) / 64;
+  if (rows_a <= 64) {
+    s.gemv = true;
+    s.rb = rows_a <= 16 ? 1 : rows_a <= 32 ? 2 : 4;
+    const int RA = 16 * s.rb;
+    s.cg = (N + 31) / 32 >= cus ? 2 : 1;
+    s.ks_waves = 16 / s.cg;
+    const int BNC = 16 * s.cg;
+    s.tiles_x = (N + BNC - 1) / BNC;
+    s.tiles_y = 1;
+    int split = 2 * s.tiles_x >= cus ? 1 : (cus + s.tiles_x - 1) / s.tiles_x;
+    // the activation slice must fit LDS (<= 96 KiB with the partial sums)
+    const size_t c_lds = (size_t)nb * RA * BNC * 4;
+    const int max_steps = (int)(((96 * 1024 - c_lds) / RA - 16) / 64);
+    while ((nst + split - 1) / split > max_steps) ++split;
+    if (split > nst) split = nst;
+    const int steps = (nst + split - 1) / split;
+    // k steps per wave: at least 2 (fewer k-slices when the block range is short); one load group when
+    // every step of the wave fits 8 loads, so all of a wave's weights are requested at once
+    while (s.ks_waves > 1 && (steps + s.ks_waves - 1) / s.ks_waves < 2) s.ks_waves /= 2;
+    if (s.ks_waves < 16 / s.cg / 4) s.ks_waves = 1;   // instantiated k-slice counts: 16/cg, 8/cg, 4/cg, 1
+    s.spw = (steps + s.ks_waves - 1) / s.ks_waves;
+    const int maxu = nb == 3 ? 4 : 8;
+    s.u = s.spw <= 2 ? 2 : s.spw <= 4 ? 4 : maxu;
+    if (s.u > maxu) s.u = maxu;
+    s.kbytes = steps * 64;
+    s.split = (nst + steps - 1) / steps;
+    s.lds = (((size_t)RA * (s.kbytes + 16) + 15) & ~(size_t)15) + c_lds;
+  } else {
+    s.gemv = false;
+    const int64_t big = (int64_t)((M_out + 127) / 128) * ((N + 127) / 128);
+    if (M_out <= 64 && 2 * ((N + 31) / 32) >= cus)
+      s.tile = T_NARROW;
+    else
+      s.tile = big >= cus ? T_BIG : T_MID;
+    const TileShape ts = (s.tile == T_BIG && na * nb == 9) ? kTileExact : kTiles[s.tile];
+    const int BM = 32 * ts.tm * ts.wm, BN = 32 * ts.tn * ts.wn;
+    s.tiles_x = (N + BN - 1) / BN;
+    s.tiles_y = (M_out + BM - 1) / BM;
+    const int tiles = s.tiles_x * s.tiles_y;
+    int split = 1;
+    if (2 * tiles < cus) {
+      split = (cus + tiles - 1) / tiles;
+      const int max_split = nst / 4 > 1 ? nst / 4 : 1;   // keep >= 4 k tiles per split
+      split = split > max_split ? max_split : split;
+    }
+    const int kper = (nst + split - 1) / split;
+    s.kbytes = kper * 64;
+    s.split = (nst + kper - 1) / kper;
+    s.lds = (size_t)ts.stages * (na * BM + nb * BN) * ts.bk;
+    if (exact) s.tmp_bytes = 3LL * M_out * K;
+  }
+  s.ws_bytes = s.split > 1 ? ws_size(M_out, N, s.tiles_x * s.tiles_y) : 0;
   return s;
 }
 
-template <int NB, int MODE>
-static int launch_skinny(LinArgs& p, const SkinnyPlan& s, hipStream_t st) {
-  p.ks = s.ks;
-  if (s.split > 1) {
-    p.ws = (int64_t*)p.ws;
-    p.sem = (int32_t*)((char*)p.ws + (((int64_t)p.M * p.N * 8 + 255) & ~255LL));
-  }
-  dim3 grid(s.tiles, s.split);
-  if (s.rb == 1)
-    skinny_kernel<NB, 1, MODE><<<grid, 256, s.lds, st>>>(p);
-  else if (s.rb == 2)
-    skinny_kernel<NB, 2, MODE><<<grid, 256, s.lds, st>>>(p);
-  else
-    skinny_kernel<NB, 4, MODE><<<grid, 256, s.lds, st>>>(p);
-  return check_launch("skinny_kernel");
+template <typename KernelT>
+static void allow_lds(KernelT kernel, size_t lds) {
+  if (lds > 64 * 1024) hipFuncSetAttribute((const void*)kernel, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
 }
 
-template <int NA, int NB, int MODE, int WM, int WN>
-static int launch_wide_cfg(LinArgs& p, hipStream_t st) {
-  constexpr int BM = 32 * WM, BN = 64 * WN;
-  const size_t lds = 2 * (size_t)(NA * BM + NB * BN) * kRow;
-  static bool attr_set[64] = {false};
-  int dev = 0;
-  hipGetDevice(&dev);
-  if (dev >= 0 && dev < 64 && !attr_set[dev]) {
-    hipFuncSetAttribute((const void*)wide_kernel<NA, NB, MODE, WM, WN>, hipFuncAttributeMaxDynamicSharedMemorySize,
-                        (int)lds);
-    attr_set[dev] = true;
+static void bind_ws(LinArgs& p, const Plan& s) {
+  if (s.split > 1) p.sem = (int32_t*)((char*)p.ws + (((int64_t)p.M * p.N * 8 + 255) & ~255LL));
+}
+
+template <int NB, int RB, int CG, int KS, int U, int MODE>
+static int launch_gemv_cfg(LinArgs& p, const Plan& s, hipStream_t st) {
+  allow_lds(gemv_kernel<NB, RB, CG, KS, U, MODE>, s.lds);
+  gemv_kernel<NB, RB, CG, KS, U, MODE><<<dim3(s.tiles_x, s.split), 64 * CG * KS, s.lds, st>>>(p);
+  return check_launch("gemv_kernel");
+}
+
+template <int NB, int RB, int CG, int MODE>
+static int launch_gemv_ks(LinArgs& p, const Plan& s, hipStream_t st) {
+  constexpr int KSMAX = 16 / CG;
+  constexpr int UMAX = NB == 3 ? 4 : 8;
+  switch (s.ks_waves * 10 + s.u) {
+#define BX_KS(KSV)                                                             \
+  case KSV * 10 + 2: return launch_gemv_cfg<NB, RB, CG, KSV, 2, MODE>(p, s, st); \
+  case KSV * 10 + 4: return launch_gemv_cfg<NB, RB, CG, KSV, 4, MODE>(p, s, st); \
+  case KSV * 10 + 8: return launch_gemv_cfg<NB, RB, CG, KSV, UMAX, MODE>(p, s, st);
+    BX_KS(KSMAX) BX_KS(KSMAX / 2) BX_KS(KSMAX / 4) BX_KS(1)
+#undef BX_KS
+    default:
+      set_error("gemv: no kernel for %d k-slices, %d steps per group", s.ks_waves, s.u);
+      return BX_EINVAL;
   }
-  dim3 grid((p.N + BN - 1) / BN, (p.M + BM - 1) / BM);
-  wide_kernel<NA, NB, MODE, WM, WN><<<grid, WM * WN * 64, lds, st>>>(p);
-  return check_launch("wide_kernel");
+}
+
+template <int NB, int MODE>
+static int launch_gemv(LinArgs& p, const Plan& s, hipStream_t st) {
+  p.ks = s.kbytes;
+  p.spw = s.spw;
+  bind_ws(p, s);
+  if (s.cg == 2) {
+    if (s.rb == 1) return launch_gemv_ks<NB, 1, 2, MODE>(p, s, st);
+    if (s.rb == 2) return launch_gemv_ks<NB, 2, 2, MODE>(p, s, st);
+    return launch_gemv_ks<NB, 4, 2, MODE>(p, s, st);
+  }
+  if (s.rb == 1) return launch_gemv_ks<NB, 1, 1, MODE>(p, s, st);
+  if (s.rb == 2) return launch_gemv_ks<NB, 2, 1, MODE>(p, s, st);
+  return launch_gemv_ks<NB, 4, 1, MODE>(p, s, st);
+}
+
+template <int NA, int NB, int MODE, int WM, int WN, int TM, int TN, int BK, int S>
+static int launch_tile_cfg(LinArgs& p, const Plan& s, hipStream_t st) {
+  allow_lds(tile_kernel<NA, NB, MODE, WM, WN, TM, TN, BK, S>, s.lds);
+  tile_kernel<NA, NB, MODE, WM, WN, TM, TN, BK, S><<<dim3(s.tiles_x, s.tiles_y, s.split), WM * WN * 64, s.lds, st>>>(p);
+  return check_launch("tile_kernel");
 }
 
 template <int NA, int NB, int MODE>
-static int launch_wide(LinArgs& p, hipStream_t st) {
-  const int64_t big = (int64_t)((p.M + 127) / 128) * ((p.N + 127) / 128);
-  if (big >= device_cus()) return launch_wide_cfg<NA, NB, MODE, 4, 2>(p, st);
-  return launch_wide_cfg<NA, NB, MODE, 2, 2>(p, st);
+static int launch_tile(LinArgs& p, const Plan& s, hipStream_t st) {
+  p.ks = s.kbytes;
+  bind_ws(p, s);
+  if (s.tile == T_BIG) {
+    if constexpr (NA * NB == 9)
+      return launch_tile_cfg<NA, NB, MODE, 4, 2, 1, 2, 64, 3>(p, s, st);   // kTileExact
+    else
+      return launch_tile_cfg<NA, NB, MODE, 2, 2, 2, 2, 64, 3>(p, s, st);
+  }
+  if (s.tile == T_MID) return launch_tile_cfg<NA, NB, MODE, 2, 2, 1, 2, 64, 3>(p, s, st);
+  return launch_tile_cfg<NA, NB, MODE, 2, 1, 1, 1, 64, 8>(p, s, st);
 }
 
 static bool aligned16(const void* x) { return ((uintptr_t)x & 15) == 0; }
+
+static int need_ws(const LinArgs& p, const Plan& s, int64_t ws_bytes, const void* tmp, int64_t tmp_bytes) {
+  if (s.split > 1)
+    BX_REQUIRE(p.ws != nullptr && ws_bytes >= s.ws_bytes, "workspace too small (%lld < %lld)", (long long)ws_bytes,
+               (long long)s.ws_bytes);
+  if (s.tmp_bytes > 0)
+    BX_REQUIRE(tmp != nullptr && tmp_bytes >= s.tmp_bytes && aligned16(tmp), "scratch too small (%lld < %lld)",
+               (long long)tmp_bytes, (long long)s.tmp_bytes);
+  return BX_OK;
+}
 
 }  // namespace bx
 
 using namespace bx;
 
-static int exact_common(LinArgs& p, int mode, int64_t ws_bytes, hipStream_t st) {
+static int exact_common(LinArgs& p, int mode, int64_t ws_bytes, void* tmp, int64_t tmp_bytes, hipStream_t st) {
   BX_REQUIRE(p.M >= 0 && p.N >= 0 && p.K >= 0, "negative size");
   BX_REQUIRE(p.K % 16 == 0, "K %% 16 != 0 (K=%d)", p.K);
   BX_REQUIRE(p.K < 43690, "K >= 43690: int32 limb sums could overflow");
@@ -435,21 +742,26 @@ static int exact_common(LinArgs& p, int mode, int64_t ws_bytes, hipStream_t st) 
   BX_REQUIRE(p.ld_row % 16 == 0 && p.ld_plane % 16 == 0, "limb strides must be multiples of 16");
   BX_REQUIRE(aligned16(p.q) && aligned16(p.w), "q and limbs must be 16-byte aligned");
   if (p.M == 0 || p.N == 0) return BX_OK;
+  BX_REQUIRE(p.K > 0, "K == 0");
   p.rows_a = 3 * p.M;
-  if (p.rows_a <= 64) {
-    SkinnyPlan s = plan_skinny(p.rows_a, p.M, p.N, p.K, 3);
-    if (s.split > 1) BX_REQUIRE(p.ws != nullptr && ws_bytes >= s.ws_bytes, "workspace too small (%lld < %lld)",
-                                (long long)ws_bytes, (long long)s.ws_bytes);
-    return mode == EXACT ? launch_skinny<3, EXACT>(p, s, st) : launch_skinny<3, WMM_T>(p, s, st);
-  }
-  return mode == EXACT ? launch_wide<3, 3, EXACT>(p, st) : launch_wide<3, 3, WMM_T>(p, st);
+  const Plan s = make_plan(p.rows_a, p.M, p.N, p.K, 3, 3, true);
+  if (int rc = need_ws(p, s, ws_bytes, tmp, tmp_bytes)) return rc;
+  if (s.gemv) return mode == EXACT ? launch_gemv<3, EXACT>(p, s, st) : launch_gemv<3, WMM_T>(p, s, st);
+  int8_t* planes = (int8_t*)tmp;
+  const int64_t chunks = (int64_t)p.M * (p.K / 16);
+  const int blocks = (int)((chunks + 255) / 256 < 4096 ? (chunks + 255) / 256 : 4096);
+  split_q_kernel<<<blocks, 256, 0, st>>>(p.q, p.ldq, p.M, p.K, planes);
+  if (int rc = check_launch("split_q_kernel")) return rc;
+  p.a = planes;
+  return mode == EXACT ? launch_tile<3, 3, EXACT>(p, s, st) : launch_tile<3, 3, WMM_T>(p, s, st);
 }
 
 extern "C" int bx_exact_linear(const int32_t* q, int64_t ldq, const int64_t* sh, const int8_t* limbs,
                                int64_t ld_plane, int64_t ld_row, const int64_t* d, const int64_t* g,
                                const int32_t* ell_cnt, const int32_t* ell_col, const int64_t* ell_val, int32_t R,
                                int64_t* y, int32_t M, int32_t N, int32_t K, int32_t FR, int32_t checked,
-                               int32_t* flag, void* ws, int64_t ws_bytes, bx_stream_t stream) {
+                               int32_t* flag, void* ws, int64_t ws_bytes, void* tmp, int64_t tmp_bytes,
+                               bx_stream_t stream) {
   LinArgs p = {};
   p.q = q; p.ldq = ldq; p.w = limbs; p.ld_plane = ld_plane; p.ld_row = ld_row;
   p.sh = sh; p.d = d; p.g = g; p.cnt = ell_cnt; p.ecol = ell_col; p.eval = ell_val; p.R = R;
@@ -458,21 +770,27 @@ extern "C" int bx_exact_linear(const int32_t* q, int64_t ldq, const int64_t* sh,
   BX_REQUIRE(R >= 0 && (R == 0 || (ell_cnt && ell_col && ell_val)), "ELL residual arrays missing");
   BX_REQUIRE(!checked || flag, "checked needs a flag pointer");
   BX_REQUIRE(sh && d && g && y, "null pointer");
-  return exact_common(p, EXACT, ws_bytes, (hipStream_t)stream);
+  return exact_common(p, EXACT, ws_bytes, tmp, tmp_bytes, (hipStream_t)stream);
 }
 
 extern "C" int bx_exact_wmm(const int32_t* q, int64_t ldq, const int8_t* limbs, int64_t ld_plane, int64_t ld_row,
-                            int64_t* T, int32_t M, int32_t N, int32_t K, void* ws, int64_t ws_bytes,
-                            bx_stream_t stream) {
+                            int64_t* T, int32_t M, int32_t N, int32_t K, void* ws, int64_t ws_bytes, void* tmp,
+                            int64_t tmp_bytes, bx_stream_t stream) {
   LinArgs p = {};
   p.q = q; p.ldq = ldq; p.w = limbs; p.ld_plane = ld_plane; p.ld_row = ld_row;
   p.out = T; p.M = M; p.N = N; p.K = K; p.ws = (int64_t*)ws;
-  return exact_common(p, WMM_T, ws_bytes, (hipStream_t)stream);
+  BX_REQUIRE(T, "null pointer");
+  return exact_common(p, WMM_T, ws_bytes, tmp, tmp_bytes, (hipStream_t)stream);
 }
 
 extern "C" int64_t bx_exact_linear_workspace(int32_t M, int32_t N, int32_t K) {
-  if (M <= 0 || N <= 0 || K <= 0 || 3 * M > 64) return 0;
-  return plan_skinny(3 * M, M, N, K, 3).ws_bytes;
+  if (M <= 0 || N <= 0 || K <= 0) return 0;
+  return make_plan(3 * M, M, N, K, 3, 3, true).ws_bytes;
+}
+
+extern "C" int64_t bx_exact_linear_scratch(int32_t M, int32_t N, int32_t K) {
+  if (M <= 0 || N <= 0 || K <= 0) return 0;
+  return make_plan(3 * M, M, N, K, 3, 3, true).tmp_bytes;
 }
 
 static int int8_common(LinArgs& p, int mode, int64_t ws_bytes, hipStream_t st) {
@@ -481,16 +799,15 @@ static int int8_common(LinArgs& p, int mode, int64_t ws_bytes, hipStream_t st) {
   BX_REQUIRE((int64_t)p.K * 127 * 128 < (1LL << 31), "K too large for exact int32 sums");
   BX_REQUIRE(aligned16(p.a) && aligned16(p.w), "a and w must be 16-byte aligned");
   if (p.M == 0 || p.N == 0) return BX_OK;
-  if (p.rows_a <= 64) {
-    SkinnyPlan s = plan_skinny(p.rows_a, p.M, p.N, p.K, 1);
-    if (s.split > 1) BX_REQUIRE(p.ws != nullptr && ws_bytes >= s.ws_bytes, "workspace too small (%lld < %lld)",
-                                (long long)ws_bytes, (long long)s.ws_bytes);
-    return mode == JOIN ? launch_skinny<1, JOIN>(p, s, st) : launch_skinny<1, RAW32>(p, s, st);
-  }
-  if (mode == RAW32) return launch_wide<1, 1, RAW32>(p, st);
-  if (p.nl == 1) return launch_wide<1, 1, JOIN>(p, st);
-  if (p.nl == 2) return launch_wide<2, 1, JOIN>(p, st);
-  return launch_wide<3, 1, JOIN>(p, st);
+  BX_REQUIRE(p.K > 0, "K == 0");
+  const int na = mode == RAW32 ? 1 : p.nl;
+  const Plan s = make_plan(p.rows_a, p.M, p.N, p.K, 1, na, false);
+  if (int rc = need_ws(p, s, ws_bytes, nullptr, 0)) return rc;
+  if (s.gemv) return mode == JOIN ? launch_gemv<1, JOIN>(p, s, st) : launch_gemv<1, RAW32>(p, s, st);
+  if (mode == RAW32) return launch_tile<1, 1, RAW32>(p, s, st);
+  if (p.nl == 1) return launch_tile<1, 1, JOIN>(p, s, st);
+  if (p.nl == 2) return launch_tile<2, 1, JOIN>(p, s, st);
+  return launch_tile<3, 1, JOIN>(p, s, st);
 }
 
 extern "C" int bx_int8_gemm(const int8_t* a, const int8_t* w, int32_t* c, int32_t R, int32_t N, int32_t K, void* ws,
@@ -498,6 +815,7 @@ extern "C" int bx_int8_gemm(const int8_t* a, const int8_t* w, int32_t* c, int32_
   LinArgs p = {};
   p.a = a; p.w = w; p.ld_row = K; p.ld_plane = 0; p.out = c; p.M = R; p.N = N; p.K = K;
   p.rows_a = R; p.nl = 1; p.ws = (int64_t*)ws;
+  BX_REQUIRE(c, "null pointer");
   return int8_common(p, RAW32, ws_bytes, (hipStream_t)stream);
 }
 
@@ -507,11 +825,11 @@ extern "C" int bx_int8_gemm_join(const int8_t* a, const int8_t* w, int64_t* y, i
   LinArgs p = {};
   p.a = a; p.w = w; p.ld_row = K; p.ld_plane = 0; p.out = y; p.M = M; p.N = N; p.K = K;
   p.rows_a = nl * M; p.nl = nl; p.ws = (int64_t*)ws;
+  BX_REQUIRE(y, "null pointer");
   return int8_common(p, JOIN, ws_bytes, (hipStream_t)stream);
 }
 
-extern "C" int64_t bx_int8_gemm_workspace(int32_t rows, int32_t N, int32_t K) {
-  if (rows <= 0 || N <= 0 || K <= 0 || rows > 64) return 0;
-  // the join output has fewer rows than the stacked input; size for the larger (raw) case
-  return plan_skinny(rows, rows, N, K, 1).ws_bytes;
+extern "C" int64_t bx_int8_gemm_workspace(int32_t M, int32_t N, int32_t K, int32_t nl) {
+  if (M <= 0 || N <= 0 || K <= 0 || nl < 1 || nl > 3) return 0;
+  return make_plan(nl * M, M, N, K, 1, nl, false).ws_bytes;
 }

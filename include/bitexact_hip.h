@@ -5,10 +5,11 @@
  * BX_EINVAL is an argument/shape contract violation (the Python layer re-raises it as AssertionError, as the
  * reference's `assert`s do). Numeric bound violations never fail a call: they set the caller's int32 flag
  * (flag[0] = 1, never cleared), the reference's sticky device flag (src/bitexact/vllm_plugin/exact_gemm.py:110-118).
- * No call synchronizes the host with the device and no call allocates device memory: temporary buffers are
- * the caller's `ws` workspace (size from the matching *_workspace function; zero-filled once by the caller
- * before its first use, and left zero-filled by every call). Calls that share one workspace must not overlap
- * in time (use one workspace per stream).
+ * No call synchronizes the host with the device and no call allocates device memory. Temporary buffers are
+ * the caller's: `ws` (split-K partial sums; size from the matching *_workspace function; zero-filled once by
+ * the caller before its first use and left zero-filled by every call) and, for the exact linear, `tmp`
+ * (scratch for the int8 limb planes of q; size from bx_exact_linear_scratch; no initial contents needed).
+ * Calls that share one workspace or scratch buffer must not overlap in time (use one pair per stream).
  *
  * Layouts (row-major, k contiguous unless a stride says otherwise):
  *   q       int32 [M, ldq]            exact-mode activations, |q| <= 2^22
@@ -44,14 +45,16 @@ int bx_version(void);
 int bx_exact_linear(const int32_t* q, int64_t ldq, const int64_t* sh, const int8_t* limbs, int64_t ld_plane,
                     int64_t ld_row, const int64_t* d, const int64_t* g, const int32_t* ell_cnt,
                     const int32_t* ell_col, const int64_t* ell_val, int32_t R, int64_t* y, int32_t M, int32_t N,
-                    int32_t K, int32_t FR, int32_t checked, int32_t* flag, void* ws, int64_t ws_bytes,
-                    bx_stream_t stream);
+                    int32_t K, int32_t FR, int32_t checked, int32_t* flag, void* ws, int64_t ws_bytes, void* tmp,
+                    int64_t tmp_bytes, bx_stream_t stream);
 int64_t bx_exact_linear_workspace(int32_t M, int32_t N, int32_t K);
+int64_t bx_exact_linear_scratch(int32_t M, int32_t N, int32_t K);
 
 /* Replaces wmm_triton / wmm_cublas / wmm_cpu (src/bitexact/exact/wmm.py:79-121): the exact dense product
  * T int64 [M, N] = q W^T (one slice of the reference's [split, M, N] partials). */
 int bx_exact_wmm(const int32_t* q, int64_t ldq, const int8_t* limbs, int64_t ld_plane, int64_t ld_row,
-                 int64_t* T, int32_t M, int32_t N, int32_t K, void* ws, int64_t ws_bytes, bx_stream_t stream);
+                 int64_t* T, int32_t M, int32_t N, int32_t K, void* ws, int64_t ws_bytes, void* tmp,
+                 int64_t tmp_bytes, bx_stream_t stream);
 
 /* Replaces consts.decompose (src/bitexact/exact/consts.py:67-107) on the device, pass 1 of 2: bf16 raw bits
  * w [N, K] -> limbs int8 [3, N, K], g, d int64 [N], cnt int32 [N] (residual entries per row). Sets err[0] = 1
@@ -74,7 +77,7 @@ int bx_int8_gemm(const int8_t* a, const int8_t* w, int32_t* c, int32_t R, int32_
  * y int64 [M, N] = sum_{i < nl} (a[i M:(i+1) M] @ w^T) 2^(8 i); a holds nl limb row blocks of M rows. */
 int bx_int8_gemm_join(const int8_t* a, const int8_t* w, int64_t* y, int32_t M, int32_t N, int32_t K, int32_t nl,
                       void* ws, int64_t ws_bytes, bx_stream_t stream);
-int64_t bx_int8_gemm_workspace(int32_t rows, int32_t N, int32_t K);
+int64_t bx_int8_gemm_workspace(int32_t M, int32_t N, int32_t K, int32_t nl); /* raw int_mm: M = R, nl = 1 */
 
 #ifdef __cplusplus
 }
