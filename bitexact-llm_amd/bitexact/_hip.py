@@ -31,6 +31,17 @@ SIGNATURES = {
     "bx_int8_gemm": (ctypes.c_int, [P, P, P, I32, I32, I32, P, I64, P]),
     "bx_int8_gemm_join": (ctypes.c_int, [P, P, P, I32, I32, I32, I32, P, I64, P]),
     "bx_int8_gemm_workspace": (I64, [I32, I32, I32, I32]),
+    "bx_exact_attn_paged": (ctypes.c_int, [P, P, P, I64, P, I64, I64, I64, I32, P, I64, I32, P, P, I64, P, P, I32, I32,
+                                           I32, I32, I32, P, I64, P]),
+    "bx_attn_paged_workspace": (I64, [I32, I32, I32, I32]),
+    "bx_exact_attn_prefill": (ctypes.c_int, [P, I64, I64, P, I64, P, I64, I64, P, I64, I64, P, I64, I64, I32, P, I64,
+                                             P, P, I32, I32, I32, P]),
+    "bx_kv_store": (ctypes.c_int, [P, I64, I64, I64, I32, P, P, I64, I64, P, I64, I64, I32, I32, I32, I32, P]),
+    "bx_limb_bmm": (ctypes.c_int, [P, I32, I64, I64, I64, P, I32, I64, I64, I64, P, I64, I64, I64, I32, I32, I32, I32,
+                                   I32, I32, P]),
+    "bx_rmsnorm_quant": (ctypes.c_int, [P, I64, P, P, P, I64, P, I32, I32, I32, I32, P, P]),
+    "bx_softmax_w": (ctypes.c_int, [P, I64, P, P, I32, I32, I32, P, I64, I32, P, I64, P, P]),
+    "bx_attn_out": (ctypes.c_int, [P, I64, I64, P, I64, I32, I32, I32, I32, I32, I32, I32, P, I64, P, P]),
 }
 
 

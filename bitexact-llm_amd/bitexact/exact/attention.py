@@ -1,0 +1,30 @@
+"""Exact-mode attention over the contiguous integer cache, fused (src/bitexact/exact/model.py:304-311):
+num, den = prefill(qg, shg, K, V, qpos, lut, l2e) computes bmm(qg, K^T) -> segs.softmax -> bmm(p, V) in one
+HIP kernel without materializing the score matrix.
+
+qg int32 [Z, gT, HD], shg int64 [Z, gT, 1], K / V int32 [Z, S, HD] (any row strides, e.g. the reference Cache
+[B, HKV, L, HD] viewed as [B * HKV, L, HD]), qpos int64 [Z, gT, 1] (key s visible iff s <= qpos) ->
+num int64 [Z, gT, HD], den int64 [Z, gT, 1].
+"""
+
+import torch
+
+from bitexact import _hip
+
+
+def prefill(qg, shg, K, V, qpos, lut, l2e):
+    _hip.require_cuda(qg, shg, K, V, qpos, lut)
+    Z, gT, HD = qg.shape
+    S = K.shape[1]
+    assert K.shape == V.shape and K.shape[0] == Z and K.shape[2] == HD
+    assert qg.dtype == torch.int32 and K.dtype == torch.int32 and V.dtype == torch.int32
+    assert qg.stride(2) == 1 and K.stride(2) == 1 and V.stride(2) == 1
+    shg = shg.reshape(Z, gT).contiguous().long()
+    qpos = qpos.reshape(Z, gT).long()
+    lut = lut.contiguous().long()
+    num = torch.empty(Z, gT, HD, dtype=torch.long, device=qg.device)
+    den = torch.empty(Z, gT, 1, dtype=torch.long, device=qg.device)
+    _hip.call("bx_exact_attn_prefill", _hip.ptr(qg), qg.stride(0), qg.stride(1), _hip.ptr(shg), gT, _hip.ptr(qpos),
+              qpos.stride(0), qpos.stride(1), _hip.ptr(K), K.stride(0), K.stride(1), _hip.ptr(V), V.stride(0),
+              V.stride(1), S, _hip.ptr(lut), int(l2e), _hip.ptr(num), _hip.ptr(den), Z, gT, HD, _hip.stream_of(qg))
+    return num, den

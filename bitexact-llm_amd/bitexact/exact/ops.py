@@ -1,0 +1,65 @@
+"""Exact-mode row stages on HIP (src/bitexact/exact/segs.py, src/bitexact/exact/ops.py).
+
+norm_quant(x, gm, ge, err)      segs.norm_quant: RMSNorm + quantization at -FN -> (q int32, sh, err)
+softmax(raw, qpos, shg, lut, l2e) segs.softmax: masked weights at FP -> (p int32, den)
+attn_out(num, den, T, hkv)      Segs.attn_out: div_round + regroup + quantization at -FR -> (q int32, sh)
+"""
+
+import torch
+
+from bitexact import _hip
+from bitexact.exact.consts import FR
+
+FN = 40
+FK, FV, FP = 17, 19, 22
+L2E28 = 387270501
+L2E28_HD = {64: L2E28, 128: 273841598}
+
+
+def norm_quant(x, gm, ge, err=None):
+    _hip.require_cuda(x, gm, ge)
+    assert x.dtype == torch.int64 and x.stride(-1) == 1
+    M, D = x.shape
+    q = torch.empty(M, D, dtype=torch.int32, device=x.device)
+    sh = torch.empty(M, dtype=torch.long, device=x.device)
+    flag = torch.zeros(1, dtype=torch.int32, device=x.device)
+    gm, ge = gm.contiguous().long(), ge.contiguous().long()     # kept alive until the launch is queued
+    _hip.call("bx_rmsnorm_quant", _hip.ptr(x), x.stride(0), _hip.ptr(gm), _hip.ptr(ge), _hip.ptr(q), D, _hip.ptr(sh),
+              M, D, FR, FN, _hip.ptr(flag), _hip.stream_of(x))
+    e = flag[0].bool()
+    return q, sh, e if err is None else (err | e)
+
+
+def softmax(raw, qpos, shg, lut, l2e, kbits=FK, fp=FP):
+    """raw int64 [..., S] scores, qpos / shg broadcastable [..., 1] -> (p int32 [..., S], den int64 [..., 1])."""
+    _hip.require_cuda(raw, qpos, shg, lut)
+    S = raw.shape[-1]
+    lead = raw.shape[:-1]
+    r2 = raw.reshape(-1, S)
+    rows = r2.shape[0]
+    qp = qpos.expand(*lead, 1).reshape(rows).contiguous().long()
+    sh = shg.expand(*lead, 1).reshape(rows).contiguous().long()
+    p = torch.empty(rows, S, dtype=torch.int32, device=raw.device)
+    den = torch.empty(rows, dtype=torch.long, device=raw.device)
+    if r2.stride(-1) != 1:
+        r2 = r2.contiguous()
+    lut = lut.contiguous().long()
+    _hip.call("bx_softmax_w", _hip.ptr(r2), r2.stride(0), _hip.ptr(qp), _hip.ptr(sh), rows, S, kbits, _hip.ptr(lut),
+              int(l2e), fp, _hip.ptr(p), S, _hip.ptr(den), _hip.stream_of(raw))
+    return p.view(*lead, S), den.view(*lead, 1)
+
+
+def attn_out(num, den, T, hkv):
+    """num int64 [Z = B HKV, g T, HD], den [Z, g T, 1] -> (q int32 [B T, H HD], sh int64 [B T])."""
+    _hip.require_cuda(num, den)
+    Z, gT, HD = num.shape
+    g = gT // T
+    B = Z // hkv
+    assert num.stride(2) == 1
+    den2 = den.reshape(Z, gT).contiguous().long()
+    rows = B * T
+    q = torch.empty(rows, hkv * g * HD, dtype=torch.int32, device=num.device)
+    sh = torch.empty(rows, dtype=torch.long, device=num.device)
+    _hip.call("bx_attn_out", _hip.ptr(num), num.stride(0), num.stride(1), _hip.ptr(den2), gT, rows, T, hkv, g, HD, FR,
+              FV, _hip.ptr(q), q.stride(0), _hip.ptr(sh), _hip.stream_of(num))
+    return q, sh

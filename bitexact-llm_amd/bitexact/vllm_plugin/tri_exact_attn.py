@@ -1,0 +1,41 @@
+"""Exact-mode attention on the paged limb-plane KV cache (src/bitexact/vllm_plugin/tri_exact_attn.py:138-165),
+on one HIP kernel (two launches when the keys are split over blocks).
+
+attend(q, sh, qpos, cache, bt, rmap, lut, l2e, nsplit=None) -> (num int64 [R, HKV, M, HD], den int64 [R, HKV, M, 1])
+with the reference's argument meaning; bn / warps are accepted for signature parity (tiles never change the
+integers).
+"""
+
+import torch
+
+from bitexact import _hip
+
+BQ = 4
+BLOCK_TARGET = 512          # blocks to aim for: 2 per MI355X compute unit
+
+
+def default_nsplit(R, HKV, nblk, bs):
+    """Key splits: enough blocks to fill the device, at least 128 keys per split."""
+    tiles = max(1, R * HKV)
+    keys = max(1, nblk * bs)
+    return max(1, min(64, BLOCK_TARGET // tiles, (keys + 127) // 128))
+
+
+def attend(q, sh, qpos, cache, bt, rmap, lut, l2e, nsplit=None, bn=64, warps=4):
+    _hip.require_cuda(q, sh, qpos, cache, bt, rmap, lut)
+    R, HKV, M, HD = q.shape
+    assert M <= BQ and cache.shape[1] == HKV and cache.shape[3] >= 6 * HD and cache.stride(3) == 1
+    assert bt.shape[1] * cache.shape[2] < 43690
+    assert q.dtype == torch.int32 and cache.dtype == torch.int8 and bt.dtype == torch.int32
+    q, sh, qpos = q.contiguous(), sh.contiguous().long(), qpos.contiguous().long()
+    rmap, lut = rmap.contiguous().long(), lut.contiguous().long()
+    if nsplit is None:
+        nsplit = default_nsplit(R, HKV, bt.shape[1], cache.shape[2])
+    num = torch.empty(R, HKV, M, HD, dtype=torch.long, device=q.device)
+    den = torch.empty(R, HKV, M, 1, dtype=torch.long, device=q.device)
+    ws, wsb = _hip.workspace(q.device, _hip.lib().bx_attn_paged_workspace(R, HKV, M, HD) if nsplit > 1 else 0)
+    _hip.call("bx_exact_attn_paged", _hip.ptr(q), _hip.ptr(sh), _hip.ptr(qpos), qpos.stride(0), _hip.ptr(cache),
+              cache.stride(0), cache.stride(1), cache.stride(2), cache.shape[2], _hip.ptr(bt), bt.stride(0),
+              bt.shape[1], _hip.ptr(rmap), _hip.ptr(lut), int(l2e), _hip.ptr(num), _hip.ptr(den), R, HKV, M, HD,
+              int(nsplit), _hip.ptr(ws), wsb, _hip.stream_of(q))
+    return num, den

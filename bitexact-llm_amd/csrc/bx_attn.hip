@@ -1,0 +1,471 @@
+// Exact integer attention for gfx950: paged limb-plane KV store, paged decode attention, and fused prefill
+// attention over a contiguous integer cache.
+//
+// What is computed (src/bitexact/exact/ops.py:133-143, src/bitexact/vllm_plugin/tri_exact_attn.py:1-15):
+//   raw[i, s] = sum_d q[i, d] K[s, d]                 exact int64 (|q|, |K| within 3 signed base-256 limbs)
+//   mx[i]     = max over visible keys s <= qpos[i] of raw[i, s]
+//   zf        = min(rshc(mx - raw, FK + 3 - sh[i] - FZ), 48 << FZ); t = rshc(zf l2e, 28)
+//   p         = exp2neg_lut(t, lut, FP)   (2^-f table at 2^60 + linear interpolation; 0 for hidden keys)
+//   den[i]    = sum_s p,   num[i, d] = sum_s p V[s, d]                  exact int64
+// Two sweeps over the keys are required (the quantized exp table does not allow online rescaling,
+// src/bitexact/vllm_plugin/tri_paged.py:16-19). Maxima and sums are exact in any order, so the key split and
+// the tiling never change a bit.
+//
+// Kernel shape: one block of 256 threads per (query tile, key range). 64-key tiles are staged in LDS as
+// int32 K / V rows (paged caches hold int8 limb planes that are joined on the way in). Thread t = (wave w,
+// lane l) owns key l of the tile for the scores of queries w, w + 4, ... and output dims l, l + 64 of the
+// same queries for p V, so query-indexed LDS reads are wave-uniform broadcasts and key/dim-indexed reads
+// hit distinct banks (rows padded by one word).
+#include "bx_common.h"
+
+namespace bx {
+
+constexpr int kFK = 17, kFZ = 26, kFP = 22, kFT2 = 26, kExp2Bits = 14, kExp2One = 60;
+
+// softmax_w's weight of one visible key (src/bitexact/exact/ops.py:133-143 over exp2neg_lut, 108-116).
+__device__ __forceinline__ int64_t attn_weight(int64_t z, int64_t zshift, const int64_t* lut, int64_t l2e) {
+  int64_t zf = rshc(z, zshift);
+  zf = imin(zf, 48LL << kFZ);
+  const int64_t t = rshc(mul_wrap(zf, l2e), kFZ + 28 - kFT2);
+  const int64_t n = t >> kFT2;
+  const int64_t f = t & ((1LL << kFT2) - 1);
+  const int64_t idx = f >> (kFT2 - kExp2Bits);
+  const int64_t rr = f & ((1LL << (kFT2 - kExp2Bits)) - 1);
+  const int64_t a = lut[idx];
+  const int64_t v = add_wrap(a, rshc(mul_wrap(lut[idx + 1] - a, rr), kFT2 - kExp2Bits));
+  return rshc(v, kExp2One - kFP + n);
+}
+
+// int32 value -> the value of its first three signed base-256 digits (what a 3-limb split keeps).
+__device__ __forceinline__ int32_t keep3(int32_t x) {
+  const int32_t a0 = limb_lo(x);
+  int32_t r = (x - a0) >> 8;
+  const int32_t a1 = limb_lo(r);
+  r = (r - a1) >> 8;
+  const int32_t a2 = limb_lo(r);
+  return a0 + a1 * 256 + a2 * 65536;
+}
+
+struct AttnArgs {
+  // queries
+  const int32_t* q;
+  int64_t sq_tile, sq_row;        // element strides: between query groups (z or (r,h)) and between queries
+  const int64_t* sh;              // per query exponent, index = group * sh_tile + query
+  int64_t sh_tile;
+  const int64_t* qpos;            // per query position: qpos[(group / qpos_div) * qpos_tile + query * qpos_row]
+  int64_t qpos_tile, qpos_row;
+  int qpos_div;
+  int nq;                         // queries per group (decode M <= 4, prefill gT)
+  // keys: paged limb planes or contiguous int32
+  const int8_t* cache;            // [nb, HKV, bs, 8 HD]
+  int64_t sc_nb, sc_h, sc_bs;
+  const int32_t* bt;
+  int64_t sbt;
+  const int64_t* rmap;
+  int bs, hkv;
+  const int32_t* K;               // contiguous: [Z, S, HD] with strides
+  const int32_t* V;
+  int64_t sk_z, sk_s, sv_z, sv_s;
+  int S;                          // contiguous: keys available
+  // table, scale
+  const int64_t* lut;
+  int64_t l2e;
+  // outputs
+  int64_t* num;
+  int64_t* den;
+  int64_t snum_tile, snum_row;
+  int64_t sden_tile;
+  // split-KV state
+  int nsplit;
+  int64_t* mx_ws;                 // [groups, nq] running maxima stored as mx - NEG (0 = none yet)
+  int64_t* num_ws;                // [groups, nq, HD]
+  int64_t* den_ws;                // [groups, nq]
+  int32_t* sem;                   // [groups]
+};
+
+template <int QT, int HD>
+struct AttnSmem {
+  int32_t Qs[QT][HD];
+  int32_t Ks[64][HD + 1];
+  int32_t Vs[64][HD + 1];
+  int32_t Ps[QT][65];
+  int64_t qpos[QT];
+  int64_t shift[QT];              // per query: FK + 3 - FZ - sh
+  int64_t mx[QT];
+  int s_last;
+};
+
+template <int QT, int HD, bool PAGED>
+__device__ __forceinline__ void load_kv_tile(const AttnArgs& p, AttnSmem<QT, HD>& sm, int group, int h, int key0, int nkeys,
+                                             bool want_v) {
+  constexpr int UNITS = 64 * (HD / 16);          // (key, 16-dim chunk) units per tile
+  for (int u = threadIdx.x; u < UNITS; u += 256) {
+    const int kk = u / (HD / 16), c = u % (HD / 16);
+    const int s = key0 + kk;
+    int32_t kv[16], vv[16];
+    if (kk < nkeys) {
+      if (PAGED) {
+        const int64_t brow = p.rmap[group / p.hkv];
+        const int blk = p.bt[brow * p.sbt + s / p.bs];
+        const int8_t* row = p.cache + (int64_t)blk * p.sc_nb + (int64_t)h * p.sc_h + (int64_t)(s % p.bs) * p.sc_bs;
+        const v4i k0 = *(const v4i*)(row + c * 16), k1 = *(const v4i*)(row + HD + c * 16),
+                  k2 = *(const v4i*)(row + 2 * HD + c * 16);
+        v4i v0 = {0, 0, 0, 0}, v1 = v0, v2 = v0;
+        if (want_v) {
+          v0 = *(const v4i*)(row + 3 * HD + c * 16);
+          v1 = *(const v4i*)(row + 4 * HD + c * 16);
+          v2 = *(const v4i*)(row + 5 * HD + c * 16);
+        }
+        const int8_t* pk0 = (const int8_t*)&k0;
+        const int8_t* pk1 = (const int8_t*)&k1;
+        const int8_t* pk2 = (const int8_t*)&k2;
+        const int8_t* pv0 = (const int8_t*)&v0;
+        const int8_t* pv1 = (const int8_t*)&v1;
+        const int8_t* pv2 = (const int8_t*)&v2;
+#pragma unroll
+        for (int e = 0; e < 16; ++e) {
+          kv[e] = (int32_t)pk0[e] + (int32_t)pk1[e] * 256 + (int32_t)pk2[e] * 65536;
+          vv[e] = (int32_t)pv0[e] + (int32_t)pv1[e] * 256 + (int32_t)pv2[e] * 65536;
+        }
+      } else {
+        const int32_t* kr = p.K + (int64_t)group * p.sk_z + (int64_t)s * p.sk_s + c * 16;
+        const int32_t* vr = p.V + (int64_t)group * p.sv_z + (int64_t)s * p.sv_s + c * 16;
+#pragma unroll
+        for (int e = 0; e < 16; ++e) {
+          kv[e] = keep3(kr[e]);
+          vv[e] = want_v ? keep3(vr[e]) : 0;
+        }
+      }
+    } else {
+#pragma unroll
+      for (int e = 0; e < 16; ++e) kv[e] = vv[e] = 0;
+    }
+#pragma unroll
+    for (int e = 0; e < 16; ++e) {
+      sm.Ks[kk][c * 16 + e] = kv[e];
+      if (want_v) sm.Vs[kk][c * 16 + e] = vv[e];
+    }
+  }
+}
+
+// raw scores of this thread's queries (w + 4 j) against key lane l of the staged tile
+template <int QT, int HD>
+__device__ __forceinline__ void tile_scores(const AttnSmem<QT, HD>& sm, int64_t (&raw)[QT / 4]) {
+  const int l = threadIdx.x & 63, w = threadIdx.x >> 6;
+#pragma unroll
+  for (int j = 0; j < QT / 4; ++j) raw[j] = 0;
+#pragma unroll 8
+  for (int d = 0; d < HD; ++d) {
+    const int64_t kd = sm.Ks[l][d];
+#pragma unroll
+    for (int j = 0; j < QT / 4; ++j) raw[j] += (int64_t)sm.Qs[w + 4 * j][d] * kd;
+  }
+}
+
+// Stage queries of the tile (3-limb values), their exponents / positions; returns the visible key count.
+template <int QT, int HD>
+__device__ __forceinline__ int64_t stage_queries(const AttnArgs& p, AttnSmem<QT, HD>& sm, int group, int q0, int nvalid) {
+  for (int u = threadIdx.x; u < QT * HD; u += 256) {
+    const int i = u / HD, d = u % HD;
+    sm.Qs[i][d] = i < nvalid ? keep3(p.q[group * p.sq_tile + (int64_t)(q0 + i) * p.sq_row + d]) : 0;
+  }
+  if (threadIdx.x < QT) {
+    const int i = threadIdx.x;
+    const bool ok = i < nvalid;
+    sm.qpos[i] = ok ? p.qpos[(group / p.qpos_div) * p.qpos_tile + (int64_t)(q0 + i) * p.qpos_row] : -1;
+    sm.shift[i] = ok ? (int64_t)(kFK + 3 - kFZ) - p.sh[group * p.sh_tile + q0 + i] : 0;
+    sm.mx[i] = kNeg;
+  }
+  __syncthreads();
+  int64_t kend = 0;
+  for (int i = 0; i < QT; ++i) kend = imax(kend, sm.qpos[i] + 1);
+  return kend;
+}
+
+// Sweep 1: per-query maxima over visible keys in [lo, hi) into sm.mx (LDS atomic max).
+template <int QT, int HD, bool PAGED>
+__device__ void sweep_max(const AttnArgs& p, AttnSmem<QT, HD>& sm, int group, int h, int64_t lo, int64_t hi) {
+  const int l = threadIdx.x & 63, w = threadIdx.x >> 6;
+  int64_t best[QT / 4];
+#pragma unroll
+  for (int j = 0; j < QT / 4; ++j) best[j] = kNeg;
+  for (int64_t k0 = lo; k0 < hi; k0 += 64) {
+    const int nk = (int)imin(64, hi - k0);
+    __syncthreads();
+    load_kv_tile<QT, HD, PAGED>(p, sm, group, h, (int)k0, nk, false);
+    __syncthreads();
+    int64_t raw[QT / 4];
+    tile_scores<QT, HD>(sm, raw);
+#pragma unroll
+    for (int j = 0; j < QT / 4; ++j) {
+      const bool vis = l < nk && k0 + l <= sm.qpos[w + 4 * j];
+      if (vis) best[j] = imax(best[j], raw[j]);
+    }
+  }
+#pragma unroll
+  for (int j = 0; j < QT / 4; ++j) {
+    const int64_t m = wave_max64(best[j]);
+    if (l == 0) atomicMax((long long*)&sm.mx[w + 4 * j], (long long)m);
+  }
+  __syncthreads();
+}
+
+// Sweep 2: weights from the maxima in sm.mx; accumulates den / num for the thread's queries.
+template <int QT, int HD, bool PAGED>
+__device__ void sweep_acc(const AttnArgs& p, AttnSmem<QT, HD>& sm, int group, int h, int64_t lo, int64_t hi,
+                          int64_t (&den)[QT / 4], int64_t (&num)[QT / 4][HD / 64]) {
+  const int l = threadIdx.x & 63, w = threadIdx.x >> 6;
+#pragma unroll
+  for (int j = 0; j < QT / 4; ++j) {
+    den[j] = 0;
+#pragma unroll
+    for (int c = 0; c < HD / 64; ++c) num[j][c] = 0;
+  }
+  for (int64_t k0 = lo; k0 < hi; k0 += 64) {
+    const int nk = (int)imin(64, hi - k0);
+    __syncthreads();
+    load_kv_tile<QT, HD, PAGED>(p, sm, group, h, (int)k0, nk, true);
+    __syncthreads();
+    int64_t raw[QT / 4];
+    tile_scores<QT, HD>(sm, raw);
+#pragma unroll
+    for (int j = 0; j < QT / 4; ++j) {
+      const int i = w + 4 * j;
+      const bool vis = l < nk && k0 + l <= sm.qpos[i];
+      const int64_t pw = vis ? attn_weight(sm.mx[i] - raw[j], sm.shift[i], p.lut, p.l2e) : 0;
+      den[j] += pw;
+      sm.Ps[i][l] = (int32_t)pw;
+    }
+    __syncthreads();
+#pragma unroll 4
+    for (int s = 0; s < nk; ++s) {
+#pragma unroll
+      for (int c = 0; c < HD / 64; ++c) {
+        const int64_t vd = sm.Vs[s][l + 64 * c];
+#pragma unroll
+        for (int j = 0; j < QT / 4; ++j) num[j][c] += (int64_t)sm.Ps[w + 4 * j][s] * vd;
+      }
+    }
+  }
+#pragma unroll
+  for (int j = 0; j < QT / 4; ++j) den[j] = wave_sum64(den[j]);
+}
+
+// Key range [lo, hi) of split `sp` of [0, kend) in 64-key multiples.
+__device__ __forceinline__ void split_range(int64_t kend, int nsplit, int sp, int64_t& lo, int64_t& hi) {
+  const int64_t chunk = ((kend + nsplit - 1) / nsplit + 63) / 64 * 64;
+  lo = imin(kend, sp * chunk);
+  hi = imin(kend, lo + chunk);
+}
+
+// grid (groups * query tiles, nsplit). nsplit == 1: both sweeps, outputs written directly.
+// nsplit > 1 and PHASE 0: maxima only (atomic max into mx_ws). PHASE 1: sums into the workspace; the last
+// block of a group writes the outputs and restores the workspace (maxima, sums and counter back to 0).
+template <int QT, int HD, bool PAGED, int PHASE>
+__global__ __launch_bounds__(256) void attn_kernel(AttnArgs p) {
+  extern __shared__ __align__(16) char smem_raw[];
+  AttnSmem<QT, HD>& sm = *(AttnSmem<QT, HD>*)smem_raw;
+  const int tiles = (p.nq + QT - 1) / QT;
+  const int group = blockIdx.x / tiles, q0 = (blockIdx.x % tiles) * QT;
+  const int nvalid = min(QT, p.nq - q0);
+  const int h = PAGED ? group % p.hkv : 0;
+  const int l = threadIdx.x & 63, w = threadIdx.x >> 6;
+  const int64_t kend = stage_queries<QT, HD>(p, sm, group, q0, nvalid);
+  int64_t lo, hi;
+  split_range(kend, gridDim.y, blockIdx.y, lo, hi);
+
+  if (gridDim.y == 1) {
+    sweep_max<QT, HD, PAGED>(p, sm, group, h, lo, hi);
+    int64_t den[QT / 4], num[QT / 4][HD / 64];
+    sweep_acc<QT, HD, PAGED>(p, sm, group, h, lo, hi, den, num);
+#pragma unroll
+    for (int j = 0; j < QT / 4; ++j) {
+      const int i = w + 4 * j;
+      if (i < nvalid) {
+#pragma unroll
+        for (int c = 0; c < HD / 64; ++c)
+          p.num[group * p.snum_tile + (int64_t)(q0 + i) * p.snum_row + l + 64 * c] = num[j][c];
+        if (l == 0) p.den[group * p.sden_tile + q0 + i] = den[j];
+      }
+    }
+    return;
+  }
+  const int64_t gq = (int64_t)group * p.nq + q0;   // workspace row of the tile's first query
+  if (PHASE == 0) {
+    sweep_max<QT, HD, PAGED>(p, sm, group, h, lo, hi);
+    if (threadIdx.x < nvalid && hi > lo)
+      atomicMax((long long*)&p.mx_ws[gq + threadIdx.x], (long long)(sm.mx[threadIdx.x] - kNeg));
+    return;
+  }
+  if (threadIdx.x < QT) sm.mx[threadIdx.x] = threadIdx.x < nvalid ? p.mx_ws[gq + threadIdx.x] + kNeg : kNeg;
+  __syncthreads();
+  int64_t den[QT / 4], num[QT / 4][HD / 64];
+  sweep_acc<QT, HD, PAGED>(p, sm, group, h, lo, hi, den, num);
+  if (hi > lo) {
+#pragma unroll
+    for (int j = 0; j < QT / 4; ++j) {
+      const int i = w + 4 * j;
+      if (i < nvalid) {
+#pragma unroll
+        for (int c = 0; c < HD / 64; ++c)
+          atomicAdd((unsigned long long*)&p.num_ws[(gq + i) * HD + l + 64 * c], (unsigned long long)num[j][c]);
+        if (l == 0) atomicAdd((unsigned long long*)&p.den_ws[gq + i], (unsigned long long)den[j]);
+      }
+    }
+  }
+  // every split arrives (empty ones too), the last one publishes and restores the workspace
+  __builtin_amdgcn_s_waitcnt(0);
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    const int tile_id = blockIdx.x;
+    const bool last = atomicAdd(&p.sem[tile_id], 1) == (int)gridDim.y - 1;
+    if (last) atomicExch(&p.sem[tile_id], 0);
+    sm.s_last = last;
+  }
+  __syncthreads();
+  if (!sm.s_last) return;
+  for (int u = threadIdx.x; u < nvalid * HD; u += 256) {
+    const int i = u / HD, d = u % HD;
+    p.num[group * p.snum_tile + (int64_t)(q0 + i) * p.snum_row + d] =
+        (int64_t)atomicExch((unsigned long long*)&p.num_ws[(gq + i) * HD + d], 0ull);
+  }
+  if (threadIdx.x < nvalid) {
+    p.den[group * p.sden_tile + q0 + threadIdx.x] =
+        (int64_t)atomicExch((unsigned long long*)&p.den_ws[gq + threadIdx.x], 0ull);
+    atomicExch((unsigned long long*)&p.mx_ws[gq + threadIdx.x], 0ull);
+  }
+}
+
+// ---- KV store into the limb-plane cache (tri_paged.store, src/bitexact/vllm_plugin/tri_paged.py:311-335) ----
+template <typename T>
+__global__ __launch_bounds__(128) void kv_store_kernel(int8_t* cache, int64_t sc_nb, int64_t sc_h, int64_t sc_bs,
+                                                       const int64_t* slot, const T* k, int64_t skn, int64_t skh,
+                                                       const T* v, int64_t svn, int64_t svh, int HD, int bs) {
+  const int64_t n = blockIdx.x, h = blockIdx.y;
+  const int64_t sl = slot[n];
+  if (sl < 0) return;                                  // dummy / padded tokens carry slot -1
+  int8_t* base = cache + (sl / bs) * sc_nb + h * sc_h + (sl % bs) * sc_bs;
+  for (int d = threadIdx.x; d < HD; d += blockDim.x) {
+    int32_t kr = (int32_t)k[n * skn + h * skh + d], vr = (int32_t)v[n * svn + h * svh + d];
+#pragma unroll
+    for (int i = 0; i < 3; ++i) {
+      const int32_t k0 = limb_lo(kr), v0 = limb_lo(vr);
+      base[i * HD + d] = (int8_t)k0;
+      base[(3 + i) * HD + d] = (int8_t)v0;
+      kr = (kr - k0) >> 8;
+      vr = (vr - v0) >> 8;
+    }
+  }
+}
+
+}  // namespace bx
+
+using namespace bx;
+
+// ======================================== C ABI ========================================
+
+template <int QT, int HD, bool PAGED>
+static int launch_attn(AttnArgs& p, int groups, hipStream_t st) {
+  const int tiles = (p.nq + QT - 1) / QT;
+  const size_t lds = sizeof(AttnSmem<QT, HD>);
+  dim3 grid(groups * tiles, p.nsplit);
+  if (lds > 64 * 1024) {
+    hipFuncSetAttribute((const void*)attn_kernel<QT, HD, PAGED, 0>, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+    hipFuncSetAttribute((const void*)attn_kernel<QT, HD, PAGED, 1>, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+  }
+  if (p.nsplit > 1) {
+    attn_kernel<QT, HD, PAGED, 0><<<grid, 256, lds, st>>>(p);
+    if (int rc = check_launch("attn_kernel(max)")) return rc;
+  }
+  attn_kernel<QT, HD, PAGED, 1><<<grid, 256, lds, st>>>(p);
+  return check_launch("attn_kernel");
+}
+
+// split-KV workspace: mx [Gq] + num [Gq, HD] + den [Gq] + counters [tiles]; zero-filled = idle
+static int64_t attn_ws_bytes(int64_t gq, int64_t tiles, int HD) { return gq * 8 * (2 + HD) + tiles * 4 + 256; }
+
+static void bind_attn_ws(AttnArgs& p, void* ws, int64_t gq, int HD) {
+  char* b = (char*)ws;
+  p.mx_ws = (int64_t*)b;
+  p.num_ws = (int64_t*)(b + gq * 8);
+  p.den_ws = (int64_t*)(b + gq * 8 * (1 + HD));
+  p.sem = (int32_t*)(b + gq * 8 * (2 + HD));
+}
+
+extern "C" int64_t bx_attn_paged_workspace(int32_t R, int32_t HKV, int32_t M, int32_t HD) {
+  return attn_ws_bytes((int64_t)R * HKV * M, (int64_t)R * HKV, HD);
+}
+
+extern "C" int bx_exact_attn_paged(const int32_t* q, const int64_t* sh, const int64_t* qpos, int64_t sqpos_r,
+                                   const int8_t* cache, int64_t sc_nb, int64_t sc_h, int64_t sc_bs, int32_t bs,
+                                   const int32_t* bt, int64_t sbt, int32_t nblk, const int64_t* rmap, const int64_t* lut,
+                                   int64_t l2e, int64_t* num, int64_t* den, int32_t R, int32_t HKV, int32_t M,
+                                   int32_t HD, int32_t nsplit, void* ws, int64_t ws_bytes, bx_stream_t stream) {
+  BX_REQUIRE(R >= 0 && HKV > 0 && M >= 1 && M <= 4, "need 1 <= M <= 4 queries per (row, KV head)");
+  BX_REQUIRE(HD == 64 || HD == 128, "head_dim must be 64 or 128");
+  BX_REQUIRE((int64_t)nblk * bs < 43690, "keys per row must stay below 43690");
+  BX_REQUIRE(nsplit >= 1 && nsplit <= 64, "nsplit in [1, 64]");
+  BX_REQUIRE(sc_bs >= 6 * HD && sc_nb % 16 == 0 && sc_h % 16 == 0 && sc_bs % 16 == 0 && ((uintptr_t)cache & 15) == 0,
+             "cache rows must hold the 6 HD limb bytes, 16-byte aligned");
+  BX_REQUIRE(q && sh && qpos && bt && rmap && lut && num && den, "null pointer");
+  if (R == 0) return BX_OK;
+  AttnArgs p = {};
+  p.q = q; p.sq_tile = (int64_t)M * HD; p.sq_row = HD;
+  p.sh = sh; p.sh_tile = M;
+  p.qpos = qpos; p.qpos_tile = sqpos_r; p.qpos_row = 1; p.qpos_div = HKV; p.nq = M;
+  p.cache = cache; p.sc_nb = sc_nb; p.sc_h = sc_h; p.sc_bs = sc_bs; p.bt = bt; p.sbt = sbt; p.rmap = rmap;
+  p.bs = bs; p.hkv = HKV;
+  p.lut = lut; p.l2e = l2e;
+  p.num = num; p.den = den; p.snum_tile = (int64_t)M * HD; p.snum_row = HD; p.sden_tile = M;
+  p.nsplit = nsplit;
+  if (nsplit > 1) {
+    const int64_t need = attn_ws_bytes((int64_t)R * HKV * M, (int64_t)R * HKV, HD);
+    BX_REQUIRE(ws != nullptr && ws_bytes >= need, "workspace too small (%lld < %lld)", (long long)ws_bytes,
+               (long long)need);
+    bind_attn_ws(p, ws, (int64_t)R * HKV * M, HD);
+  }
+  return HD == 64 ? launch_attn<4, 64, true>(p, R * HKV, (hipStream_t)stream)
+                  : launch_attn<4, 128, true>(p, R * HKV, (hipStream_t)stream);
+}
+
+extern "C" int bx_exact_attn_prefill(const int32_t* qg, int64_t sq_z, int64_t sq_row, const int64_t* shg,
+                                     int64_t ssh_z, const int64_t* qpos, int64_t sqpos_z, int64_t sqpos_row,
+                                     const int32_t* K, int64_t sk_z, int64_t sk_s, const int32_t* V, int64_t sv_z,
+                                     int64_t sv_s, int32_t S, const int64_t* lut, int64_t l2e, int64_t* num,
+                                     int64_t* den, int32_t Z, int32_t gT, int32_t HD, bx_stream_t stream) {
+  BX_REQUIRE(Z >= 0 && gT >= 0 && S >= 0, "negative size");
+  BX_REQUIRE(HD == 64 || HD == 128, "head_dim must be 64 or 128");
+  BX_REQUIRE(S < 43690, "keys must stay below 43690");
+  BX_REQUIRE(qg && shg && qpos && K && V && lut && num && den, "null pointer");
+  BX_REQUIRE(ssh_z == gT, "shg must be [Z, gT, 1] contiguous");
+  if (Z == 0 || gT == 0) return BX_OK;
+  AttnArgs p = {};
+  p.q = qg; p.sq_tile = sq_z; p.sq_row = sq_row;
+  p.sh = shg; p.sh_tile = ssh_z;
+  p.qpos = qpos; p.qpos_tile = sqpos_z; p.qpos_row = sqpos_row; p.qpos_div = 1; p.nq = gT;
+  p.K = K; p.V = V; p.sk_z = sk_z; p.sk_s = sk_s; p.sv_z = sv_z; p.sv_s = sv_s; p.S = S;
+  p.lut = lut; p.l2e = l2e;
+  p.num = num; p.den = den; p.snum_tile = (int64_t)gT * HD; p.snum_row = HD; p.sden_tile = gT;
+  p.nsplit = 1;
+  // keys visible to a query never exceed the cache length S: qpos beyond S - 1 is the caller's contract
+  return HD == 64 ? launch_attn<64, 64, false>(p, Z, (hipStream_t)stream)
+                  : launch_attn<64, 128, false>(p, Z, (hipStream_t)stream);
+}
+
+extern "C" int bx_kv_store(int8_t* cache, int64_t sc_nb, int64_t sc_h, int64_t sc_bs, int32_t bs, const int64_t* slot,
+                           const void* k, int64_t skn, int64_t skh, const void* v, int64_t svn, int64_t svh,
+                           int32_t elem_bytes, int32_t N, int32_t HKV, int32_t HD, bx_stream_t stream) {
+  BX_REQUIRE(N >= 0 && HKV > 0 && HD > 0 && bs > 0, "bad sizes");
+  BX_REQUIRE(elem_bytes == 4 || elem_bytes == 8, "k / v must be int32 or int64");
+  BX_REQUIRE(sc_bs >= 6 * HD, "cache rows must hold the 6 HD limb bytes");
+  if (N == 0) return BX_OK;
+  BX_REQUIRE(cache && slot && k && v, "null pointer");
+  dim3 grid(N, HKV);
+  if (elem_bytes == 8)
+    kv_store_kernel<int64_t><<<grid, 128, 0, (hipStream_t)stream>>>(cache, sc_nb, sc_h, sc_bs, slot, (const int64_t*)k,
+                                                                   skn, skh, (const int64_t*)v, svn, svh, HD, bs);
+  else
+    kv_store_kernel<int32_t><<<grid, 128, 0, (hipStream_t)stream>>>(cache, sc_nb, sc_h, sc_bs, slot, (const int32_t*)k,
+                                                                   skn, skh, (const int32_t*)v, svn, svh, HD, bs);
+  return check_launch("kv_store_kernel");
+}

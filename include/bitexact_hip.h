@@ -79,6 +79,64 @@ int bx_int8_gemm_join(const int8_t* a, const int8_t* w, int64_t* y, int32_t M, i
                       void* ws, int64_t ws_bytes, bx_stream_t stream);
 int64_t bx_int8_gemm_workspace(int32_t M, int32_t N, int32_t K, int32_t nl); /* raw int_mm: M = R, nl = 1 */
 
+/* ---- integer attention ---- */
+
+/* Replaces tri_exact_attn.attend (src/bitexact/vllm_plugin/tri_exact_attn.py:138-165): paged exact attention for
+ * M <= 4 queries per (row, KV head). q int32 [R, HKV, M, HD] contiguous, sh int64 [R, HKV, M], qpos int64
+ * [R, M] (row stride sqpos_r; key s visible to query i iff s <= qpos[r, i]), cache int8 limb planes
+ * [nb, HKV, bs, >= 6 HD] (element strides sc_nb, sc_h, sc_bs; K limbs at bytes [0, 3 HD), V at [3 HD, 6 HD)),
+ * bt int32 block table (row stride sbt, nblk columns), rmap int64 [R] (block-table row of each q row),
+ * lut int64 [2^14 + 1] (2^-f at 2^60), l2e = round(log2(e) / sqrt(HD / 64) 2^28). Outputs num int64
+ * [R, HKV, M, HD], den int64 [R, HKV, M]. nsplit > 1 splits the keys over blocks (two launches) and needs ws. */
+int bx_exact_attn_paged(const int32_t* q, const int64_t* sh, const int64_t* qpos, int64_t sqpos_r, const int8_t* cache,
+                        int64_t sc_nb, int64_t sc_h, int64_t sc_bs, int32_t bs, const int32_t* bt, int64_t sbt,
+                        int32_t nblk, const int64_t* rmap, const int64_t* lut, int64_t l2e, int64_t* num, int64_t* den,
+                        int32_t R, int32_t HKV, int32_t M, int32_t HD, int32_t nsplit, void* ws, int64_t ws_bytes,
+                        bx_stream_t stream);
+int64_t bx_attn_paged_workspace(int32_t R, int32_t HKV, int32_t M, int32_t HD);
+
+/* Fused form of exact/model.py's attention (src/bitexact/exact/model.py:304-311: bmm(qg, K^T), segs.softmax,
+ * bmm(p, V)): qg int32 [Z, gT, HD] (strides sq_z, sq_row), shg int64 [Z, gT] (ssh_z = gT), qpos int64 [Z, gT]
+ * (strides), K / V int32 [Z, S, HD] (strides; the integer Cache layout), outputs num int64 [Z, gT, HD],
+ * den int64 [Z, gT]. The score matrix is never materialized. */
+int bx_exact_attn_prefill(const int32_t* qg, int64_t sq_z, int64_t sq_row, const int64_t* shg, int64_t ssh_z,
+                          const int64_t* qpos, int64_t sqpos_z, int64_t sqpos_row, const int32_t* K, int64_t sk_z,
+                          int64_t sk_s, const int32_t* V, int64_t sv_z, int64_t sv_s, int32_t S, const int64_t* lut,
+                          int64_t l2e, int64_t* num, int64_t* den, int32_t Z, int32_t gT, int32_t HD, bx_stream_t stream);
+
+/* Replaces tri_paged.store (src/bitexact/vllm_plugin/tri_paged.py:311-335): K / V (int32 or int64 [N, HKV, HD] with
+ * token / head strides) written as 3 int8 limb planes each at cache slots slot int64 [N]; slot < 0 is skipped. */
+int bx_kv_store(int8_t* cache, int64_t sc_nb, int64_t sc_h, int64_t sc_bs, int32_t bs, const int64_t* slot,
+                const void* k, int64_t skn, int64_t skh, const void* v, int64_t svn, int64_t svh, int32_t elem_bytes,
+                int32_t N, int32_t HKV, int32_t HD, bx_stream_t stream);
+
+/* Replaces bitexact.bmm.bmm (src/bitexact/bmm.py:78-102): exact int64 c [Z, M, N] = a [Z, M, K] @ b [Z, K, N] for
+ * int32 / int64 operands (element sizes a_bytes / b_bytes) with arbitrary strides, each within na / nb limbs. */
+int bx_limb_bmm(const void* a, int32_t a_bytes, int64_t saz, int64_t sam, int64_t sak, const void* b, int32_t b_bytes,
+                int64_t sbz, int64_t sbk, int64_t sbn, int64_t* c, int64_t scz, int64_t scm, int64_t scn, int32_t Z,
+                int32_t M, int32_t N, int32_t K, int32_t na, int32_t nb, bx_stream_t stream);
+
+/* ---- row stages ---- */
+
+/* Replaces segs.norm_quant (src/bitexact/exact/segs.py:59-63): RMSNorm of x int64 [M, D] at FR with gamma
+ * (gm 2^ge per column), then per-row quantization at -FN: q int32 [M, D], sh int64 [M]; err[0] = 1 when
+ * max |x| >= 2^40. D a power of two <= 4096. */
+int bx_rmsnorm_quant(const int64_t* x, int64_t ldx, const int64_t* gm, const int64_t* ge, int32_t* q, int64_t ldq,
+                     int64_t* sh, int32_t M, int32_t D, int32_t FR, int32_t FN, int32_t* err, bx_stream_t stream);
+
+/* Replaces segs.softmax (src/bitexact/exact/segs.py:102-105, ops.softmax_w): weights p int32 [rows, S] at fp bits of
+ * the scores raw int64 [rows, S] (key s visible iff s <= qpos[row]; hidden keys weigh 0) and den int64 [rows]. */
+int bx_softmax_w(const int64_t* raw, int64_t ldr, const int64_t* qpos, const int64_t* sh, int32_t rows, int32_t S,
+                 int32_t kbits, const int64_t* lut, int64_t l2e, int32_t fp, int32_t* p, int64_t ldp, int64_t* den,
+                 bx_stream_t stream);
+
+/* Replaces Segs.attn_out (src/bitexact/exact/segs.py:108-113, 187-188): o = div_round(num, FR - FV, den) regrouped to
+ * rows of H HD values (row o, head hh reads group (o / T) HKV + hh / g, query (hh % g) T + o % T), then
+ * quantized per row at -FR: q int32 [rows, H HD], sh int64 [rows]. */
+int bx_attn_out(const int64_t* num, int64_t sn_group, int64_t sn_query, const int64_t* den, int64_t sd_group,
+                int32_t rows, int32_t T, int32_t HKV, int32_t g, int32_t HD, int32_t FR, int32_t FV, int32_t* q,
+                int64_t ldq, int64_t* sh, bx_stream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

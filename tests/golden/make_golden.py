@@ -1,0 +1,87 @@
+"""Writes tests/golden/reference_vectors.npz: input/output vectors of the reference's CPU integer rules that
+closed forms do not pin bit for bit (ops.rms, ops.exp2neg_lut, ops.softmax_w, segs.norm_quant, ops.div_round,
+int8 ops.quant_rows). Run in the development container only, where the reference checkout is present:
+
+    python tests/golden/make_golden.py /root/reference
+
+The reference's own functions compute the expected outputs (src/bitexact/exact/ops.py:92-143,
+src/bitexact/exact/segs.py:59-63, src/bitexact/int8/ops.py:24-35); the inputs are seeded here. Only the
+resulting arrays are committed; nothing from the reference is copied.
+"""
+
+import os
+import sys
+
+import numpy as np
+import torch
+
+
+def main(ref_root):
+    sys.path.insert(0, os.path.join(ref_root, "src"))
+    from bitexact.exact import ops                     # noqa: E402  (reference, CPU paths only)
+    from bitexact.exact import segs                    # noqa: E402
+    from bitexact.int8 import ops as iops              # noqa: E402
+
+    out = {}
+    g = torch.Generator().manual_seed(20261201)
+    f = torch.arange((1 << 14) + 1, dtype=torch.float64) / (1 << 14)
+    lut = torch.round(torch.pow(2.0, -f) * 2.0 ** 60).long()
+
+    # rms and norm_quant: rows of several magnitudes, widths 512 / 2048 / 4096
+    for D in (512, 2048, 4096):
+        x = torch.randint(-(200 << 24), 200 << 24, (6, D), generator=g)
+        x[1] //= 1 << 12
+        x[2] = (1 << 40) - 1
+        x[3] = x[3] >> 20
+        x[4, :] = 0
+        x[4, 7] = 3
+        x[5] = -x[5].abs() >> 3
+        r, er = ops.rms(x)
+        gm = torch.randint(-255, 256, (D,), generator=g)
+        ge = torch.randint(-14, -6, (D,), generator=g)
+        q, sh, err = segs.norm_quant(x, gm, ge, torch.zeros((), dtype=torch.bool))
+        out[f"rms{D}_x"], out[f"rms{D}_r"], out[f"rms{D}_er"] = x.numpy(), r.numpy(), er.numpy()
+        out[f"nq{D}_gm"], out[f"nq{D}_ge"] = gm.numpy(), ge.numpy()
+        out[f"nq{D}_q"], out[f"nq{D}_sh"], out[f"nq{D}_err"] = q.numpy(), sh.numpy(), np.array(bool(err))
+
+    # exp2neg_lut over its whole argument range and several output widths
+    t = torch.cat([torch.randint(0, 60 << 26, (3000,), generator=g), torch.arange(0, 1 << 16),
+                   torch.tensor([0, 1, (1 << 26) - 1, 1 << 26, (48 << 26) * 2])])
+    for bits in (22, 30, 40):
+        out[f"exp2_t"] = t.numpy()
+        out[f"exp2_o{bits}"] = ops.exp2neg_lut(t, lut, bits).numpy()
+
+    # softmax_w: scores with masks, per-row exponents, head_dim 64 and 128 constants
+    for hd in (64, 128):
+        raw = torch.randint(-(1 << 50), 1 << 50, (24, 300), generator=g)
+        raw[3] = raw[3] >> 30
+        raw[4] = 7
+        sh = torch.randint(-40, -10, (24, 1), generator=g)
+        qpos = torch.randint(-1, 300, (24, 1), generator=g)
+        qpos[0] = -1                                             # no visible key
+        qpos[1] = 299
+        ok = torch.arange(300)[None, :] <= qpos
+        p, den = ops.softmax_w(raw, ok, sh, 17, lut, 22, ops.L2E28_HD[hd])
+        out[f"sm{hd}_raw"], out[f"sm{hd}_sh"], out[f"sm{hd}_qpos"] = raw.numpy(), sh.numpy(), qpos.numpy()
+        out[f"sm{hd}_p"], out[f"sm{hd}_den"] = p.numpy(), den.numpy()
+
+    # div_round as attn_div uses it, and quant at -FR
+    num = torch.randint(-(1 << 60), 1 << 60, (2000,), generator=g)
+    den = torch.randint(1 << 22, 1 << 34, (2000,), generator=g)
+    out["dr_num"], out["dr_den"] = num.numpy(), den.numpy()
+    out["dr_o"] = ops.div_round(num, 24 - 19, den).numpy()
+
+    # int8 quant_rows with 2 limbs
+    z = torch.randint(-(1 << 44), 1 << 44, (8, 256), generator=g)
+    z[1] //= 1 << 40
+    z[2] = 0
+    q, as_, sh = iops.quant_rows(z, 2)
+    out["qr_z"], out["qr_q"], out["qr_as"], out["qr_sh"] = z.numpy(), q.numpy(), as_.numpy(), sh.numpy()
+
+    path = os.path.join(os.path.dirname(os.path.abspath(__file__)), "reference_vectors.npz")
+    np.savez_compressed(path, **out)
+    print("wrote", path, sum(v.nbytes for v in out.values()), "bytes")
+
+
+if __name__ == "__main__":
+    main(sys.argv[1] if len(sys.argv) > 1 else "/root/reference")

@@ -1,0 +1,140 @@
+"""HIP attention-side kernels against the CPU oracle, bit for bit: paged exact attention (reference
+tests/test_vllm_exact_attn.py: head_dim 64 / 128, three magnitudes, five (R, M, P) cases, four splits),
+the paged KV store, the fused prefill attention (exact/model.py's bmm -> softmax -> bmm), and the limb bmm
+(reference tests/test_gpu_kernels.py:9-19)."""
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import bxref as R
+
+pytestmark = pytest.mark.gpu
+
+
+def _lut(dev):
+    return torch.from_numpy(R.exp2_table()).to(dev)
+
+
+def test_kv_store_matches_oracle(dev):
+    from bitexact.vllm_plugin.tri_paged import store, to_limbs
+    g = torch.Generator().manual_seed(0)
+    c = torch.randint(-R.LIM3, R.LIM3 + 1, (5, 3, 16, 2 * 64), generator=g).to(torch.int32)
+    assert np.array_equal(to_limbs(c.to(dev)).cpu().numpy(), R.to_limbs(c.numpy()))
+    # store with skipped slots and int64 input
+    cache = torch.zeros(4, 2, 16, 8 * 64, dtype=torch.int8, device=dev)
+    k = torch.randint(-R.LIM3, R.LIM3 + 1, (6, 2, 64), generator=g)
+    v = torch.randint(-R.LIM3, R.LIM3 + 1, (6, 2, 64), generator=g)
+    slot = torch.tensor([0, 17, -1, 33, 63, 5])
+    store(cache, slot.to(dev), k.to(dev), v.to(dev))
+    ref = np.zeros((4, 2, 16, 8 * 64), np.int8)
+    kv = np.concatenate([k.numpy(), v.numpy()], -1)
+    lim = R.to_limbs(kv[:, :, None, :].transpose(0, 1, 2, 3).reshape(6, 2, 1, 128))
+    for n, s in enumerate(slot.tolist()):
+        if s >= 0:
+            ref[s // 16, :, s % 16] = lim[n, :, 0]
+    assert np.array_equal(cache.cpu().numpy(), ref)
+
+
+@pytest.mark.parametrize("HD", [64, 128])
+def test_exact_paged_attention(dev, HD):
+    from bitexact.vllm_plugin import tri_exact_attn, tri_paged
+    g = torch.Generator().manual_seed(HD)
+    lut = _lut(dev)
+    nb, bs, HKV = 96, 16, 8
+    l2e = R.L2E28_HD[HD]
+    for lim in (R.LIM3, 1 << 13, 1 << 10):
+        c = torch.randint(-lim, lim + 1, (nb, HKV, bs, 2 * HD), generator=g).to(torch.int32)
+        cl = tri_paged.to_limbs(c.to(dev))
+        for Rr, M, P in [(3, 4, 600), (5, 4, 3000), (6, 1, 900), (2, 3, 50), (7, 4, 5)]:
+            bt = torch.randint(1, nb, (Rr, 200), generator=g).to(torch.int32)
+            qpos = torch.randint(0, P, (Rr, M), generator=g)
+            q = torch.randint(-(1 << 22), (1 << 22) + 1, (Rr, HKV, M, HD), generator=g).to(torch.int32)
+            sh = torch.randint(-40, -10, (Rr, HKV, M), generator=g)
+            rmap = torch.arange(Rr)
+            ref_num, ref_den = R.paged_attend(q.numpy(), sh.numpy(), qpos.numpy(), c.numpy(), bt.numpy(),
+                                              rmap.numpy(), R.exp2_table(), l2e)
+            for ns in (None, 1, 5, 64):
+                num, den = tri_exact_attn.attend(q.to(dev), sh.to(dev), qpos.to(dev), cl, bt.to(dev), rmap.to(dev),
+                                                 lut, l2e, nsplit=ns)
+                assert np.array_equal(num.cpu().numpy(), ref_num), (Rr, M, ns, lim)
+                assert np.array_equal(den.cpu().numpy(), ref_den), (Rr, M, ns, lim)
+
+
+def test_paged_attention_rmap_and_empty_rows(dev):
+    """Rows mapped to shared block-table rows, a query with no visible key (qpos -1), repeated calls
+    (the split workspace is restored after each call)."""
+    from bitexact.vllm_plugin import tri_exact_attn, tri_paged
+    g = torch.Generator().manual_seed(7)
+    HD, nb, bs, HKV = 64, 20, 16, 2
+    c = torch.randint(-R.LIM3, R.LIM3 + 1, (nb, HKV, bs, 2 * HD), generator=g).to(torch.int32)
+    cl = tri_paged.to_limbs(c.to(dev))
+    bt = torch.randint(0, nb, (2, 8), generator=g).to(torch.int32)
+    rmap = torch.tensor([1, 0, 1])
+    qpos = torch.tensor([[100, -1, 3, 127], [5, 6, 7, 8], [0, 0, 0, 0]])
+    q = torch.randint(-(1 << 22), (1 << 22) + 1, (3, HKV, 4, HD), generator=g).to(torch.int32)
+    sh = torch.randint(-40, -10, (3, HKV, 4), generator=g)
+    ref = R.paged_attend(q.numpy(), sh.numpy(), qpos.numpy(), c.numpy(), bt.numpy(), rmap.numpy(), R.exp2_table(),
+                         R.L2E28)
+    for ns in (3, 3, 1, 8):
+        num, den = tri_exact_attn.attend(q.to(dev), sh.to(dev), qpos.to(dev), cl, bt.to(dev), rmap.to(dev), _lut(dev),
+                                         R.L2E28, nsplit=ns)
+        assert np.array_equal(num.cpu().numpy(), ref[0]) and np.array_equal(den.cpu().numpy(), ref[1]), ns
+
+
+@pytest.mark.parametrize("HD", [64, 128])
+def test_prefill_attention(dev, HD):
+    from bitexact.exact.attention import prefill
+    g = torch.Generator().manual_seed(3 + HD)
+    B, HKV, grp, T, L = 2, 2, 4, 70, 96
+    Z = B * HKV
+    qg = torch.randint(-(1 << 22), (1 << 22) + 1, (Z, grp * T, HD), generator=g).to(torch.int32)
+    shg = torch.randint(-40, -10, (Z, grp * T, 1), generator=g)
+    cache_k = torch.randint(-R.LIM3, R.LIM3 + 1, (B, HKV, L, HD), generator=g).to(torch.int32)
+    cache_v = torch.randint(-R.LIM3, R.LIM3 + 1, (B, HKV, L, HD), generator=g).to(torch.int32)
+    pos = torch.arange(T)[None].expand(B, T) + torch.tensor([[0], [20]])           # two sequences, offsets
+    S = int(pos.max()) + 1
+    qpos = pos[:, None, None, :].expand(B, HKV, grp, T).reshape(Z, grp * T, 1)
+    Kc = cache_k[:, :, :S].reshape(Z, S, HD)
+    Vc = cache_v[:, :, :S].reshape(Z, S, HD)
+    ref_num, ref_den = R.attention_prefill(qg.numpy(), shg.numpy(), Kc.numpy(), Vc.numpy(), qpos.numpy(),
+                                           R.exp2_table(), R.L2E28_HD[HD])
+    kd = cache_k.to(dev)[:, :, :S].reshape(Z, S, HD)      # strided view of the cache (row stride L * HD)
+    vd = cache_v.to(dev)[:, :, :S].reshape(Z, S, HD)
+    num, den = prefill(qg.to(dev), shg.to(dev), kd, vd, qpos.to(dev), _lut(dev), R.L2E28_HD[HD])
+    assert np.array_equal(num.cpu().numpy(), ref_num) and np.array_equal(den.cpu().numpy(), ref_den)
+
+
+def test_bmm_exact(dev):
+    from bitexact.bmm import bmm
+    g = torch.Generator().manual_seed(0)
+    for Z, M, K, N in [(3, 5, 64, 70), (16, 4, 700, 64), (2, 130, 64, 129)]:
+        a = torch.randint(-R.LIM3, R.LIM3 + 1, (Z, M, K), generator=g)
+        b = torch.randint(-R.LIM3, R.LIM3 + 1, (Z, K, N), generator=g).to(torch.int32)
+        ref = R.bmm(a.numpy(), b.numpy())
+        assert np.array_equal(bmm(a.to(dev), b.to(dev)).cpu().numpy(), ref)
+        bt = b.to(dev).transpose(1, 2).contiguous().transpose(1, 2)
+        assert np.array_equal(bmm(a.to(dev), bt).cpu().numpy(), ref)
+    # fewer limbs: values within 1 limb times 3-limb values
+    a = torch.randint(-128, 128, (2, 9, 33), generator=g)
+    b = torch.randint(-R.LIM3, R.LIM3 + 1, (2, 33, 11), generator=g)
+    assert np.array_equal(bmm(a.to(dev), b.to(dev), na=1).cpu().numpy(), R.bmm(a.numpy(), b.numpy()))
+
+
+def test_unfused_equals_fused_attention(dev):
+    """GPU bmm -> GPU softmax -> GPU bmm (the reference model's unfused order) against the fused prefill."""
+    from bitexact.bmm import bmm
+    from bitexact.exact import ops
+    from bitexact.exact.attention import prefill
+    g = torch.Generator().manual_seed(11)
+    Z, gT, S, HD = 4, 96, 96, 64
+    qg = torch.randint(-(1 << 22), (1 << 22) + 1, (Z, gT, HD), generator=g).to(torch.int32).to(dev)
+    shg = torch.randint(-40, -10, (Z, gT, 1), generator=g).to(dev)
+    K = torch.randint(-R.LIM3, R.LIM3 + 1, (Z, S, HD), generator=g).to(torch.int32).to(dev)
+    V = torch.randint(-R.LIM3, R.LIM3 + 1, (Z, S, HD), generator=g).to(torch.int32).to(dev)
+    qpos = (torch.arange(gT) % 24 * 4).reshape(1, gT, 1).expand(Z, gT, 1).contiguous().to(dev)
+    raw = bmm(qg, K.transpose(-1, -2))
+    p, den = ops.softmax(raw, qpos, shg, _lut(dev), R.L2E28)
+    num = bmm(p, V)
+    num2, den2 = prefill(qg, shg, K, V, qpos, _lut(dev), R.L2E28)
+    assert torch.equal(num, num2) and torch.equal(den, den2)
