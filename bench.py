@@ -12,7 +12,13 @@ Also measured (config 3): exact-mode prefill, M = 2048 over every Llama-3.2-1B l
 TOPS = 9 x 2 M N K / time and as a fraction of the 5.0 POP/s dense int8 peak. And a CPU baseline: the oracle's
 float64 restatement of the same GEMMs (oracle/bxref.py imm, the reference's CPU path) on a bounded sample.
 
-Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-prefill] [--no-cpu]
+Config 4 (integer attention, B=4, H=32, HKV=8, HD=64, causal, S=2048) is measured too: the paged decode step
+(HBM bytes B HKV S 6 HD of limb planes per call, caches rotated over >= 1 GiB) and the fused prefill attention
+(effective limb-op TOPS, 2 x 9 x 2 HD B H T(T+1)/2 per call).
+
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-prefill] [--no-attn] [--no-cpu]
+       python bench.py --eager ...        launches without graphs (for counter collection)
+       python bench.py --copy-calibrate   only a 1 GiB device copy, 20 times (HBM counter scale)
 """
 
 import argparse
@@ -77,10 +83,25 @@ def quant40(x):
     return q.to(torch.int32).contiguous(), sh
 
 
+EAGER = False
+
+
 def time_graph(fn_steps, warmup, steps, stream):
     """Capture `steps` calls of fn_steps(i) in one graph (and `warmup` in another); return seconds for the
     timed replay, measured with HIP events recorded on the capture/launch stream."""
     import torch
+    if EAGER:
+        with torch.cuda.stream(stream):
+            for i in range(warmup):
+                fn_steps(i)
+            torch.cuda.synchronize()
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            e0.record(stream)
+            for i in range(steps):
+                fn_steps(warmup + i)
+            e1.record(stream)
+            torch.cuda.synchronize()
+        return e0.elapsed_time(e1) / 1e3
     gw, gt = torch.cuda.CUDAGraph(), torch.cuda.CUDAGraph()
     with torch.cuda.stream(stream):
         fn_steps(0)                      # allocations (outputs, workspaces) before capture
@@ -177,6 +198,72 @@ def bench_prefill(dev, reps=10):
     return res, tot_ops / tot_s / 1e12
 
 
+def bench_attention(dev, reps=20):
+    """Config 4: paged exact decode attention (one query per head, group 4 -> M = 4 per KV head) over a
+    2048-token context per sequence, and the fused exact prefill attention over the whole causal T = 2048."""
+    import torch
+    from bitexact.exact.attention import prefill
+    from bitexact.exact.consts import exp2_table
+    from bitexact.vllm_plugin import tri_exact_attn
+    B, H, HKV, HD, S, bs = 4, 32, 8, 64, 2048, 16
+    grp = H // HKV
+    lim = 8355711
+    l2e = 387270501
+    lut = exp2_table(dev)
+    g = torch.Generator(device=dev).manual_seed(77)
+    nblk = S // bs
+    nb = B * nblk
+    cache_bytes = nb * HKV * bs * 8 * HD
+    ncop = max(4, -(-(1 << 30) // cache_bytes))
+    caches = [torch.randint(-128, 128, (nb, HKV, bs, 8 * HD), dtype=torch.int8, device=dev, generator=g)
+              for _ in range(ncop)]
+    bt = torch.randperm(nb, device=dev, generator=g).to(torch.int32).reshape(B, nblk)
+    rmap = torch.arange(B, device=dev)
+    q = torch.randint(-(1 << 22), (1 << 22) + 1, (B, HKV, grp, HD), device=dev, generator=g).to(torch.int32)
+    sh = torch.randint(-40, -25, (B, HKV, grp), device=dev, generator=g)
+    qpos = torch.full((B, grp), S - 1, dtype=torch.long, device=dev)
+    stream = torch.cuda.Stream(dev)
+    outs = {}
+
+    def dstep(i):
+        outs[0] = tri_exact_attn.attend(q, sh, qpos, caches[i % ncop], bt, rmap, lut, l2e)
+    s_dec = time_graph(dstep, 4, reps * 4, stream) / (reps * 4)
+    dbytes = B * HKV * S * 6 * HD
+    del caches
+    torch.cuda.empty_cache()
+    # prefill: qg [B HKV, grp T, HD] grouped queries, K / V [B HKV, S, HD], causal positions
+    T = S
+    Z = B * HKV
+    qg = torch.randint(-(1 << 22), (1 << 22) + 1, (Z, grp * T, HD), device=dev, generator=g).to(torch.int32)
+    shg = torch.randint(-40, -25, (Z, grp * T, 1), device=dev, generator=g)
+    K = torch.randint(-lim, lim + 1, (Z, S, HD), device=dev, generator=g).to(torch.int32)
+    V = torch.randint(-lim, lim + 1, (Z, S, HD), device=dev, generator=g).to(torch.int32)
+    qp = torch.arange(T, device=dev).repeat(grp).reshape(1, grp * T, 1).expand(Z, grp * T, 1).contiguous()
+
+    def pstep(i):
+        outs[1] = prefill(qg, shg, K, V, qp, lut, l2e)
+    s_pre = time_graph(pstep, 1, 3, stream) / 3
+    ops = 2 * 9 * 2 * HD * B * H * T * (T + 1) // 2
+    return {"workload": "config 4: B=4, H=32, HKV=8, HD=64, causal, context 2048, paged block 16",
+            "decode_us": round(s_dec * 1e6, 2), "decode_bytes": dbytes,
+            "decode_GBps": round(dbytes / s_dec / 1e9, 1), "decode_frac_hbm": round(dbytes / s_dec / 1e9 / HBM_PEAK_GBS, 4),
+            "prefill_ms": round(s_pre * 1e3, 3), "prefill_limb_ops": ops,
+            "prefill_TOPS": round(ops / s_pre / 1e12, 2),
+            "prefill_frac_int8_peak": round(ops / s_pre / 1e12 / INT8_PEAK_TOPS, 4)}
+
+
+def copy_calibrate(dev):
+    """A plain 1 GiB device copy, 20 times: the HBM counters read for it scale the bench's counters."""
+    import torch
+    a = torch.empty(1 << 30, dtype=torch.uint8, device=dev)
+    b = torch.empty_like(a)
+    a.fill_(1)
+    for _ in range(20):
+        b.copy_(a)
+    torch.cuda.synchronize()
+    print(json.dumps({"copy_bytes_each_way": 1 << 30, "copies": 20}), flush=True)
+
+
 def cpu_baseline(budget_s=20.0):
     """oracle/bxref.py's float64 restatement of the int8 GEMM (the reference's CPU path imm,
     src/bitexact/int8/ops.py:87-90) on the config-2 shapes at M = 8, on the host cores; GB/s of the same
@@ -209,8 +296,13 @@ def main():
     ap.add_argument("--steps", type=int, default=60)
     ap.add_argument("--warmup", type=int, default=6)
     ap.add_argument("--no-prefill", action="store_true")
+    ap.add_argument("--no-attn", action="store_true")
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--eager", action="store_true")
+    ap.add_argument("--copy-calibrate", action="store_true")
     args = ap.parse_args()
+    global EAGER
+    EAGER = args.eager
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py: this build runs on one GPU only (the hot path has no collectives); use --gpus 1",
               file=sys.stderr)
@@ -220,6 +312,9 @@ def main():
         print("bench.py: no GPU visible", file=sys.stderr)
         sys.exit(1)
     dev = torch.device("cuda:0")
+    if args.copy_calibrate:
+        copy_calibrate(dev)
+        return
     log("decode GEMMs ...")
     sec, step_bytes, launches, per = bench_decode(dev, args.steps, args.warmup)
     value = step_bytes * args.steps / sec / 1e9
@@ -241,6 +336,9 @@ def main():
                                             "weights, 3-limb N(0,1) activations), fused epilogue",
                                 "TOPS": round(tops, 1), "frac_int8_peak": round(tops / INT8_PEAK_TOPS, 4),
                                 "peak_TOPS": INT8_PEAK_TOPS, "per_gemm": res}
+    if not args.no_attn:
+        log("attention ...")
+        out["exact_attention"] = bench_attention(dev)
     if not args.no_cpu:
         log("cpu baseline ...")
         out["cpu_baseline"] = cpu_baseline()

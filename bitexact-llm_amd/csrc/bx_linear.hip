@@ -19,6 +19,8 @@
 // change a bit.
 #include "bx_common.h"
 
+#include <algorithm>
+
 namespace bx {
 
 enum Mode { RAW32 = 0, JOIN = 1, WMM_T = 2, EXACT = 3 };
@@ -46,6 +48,8 @@ struct LinArgs {
   int32_t* sem;          // split-K counters, one per output tile
   int ks;                // K bytes per block (multiple of 64)
   int spw;               // gemv: k steps per wave
+  int nla;               // gemv: stacked activation groups (exact 3, JOIN nl, RAW32 1); rows_a = nla M
+  int tiles, parts_lg, mp;   // gemv: column tiles, log2 of the row parts per tile, output rows per part
 };
 
 // ---- epilogue shared by both kernels: one output element from its exact int64 dense value ----
@@ -184,55 +188,172 @@ __device__ __forceinline__ void ring_barrier() {
 // =====================================================================================================
 // gemv kernel (decode)
 // =====================================================================================================
-template <int RA, int MODE, int NT>
-__device__ __forceinline__ void stage_a(const LinArgs& p, int8_t* As, int k0, int kend, int kpad, int LDA) {
-  const int tid = threadIdx.x;
+// Activation staging, in two phases so that the activation loads are issued before the weight loads: vector
+// memory operations complete in order, so activations requested after the weights could only be written to
+// LDS once every weight had arrived. Chunk c of the block's slice is 4 int32 of q (exact: row c / nq, split
+// into 3 limb rows while stored) or 16 int8 of a stacked row (JOIN / RAW32: local row c / nq, which is group
+// i = row / Ml, output row m0 + row % Ml). Local row layout: group i at rows [i Ml, (i + 1) Ml), zero rows up
+// to RA, zero columns past kend.
+constexpr int kAB = 8;   // chunks per thread requested ahead of the weights
+
+// Raw buffer loads (stride 0, byte range [0, kBufRange)): an offset at or past the range returns zero without
+// a memory access but still counts as an outstanding load, so a skipped step costs no traffic and the
+// compiler's wait counts stay the same on every path.
+constexpr int kBufRange = 0x7fffffff;
+constexpr int kBufSkip = 0x7fffffff;   // offset of a skipped load
+
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t buf_rsrc(const void* base) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, kBufRange, 0x00020000);
+}
+
+__device__ __forceinline__ v4i buf_load16(__amdgpu_buffer_rsrc_t r, int off) {
+  return __builtin_bit_cast(v4i, __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 0));
+}
+
+// floor(x / d) for 0 <= x < 2^21 from rcp ~ 1 / d (v_rcp_f32, relative error <= 2^-23): the quotient of
+// x + 1/2 is at least 1 / (2 d) away from an integer and its float error is below (x + 1/2) 2^-22 / d.
+__device__ __forceinline__ int qdiv(int x, float rcp) { return (int)(((float)x + 0.5f) * rcp); }
+
+struct ASlice {
+  int m0, Ml, k0, kend, nq, rows, total, LDA;
+  float ml_rcp, nq_rcp;
+};
+
+template <int MODE>
+__device__ __forceinline__ ASlice a_slice(const LinArgs& p, int m0, int Ml, int k0, int kend, int kpad, int LDA) {
+  ASlice a;
+  a.m0 = m0; a.Ml = Ml; a.k0 = k0; a.kend = kend; a.LDA = LDA;
+  a.nq = (MODE == EXACT || MODE == WMM_T) ? kpad >> 2 : kpad >> 4;
+  a.rows = (MODE == EXACT || MODE == WMM_T) ? Ml : p.nla * Ml;
+  a.total = a.rows * a.nq;
+  a.ml_rcp = __builtin_amdgcn_rcpf((float)Ml);
+  a.nq_rcp = __builtin_amdgcn_rcpf((float)a.nq);
+  return a;
+}
+
+// chunk (r, kq) of the slice: row r, 4-int32 (exact) or 16-byte column kq
+// Chunks past the slice read the slice's first chunk (unconditional loads, no branches; a wave past the end
+// issues one request per instruction).
+// ares: buffer resource at the activations (exact: q, else the stacked rows); chunks past the slice are
+// skipped loads.
+template <int MODE>
+__device__ __forceinline__ v4i a_load(const LinArgs& p, __amdgpu_buffer_rsrc_t ares, const ASlice& a, int r, int kq) {
+  int off;
   if (MODE == EXACT || MODE == WMM_T) {
-    const int nq = kpad >> 2, total = p.M * nq;
-    for (int c0 = tid; c0 < total; c0 += NT * 4) {
-      v4i v[4];
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {   // unconditional (clamped) loads, then select: no per-lane branches
-        const int c = min(c0 + i * NT, total - 1), m = c / nq, k = k0 + (c - m * nq) * 4;
-        v[i] = *(const v4i*)(p.q + (int64_t)m * p.ldq + min(k, p.K - 4));
-      }
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const int c = c0 + i * NT;
-        if (c < total) {
-          const int m = c / nq, kq = c - m * nq;
-          uint32_t l0 = 0, l1 = 0, l2 = 0;
-          if (k0 + kq * 4 < kend) split3(v[i], l0, l1, l2);
-          *(uint32_t*)(As + (0 * p.M + m) * LDA + kq * 4) = l0;
-          *(uint32_t*)(As + (1 * p.M + m) * LDA + kq * 4) = l1;
-          *(uint32_t*)(As + (2 * p.M + m) * LDA + kq * 4) = l2;
-        }
-      }
-    }
-    const int nc = kpad >> 4;
-    for (int c = tid; c < (RA - 3 * p.M) * nc; c += NT) {
-      const int r = 3 * p.M + c / nc, kc = c % nc;
-      *(v4i*)(As + r * LDA + kc * 16) = v4i{0, 0, 0, 0};
-    }
+    off = ((a.m0 + r) * (int)p.ldq + min(a.k0 + kq * 4, p.K - 4)) * 4;
   } else {
-    const int nc = kpad >> 4, total = RA * nc;
-    for (int c0 = tid; c0 < total; c0 += NT * 4) {
-      v4i v[4];
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const int c = min(c0 + i * NT, total - 1), r = min(c / nc, p.rows_a - 1), k = k0 + (c % nc) * 16;
-        v[i] = *(const v4i*)(p.a + (int64_t)r * p.K + min(k, p.K - 16));
-      }
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const int c = c0 + i * NT;
-        if (c < total) {
-          const int r = c / nc, kc = c - r * nc;
-          const bool ok = r < p.rows_a && k0 + kc * 16 < kend;
-          *(v4i*)(As + r * LDA + kc * 16) = ok ? v[i] : v4i{0, 0, 0, 0};
-        }
-      }
+    const int grp = qdiv(r, a.ml_rcp), grow = grp * p.M + a.m0 + (r - grp * a.Ml);
+    off = grow * p.K + min(a.k0 + kq * 16, p.K - 16);
+  }
+  return buf_load16(ares, r < a.rows ? off : kBufSkip);
+}
+
+// Stores one chunk; chunks past the slice go to a 64-byte dummy slot of LDS (unconditional stores: a store
+// under a branch lets the compiler sink its load into the branch, where it waits for every earlier load).
+template <int MODE>
+__device__ __forceinline__ void a_store(int8_t* As, int8_t* dummy, const ASlice& a, int r, int kq, v4i v) {
+  const bool in = r < a.rows;
+  if (MODE == EXACT || MODE == WMM_T) {
+    uint32_t l0, l1, l2;
+    split3(v, l0, l1, l2);
+    const bool z = a.k0 + kq * 4 >= a.kend;
+    int8_t* d = in ? As + r * a.LDA + kq * 4 : dummy;
+    const int pl = in ? a.Ml * a.LDA : 16;
+    *(uint32_t*)d = z ? 0u : l0;
+    *(uint32_t*)(d + pl) = z ? 0u : l1;
+    *(uint32_t*)(d + 2 * pl) = z ? 0u : l2;
+  } else {
+    *(v4i*)(in ? As + r * a.LDA + kq * 16 : dummy) = a.k0 + kq * 16 < a.kend ? v : v4i{0, 0, 0, 0};
+  }
+}
+
+// Chunk walk of one thread: chunks tid, tid + NT, tid + 2 NT, ... as (row, column) pairs, stepped without
+// divisions.
+struct AWalk {
+  int r, kq, dr, dq;
+  __device__ __forceinline__ void init(const ASlice& a, int c, int NT) {   // c, NT < 2^21
+    r = qdiv(c, a.nq_rcp);
+    kq = c - r * a.nq;
+    dr = qdiv(NT, a.nq_rcp);
+    dq = NT - dr * a.nq;
+  }
+  __device__ __forceinline__ void step(const ASlice& a) {
+    r += dr;
+    kq += dq;
+    if (kq >= a.nq) {
+      kq -= a.nq;
+      ++r;
     }
+  }
+};
+
+// phase 1: the first kAB chunks of this thread. Batches wholly past the slice are not issued (a block-uniform
+// branch: every vector memory instruction costs address-unit time, even one that reads nothing); these
+// loads precede the weight loads, so skipping them does not change any wait on a weight.
+template <int MODE, int NT>
+__device__ __forceinline__ void a_issue(const LinArgs& p, __amdgpu_buffer_rsrc_t ares, const ASlice& a,
+                                        v4i (&v)[kAB]) {
+  AWalk w;
+  w.init(a, threadIdx.x, NT);
+#pragma unroll
+  for (int i = 0; i < kAB; ++i) {
+    if (i * NT < a.total) v[i] = a_load<MODE>(p, ares, a, w.r, w.kq);
+    w.step(a);
+  }
+}
+
+// phase 2: store them, load + store the rest (slices beyond kAB NT chunks), zero the padding rows
+template <int RA, int MODE, int NT>
+__device__ __forceinline__ void a_finish(const LinArgs& p, __amdgpu_buffer_rsrc_t ares, const ASlice& a,
+                                         const v4i (&v)[kAB], int8_t* As, int8_t* dummy, int kpad) {
+  const int tid = threadIdx.x;
+  AWalk w;
+  w.init(a, tid, NT);
+#pragma unroll
+  for (int i = 0; i < kAB; ++i) {
+    if (i * NT < a.total) a_store<MODE>(As, dummy, a, w.r, w.kq, v[i]);
+    w.step(a);
+  }
+  for (int b = kAB * NT; b < a.total; b += 4 * NT) {
+    AWalk w2 = w;
+    v4i x[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      x[i] = a_load<MODE>(p, ares, a, w2.r, w2.kq);
+      w2.step(a);
+    }
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      a_store<MODE>(As, dummy, a, w.r, w.kq, x[i]);
+      w.step(a);
+    }
+  }
+  const int used = (MODE == EXACT || MODE == WMM_T ? 3 : p.nla) * a.Ml, nc = kpad >> 4;
+  for (int c = tid; c < (RA - used) * nc; c += NT) {
+    const int r = used + c / nc, kc = c % nc;
+    *(v4i*)(As + r * a.LDA + kc * 16) = v4i{0, 0, 0, 0};
+  }
+}
+
+// Block barrier for LDS only: waits for this wave's LDS operations (lgkmcnt 0) but not for its outstanding
+// global loads (vmcnt left at its maximum), unlike __syncthreads(), whose fence waits for every load.
+__device__ __forceinline__ void lds_barrier() {
+  __builtin_amdgcn_s_waitcnt(15 | (3 << 14) | (7 << 4));
+  asm volatile("s_barrier" ::: "memory");
+}
+
+// gemv block -> (column tile, row part). With several parts the parts of one column tile are consecutive
+// blocks of one XCD (blocks are dispatched to the 8 XCDs round-robin), so the later parts' weight reads hit
+// that XCD's L2 instead of HBM. Any mapping gives the same integers.
+__device__ __forceinline__ void gemv_block(const LinArgs& p, int& tile, int& part) {
+  const int L = blockIdx.x, lg = p.parts_lg;   // parts = 2^lg
+  if (lg > 0 && (p.tiles & 7) == 0) {
+    const int xcd = L & 7, slot = L >> 3;
+    part = slot & ((1 << lg) - 1);
+    tile = (slot >> lg) * 8 + xcd;
+  } else {
+    tile = L >> lg;
+    part = L & ((1 << lg) - 1);
   }
 }
 
@@ -243,7 +364,10 @@ __global__ __launch_bounds__(64 * CG * KS) void gemv_kernel(LinArgs p) {
   __shared__ int s_last;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int cg = wave % CG, kslice = wave / CG;
-  const int n0 = blockIdx.x * BNC;
+  int tile, part;
+  gemv_block(p, tile, part);
+  const int n0 = tile * BNC;
+  const int m0 = part * p.mp, Ml = min(p.mp, p.M - m0);
   const int k0 = blockIdx.y * p.ks;
   const int kend = min(p.K, k0 + p.ks);
   const int nst = (kend - k0 + 63) >> 6;           // k steps of 64 in this block
@@ -254,16 +378,21 @@ __global__ __launch_bounds__(64 * CG * KS) void gemv_kernel(LinArgs p) {
 
   // this wave's weight row and k steps [s0, s1)
   const int kl = (lane >> 4) * 16;
-  const int8_t* wrow = p.w + (int64_t)min(n0 + cg * 16 + (lane & 15), p.N - 1) * p.ld_row;
+  const __amdgpu_buffer_rsrc_t wres = buf_rsrc(p.w + (int64_t)n0 * p.ld_row);
+  const int wrow = (min(n0 + cg * 16 + (lane & 15), p.N - 1) - n0) * (int)p.ld_row;
   const int s0 = kslice * p.spw, s1 = min(nst, s0 + p.spw);
   const int ngroups = s1 > s0 ? (s1 - s0 + U - 1) / U : 0;
   const int kmax = p.K - 16;
+  // Steps past this wave's range are range-checked buffer loads that read nothing (the first group is issued
+  // unconditionally so that the waits for the activation stores never include it).
   auto issue = [&](v4i(&b)[U][NB], int s) {
 #pragma unroll
     for (int u = 0; u < U; ++u)
 #pragma unroll
-      for (int j = 0; j < NB; ++j)
-        b[u][j] = *(const v4i*)(wrow + j * p.ld_plane + min(k0 + (s + u) * 64 + kl, kmax));
+      for (int j = 0; j < NB; ++j) {
+        const int off = wrow + j * (int)p.ld_plane + min(k0 + (s + u) * 64 + kl, kmax);
+        b[u][j] = buf_load16(wres, s + u < s1 ? off : kBufSkip);
+      }
   };
   v4i acc[RB][NB];
 #pragma unroll
@@ -285,12 +414,25 @@ __global__ __launch_bounds__(64 * CG * KS) void gemv_kernel(LinArgs p) {
     }
   };
 
+  // activations first, then the weights (the first group, and the second when there is one); the activation
+  // rows are written to LDS while the weights are in flight
+  const ASlice asl = a_slice<MODE>(p, m0, Ml, k0, kend, kpad, LDA);
+  const __amdgpu_buffer_rsrc_t ares = buf_rsrc(MODE == EXACT || MODE == WMM_T ? (const void*)p.q : (const void*)p.a);
+  v4i av[kAB];
+  a_issue<MODE, NT>(p, ares, asl, av);
   v4i b0[U][NB], b1[U][NB];
-  if (ngroups > 0) issue(b0, s0);                   // weights in flight while the activations are staged
-  stage_a<RA, MODE, NT>(p, As, k0, kend, kpad, LDA);
+  issue(b0, s0);
+  // keep every weight request ahead of the first wait for an activation: the memory clobber orders the
+  // loads, the register operands stop uses of the activation values (and their waits) from moving up
+  asm volatile("" ::: "memory");
+#pragma unroll
+  for (int i = 0; i < kAB; ++i) asm volatile("" : "+v"(av[i]));
+  a_finish<RA, MODE, NT>(p, ares, asl, av, As, (int8_t*)(Cs + NB * RA * BNC), kpad);
   for (int i = tid; i < NB * RA * BNC; i += NT) Cs[i] = 0;
-  __syncthreads();
+  lds_barrier();
 
+  // later groups: one more in flight while a group is consumed (block-uniform conditions: no load is issued
+  // that reads nothing)
   for (int gi = 0; gi < ngroups; gi += 2) {
     const int sa = s0 + gi * U, sb = sa + U;
     if (gi + 1 < ngroups) issue(b1, sb);
@@ -316,7 +458,7 @@ __global__ __launch_bounds__(64 * CG * KS) void gemv_kernel(LinArgs p) {
 
   bool bad = false;
   const int nsplit = gridDim.y;
-  for (int e = tid; e < p.M * BNC; e += NT) {
+  for (int e = tid; e < Ml * BNC; e += NT) {
     const int m = e / BNC, c = e - m * BNC, n = n0 + c;
     if (n >= p.N) continue;
     int64_t v;
@@ -324,23 +466,23 @@ __global__ __launch_bounds__(64 * CG * KS) void gemv_kernel(LinArgs p) {
       v = Cs[m * BNC + c];
     } else if (MODE == JOIN) {
       v = 0;
-      for (int i = 0; i < p.nl; ++i) v += (int64_t)Cs[(i * p.M + m) * BNC + c] << (8 * i);
+      for (int i = 0; i < p.nl; ++i) v += (int64_t)Cs[(i * Ml + m) * BNC + c] << (8 * i);
     } else {
       v = 0;
 #pragma unroll
       for (int i = 0; i < 3; ++i)
 #pragma unroll
-        for (int j = 0; j < NB; ++j) v += (int64_t)Cs[(j * RA + i * p.M + m) * BNC + c] << (8 * (i + j));
+        for (int j = 0; j < NB; ++j) v += (int64_t)Cs[(j * RA + i * Ml + m) * BNC + c] << (8 * (i + j));
     }
     if (nsplit > 1)
-      ws_add(p, m, n, v);
+      ws_add(p, m0 + m, n, v);
     else
-      finalize<MODE>(p, m, n, v, bad);
+      finalize<MODE>(p, m0 + m, n, v, bad);
   }
   if (nsplit > 1 && splitk_last(p, blockIdx.x, nsplit, &s_last)) {
-    for (int e = tid; e < p.M * BNC; e += NT) {
+    for (int e = tid; e < Ml * BNC; e += NT) {
       const int m = e / BNC, n = n0 + (e - m * BNC);
-      if (n < p.N) finalize<MODE>(p, m, n, ws_take(p, m, n), bad);
+      if (n < p.N) finalize<MODE>(p, m0 + m, n, ws_take(p, m0 + m, n), bad);
     }
   }
   if (MODE == EXACT && p.checked && bad) p.flag[0] = 1;
@@ -578,6 +720,7 @@ static const TileShape kTileExact = {4, 2, 1, 2, 64, 3};   // 5 accumulator sets
 struct Plan {
   bool gemv;
   int rb, cg, ks_waves, u, spw;   // gemv
+  int parts, mp;                  // gemv row parts, output rows per part
   int tile;                       // tile config
   int tiles_x, tiles_y, split, kbytes;
   size_t lds;
@@ -589,38 +732,87 @@ static int64_t ws_size(int M_out, int N, int tiles) {
   return (((int64_t)M_out * N * 8 + 255) & ~255LL) + (int64_t)tiles * 4;
 }
 
+constexpr size_t kGemvLds = 150 * 1024;   // of the 160 KiB per CU
+
+// Decode-kernel shape: column group count cg (16 cg columns per block), row parts (output rows per block
+// mp = ceil(M / parts), na mp stacked rows <= 64) and k splits, chosen by a cost in HBM-byte equivalents:
+// the weight bytes once, the extra L2-to-CU traffic (weights re-read by the other parts, activations re-read
+// by every column tile) at 1/5 of that, the split-K atomics (three 8-byte operations per output per split),
+// a chip that is not full and a second round of blocks. Returns false when no shape fits.
+static bool gemv_shape(int na, int M, int N, int K, int nb, bool exact, int cus, Plan& best) {
+  const int nst = (K + 63) / 64;
+  const double W = (double)N * K * nb;
+  const double A = exact ? 4.0 * M * K : (double)na * M * K;
+  double best_cost = 1e300;
+  bool found = false;
+  for (int cg = 1; cg <= 4; cg *= 2) {
+    const int BNC = 16 * cg, NT = 64 * 16;
+    const int c = (N + BNC - 1) / BNC;
+    for (int parts = 1; parts <= 8 && parts <= M; parts *= 2) {
+      const int mp = (M + parts - 1) / parts;
+      if ((M + mp - 1) / mp != parts) continue;        // no empty part
+      const int rows = na * mp;
+      if (rows > 64) continue;
+      const int RA = rows <= 16 ? 16 : rows <= 32 ? 32 : 64;
+      const size_t c_lds = (size_t)nb * RA * BNC * 4;
+      int split = 0;
+      size_t lds = 0;
+      for (int k = 1; k <= nst; ++k) {
+        const int steps = (nst + k - 1) / k;
+        lds = (((size_t)RA * (steps * 64 + 16) + 15) & ~(size_t)15) + c_lds + 64;
+        if (lds > kGemvLds) continue;
+        split = (nst + steps - 1) / steps;
+        if ((int64_t)c * parts * split >= cus) break;
+      }
+      if (split == 0) continue;
+      const int64_t blocks = (int64_t)c * parts * split;
+      const int per_cu = (int)std::min<size_t>(160 * 1024 / lds, 2048 / NT);
+      const int64_t rounds = (blocks + (int64_t)cus * per_cu - 1) / ((int64_t)cus * per_cu);
+      double cost = W + 0.2 * (W * (parts - 1) + A * c);
+      if (split > 1) cost += 24.0 * M * N * split;
+      if (blocks < cus) cost += W * ((double)cus / blocks - 1.0);
+      cost += W * 0.5 * (rounds - 1);
+      if (cost < best_cost) {
+        best_cost = cost;
+        found = true;
+        best.cg = cg;
+        best.parts = parts;
+        best.mp = mp;
+        best.rb = RA / 16;
+        best.split = split;
+      }
+    }
+  }
+  return found;
+}
+
 // rows_a: stacked activation rows; nb: weight planes (exact 3, int8 1); na: activation planes on the tile path
+static bool gemv_shape(int na, int M, int N, int K, int nb, bool exact, int cus, Plan& best);
+
 static Plan make_plan(int rows_a, int M_out, int N, int K, int nb, int na, bool exact) {
   Plan s = {};
   const int cus = device_cus();
   const int nst = (K + 63) / 64;
-  if (rows_a <= 64) {
+  if (rows_a <= 128 && gemv_shape(na, M_out, N, K, nb, exact, cus, s)) {
     s.gemv = true;
-    s.rb = rows_a <= 16 ? 1 : rows_a <= 32 ? 2 : 4;
-    const int RA = 16 * s.rb;
-    s.cg = (N + 31) / 32 >= cus ? 2 : 1;
-    s.ks_waves = 16 / s.cg;
-    const int BNC = 16 * s.cg;
-    s.tiles_x = (N + BNC - 1) / BNC;
-    s.tiles_y = 1;
-    int split = 2 * s.tiles_x >= cus ? 1 : (cus + s.tiles_x - 1) / s.tiles_x;
-    // the activation slice must fit LDS (<= 96 KiB with the partial sums)
-    const size_t c_lds = (size_t)nb * RA * BNC * 4;
-    const int max_steps = (int)(((96 * 1024 - c_lds) / RA - 16) / 64);
-    while ((nst + split - 1) / split > max_steps) ++split;
-    if (split > nst) split = nst;
-    const int steps = (nst + split - 1) / split;
+    const int RA = 16 * s.rb, BNC = 16 * s.cg;
+    const int steps = (nst + s.split - 1) / s.split;
     // k steps per wave: at least 2 (fewer k-slices when the block range is short); one load group when
     // every step of the wave fits 8 loads, so all of a wave's weights are requested at once
+    s.ks_waves = 16 / s.cg;
     while (s.ks_waves > 1 && (steps + s.ks_waves - 1) / s.ks_waves < 2) s.ks_waves /= 2;
     if (s.ks_waves < 16 / s.cg / 4) s.ks_waves = 1;   // instantiated k-slice counts: 16/cg, 8/cg, 4/cg, 1
     s.spw = (steps + s.ks_waves - 1) / s.ks_waves;
-    const int maxu = nb == 3 ? 4 : 8;
+    // three weight planes: two k steps per group (four would need more than the 128 registers a lane of a
+    // 1024-thread block has, and spill)
+    const int maxu = nb == 3 ? 2 : 8;
     s.u = s.spw <= 2 ? 2 : s.spw <= 4 ? 4 : maxu;
     if (s.u > maxu) s.u = maxu;
     s.kbytes = steps * 64;
     s.split = (nst + steps - 1) / steps;
-    s.lds = (((size_t)RA * (s.kbytes + 16) + 15) & ~(size_t)15) + c_lds;
+    s.tiles_x = (N + BNC - 1) / BNC;
+    s.tiles_y = s.parts;
+    s.lds = (((size_t)RA * (s.kbytes + 16) + 15) & ~(size_t)15) + (size_t)nb * RA * BNC * 4 + 64;
   } else {
     s.gemv = false;
     const int64_t big = (int64_t)((M_out + 127) / 128) * ((N + 127) / 128);
@@ -661,40 +853,57 @@ static void bind_ws(LinArgs& p, const Plan& s) {
 template <int NB, int RB, int CG, int KS, int U, int MODE>
 static int launch_gemv_cfg(LinArgs& p, const Plan& s, hipStream_t st) {
   allow_lds(gemv_kernel<NB, RB, CG, KS, U, MODE>, s.lds);
-  gemv_kernel<NB, RB, CG, KS, U, MODE><<<dim3(s.tiles_x, s.split), 64 * CG * KS, s.lds, st>>>(p);
+  gemv_kernel<NB, RB, CG, KS, U, MODE><<<dim3(s.tiles_x * s.parts, s.split), 64 * CG * KS, s.lds, st>>>(p);
   return check_launch("gemv_kernel");
+}
+
+template <int NB, int RB, int CG, int KS, int MODE>
+static int launch_gemv_u(LinArgs& p, const Plan& s, hipStream_t st) {
+  if constexpr (NB == 3) {
+    return launch_gemv_cfg<NB, RB, CG, KS, 2, MODE>(p, s, st);
+  } else {
+    if (s.u == 2) return launch_gemv_cfg<NB, RB, CG, KS, 2, MODE>(p, s, st);
+    if (s.u == 4) return launch_gemv_cfg<NB, RB, CG, KS, 4, MODE>(p, s, st);
+    return launch_gemv_cfg<NB, RB, CG, KS, 8, MODE>(p, s, st);
+  }
 }
 
 template <int NB, int RB, int CG, int MODE>
 static int launch_gemv_ks(LinArgs& p, const Plan& s, hipStream_t st) {
   constexpr int KSMAX = 16 / CG;
-  constexpr int UMAX = NB == 3 ? 4 : 8;
-  switch (s.ks_waves * 10 + s.u) {
-#define BX_KS(KSV)                                                             \
-  case KSV * 10 + 2: return launch_gemv_cfg<NB, RB, CG, KSV, 2, MODE>(p, s, st); \
-  case KSV * 10 + 4: return launch_gemv_cfg<NB, RB, CG, KSV, 4, MODE>(p, s, st); \
-  case KSV * 10 + 8: return launch_gemv_cfg<NB, RB, CG, KSV, UMAX, MODE>(p, s, st);
-    BX_KS(KSMAX) BX_KS(KSMAX / 2) BX_KS(KSMAX / 4) BX_KS(1)
-#undef BX_KS
-    default:
-      set_error("gemv: no kernel for %d k-slices, %d steps per group", s.ks_waves, s.u);
-      return BX_EINVAL;
-  }
+  if (s.ks_waves == KSMAX) return launch_gemv_u<NB, RB, CG, KSMAX, MODE>(p, s, st);
+  if (s.ks_waves == KSMAX / 2) return launch_gemv_u<NB, RB, CG, KSMAX / 2, MODE>(p, s, st);
+  if constexpr (KSMAX / 4 > 1)
+    if (s.ks_waves == KSMAX / 4) return launch_gemv_u<NB, RB, CG, KSMAX / 4, MODE>(p, s, st);
+  if (s.ks_waves == 1) return launch_gemv_u<NB, RB, CG, 1, MODE>(p, s, st);
+  set_error("gemv: no kernel for %d k-slices", s.ks_waves);
+  return BX_EINVAL;
+}
+
+template <int NB, int CG, int MODE>
+static int launch_gemv_rb(LinArgs& p, const Plan& s, hipStream_t st) {
+  if (s.rb == 1) return launch_gemv_ks<NB, 1, CG, MODE>(p, s, st);
+  if (s.rb == 2) return launch_gemv_ks<NB, 2, CG, MODE>(p, s, st);
+  return launch_gemv_ks<NB, 4, CG, MODE>(p, s, st);
 }
 
 template <int NB, int MODE>
 static int launch_gemv(LinArgs& p, const Plan& s, hipStream_t st) {
+  // 32-bit buffer offsets: a block's weight rows in every plane, and the whole activation array
+  const int64_t wspan = (int64_t)(NB - 1) * p.ld_plane + (int64_t)64 * p.ld_row + p.K;
+  const int64_t aspan = MODE == EXACT || MODE == WMM_T ? (int64_t)p.M * p.ldq * 4 : (int64_t)p.rows_a * p.K;
+  BX_REQUIRE(wspan < kBufRange - 16 && aspan < kBufRange - 16 && p.ld_plane >= 0,
+             "decode path: limb planes and activations must span less than 2 GiB");
   p.ks = s.kbytes;
   p.spw = s.spw;
+  p.tiles = s.tiles_x;
+  p.parts_lg = s.parts == 1 ? 0 : s.parts == 2 ? 1 : s.parts == 4 ? 2 : 3;
+  p.mp = s.mp;
+  p.nla = MODE == EXACT || MODE == WMM_T ? 3 : MODE == JOIN ? p.nl : 1;
   bind_ws(p, s);
-  if (s.cg == 2) {
-    if (s.rb == 1) return launch_gemv_ks<NB, 1, 2, MODE>(p, s, st);
-    if (s.rb == 2) return launch_gemv_ks<NB, 2, 2, MODE>(p, s, st);
-    return launch_gemv_ks<NB, 4, 2, MODE>(p, s, st);
-  }
-  if (s.rb == 1) return launch_gemv_ks<NB, 1, 1, MODE>(p, s, st);
-  if (s.rb == 2) return launch_gemv_ks<NB, 2, 1, MODE>(p, s, st);
-  return launch_gemv_ks<NB, 4, 1, MODE>(p, s, st);
+  if (s.cg == 4) return launch_gemv_rb<NB, 4, MODE>(p, s, st);
+  if (s.cg == 2) return launch_gemv_rb<NB, 2, MODE>(p, s, st);
+  return launch_gemv_rb<NB, 1, MODE>(p, s, st);
 }
 
 template <int NA, int NB, int MODE, int WM, int WN, int TM, int TN, int BK, int S>
