@@ -31,6 +31,10 @@ HERE = os.path.dirname(os.path.abspath(__file__))
 sys.path.insert(0, os.path.join(HERE, "bitexact-llm_amd"))
 
 HBM_PEAK_GBS = 8000.0
+# HBM bytes per decode launch (average over the step's 9 GEMMs) from rocprofv3 --pmc FETCH_SIZE and WRITE_SIZE
+# runs of `bench.py --eager --no-prefill --no-attn --no-cpu`, each scaled by what the same counter reads for a
+# plain 1 GiB device copy (profiles/decode_gemv_config2_hbm_traffic.txt).
+DECODE_TRAFFIC_PER_LAUNCH = 20356654
 INT8_PEAK_TOPS = 5000.0
 DECODE_SHAPES = [("gate", 8192, 2048), ("up", 8192, 2048), ("down", 2048, 8192)]
 DECODE_M = (1, 8, 64)
@@ -90,6 +94,10 @@ def time_graph(fn_steps, warmup, steps, stream):
     """Capture `steps` calls of fn_steps(i) in one graph (and `warmup` in another); return seconds for the
     timed replay, measured with HIP events recorded on the capture/launch stream."""
     import torch
+    # inputs (weights, decompositions, index arrays such as the ELL residual columns and block tables) were
+    # written on the default stream; the launch stream is a separate non-blocking stream, so wait for them
+    # before the first launch
+    torch.cuda.synchronize()
     if EAGER:
         with torch.cuda.stream(stream):
             for i in range(warmup):
@@ -295,6 +303,7 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=60)
     ap.add_argument("--warmup", type=int, default=6)
+    ap.add_argument("--no-decode", action="store_true", help="profiling runs: skip the decode step (no value)")
     ap.add_argument("--no-prefill", action="store_true")
     ap.add_argument("--no-attn", action="store_true")
     ap.add_argument("--no-cpu", action="store_true")
@@ -315,19 +324,32 @@ def main():
     if args.copy_calibrate:
         copy_calibrate(dev)
         return
-    log("decode GEMMs ...")
-    sec, step_bytes, launches, per = bench_decode(dev, args.steps, args.warmup)
-    value = step_bytes * args.steps / sec / 1e9
+    if args.no_decode:
+        sec, step_bytes, launches, per, value = 1.0, 0, 1, [], None
+    else:
+        log("decode GEMMs ...")
+        sec, step_bytes, launches, per = bench_decode(dev, args.steps, args.warmup)
+        value = step_bytes * args.steps / sec / 1e9
+
+    def r(x, n):
+        return None if x is None else round(x, n)
+    # roofline of the dominant kernel: every decode launch is one gemv_kernel; algorithmic bytes per launch
+    # over its average duration (graph replay timed with HIP events on the launch stream)
+    per_launch_s = sec / args.steps / launches
+    achieved = None if value is None else step_bytes / launches / per_launch_s / 1e9
     out = {"metric": "int8 decode GEMM HBM GB/s (config 2); exact prefill limb-GEMM TOPS and % int8 MFMA peak "
                      "(config 3); 1 GPU",
-           "value": round(value, 1), "unit": "GB/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+           "value": r(value, 1), "unit": "GB/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
            "ms_per_step": round(sec / args.steps * 1e3, 4), "higher_is_better": True, "scaling": "weak",
            "vs_baseline": None, "dtype": "int8 (int32 accumulate, int64 join)", "data": "synthetic",
            "config": {"workload": "config 2: int8-mode decode GEMMs, M in {1,8,64} x gate/up (K=2048, N=8192), "
                                   "down (K=8192, N=2048), 2 activation limbs, int64 joined output",
                       "gemms_per_step": launches, "bytes_per_step": step_bytes, "weight_rotation": ">=1 GiB/shape"},
-           "roofline": {"bound": "hbm", "achieved": round(value, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                        "frac": round(value / HBM_PEAK_GBS, 4), "traffic": None},
+           "roofline": {"bound": "hbm", "kernel": "gemv_kernel (each of the step's decode GEMMs is one launch)",
+                        "achieved": r(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                        "frac": r(None if achieved is None else achieved / HBM_PEAK_GBS, 4),
+                        "traffic": DECODE_TRAFFIC_PER_LAUNCH, "algorithmic_bytes_per_launch": step_bytes // launches,
+                        "launch_us": round(per_launch_s * 1e6, 3)},
            "per_gemm": per}
     if not args.no_prefill:
         log("exact prefill GEMMs ...")

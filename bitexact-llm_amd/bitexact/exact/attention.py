@@ -1,4 +1,4 @@
-"""Exact-mode attention over the contiguous integer cache, fused (src/bitexact/exact/model.py:304-311):
+"""Exact-mode attention over the contiguous integer cache, fused (src/bitexact/exact/model.py:113-119):
 num, den = prefill(qg, shg, K, V, qpos, lut, l2e) computes bmm(qg, K^T) -> segs.softmax -> bmm(p, V) in one
 HIP kernel without materializing the score matrix.
 

@@ -1,7 +1,7 @@
-"""Exact-mode linear layer over a constants dict (src/bitexact/exact/model.py:223-262), gemm = "hip".
+"""Exact-mode linear layer over a constants dict (src/bitexact/exact/model.py:31-70), gemm = "hip".
 
 Lin(c, name, device) reads c[f"{name}.limbs" | ".g" | ".d" | ".rr" | ".rc" | ".rv"] (the reference's key
-layout) and builds the ELL residual once (src/bitexact/exact/model.py:231-240). __call__(q) keeps the
+layout) and builds the ELL residual once (src/bitexact/exact/model.py:39-48). __call__(q) keeps the
 reference's (C, rs, d, g) contract for segs.lin_y; y(q, sh, checked) is the fused HIP linear.
 """
 

@@ -1,4 +1,4 @@
-"""int8-mode GEMM (src/bitexact/int8/gemm_skinny.py:188-205) on gfx950 MFMA.
+"""int8-mode GEMM (src/bitexact/int8/gemm_skinny.py:80-97) on gfx950 MFMA.
 
 int_mm(a, w) -> int32 [R, N] = a int8 [R, K] @ w int8 [N, K]^T, the reference's contract (exact while
 K * 127 * 128 < 2^31). int_mm_join(a, w, M, nl) also joins the nl limb row blocks of a in int64

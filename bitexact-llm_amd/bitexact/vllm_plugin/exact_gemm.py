@@ -1,4 +1,4 @@
-"""Exact-mode linear of the plugin (src/bitexact/vllm_plugin/exact_gemm.py:453-541) on one HIP launch.
+"""Exact-mode linear of the plugin (src/bitexact/vllm_plugin/exact_gemm.py:228-316) on one HIP launch.
 
 FusedLin(lin)(q, sh, flag, checked=True) -> y int64 [M, N] at FR: the 9 limb products (MFMA), the ELL sparse
 residual, wmm.epilogue's rounding and, when checked, flag[0] = 1 wherever the reference's checked epilogue

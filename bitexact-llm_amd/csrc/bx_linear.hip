@@ -52,6 +52,10 @@ struct LinArgs {
   int tiles, parts_lg, mp;   // gemv: column tiles, log2 of the row parts per tile, output rows per part
 };
 
+// Residual column index kept inside the row of q (valid ELL data is always in [0, K); a corrupt index reads a
+// wrong value instead of memory outside q).
+__device__ __forceinline__ int kcol(const LinArgs& p, int32_t c) { return (int)min((uint32_t)c, (uint32_t)(p.K - 1)); }
+
 // ---- epilogue shared by both kernels: one output element from its exact int64 dense value ----
 template <int MODE>
 __device__ __forceinline__ void finalize(const LinArgs& p, int m, int n, int64_t v, bool& bad) {
@@ -64,11 +68,11 @@ __device__ __forceinline__ void finalize(const LinArgs& p, int m, int n, int64_t
     // segs.lin_y (src/bitexact/exact/segs.py:25-32): B from the ELL residual, then wmm.epilogue.
     int64_t B = 0;
     if (p.R > 0) {
-      const int c = p.cnt[n];
+      const int c = min(max(p.cnt[n], 0), p.R);
       const int32_t* qr = p.q + (int64_t)m * p.ldq;
       const int32_t* ec = p.ecol + (int64_t)n * p.R;
       const int64_t* ev = p.eval + (int64_t)n * p.R;
-      for (int j = 0; j < c; ++j) B = add_wrap(B, mul_wrap((int64_t)qr[ec[j]], ev[j]));
+      for (int j = 0; j < c; ++j) B = add_wrap(B, mul_wrap((int64_t)qr[kcol(p, ec[j])], ev[j]));
     }
     const int64_t dn = p.d[n];
     const int64_t pe = p.sh[m] + p.g[n] - dn + p.FR;
@@ -95,7 +99,7 @@ __device__ __forceinline__ ColCtx col_ctx(const LinArgs& p, int n) {
   const int nn = min(n, p.N - 1);
   c.d = p.d[nn];
   c.gdr = p.g[nn] - c.d + p.FR;
-  c.cnt = p.R > 0 ? p.cnt[nn] : 0;
+  c.cnt = p.R > 0 ? min(max(p.cnt[nn], 0), p.R) : 0;   // entries stay inside the row's R slots
   c.ecp = p.ecol + (int64_t)nn * p.R;
   c.evp = p.eval + (int64_t)nn * p.R;
 #pragma unroll
@@ -113,8 +117,8 @@ __device__ __forceinline__ int64_t residual_col(const LinArgs& p, const ColCtx& 
   if (cc.cnt > 0) {
     const int32_t* qr = p.q + (int64_t)m * p.ldq;
 #pragma unroll
-    for (int j = 0; j < kRes; ++j) B = add_wrap(B, mul_wrap((int64_t)qr[cc.ec[j]], cc.ev[j]));   // padded: ev = 0
-    for (int j = kRes; j < cc.cnt; ++j) B = add_wrap(B, mul_wrap((int64_t)qr[cc.ecp[j]], cc.evp[j]));
+    for (int j = 0; j < kRes; ++j) B = add_wrap(B, mul_wrap((int64_t)qr[kcol(p, cc.ec[j])], cc.ev[j]));   // padded: ev = 0
+    for (int j = kRes; j < cc.cnt; ++j) B = add_wrap(B, mul_wrap((int64_t)qr[kcol(p, cc.ecp[j])], cc.evp[j]));
   }
   return B;
 }

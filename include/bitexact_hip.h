@@ -37,8 +37,8 @@ int bx_version(void);
 
 /* ---- exact mode linear ---- */
 
-/* Replaces FusedLin.__call__ (src/bitexact/vllm_plugin/exact_gemm.py:509-541) and
- * segs.lin_y(*Lin(q), sh, checked) (src/bitexact/exact/segs.py:25-32, src/bitexact/exact/model.py:253-262):
+/* Replaces FusedLin.__call__ (src/bitexact/vllm_plugin/exact_gemm.py:284-316) and
+ * segs.lin_y(*Lin(q), sh, checked) (src/bitexact/exact/segs.py:25-32, src/bitexact/exact/model.py:61-70):
  * y int64 [M, N] = round((q W^T 2^d + B) 2^(sh + g - d + FR)) with B = sum_j q[m, col[n,j]] val[n,j];
  * when `checked`, sets flag[0] = 1 where wmm.epilogue(checked=True) would (src/bitexact/exact/wmm.py:132-150).
  * Requires K % 16 == 0, ldq % 4 == 0, ld_row % 16 == 0, 16-byte aligned q and limbs. */
@@ -68,12 +68,12 @@ int bx_decompose_residual(const uint16_t* w, int32_t N, int32_t K, const int64_t
 
 /* ---- int8 mode GEMM ---- */
 
-/* Replaces gemm_skinny.int_mm (src/bitexact/int8/gemm_skinny.py:188-205) and torch._int_mm:
+/* Replaces gemm_skinny.int_mm (src/bitexact/int8/gemm_skinny.py:80-97) and torch._int_mm:
  * c int32 [R, N] = a int8 [R, K] @ w int8 [N, K]^T (exact while K * 127 * 128 < 2^31).
  * Requires K % 16 == 0 and 16-byte aligned a, w. */
 int bx_int8_gemm(const int8_t* a, const int8_t* w, int32_t* c, int32_t R, int32_t N, int32_t K, void* ws,
                  int64_t ws_bytes, bx_stream_t stream);
-/* int_mm followed by intops.join_limbs (src/bitexact/intops.py:82-87, src/bitexact/int8/segs.py:338):
+/* int_mm followed by intops.join_limbs (src/bitexact/intops.py:82-87, src/bitexact/int8/segs.py:126):
  * y int64 [M, N] = sum_{i < nl} (a[i M:(i+1) M] @ w^T) 2^(8 i); a holds nl limb row blocks of M rows. */
 int bx_int8_gemm_join(const int8_t* a, const int8_t* w, int64_t* y, int32_t M, int32_t N, int32_t K, int32_t nl,
                       void* ws, int64_t ws_bytes, bx_stream_t stream);
@@ -95,7 +95,7 @@ int bx_exact_attn_paged(const int32_t* q, const int64_t* sh, const int64_t* qpos
                         bx_stream_t stream);
 int64_t bx_attn_paged_workspace(int32_t R, int32_t HKV, int32_t M, int32_t HD);
 
-/* Fused form of exact/model.py's attention (src/bitexact/exact/model.py:304-311: bmm(qg, K^T), segs.softmax,
+/* Fused form of exact/model.py's attention (src/bitexact/exact/model.py:113-119: bmm(qg, K^T), segs.softmax,
  * bmm(p, V)): qg int32 [Z, gT, HD] (strides sq_z, sq_row), shg int64 [Z, gT] (ssh_z = gT), qpos int64 [Z, gT]
  * (strides), K / V int32 [Z, S, HD] (strides; the integer Cache layout), outputs num int64 [Z, gT, HD],
  * den int64 [Z, gT]. The score matrix is never materialized. */
