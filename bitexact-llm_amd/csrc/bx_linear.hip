@@ -88,6 +88,7 @@ constexpr int kRes = 4;
 struct ColCtx {
   int64_t d, gdr;        // d[n] and g[n] - d[n] + FR
   int cnt;
+  int wmax;              // largest count over the wave's columns (wave-uniform loop bound)
   int32_t ec[kRes];
   int64_t ev[kRes];
   const int32_t* ecp;
@@ -100,6 +101,7 @@ __device__ __forceinline__ ColCtx col_ctx(const LinArgs& p, int n) {
   c.d = p.d[nn];
   c.gdr = p.g[nn] - c.d + p.FR;
   c.cnt = p.R > 0 ? min(max(p.cnt[nn], 0), p.R) : 0;   // entries stay inside the row's R slots
+  c.wmax = (int)wave_max64(c.cnt);
   c.ecp = p.ecol + (int64_t)nn * p.R;
   c.evp = p.eval + (int64_t)nn * p.R;
 #pragma unroll
@@ -114,10 +116,11 @@ __device__ __forceinline__ ColCtx col_ctx(const LinArgs& p, int n) {
 // The sparse residual B of row m in column cc (segs.lin_y's ELL gather, src/bitexact/exact/segs.py:31).
 __device__ __forceinline__ int64_t residual_col(const LinArgs& p, const ColCtx& cc, int m) {
   int64_t B = 0;
-  if (cc.cnt > 0) {
+  if (cc.wmax > 0) {   // wave-uniform
     const int32_t* qr = p.q + (int64_t)m * p.ldq;
 #pragma unroll
-    for (int j = 0; j < kRes; ++j) B = add_wrap(B, mul_wrap((int64_t)qr[kcol(p, cc.ec[j])], cc.ev[j]));   // padded: ev = 0
+    for (int j = 0; j < kRes; ++j)   // padded entries have ev = 0; entries past every lane's count are skipped
+      if (j < cc.wmax) B = add_wrap(B, mul_wrap((int64_t)qr[kcol(p, cc.ec[j])], cc.ev[j]));
     for (int j = kRes; j < cc.cnt; ++j) B = add_wrap(B, mul_wrap((int64_t)qr[kcol(p, cc.ecp[j])], cc.evp[j]));
   }
   return B;
