@@ -3,6 +3,7 @@
 norm_quant(x, gm, ge, err)      segs.norm_quant: RMSNorm + quantization at -FN -> (q int32, sh, err)
 softmax(raw, qpos, shg, lut, l2e) segs.softmax: masked weights at FP -> (p int32, den)
 attn_out(num, den, T, hkv)      Segs.attn_out: div_round + regroup + quantization at -FR -> (q int32, sh)
+qkv_y(y, pos, cos, sin, B, T, dm, err)  Segs.qkv_y: RoPE + q quantization + regroup -> (qg, shg, k, v, err)
 """
 
 import torch
@@ -12,6 +13,8 @@ from bitexact.exact.consts import FR
 
 FN = 40
 FK, FV, FP = 17, 19, 22
+FT = 30                         # cos / sin fractional bits (src/bitexact/exact/consts.py:24)
+FZ = 26
 L2E28 = 387270501
 L2E28_HD = {64: L2E28, 128: 273841598}
 
@@ -63,3 +66,28 @@ def attn_out(num, den, T, hkv):
     _hip.call("bx_attn_out", _hip.ptr(num), num.stride(0), num.stride(1), _hip.ptr(den2), gT, rows, T, hkv, g, HD, FR,
               FV, _hip.ptr(q), q.stride(0), _hip.ptr(sh), _hip.stream_of(num))
     return q, sh
+
+
+def qkv_y(y, pos, cos, sin, B, T, dm, err=None):
+    """Segs.qkv_y (src/bitexact/exact/segs.py:170-173): y int64 [B T, (H + 2 HKV) HD] at FR, pos int64 [B, T],
+    cos / sin int64 [n_pos, HD / 2] at FT, dm = (H, HKV, HD) -> qg int32 [B HKV, g T, HD], shg int64
+    [B HKV, g T, 1], k / v int64 [B, T, HKV, HD], err (bool tensor, or'ed into `err`)."""
+    _hip.require_cuda(y, pos, cos, sin)
+    H, HKV, HD = dm
+    assert y.dtype == torch.int64 and y.stride(-1) == 1 and y.shape[0] == B * T
+    assert y.shape[1] >= (H + 2 * HKV) * HD and H % HKV == 0
+    g = H // HKV
+    dev = y.device
+    pos = pos.long()
+    cos, sin = cos.contiguous().long(), sin.contiguous().long()
+    assert cos.shape == sin.shape and cos.shape[1] == HD // 2
+    qg = torch.empty(B * HKV, g * T, HD, dtype=torch.int32, device=dev)
+    shg = torch.empty(B * HKV, g * T, 1, dtype=torch.long, device=dev)
+    k = torch.empty(B, T, HKV, HD, dtype=torch.long, device=dev)
+    v = torch.empty(B, T, HKV, HD, dtype=torch.long, device=dev)
+    flag = torch.zeros(1, dtype=torch.int32, device=dev)
+    _hip.call("bx_rope_qgroup", _hip.ptr(y), y.stride(0), _hip.ptr(pos), pos.stride(0), pos.stride(1),
+              _hip.ptr(cos), _hip.ptr(sin), cos.shape[0], B, T, H, HKV, HD, FR, FT, FK, FV, FZ, _hip.ptr(qg),
+              _hip.ptr(shg), _hip.ptr(k), _hip.ptr(v), _hip.ptr(flag), _hip.stream_of(y))
+    e = flag[0].bool()
+    return qg, shg, k, v, e if err is None else (err | e)

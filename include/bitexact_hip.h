@@ -137,6 +137,30 @@ int bx_attn_out(const int64_t* num, int64_t sn_group, int64_t sn_query, const in
                 int32_t rows, int32_t T, int32_t HKV, int32_t g, int32_t HD, int32_t FR, int32_t FV, int32_t* q,
                 int64_t ldq, int64_t* sh, bx_stream_t stream);
 
+/* ---- element-wise segments ---- */
+
+/* Replaces Segs.qkv_y = segs.rope_y + segs.q_group (src/bitexact/exact/segs.py:78-99, 170-173): y int64 [B T, ldy]
+ * (q heads, k heads, v heads at FR), positions pos [B, T] (element strides spb, spt), integer cos / sin tables
+ * [npos, HD / 2] at FT -> qg int32 [B HKV, g T, HD] (q quantized per (token, head) at -(FR + FT), grouped by KV
+ * head), shg int64 [B HKV, g T], k int64 [B, T, HKV, HD] at FK, v at FV. err[0] = 1 where q_group's check fails
+ * (|y| >= 2^31, |k| or |v| > 8355711, q exponent > FK + 3 - FZ) or a position lies outside the tables. */
+int bx_rope_qgroup(const int64_t* y, int64_t ldy, const int64_t* pos, int64_t spb, int64_t spt, const int64_t* cos,
+                   const int64_t* sin, int32_t npos, int32_t B, int32_t T, int32_t H, int32_t HKV, int32_t HD,
+                   int32_t FR, int32_t FT, int32_t FK, int32_t FV, int32_t FZ, int32_t* qg, int64_t* shg, int64_t* k,
+                   int64_t* v, int32_t* err, bx_stream_t stream);
+
+/* Replaces int8 ops.quant_rows + intops.stack_limbs (src/bitexact/int8/ops.py:24-35, src/bitexact/intops.py:73-79)
+ * and, with mant / e given, segs.pre_plain's row scale norm24(as_, sh - FR) (src/bitexact/int8/segs.py:56-59):
+ * z int64 [M, ldz] -> a int8 [nl M, K] (limb i of row m at row i M + m, no padding rows), as_, sh [M]. */
+int bx_int8_quant_rows(const int64_t* z, int64_t ldz, int32_t M, int32_t K, int32_t nl, int32_t FR, int8_t* a,
+                       int64_t* as_, int64_t* sh, int64_t* mant, int64_t* e, bx_stream_t stream);
+
+/* Replaces int8 segs.post (src/bitexact/int8/segs.py:62-67) on the joined products acc int64 [M, ldacc]:
+ * y = rsh(rsh(acc m_c, fmsh) mant_r, 24 - FR - e_r); flag[0] = 1 when some |rsh(acc m_c, fmsh)| >= 2^38. */
+int bx_int8_post(const int64_t* acc, int64_t ldacc, const int64_t* m, int32_t fmsh, const int64_t* mant,
+                 const int64_t* e, int32_t FR, int64_t* y, int64_t ldy, int32_t M, int32_t N, int32_t* flag,
+                 bx_stream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -529,3 +529,60 @@ def llama3_inv_freq(hd=64, theta=500000.0, factor=32.0, low=1.0, high=4.0, orig=
 def rope_tables(n_pos, bits, inv_freq):
     ang = np.arange(n_pos, dtype=np.float64)[:, None] * inv_freq[None, :]
     return np.round(np.cos(ang) * 2.0 ** bits).astype(I64), np.round(np.sin(ang) * 2.0 ** bits).astype(I64)
+
+# ---- RoPE + q quantization + regroup (src/bitexact/exact/segs.py:66-99) ----
+FT_ROPE = 30                                    # cos / sin fractional bits (src/bitexact/exact/consts.py:24)
+
+
+def _rope_full(x, c, s):
+    """(x1 c - x2 s, x2 c + x1 s) over the two halves of the last axis (src/bitexact/exact/segs.py:66-69)."""
+    hd = x.shape[-1]
+    x1, x2 = x[..., :hd // 2], x[..., hd // 2:]
+    return np.concatenate([x1 * c - x2 * s, x2 * c + x1 * s], -1)
+
+
+def rope_y(y, pos, cos, sin, B, T, dm):
+    """segs.rope_y (src/bitexact/exact/segs.py:78-86): y int64 [B T, (H + 2 HKV) HD] at FR, positions [B, T],
+    integer tables [n_pos, HD / 2] -> (Pq [B, T, H, HD] at FR + FT, k [B, T, HKV, HD] at FK, v at FV)."""
+    h, hkv, hd = dm
+    y = _a(y).reshape(B, T, -1)
+    pos = _a(pos)
+    c, s = _a(cos)[pos][:, :, None], _a(sin)[pos][:, :, None]
+    Pq = _rope_full(y[..., :h * hd].reshape(B, T, h, hd), c, s)
+    k = rshc(_rope_full(y[..., h * hd:(h + hkv) * hd].reshape(B, T, hkv, hd), c, s), FR + FT_ROPE - FK)
+    v = rshc(y[..., (h + hkv) * hd:].reshape(B, T, hkv, hd), FR - FV)
+    return Pq, k, v
+
+
+def q_group(Pq, k, v, y):
+    """segs.q_group (src/bitexact/exact/segs.py:89-99): per (token, head) quant of q at -(FR + FT), grouped by
+    KV head -> (qg int32 [B HKV, g T, HD], shg [B HKV, g T, 1], err)."""
+    B, T, h, hd = Pq.shape
+    hkv = k.shape[2]
+    qi, shq = quant(Pq, -(FR + FT_ROPE))
+    g = h // hkv
+    qg = qi.reshape(B, T, hkv, g, hd).transpose(0, 2, 3, 1, 4).reshape(B * hkv, g * T, hd).astype(np.int32)
+    shg = shq.reshape(B, T, hkv, g).transpose(0, 2, 3, 1).reshape(B * hkv, g * T, 1)
+    err = bool((np.abs(_a(y)) >= 1 << 31).any() or (np.abs(k) > LIM3).any() or (np.abs(v) > LIM3).any()
+               or (shq.max() > FK + 3 - FZ))
+    return qg, shg, err
+
+
+# ---- int8-mode row scales and the linear post-segment (src/bitexact/int8/ops.py:73-77,
+# src/bitexact/int8/segs.py:62-67) ----
+FR8 = 16                                        # int8 engine residual stream (src/bitexact/int8/consts.py:26)
+
+
+def norm24(mant, e):
+    """(mant, e) -> the same value with mant in [2^23, 2^24] (src/bitexact/int8/ops.py:73-76)."""
+    b = bitlen(_a(mant)) - 24
+    return rsh(_a(mant), b), _a(e) + b
+
+
+def int8_post(acc, m, fmsh, mant, e, FR_=FR8):
+    """segs.post (src/bitexact/int8/segs.py:62-67): t = rsh(acc m_c, fmsh); y = rsh(t mant_r, 24 - FR - e_r).
+    Returns (y, flag) with flag = max |t| >= 2^38."""
+    t = rsh(_a(acc) * _a(m)[None, :], int(fmsh))
+    flag = bool(np.abs(t).max() >= 1 << 38) if t.size else False
+    return rsh(t * _a(mant)[:, None], (24 - FR_ - _a(e))[:, None]), flag
+

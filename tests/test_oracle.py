@@ -283,3 +283,55 @@ def test_rope_inv_freq_llama3():
     assert np.isclose(inv[-1], base[-1] / 32)      # low frequency: divided by the factor
     c, s = R.rope_tables(16, R.FT, inv)
     assert (c[0] == 1 << 30).all() and (s[0] == 0).all()
+
+
+def test_rope_position_zero_is_a_scale():
+    """At position 0 the tables are cos = 2^FT, sin = 0: rope is a plain scale, so q = y 2^FT and k, v are
+    single roundings of y (closed forms independent of the rope formula)."""
+    cos, sin = R.rope_tables(4, R.FT_ROPE, R.llama3_inv_freq(64))
+    assert cos[0].tolist() == [1 << R.FT_ROPE] * 32 and not sin[0].any()
+    rng = np.random.default_rng(3)
+    B, T, H, HKV, HD = 1, 1, 4, 2, 64
+    y = rng.integers(-(1 << 30), 1 << 30, (1, (H + 2 * HKV) * HD))
+    Pq, k, v = R.rope_y(y, np.zeros((1, 1), np.int64), cos, sin, B, T, (H, HKV, HD))
+    yy = [int(x) for x in y[0]]
+    assert [int(x) for x in Pq.reshape(-1)] == [x << R.FT_ROPE for x in yy[:H * HD]]
+    rnd = lambda x, s: math.floor(Fraction(x, 1 << s) + Fraction(1, 2))
+    assert [int(x) for x in k.reshape(-1)] == [rnd(x << R.FT_ROPE, R.FR + R.FT_ROPE - R.FK) for x in yy[H * HD:(H + HKV) * HD]]
+    assert [int(x) for x in v.reshape(-1)] == [rnd(x, R.FR - R.FV) for x in yy[(H + HKV) * HD:]]
+
+
+def test_rope_is_a_rotation():
+    """The integer rope of (x1, x2) by (c, s) preserves x1^2 + x2^2 up to c^2 + s^2 (a rotation scaled by the
+    table's modulus), for every position of the tables."""
+    cos, sin = R.rope_tables(64, R.FT_ROPE, R.llama3_inv_freq(64))
+    rng = np.random.default_rng(4)
+    y = rng.integers(-(1 << 20), 1 << 20, (64, 3 * 64))
+    pos = np.arange(64).reshape(1, 64)
+    Pq, _, _ = R.rope_y(y, pos, cos, sin, 1, 64, (1, 1, 64))
+    for t in range(64):
+        x = [int(a) for a in y[t, :64]]
+        p = [int(a) for a in Pq[0, t, 0]]
+        for d in range(32):
+            c, s = int(cos[t, d]), int(sin[t, d])
+            assert p[d] ** 2 + p[d + 32] ** 2 == (x[d] ** 2 + x[d + 32] ** 2) * (c * c + s * s)
+
+
+def test_norm24_and_int8_post_closed_forms():
+    rng = np.random.default_rng(5)
+    rnd = lambda x, s: math.floor(Fraction(x, 1 << s) + Fraction(1, 2)) if s > 0 else x << -s
+    mant0 = rng.integers(1, 1 << 40, 200)
+    e0 = rng.integers(-50, 10, 200)
+    mant, e = R.norm24(mant0, e0)
+    for a, b, mm, ee in zip(mant0.tolist(), e0.tolist(), mant.tolist(), e.tolist()):
+        assert (1 << 23) <= mm <= (1 << 24)
+        assert abs(Fraction(mm) * Fraction(2) ** ee - Fraction(a) * Fraction(2) ** b) <= Fraction(2) ** (ee - 1)
+    acc = rng.integers(-(1 << 38), 1 << 38, (3, 50))
+    m = rng.integers(-(1 << 20), 1 << 20, 50)
+    mant = rng.integers(1 << 23, (1 << 24) + 1, 3)
+    e = rng.integers(-40, -10, 3)
+    y, flag = R.int8_post(acc, m, 40, mant, e)
+    for i in range(3):
+        for j in range(50):
+            t = rnd(int(acc[i, j]) * int(m[j]), 40)
+            assert int(y[i, j]) == rnd(t * int(mant[i]), 24 - R.FR8 - int(e[i]))
