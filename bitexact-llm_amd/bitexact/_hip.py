@@ -42,6 +42,8 @@ SIGNATURES = {
     "bx_rmsnorm_quant": (ctypes.c_int, [P, I64, P, P, P, I64, P, I32, I32, I32, I32, P, P]),
     "bx_softmax_w": (ctypes.c_int, [P, I64, P, P, I32, I32, I32, P, I64, I32, P, I64, P, P]),
     "bx_attn_out": (ctypes.c_int, [P, I64, I64, P, I64, I32, I32, I32, I32, I32, I32, I32, P, I64, P, P]),
+    "bx_int8_attn_paged": (ctypes.c_int, [P, P, I64, P, I64, I64, I64, I32, P, I64, I32, P, I32, P, P, I32, I32, I32,
+                                          I32, I32, P, I64, P]),
     "bx_rope_qgroup": (ctypes.c_int, [P, I64, P, I64, I64, P, P, I32, I32, I32, I32, I32, I32, I32, I32, I32, I32,
                                       I32, P, P, P, P, P, P]),
     "bx_int8_quant_rows": (ctypes.c_int, [P, I64, I32, I32, I32, I32, P, P, P, P, P, P]),

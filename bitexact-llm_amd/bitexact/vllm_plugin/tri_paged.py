@@ -2,7 +2,8 @@
 
 Layout: int8 [nb, HKV, bs, 8 HD]; row (block, head, slot) holds K limbs 0, 1, 2 at bytes [0, 3 HD) and V limbs
 at [3 HD, 6 HD) (the rest unused). store() writes tokens at their slots; to_limbs() converts an int32
-[nb, HKV, bs, 2 HD] (K | V) cache into that layout (tests / reference conversions).
+[nb, HKV, bs, 2 HD] (K | V) cache into that layout (tests / reference conversions). attend() is the int8-mode
+paged attention over that cache (one HIP kernel, two launches when the keys are split).
 """
 
 import torch
@@ -34,3 +35,37 @@ def to_limbs(c):
     slot = torch.arange(nb * bs, device=c.device)
     store(out, slot, flat[..., :hd], flat[..., hd:])
     return out
+
+
+FE, FP = 30, 20                 # exp table values, int8 attention weights (src/bitexact/int8/segs.py:22)
+SM_TARGET = 512                 # blocks to aim for: 2 per MI355X compute unit
+
+
+def weight_table(lut):
+    """rsh(exp_lut, FE - FP) as int32 (src/bitexact/vllm_plugin/tri_paged.py:351-356); built once at load."""
+    t = (lut + (1 << (FE - FP - 1))) >> (FE - FP)
+    return t.to(torch.int32).contiguous()
+
+
+def attend(q, qpos, cache, bt, ptab, nsplit=None, bm=None, bn=None, warps=4):
+    """int8-mode paged attention (src/bitexact/vllm_plugin/tri_paged.py:363-401): q int64 [R, HKV, M, HD], qpos int64
+    [R, M], cache int8 [nb, HKV, bs, 8 HD], bt int32 [R, *], ptab = weight_table(exp table) -> (num int64
+    [R, HKV, M, HD], den int64 [R, HKV, M, 1]). bm / bn / warps are accepted for signature parity."""
+    _hip.require_cuda(q, qpos, cache, bt, ptab)
+    R, HKV, M, HD = q.shape
+    assert cache.shape[1] == HKV and cache.shape[3] >= 6 * HD and cache.stride(3) == 1
+    assert bt.shape[1] * cache.shape[2] < 43690
+    assert cache.dtype == torch.int8 and bt.dtype == torch.int32 and ptab.dtype == torch.int32
+    q, qpos, ptab = q.contiguous().long(), qpos.contiguous().long(), ptab.contiguous()
+    if nsplit is None:
+        tiles = max(1, R * HKV * ((M + 3) // 4))
+        keys = max(1, bt.shape[1] * cache.shape[2])
+        nsplit = max(1, min(64, SM_TARGET // tiles, (keys + 127) // 128))
+    num = torch.empty(R, HKV, M, HD, dtype=torch.long, device=q.device)
+    den = torch.empty(R, HKV, M, 1, dtype=torch.long, device=q.device)
+    ws, wsb = _hip.workspace(q.device, _hip.lib().bx_attn_paged_workspace(R, HKV, M, HD) if nsplit > 1 else 0)
+    _hip.call("bx_int8_attn_paged", _hip.ptr(q), _hip.ptr(qpos), qpos.stride(0), _hip.ptr(cache), cache.stride(0),
+              cache.stride(1), cache.stride(2), cache.shape[2], _hip.ptr(bt), bt.stride(0), bt.shape[1],
+              _hip.ptr(ptab), ptab.numel(), _hip.ptr(num), _hip.ptr(den), R, HKV, M, HD, int(nsplit), _hip.ptr(ws),
+              wsb, _hip.stream_of(q))
+    return num, den

@@ -36,6 +36,18 @@ __device__ __forceinline__ int64_t attn_weight(int64_t z, int64_t zshift, const 
   return rshc(v, kExp2One - kFP + n);
 }
 
+// int8-mode weight of a visible key (int8.segs.softmax, src/bitexact/int8/segs.py:90-99; tri_paged._zscale,
+// src/bitexact/vllm_plugin/tri_paged.py:93-99): d = raw - mx <= 0 at 2 FQ bits, z = rsh(d, zsh) (head_dim 64)
+// or rsh(max(d, -2^38) zmul, zsh) (head_dim 128, zmul = round(2^24 / sqrt 2)); the weight is the table entry
+// rsh(e^z 2^FE, FE - FP) of z at step 2^-FA over [EXP_MIN, 0], 0 below it.
+constexpr int64_t kI8ZClamp = -(1LL << 38);
+constexpr int64_t kI8ZLo = -32LL * 4096;         // EXP_MIN << FA: table index 0
+__device__ __forceinline__ int64_t int8_weight(int64_t d, int zsh, int64_t zmul, const int32_t* ptab) {
+  const int64_t z = zmul == 0 ? rsh64(d, zsh) : rsh64(mul_wrap(imax(d, kI8ZClamp), zmul), zsh);
+  const int64_t idx = imax(z, kI8ZLo - 1) - kI8ZLo;
+  return idx >= 0 ? (int64_t)ptab[idx] : 0;
+}
+
 // int32 value -> the value of its first three signed base-256 digits (what a 3-limb split keeps).
 __device__ __forceinline__ int32_t keep3(int32_t x) {
   const int32_t a0 = limb_lo(x);
@@ -67,9 +79,14 @@ struct AttnArgs {
   const int32_t* V;
   int64_t sk_z, sk_s, sv_z, sv_s;
   int S;                          // contiguous: keys available
-  // table, scale
+  // table, scale (exact mode)
   const int64_t* lut;
   int64_t l2e;
+  // int8 mode: int64 queries and the weight table (wrule 1)
+  const int64_t* q64;
+  const int32_t* ptab;
+  int wrule, zsh;
+  int64_t zmul;
   // outputs
   int64_t* num;
   int64_t* den;
@@ -105,7 +122,7 @@ __device__ __forceinline__ void load_kv_tile(const AttnArgs& p, AttnSmem<QT, HD>
     int32_t kv[16], vv[16];
     if (kk < nkeys) {
       if (PAGED) {
-        const int64_t brow = p.rmap[group / p.hkv];
+        const int64_t brow = p.rmap ? p.rmap[group / p.hkv] : group / p.hkv;
         const int blk = p.bt[brow * p.sbt + s / p.bs];
         const int8_t* row = p.cache + (int64_t)blk * p.sc_nb + (int64_t)h * p.sc_h + (int64_t)(s % p.bs) * p.sc_bs;
         const v4i k0 = *(const v4i*)(row + c * 16), k1 = *(const v4i*)(row + HD + c * 16),
@@ -167,13 +184,14 @@ template <int QT, int HD>
 __device__ __forceinline__ int64_t stage_queries(const AttnArgs& p, AttnSmem<QT, HD>& sm, int group, int q0, int nvalid) {
   for (int u = threadIdx.x; u < QT * HD; u += 256) {
     const int i = u / HD, d = u % HD;
-    sm.Qs[i][d] = i < nvalid ? keep3(p.q[group * p.sq_tile + (int64_t)(q0 + i) * p.sq_row + d]) : 0;
+    const int64_t qi = group * p.sq_tile + (int64_t)(q0 + i) * p.sq_row + d;
+    sm.Qs[i][d] = i < nvalid ? keep3(p.q64 ? (int32_t)p.q64[qi] : p.q[qi]) : 0;
   }
   if (threadIdx.x < QT) {
     const int i = threadIdx.x;
     const bool ok = i < nvalid;
     sm.qpos[i] = ok ? p.qpos[(group / p.qpos_div) * p.qpos_tile + (int64_t)(q0 + i) * p.qpos_row] : -1;
-    sm.shift[i] = ok ? (int64_t)(kFK + 3 - kFZ) - p.sh[group * p.sh_tile + q0 + i] : 0;
+    sm.shift[i] = ok && p.sh ? (int64_t)(kFK + 3 - kFZ) - p.sh[group * p.sh_tile + q0 + i] : 0;
     sm.mx[i] = kNeg;
   }
   __syncthreads();
@@ -232,7 +250,10 @@ __device__ void sweep_acc(const AttnArgs& p, AttnSmem<QT, HD>& sm, int group, in
     for (int j = 0; j < QT / 4; ++j) {
       const int i = w + 4 * j;
       const bool vis = l < nk && k0 + l <= sm.qpos[i];
-      const int64_t pw = vis ? attn_weight(sm.mx[i] - raw[j], sm.shift[i], p.lut, p.l2e) : 0;
+      int64_t pw = 0;
+      if (vis)
+        pw = p.wrule == 0 ? attn_weight(sm.mx[i] - raw[j], sm.shift[i], p.lut, p.l2e)
+                          : int8_weight(raw[j] - sm.mx[i], p.zsh, p.zmul, p.ptab);
       den[j] += pw;
       sm.Ps[i][l] = (int32_t)pw;
     }
@@ -393,7 +414,7 @@ static void bind_attn_ws(AttnArgs& p, void* ws, int64_t gq, int HD) {
 }
 
 extern "C" int64_t bx_attn_paged_workspace(int32_t R, int32_t HKV, int32_t M, int32_t HD) {
-  return attn_ws_bytes((int64_t)R * HKV * M, (int64_t)R * HKV, HD);
+  return attn_ws_bytes((int64_t)R * HKV * M, (int64_t)R * HKV * ((M + 3) / 4), HD);   // counters per query tile
 }
 
 extern "C" int bx_exact_attn_paged(const int32_t* q, const int64_t* sh, const int64_t* qpos, int64_t sqpos_r,
@@ -420,6 +441,41 @@ extern "C" int bx_exact_attn_paged(const int32_t* q, const int64_t* sh, const in
   p.nsplit = nsplit;
   if (nsplit > 1) {
     const int64_t need = attn_ws_bytes((int64_t)R * HKV * M, (int64_t)R * HKV, HD);
+    BX_REQUIRE(ws != nullptr && ws_bytes >= need, "workspace too small (%lld < %lld)", (long long)ws_bytes,
+               (long long)need);
+    bind_attn_ws(p, ws, (int64_t)R * HKV * M, HD);
+  }
+  return HD == 64 ? launch_attn<4, 64, true>(p, R * HKV, (hipStream_t)stream)
+                  : launch_attn<4, 128, true>(p, R * HKV, (hipStream_t)stream);
+}
+
+extern "C" int bx_int8_attn_paged(const int64_t* q, const int64_t* qpos, int64_t sqpos_r, const int8_t* cache,
+                                  int64_t sc_nb, int64_t sc_h, int64_t sc_bs, int32_t bs, const int32_t* bt, int64_t sbt,
+                                  int32_t nblk, const int32_t* ptab, int32_t ptab_len, int64_t* num, int64_t* den,
+                                  int32_t R, int32_t HKV, int32_t M, int32_t HD, int32_t nsplit, void* ws,
+                                  int64_t ws_bytes, bx_stream_t stream) {
+  BX_REQUIRE(R >= 0 && HKV > 0 && M >= 1, "need M >= 1 queries per (row, KV head)");
+  BX_REQUIRE(HD == 64 || HD == 128, "head_dim must be 64 or 128");
+  BX_REQUIRE((int64_t)nblk * bs < 43690, "keys per row must stay below 43690");
+  BX_REQUIRE(nsplit >= 1 && nsplit <= 64, "nsplit in [1, 64]");
+  BX_REQUIRE(ptab_len >= (int32_t)(-kI8ZLo) + 1, "weight table needs 2^17 + 1 entries");
+  BX_REQUIRE(sc_bs >= 6 * HD && sc_nb % 16 == 0 && sc_h % 16 == 0 && sc_bs % 16 == 0 && ((uintptr_t)cache & 15) == 0,
+             "cache rows must hold the 6 HD limb bytes, 16-byte aligned");
+  BX_REQUIRE(q && qpos && bt && ptab && num && den, "null pointer");
+  if (R == 0) return BX_OK;
+  AttnArgs p = {};
+  p.q64 = q; p.sq_tile = (int64_t)M * HD; p.sq_row = HD;
+  p.qpos = qpos; p.qpos_tile = sqpos_r; p.qpos_row = 1; p.qpos_div = HKV; p.nq = M;
+  p.cache = cache; p.sc_nb = sc_nb; p.sc_h = sc_h; p.sc_bs = sc_bs; p.bt = bt; p.sbt = sbt; p.rmap = nullptr;
+  p.bs = bs; p.hkv = HKV;
+  // int8.segs.score_rule (src/bitexact/int8/segs.py:29-37): FQ = 14, FA = 12; head_dim 128 scales by 2^-1/2
+  p.wrule = 1; p.ptab = ptab;
+  p.zsh = 2 * 14 + 3 - 12 + (HD == 128 ? 24 : 0);
+  p.zmul = HD == 128 ? 11863283 : 0;
+  p.num = num; p.den = den; p.snum_tile = (int64_t)M * HD; p.snum_row = HD; p.sden_tile = M;
+  p.nsplit = nsplit;
+  if (nsplit > 1) {
+    const int64_t need = attn_ws_bytes((int64_t)R * HKV * M, (int64_t)R * HKV * ((M + 3) / 4), HD);
     BX_REQUIRE(ws != nullptr && ws_bytes >= need, "workspace too small (%lld < %lld)", (long long)ws_bytes,
                (long long)need);
     bind_attn_ws(p, ws, (int64_t)R * HKV * M, HD);

@@ -46,6 +46,13 @@ __device__ __forceinline__ int64_t rshc(int64_t x, int64_t s) {
   return shl(x, -s);
 }
 
+// intops.rsh (src/bitexact/intops.py:24-33): round(x / 2^s) ties up for s > 0, x 2^-s for s <= 0, shifts by
+// 64 or more as torch's int64 shifts give them.
+__device__ __forceinline__ int64_t rsh64(int64_t x, int64_t s) {
+  if (s > 0) return sar(add_wrap(x, shl(1, s - 1)), s);
+  return shl(x, -s);
+}
+
 // intops.bitlen (src/bitexact/intops.py:14-21) for x >= 0: 64 - clz.
 __device__ __forceinline__ int64_t bitlen(int64_t x) {
   return x > 0 ? 64 - __clzll((unsigned long long)x) : 0;

@@ -12,13 +12,6 @@ namespace bx {
 constexpr int64_t kSegNegBig = -(1LL << 20);   // ops.NEG_BIG
 constexpr int kSegQB = 22;                     // |q| <= 2^22
 
-// intops.rsh (src/bitexact/intops.py:24-33): round(x / 2^s) ties up for s > 0, x 2^-s for s <= 0, shifts by
-// 64 or more as torch's int64 shifts give them.
-__device__ __forceinline__ int64_t rsh64(int64_t x, int64_t s) {
-  if (s > 0) return sar(add_wrap(x, shl(1, s - 1)), s);
-  return shl(x, -s);
-}
-
 // intops.rdiv (src/bitexact/intops.py:41-43): floor((2a + b) / (2b)), b > 0.
 __device__ __forceinline__ int64_t rdiv64(int64_t a, int64_t b) { return fdiv(add_wrap(2 * a, b), 2 * b); }
 

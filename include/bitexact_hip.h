@@ -95,6 +95,16 @@ int bx_exact_attn_paged(const int32_t* q, const int64_t* sh, const int64_t* qpos
                         bx_stream_t stream);
 int64_t bx_attn_paged_workspace(int32_t R, int32_t HKV, int32_t M, int32_t HD);
 
+/* Replaces tri_paged.attend (src/bitexact/vllm_plugin/tri_paged.py:363-430), the int8-mode paged attention: q int64
+ * [R, HKV, M, HD] (within 3 limbs; any M, tiles of 4 queries), qpos [R, M] (row stride sqpos_r), the same limb-plane
+ * cache and block table rows bt [R, *] as bx_exact_attn_paged, weight table ptab int32 (tri_paged.weight_table,
+ * 2^17 + 1 entries): raw = q.K, mx = max over visible keys, z by int8.segs.score_rule, p = ptab[z - EXP_MIN 2^FA]
+ * (0 below the table) -> num int64 [R, HKV, M, HD], den int64 [R, HKV, M, 1]. Workspace as bx_exact_attn_paged. */
+int bx_int8_attn_paged(const int64_t* q, const int64_t* qpos, int64_t sqpos_r, const int8_t* cache, int64_t sc_nb,
+                       int64_t sc_h, int64_t sc_bs, int32_t bs, const int32_t* bt, int64_t sbt, int32_t nblk,
+                       const int32_t* ptab, int32_t ptab_len, int64_t* num, int64_t* den, int32_t R, int32_t HKV,
+                       int32_t M, int32_t HD, int32_t nsplit, void* ws, int64_t ws_bytes, bx_stream_t stream);
+
 /* Fused form of exact/model.py's attention (src/bitexact/exact/model.py:113-119: bmm(qg, K^T), segs.softmax,
  * bmm(p, V)): qg int32 [Z, gT, HD] (strides sq_z, sq_row), shg int64 [Z, gT] (ssh_z = gT), qpos int64 [Z, gT]
  * (strides), K / V int32 [Z, S, HD] (strides; the integer Cache layout), outputs num int64 [Z, gT, HD],

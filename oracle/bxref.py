@@ -586,3 +586,54 @@ def int8_post(acc, m, fmsh, mant, e, FR_=FR8):
     flag = bool(np.abs(t).max() >= 1 << 38) if t.size else False
     return rsh(t * _a(mant)[:, None], (24 - FR_ - _a(e))[:, None]), flag
 
+
+# ---- int8-mode attention weights (src/bitexact/int8/segs.py:29-37, 92-100; src/bitexact/int8/ops.py:93-97)
+# and the paged attention over the limb-plane cache (src/bitexact/vllm_plugin/tri_paged.py:1-26, 363-401) ----
+FQ8, FP8 = 14, 20
+FA8, FE8, EXP_MIN8 = 12, 30, -32
+SC128 = 11863283
+ZCLAMP8 = -(1 << 38)
+
+
+def int8_exp_table():
+    """e^x at FE bits, x = EXP_MIN .. 0 at step 2^-FA (src/bitexact/int8/consts.py:50-53)."""
+    xs = np.arange(EXP_MIN8 << FA8, 1, dtype=np.float64) / (1 << FA8)
+    return np.round(np.exp(xs) * float(1 << FE8)).astype(I64)
+
+
+def int8_softmax(raw, ok, expt, hd):
+    """int8 segs.softmax with the visibility mask given (src/bitexact/int8/segs.py:92-100)."""
+    raw = np.where(ok, _a(raw), I64(NEG))
+    d = raw - raw.max(-1, keepdims=True)
+    base = 2 * FQ8 + 3 - FA8
+    z = rsh(d, base) if hd == 64 else rsh(np.maximum(d, I64(ZCLAMP8)) * I64(SC128), base + 24)
+    idx = np.maximum(z, -(1 << 40)) - I64(EXP_MIN8 << FA8)
+    val = _a(expt)[np.maximum(idx, 0)]
+    e = np.where(idx < 0, I64(0), val)                           # int8 ops.exp_of
+    p = np.where(ok, rsh(e, FE8 - FP8), I64(0))
+    return p, p.sum(-1, keepdims=True)
+
+
+def paged_attend_int8(q, qpos, c32, bt, expt):
+    """tri_paged.attend as the unfused int8 rules (int8 segs.softmax between two exact matmuls): q int64
+    [R, HKV, M, HD], qpos [R, M], c32 int32 cache [nb, HKV, bs, 2 HD], bt [R, nblk]."""
+    q, qpos, c32, bt = (_a(x) for x in (q, qpos, c32, bt))
+    R, HKV, M, HD = q.shape
+    bs = c32.shape[2]
+    num = np.zeros((R, HKV, M, HD), I64)
+    den = np.zeros((R, HKV, M, 1), I64)
+    for r in range(R):
+        S = int(qpos[r].max()) + 1
+        if S <= 0:
+            continue
+        s = np.arange(S)
+        kv = c32[bt[r, s // bs], :, s % bs]
+        for h in range(HKV):
+            K, V = kv[:, h, :HD], kv[:, h, HD:]
+            raw = bmm(q[r, h][None], K.T[None])[0]
+            ok = s[None, :] <= qpos[r][:, None]
+            p, dn = int8_softmax(raw, ok, expt, HD)
+            num[r, h] = bmm(p[None], V[None])[0]
+            den[r, h] = dn
+    return num, den
+

@@ -1,6 +1,6 @@
 """Writes tests/golden/reference_vectors.npz: input/output vectors of the reference's CPU integer rules that
 closed forms do not pin bit for bit (ops.rms, ops.exp2neg_lut, ops.softmax_w, segs.norm_quant, ops.div_round,
-int8 ops.quant_rows). Run in the development container only, where the reference checkout is present:
+int8 ops.quant_rows, int8 segs.softmax). Run in the development container only, where the reference checkout is present:
 
     python tests/golden/make_golden.py /root/reference
 
@@ -77,6 +77,23 @@ def main(ref_root):
     z[2] = 0
     q, as_, sh = iops.quant_rows(z, 2)
     out["qr_z"], out["qr_q"], out["qr_as"], out["qr_sh"] = z.numpy(), q.numpy(), as_.numpy(), sh.numpy()
+
+    # int8 segs.softmax (score rule and exp table; head_dim 64 and 128)
+    from bitexact.int8 import consts as iconsts           # noqa: E402
+    from bitexact.int8 import segs as isegs               # noqa: E402
+    expt = iconsts.exp_table()
+    import hashlib
+    out["i8_exp_sha256"] = np.frombuffer(hashlib.sha256(expt.numpy().astype("<i8").tobytes()).digest(), np.uint8)
+    for hd in (64, 128):
+        raw = torch.randint(-(1 << 36), 1 << 36, (2, 2, 12, 200), generator=g)
+        raw[0, 0, 3] >>= 20
+        raw[1, 1, 5] = 9
+        qpos = torch.randint(-1, 200, (2, 1, 12, 1), generator=g)
+        qpos[0, 0, 0] = -1
+        qpos[1, 0, 1] = 199
+        p, den = isegs.softmax(raw, qpos, expt, hd)
+        out[f"i8sm{hd}_raw"], out[f"i8sm{hd}_qpos"] = raw.numpy(), qpos.numpy()
+        out[f"i8sm{hd}_p"], out[f"i8sm{hd}_den"] = p.numpy(), den.numpy()
 
     path = os.path.join(os.path.dirname(os.path.abspath(__file__)), "reference_vectors.npz")
     np.savez_compressed(path, **out)

@@ -138,3 +138,27 @@ def test_unfused_equals_fused_attention(dev):
     num = bmm(p, V)
     num2, den2 = prefill(qg, shg, K, V, qpos, _lut(dev), R.L2E28)
     assert torch.equal(num, num2) and torch.equal(den, den2)
+
+
+@pytest.mark.parametrize("HD", [64, 128])
+def test_int8_paged_attention(dev, HD):
+    """tri_paged.attend (int8 mode) against the unfused int8 rules; M = 9 spans several 4-query tiles."""
+    from bitexact.int8.consts import exp_table
+    from bitexact.vllm_plugin import tri_paged
+    g = torch.Generator().manual_seed(100 + HD)
+    ptab = tri_paged.weight_table(exp_table(dev))
+    expt = R.int8_exp_table()
+    nb, bs, HKV = 64, 16, 4
+    for lim, qlim in ((R.LIM3, 1 << 6), (1 << 13, 1 << 12), (1 << 10, 1 << 16)):
+        c = torch.randint(-lim, lim + 1, (nb, HKV, bs, 2 * HD), generator=g).to(torch.int32)
+        cl = tri_paged.to_limbs(c.to(dev))
+        for Rr, M, P in [(3, 4, 600), (2, 9, 300), (6, 1, 900), (7, 4, 5)]:
+            bt = torch.randint(0, nb, (Rr, 64), generator=g).to(torch.int32)
+            qpos = torch.randint(0, P, (Rr, M), generator=g)
+            qpos[0, 0] = -1
+            q = torch.randint(-qlim, qlim + 1, (Rr, HKV, M, HD), generator=g)
+            ref_num, ref_den = R.paged_attend_int8(q.numpy(), qpos.numpy(), c.numpy(), bt.numpy(), expt)
+            for ns in (None, 1, 5, 64):
+                num, den = tri_paged.attend(q.to(dev), qpos.to(dev), cl, bt.to(dev), ptab, nsplit=ns)
+                assert np.array_equal(num.cpu().numpy(), ref_num), (Rr, M, ns, lim)
+                assert np.array_equal(den.cpu().numpy(), ref_den), (Rr, M, ns, lim)

@@ -1,5 +1,6 @@
 """The oracle against vectors the reference's own CPU rules produced (tests/golden/make_golden.py):
-ops.rms, segs.norm_quant, ops.exp2neg_lut, ops.softmax_w (head_dim 64 and 128), ops.div_round, int8 quant_rows."""
+ops.rms, segs.norm_quant, ops.exp2neg_lut, ops.softmax_w (head_dim 64 and 128), ops.div_round, int8 quant_rows,
+int8 segs.softmax (head_dim 64 and 128)."""
 
 import os
 
@@ -42,3 +43,15 @@ def test_div_round_attn():
 def test_quant_rows():
     q, as_, sh = R.quant_rows(GOLD["qr_z"], 2)
     assert np.array_equal(q, GOLD["qr_q"]) and np.array_equal(as_, GOLD["qr_as"]) and np.array_equal(sh, GOLD["qr_sh"])
+
+
+def test_int8_exp_table_and_softmax():
+    expt = R.int8_exp_table()
+    assert expt.shape == ((1 << 17) + 1,) and expt[-1] == 1 << R.FE8
+    import hashlib
+    assert hashlib.sha256(expt.astype("<i8").tobytes()).digest() == GOLD["i8_exp_sha256"].tobytes()
+    for hd in (64, 128):
+        raw, qpos = GOLD[f"i8sm{hd}_raw"], GOLD[f"i8sm{hd}_qpos"]
+        ok = np.arange(raw.shape[-1]) <= qpos
+        p, den = R.int8_softmax(raw, ok, expt, hd)
+        assert np.array_equal(p, GOLD[f"i8sm{hd}_p"]) and np.array_equal(den, GOLD[f"i8sm{hd}_den"])
