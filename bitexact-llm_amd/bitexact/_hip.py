@@ -44,6 +44,8 @@ SIGNATURES = {
     "bx_attn_out": (ctypes.c_int, [P, I64, I64, P, I64, I32, I32, I32, I32, I32, I32, I32, P, I64, P, P]),
     "bx_int8_attn_paged": (ctypes.c_int, [P, P, I64, P, I64, I64, I64, I32, P, I64, I32, P, I32, P, P, I32, I32, I32,
                                           I32, I32, P, I64, P]),
+    "bx_exact_epilogue": (ctypes.c_int, [P, I64, I64, I32, P, I64, P, I64, I32, P, P, I32, P, P, P, I32, I32, P, I64,
+                                         I32, I32, P, P]),
     "bx_rope_qgroup": (ctypes.c_int, [P, I64, P, I64, I64, P, P, I32, I32, I32, I32, I32, I32, I32, I32, I32, I32,
                                       I32, P, P, P, P, P, P]),
     "bx_int8_quant_rows": (ctypes.c_int, [P, I64, I32, I32, I32, I32, P, P, P, P, P, P]),

@@ -165,6 +165,38 @@ __global__ __launch_bounds__(256) void int8_post_kernel(const int64_t* acc, int6
   if (wave_or(big ? 1 : 0) && (threadIdx.x & 63) == 0) flag[0] = 1;
 }
 
+// wmm.epilogue over segs.lin_y's inputs (src/bitexact/exact/wmm.py:132-150, src/bitexact/exact/segs.py:25-32):
+// T = sum of the split partials, B = dense residual or the ELL gather sum_j q[m, ec[n, j]] ev[n, j], then the
+// one rounding at p = sh[m] + g[n] - d[n] + FR; flag[0] = 1 where the checked rule fails.
+__global__ __launch_bounds__(256) void exact_epilogue_kernel(const int64_t* T, int64_t ldt, int64_t sts, int nsplit,
+                                                             const int64_t* B, int64_t ldb, const int32_t* q,
+                                                             int64_t ldq, int K, const int32_t* ec, const int64_t* ev,
+                                                             int R, const int64_t* d, const int64_t* g,
+                                                             const int64_t* sh, int FR, int checked, int64_t* y,
+                                                             int64_t ldy, int M, int N, int32_t* flag) {
+  const int64_t total = (int64_t)M * N;
+  bool bad_any = false;
+  for (int64_t i = blockIdx.x * 256LL + threadIdx.x; i < total; i += (int64_t)gridDim.x * 256) {
+    const int m = (int)(i / N), n = (int)(i - (int64_t)m * N);
+    int64_t t = 0;
+    for (int s = 0; s < nsplit; ++s) t = add_wrap(t, T[s * sts + (int64_t)m * ldt + n]);
+    int64_t b = 0;
+    if (B) {
+      b = B[(int64_t)m * ldb + n];
+    } else {
+      for (int j = 0; j < R; ++j) {
+        const int c = (int)min((uint32_t)ec[(int64_t)n * R + j], (uint32_t)(K - 1));   // valid ELL: [0, K)
+        b = add_wrap(b, mul_wrap((int64_t)q[(int64_t)m * ldq + c], ev[(int64_t)n * R + j]));
+      }
+    }
+    const int64_t dn = d[n];
+    bool bad;
+    y[(int64_t)m * ldy + n] = exact_round(t, b, dn, sh[m] + g[n] - dn + FR, bad);
+    bad_any |= bad;
+  }
+  if (checked && wave_or(bad_any ? 1 : 0) && (threadIdx.x & 63) == 0) flag[0] = 1;
+}
+
 }  // namespace bx
 
 using namespace bx;
@@ -210,4 +242,23 @@ extern "C" int bx_int8_post(const int64_t* acc, int64_t ldacc, const int64_t* m,
   const int blocks = (int)((total + 255) / 256 < 4096 ? (total + 255) / 256 : 4096);
   int8_post_kernel<<<blocks, 256, 0, (hipStream_t)stream>>>(acc, ldacc, m, fmsh, mant, e, FR, y, ldy, M, N, flag);
   return check_launch("int8_post_kernel");
+}
+
+extern "C" int bx_exact_epilogue(const int64_t* T, int64_t ldt, int64_t sts, int32_t nsplit, const int64_t* B,
+                                 int64_t ldb, const int32_t* q, int64_t ldq, int32_t K, const int32_t* ell_col,
+                                 const int64_t* ell_val, int32_t R, const int64_t* d, const int64_t* g,
+                                 const int64_t* sh, int32_t FR, int32_t checked, int64_t* y, int64_t ldy, int32_t M,
+                                 int32_t N, int32_t* flag, bx_stream_t stream) {
+  BX_REQUIRE(M >= 0 && N >= 0 && nsplit >= 1 && ldt >= N && ldy >= N, "bad sizes");
+  BX_REQUIRE(B == nullptr || ldb >= N, "ldb too small");
+  BX_REQUIRE(B != nullptr || R == 0 || (q && ell_col && ell_val && K > 0 && ldq >= K), "residual missing");
+  BX_REQUIRE(!checked || flag, "checked needs a flag pointer");
+  if (M == 0 || N == 0) return BX_OK;
+  BX_REQUIRE(T && d && g && sh && y, "null pointer");
+  const int64_t total = (int64_t)M * N;
+  const int blocks = (int)((total + 255) / 256 < 8192 ? (total + 255) / 256 : 8192);
+  exact_epilogue_kernel<<<blocks, 256, 0, (hipStream_t)stream>>>(T, ldt, sts, nsplit, B, ldb, q, ldq, K, ell_col,
+                                                                ell_val, B ? 0 : R, d, g, sh, FR, checked, y, ldy, M,
+                                                                N, flag);
+  return check_launch("exact_epilogue_kernel");
 }

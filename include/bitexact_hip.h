@@ -159,6 +159,15 @@ int bx_rope_qgroup(const int64_t* y, int64_t ldy, const int64_t* pos, int64_t sp
                    int32_t FR, int32_t FT, int32_t FK, int32_t FV, int32_t FZ, int32_t* qg, int64_t* shg, int64_t* k,
                    int64_t* v, int32_t* err, bx_stream_t stream);
 
+/* Replaces wmm.epilogue and segs.lin_y (src/bitexact/exact/wmm.py:132-150, src/bitexact/exact/segs.py:25-32): T int64
+ * [nsplit, M, N] split partials (slice stride sts, row stride ldt) summed, residual B int64 [M, ldb] or (B null)
+ * the ELL gather sum_j q[m, ell_col[n, j]] ell_val[n, j] (R entries per column), then y = round((T 2^d + B)
+ * 2^(sh + g - d + FR)) once; with `checked`, flag[0] = 1 where wmm.epilogue(checked=True) flags. */
+int bx_exact_epilogue(const int64_t* T, int64_t ldt, int64_t sts, int32_t nsplit, const int64_t* B, int64_t ldb,
+                      const int32_t* q, int64_t ldq, int32_t K, const int32_t* ell_col, const int64_t* ell_val,
+                      int32_t R, const int64_t* d, const int64_t* g, const int64_t* sh, int32_t FR, int32_t checked,
+                      int64_t* y, int64_t ldy, int32_t M, int32_t N, int32_t* flag, bx_stream_t stream);
+
 /* Replaces int8 ops.quant_rows + intops.stack_limbs (src/bitexact/int8/ops.py:24-35, src/bitexact/intops.py:73-79)
  * and, with mant / e given, segs.pre_plain's row scale norm24(as_, sh - FR) (src/bitexact/int8/segs.py:56-59):
  * z int64 [M, ldz] -> a int8 [nl M, K] (limb i of row m at row i M + m, no padding rows), as_, sh [M]. */

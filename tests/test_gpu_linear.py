@@ -179,3 +179,31 @@ def test_config2_int8_decode(dev, M, N, K):
     a = R.stack_limbs(q, 2)
     y = int_mm_join(torch.from_numpy(a).to(dev), w.to(dev), M, 2)
     assert np.array_equal(y.cpu().numpy(), R.imm(q, w.numpy()))
+
+
+def test_standalone_epilogue_and_lin_y(dev):
+    """wmm.epilogue / segs.lin_y on the device: dense residual and ELL forms, split partials, the checked flag."""
+    from bitexact.exact import wmm
+    N, K, M = 160, 512, 37
+    w = _bf16(N, K, 23)
+    dec = _dec(w)
+    limbs = torch.from_numpy(dec["limbs"]).to(dev)
+    d, gg = torch.from_numpy(dec["d"]).to(dev), torch.from_numpy(dec["g"]).to(dev)
+    _, ec, ev, Rr = _ell(dec, N, dev)
+    g = np.random.default_rng(4)
+    for lim, shr in ((1 << 22, (-30, -20)), (3, (-70, 10))):
+        q = g.integers(-lim, lim + 1, (M, K))
+        sh = g.integers(shr[0], shr[1], M)
+        T_ref = R.wmm_f64(q, dec["W"])
+        B_ref = R.residual(q, dec["rr"], dec["rc"], dec["rv"], N)
+        ref, rflag, _ = R.epilogue(T_ref, B_ref, dec["d"], dec["g"], sh, R.FR, True)
+        qd, shd = torch.from_numpy(q).to(torch.int32).to(dev), torch.from_numpy(sh).to(dev)
+        T = wmm.wmm_hip(qd, limbs)
+        y, flag = wmm.lin_y(T, (qd, ec, ev), d, gg, shd, checked=True)
+        assert np.array_equal(y.cpu().numpy(), ref) and bool(flag) == rflag
+        y2, flag2 = wmm.epilogue(T[0], torch.from_numpy(B_ref).to(dev), d, gg, shd, R.FR, True)
+        assert np.array_equal(y2.cpu().numpy(), ref) and bool(flag2) == rflag
+        X = torch.from_numpy(g.integers(-(1 << 40), 1 << 40, (M, N))).to(dev)
+        T3 = torch.stack([T[0] - X, X])                  # two split partials summing to T
+        y3 = wmm.lin_y(T3, (qd, ec, ev), d, gg, shd)
+        assert np.array_equal(y3.cpu().numpy(), ref)
