@@ -1,8 +1,14 @@
 """Exact-mode weight format and tables (src/bitexact/exact/consts.py).
 
 decompose() runs on the device (two HIP kernels, one block per output row) and returns the reference's
-dict keys plus the ELL form of the residual that the fused linear reads.
+dict keys plus the ELL form of the residual that the fused linear reads. random_constants() builds a
+constants dict with the reference's keys (src/bitexact/exact/consts.py:118-149) for a random-init model of
+a given geometry: bf16 N(0, 0.02) weights drawn on the device, decomposed there, unit norm gammas, tied
+lm_head. The RoPE and 2^-f tables are float64 constants computed once on the host, as the reference's
+offline build computes them.
 """
+
+import math
 
 import torch
 
@@ -10,6 +16,7 @@ from bitexact import _hip
 
 FR = 24                       # residual stream, linear outputs (src/bitexact/exact/consts.py:23)
 FT = 30                       # cos / sin
+MAX_POS = 4096                # RoPE table rows
 EXP2_BITS = 14                # 2^-f table step
 EXP2_ONE = 60                 # table values at 2^60
 LIM3 = 8355711
@@ -52,3 +59,102 @@ def exp2_table(device=None):
     f = torch.arange((1 << EXP2_BITS) + 1, dtype=torch.float64) / (1 << EXP2_BITS)
     t = torch.round(torch.pow(2.0, -f) * 2.0 ** EXP2_ONE).long()
     return t if device is None else t.to(device)
+
+
+def bf16_parts(w):
+    """bf16 tensor -> (signed significand, exponent) int64: w = sm 2^ex exactly (src/bitexact/exact/consts.py:33-42)."""
+    b = w.contiguous().view(torch.int16).long() & 0xFFFF
+    e = (b >> 7) & 0xFF
+    assert not bool((e == 255).any()), "inf/nan weight"
+    m = b & 0x7F
+    mag = torch.where(e > 0, m | 0x80, m)
+    ex = torch.where(e > 0, e, torch.ones_like(e)) - 134
+    return torch.where((b >> 15) == 1, -mag, mag), ex
+
+
+def emb_fixed(w):
+    """Embedding table bf16 [V, D] -> int32 at FR, each entry rounded once (half up) to 2^-FR
+    (src/bitexact/exact/consts.py:131-135)."""
+    sm, ex = bf16_parts(w)
+    s = ex + FR
+    e = torch.where(s >= 0, sm << s.clamp(min=0),
+                    (sm + (1 << (-s - 1).clamp(min=0, max=62))) >> (-s).clamp(max=63))
+    assert int(e.abs().max()) < 1 << 31
+    return e.to(torch.int32)
+
+
+def llama3_inv_freq(hd=64, theta=500000.0, factor=32.0, low=1.0, high=4.0, orig=8192):
+    """Llama-3 scaled RoPE inverse frequencies: the transformers rule src/bitexact/llama.py:52-62 calls, in its
+    float32 arithmetic, widened to float64. Wavelengths above orig / low are divided by factor, those below
+    orig / high kept, the band between blended."""
+    inv = 1.0 / (theta ** (torch.arange(0, hd, 2, dtype=torch.int64).to(torch.float32) / hd))
+    wl = 2 * math.pi / inv
+    out = torch.where(wl > orig / low, inv / factor, inv)
+    smooth = (orig / wl - low) / (high - low)
+    mid = (1 - smooth) * out / factor + smooth * out
+    return torch.where(~(wl < orig / high) & ~(wl > orig / low), mid, out).double()
+
+
+def rope_tables(n_pos, bits, inv_freq):
+    """Integer cos / sin [n_pos, HD / 2] at `bits` fractional bits, rounded once (src/bitexact/llama.py:65-68)."""
+    ang = torch.arange(n_pos, dtype=torch.float64)[:, None] * inv_freq[None, :]
+    return torch.round(torch.cos(ang) * 2.0 ** bits).long(), torch.round(torch.sin(ang) * 2.0 ** bits).long()
+
+
+LLAMA_3_2_1B = {"hidden_size": 2048, "num_attention_heads": 32, "num_key_value_heads": 8, "head_dim": 64,
+                "intermediate_size": 8192, "vocab_size": 128256, "num_hidden_layers": 16, "rope_theta": 500000.0,
+                "rope_scaling": {"factor": 32.0, "low_freq_factor": 1.0, "high_freq_factor": 4.0,
+                                 "original_max_position_embeddings": 8192}}
+
+
+def dims(cfg):
+    """(H, HKV, HD, D, FF) of a HF Llama config dict (src/bitexact/llama.py:29-33); {} gives Llama-3.2-1B."""
+    c = LLAMA_3_2_1B
+    d = cfg.get("hidden_size", c["hidden_size"])
+    h = cfg.get("num_attention_heads", c["num_attention_heads"])
+    return (h, cfg.get("num_key_value_heads", c["num_key_value_heads"]), cfg.get("head_dim") or d // h, d,
+            cfg.get("intermediate_size", c["intermediate_size"]))
+
+
+def random_constants(cfg=None, n_layers=None, seed=0, device="cuda", keep_bf16=False):
+    """Constants dict (the reference's keys) of a random-init Llama: every linear weight bf16 N(0, 0.02) drawn on
+    `device` from `seed`, decomposed there; norm gammas 1.0; lm_head tied to the embedding. keep_bf16 also keeps
+    each weight's bf16 tensor under f"{name}.bf16" (checkers rebuild the decomposition from it)."""
+    cfg = dict(LLAMA_3_2_1B if cfg is None else cfg)
+    H, HKV, HD, D, FF = dims(cfg)
+    V = cfg.get("vocab_size", LLAMA_3_2_1B["vocab_size"])
+    L = cfg.get("num_hidden_layers", 16) if n_layers is None else n_layers
+    dev = torch.device(device)
+    gen = torch.Generator(device=dev).manual_seed(seed)
+    c = {"n_layers": L, "cfg": cfg}
+
+    def draw(n, k):
+        return (torch.randn(n, k, generator=gen, device=dev, dtype=torch.float32) * 0.02).to(torch.bfloat16)
+
+    def put(name, w):
+        dec = decompose(w)
+        for k in ("limbs", "g", "d", "rr", "rc", "rv", "ell_cnt", "ell_col", "ell_val", "R"):
+            c[f"{name}.{k}"] = dec[k]
+        if keep_bf16:
+            c[f"{name}.bf16"] = w
+
+    emb = draw(V, D)
+    c["emb"] = emb_fixed(emb)
+    one = torch.ones(D, dtype=torch.bfloat16, device=dev)
+    for i in range(L):
+        put(f"{i}.wqkv", draw((H + 2 * HKV) * HD, D))
+        put(f"{i}.wo", draw(D, H * HD))
+        put(f"{i}.wgu", draw(2 * FF, D))
+        put(f"{i}.wd", draw(D, FF))
+        for n in ("ga", "gm"):
+            c[f"{i}.{n}.m"], c[f"{i}.{n}.e"] = bf16_parts(one)
+    c["gf.m"], c["gf.e"] = bf16_parts(one)
+    put("lm", emb)
+    if keep_bf16:
+        c["emb.bf16"] = emb
+    rs = cfg.get("rope_scaling") or {}
+    inv = llama3_inv_freq(HD, cfg.get("rope_theta", 500000.0), rs.get("factor", 32.0), rs.get("low_freq_factor", 1.0),
+                          rs.get("high_freq_factor", 4.0), rs.get("original_max_position_embeddings", 8192))
+    c["cos"], c["sin"] = (t.to(dev) for t in rope_tables(MAX_POS, FT, inv))
+    c["exp2"] = exp2_table(dev)
+    return c

@@ -24,6 +24,16 @@ class Lin:
         self.rr, self.rc, self.rv = t("rr").long(), t("rc").long(), t("rv").long()
         self.gemm = gemm
         self.ell = True
+        if f"{name}.ell_cnt" in c:                    # already in ELL form (consts.decompose on the device)
+            self.R = max(R, int(c[f"{name}.R"]))
+            self.cnt = t("ell_cnt").to(torch.int32).contiguous()
+            ec, ev = t("ell_col").to(torch.int32), t("ell_val").long()
+            if ec.shape[1] < max(self.R, 1):
+                pad = max(self.R, 1) - ec.shape[1]
+                ec = torch.nn.functional.pad(ec, (0, pad))
+                ev = torch.nn.functional.pad(ev, (0, pad))
+            self.ec, self.ev = ec.contiguous(), ev.contiguous()
+            return
         rr = self.rr.cpu()
         cnt = torch.bincount(rr, minlength=self.N) if rr.numel() else torch.zeros(self.N, dtype=torch.long)
         self.R = max(R, int(cnt.max()) if rr.numel() else 0)

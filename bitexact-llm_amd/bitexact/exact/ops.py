@@ -4,6 +4,9 @@ norm_quant(x, gm, ge, err)      segs.norm_quant: RMSNorm + quantization at -FN -
 softmax(raw, qpos, shg, lut, l2e) segs.softmax: masked weights at FP -> (p int32, den)
 attn_out(num, den, T, hkv)      Segs.attn_out: div_round + regroup + quantization at -FR -> (q int32, sh)
 qkv_y(y, pos, cos, sin, B, T, dm, err)  Segs.qkv_y: RoPE + q quantization + regroup -> (qg, shg, k, v, err)
+add_norm_y(y, x, gm, ge, err)   Segs.add_norm_y: x += y in place, then norm_quant (gm None: the add alone)
+embed_norm(emb, ids, gm, ge, err)  emb[ids] + pre_norm -> (x, q, sh, err)
+gu_silu_y(y, lut, err)          Segs.gu_silu_y: silu(gate) up + quantization at -2 FR -> (q int32, sh, err)
 """
 
 import torch
@@ -91,3 +94,63 @@ def qkv_y(y, pos, cos, sin, B, T, dm, err=None):
               _hip.ptr(shg), _hip.ptr(k), _hip.ptr(v), _hip.ptr(flag), _hip.stream_of(y))
     e = flag[0].bool()
     return qg, shg, k, v, e if err is None else (err | e)
+
+
+def _flag(dev):
+    return torch.zeros(1, dtype=torch.int32, device=dev)
+
+
+def _or(err, flag):
+    e = flag[0].bool()
+    return e if err is None else (err | e)
+
+
+def add_norm_y(y, x, gm, ge, err=None):
+    """Segs.add_norm_y (src/bitexact/exact/segs.py:175-178): x int64 [M, D] += y (in place, as exact_fuse.add_norm's
+    store), then norm_quant of the sum. gm None: the add alone (returns q = sh = None)."""
+    _hip.require_cuda(x, y)
+    assert x.dtype == torch.int64 and y.dtype == torch.int64 and x.stride(-1) == 1 and y.stride(-1) == 1
+    M, D = x.shape
+    y = y.view(M, D) if y.dim() != 2 else y
+    flag = _flag(x.device)
+    if gm is None:
+        _hip.call("bx_add_rmsnorm_quant", _hip.ptr(x), x.stride(0), _hip.ptr(y), y.stride(0), None, None, None, D, None,
+                  M, D, FR, FN, _hip.ptr(flag), _hip.stream_of(x))
+        return x, None, None, _or(err, flag)
+    q = torch.empty(M, D, dtype=torch.int32, device=x.device)
+    sh = torch.empty(M, dtype=torch.long, device=x.device)
+    gm, ge = gm.contiguous().long(), ge.contiguous().long()
+    _hip.call("bx_add_rmsnorm_quant", _hip.ptr(x), x.stride(0), _hip.ptr(y), y.stride(0), _hip.ptr(gm), _hip.ptr(ge),
+              _hip.ptr(q), D, _hip.ptr(sh), M, D, FR, FN, _hip.ptr(flag), _hip.stream_of(x))
+    return x, q, sh, _or(err, flag)
+
+
+def embed_norm(emb, ids, gm, ge, err=None):
+    """x = emb[ids].long() (emb int32 [V, D]) and its pre_norm (src/bitexact/exact/model.py:130-132) -> (x, q, sh, err)."""
+    _hip.require_cuda(emb, ids, gm, ge)
+    assert emb.dtype == torch.int32 and emb.is_contiguous()
+    ids = ids.reshape(-1).contiguous().long()
+    M, D = ids.shape[0], emb.shape[1]
+    x = torch.empty(M, D, dtype=torch.long, device=emb.device)
+    q = torch.empty(M, D, dtype=torch.int32, device=emb.device)
+    sh = torch.empty(M, dtype=torch.long, device=emb.device)
+    flag = _flag(emb.device)
+    gm, ge = gm.contiguous().long(), ge.contiguous().long()
+    _hip.call("bx_embed_rmsnorm_quant", _hip.ptr(emb), _hip.ptr(ids), _hip.ptr(x), D, _hip.ptr(gm), _hip.ptr(ge),
+              _hip.ptr(q), D, _hip.ptr(sh), M, D, FR, FN, _hip.ptr(flag), _hip.stream_of(emb))
+    return x, q, sh, _or(err, flag)
+
+
+def gu_silu_y(y, lut, err=None):
+    """Segs.gu_silu_y (src/bitexact/exact/segs.py:180-182): y int64 [M, 2 ff] (gate | up) at FR ->
+    (q int32 [M, ff], sh int64 [M], err | not ok)."""
+    _hip.require_cuda(y, lut)
+    assert y.dtype == torch.int64 and y.stride(-1) == 1 and y.shape[1] % 2 == 0
+    M, ff = y.shape[0], y.shape[1] // 2
+    q = torch.empty(M, ff, dtype=torch.int32, device=y.device)
+    sh = torch.empty(M, dtype=torch.long, device=y.device)
+    flag = _flag(y.device)
+    lut = lut.contiguous().long()
+    _hip.call("bx_silu_quant", _hip.ptr(y), y.stride(0), ff, _hip.ptr(lut), FR, _hip.ptr(q), ff, _hip.ptr(sh), M,
+              _hip.ptr(flag), _hip.stream_of(y))
+    return q, sh, _or(err, flag)

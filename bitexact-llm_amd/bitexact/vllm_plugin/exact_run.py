@@ -1,0 +1,92 @@
+"""Exact-mode decode engine on the paged limb-plane KV cache (src/bitexact/vllm_plugin/exact_run.py:22-175).
+
+Every token of the step is a row: it is embedded and normalised, goes through the fused exact linears, RoPE and
+q quantization, is stored into its layer's paged cache (K at FK = 17, V at FV = 19 bits, 3 int8 limb planes)
+and attends its own sequence's keys through its block-table row; attention output, residual adds, RMSNorms,
+SiLU gating and the logits follow the reference's stages. Every rule is row-local, so the batch a token
+shares a step with cannot change a bit of its logits. One HIP launch per stage; no host synchronisation, so a
+step can be captured in a HIP graph.
+"""
+
+import torch
+
+from bitexact.exact import ops
+from bitexact.exact.consts import FR, dims
+from bitexact.exact.model import Lin
+from bitexact.intops import first_argmax
+from bitexact.vllm_plugin import tri_exact_attn, tri_paged
+from bitexact.vllm_plugin.exact_gemm import FusedLin
+
+NAMES = ("wqkv", "wo", "wgu", "wd")
+
+
+class ExactEngine:
+    """c: constants dict with the reference's keys (exact.consts.build, or random_constants here)."""
+
+    def __init__(self, c, dev):
+        dev = torch.device(dev)
+        if dev.type != "cuda":
+            raise AssertionError("bitexact (MI355X) ExactEngine runs on the GPU only")
+        self.dev = dev
+        self.L = c["n_layers"]
+        self.H, self.HKV, self.HD, self.D, self.FF = dims(c.get("cfg", {}))
+        self.G = self.H // self.HKV
+        self.FR = FR
+        self.l2e = ops.L2E28_HD[self.HD]                        # KeyError: unsupported head_dim
+        t = lambda k: c[k].to(dev)
+        self.emb = t("emb").to(torch.int32).contiguous()
+        assert self.emb.shape[1] == self.D, "constants config does not match the embedding width"
+        self.fused = {(i, n): FusedLin(Lin(c, f"{i}.{n}", dev)) for i in range(self.L) for n in NAMES}
+        self.fused["lm"] = FusedLin(Lin(c, "lm", dev))
+        self.V = self.fused["lm"].N
+        gam = lambda k: (t(f"{k}.m").long().contiguous(), t(f"{k}.e").long().contiguous())
+        self.ga = [gam(f"{i}.ga") for i in range(self.L)]
+        self.gm = [gam(f"{i}.gm") for i in range(self.L)]
+        self.gf = gam("gf")
+        self.cos, self.sin, self.exp2 = t("cos").long(), t("sin").long(), t("exp2").long()
+        self.fl = torch.zeros(1, dtype=torch.int32, device=dev)  # flags of the checked linears
+        self.err = torch.zeros((), dtype=torch.bool, device=dev)
+
+    def new_cache(self, nblocks, bs=16):
+        """One limb-plane cache per layer: int8 [nblocks, HKV, bs, 8 HD] (block 0 is the null block)."""
+        return [torch.zeros(nblocks, self.HKV, bs, 8 * self.HD, dtype=torch.int8, device=self.dev)
+                for _ in range(self.L)]
+
+    def forward(self, kvs, ids, pos, slot, bt, rmap):
+        """ids, pos, slot [N]: the step's tokens (slot < 0: padding, redirected to the null block 0); bt [*, nblk]
+        int32 block table and rmap [N] the table row of each token. Returns the residual stream [N, D] int64 at FR
+        (src/bitexact/vllm_plugin/exact_run.py:106-128 with the fused stages of its 130-155)."""
+        N, G, HKV, HD = ids.shape[0], self.G, self.HKV, self.HD
+        pos = pos.long().contiguous()
+        slot = torch.where(slot < 0, torch.zeros_like(slot), slot).long()
+        qpos = pos.view(-1, 1).expand(-1, G).contiguous()
+        err = self.err
+        x, q, sh, err = ops.embed_norm(self.emb, ids, *self.ga[0], err)
+        for i in range(self.L):
+            y = self.fused[i, "wqkv"](q, sh, self.fl, False)
+            qg, shg, k, v, err = ops.qkv_y(y, pos.view(N, 1), self.cos, self.sin, N, 1, (self.H, HKV, HD), err)
+            tri_paged.store(kvs[i], slot, k[:, 0], v[:, 0])
+            num, den = tri_exact_attn.attend(qg.view(N, HKV, G, HD), shg.view(N, HKV, G), qpos, kvs[i], bt, rmap,
+                                             self.exp2, self.l2e)
+            qo, sho = ops.attn_out(num.view(N * HKV, G, HD), den.view(N * HKV, G, 1), 1, HKV)
+            x, q, sh, err = ops.add_norm_y(self.fused[i, "wo"](qo, sho, self.fl, True), x, *self.gm[i], err)
+            q, sh, err = ops.gu_silu_y(self.fused[i, "wgu"](q, sh, self.fl, False), self.exp2, err)
+            nxt = self.ga[i + 1] if i + 1 < self.L else (None, None)
+            x, q, sh, err = ops.add_norm_y(self.fused[i, "wd"](q, sh, self.fl, True), x, *nxt, err)
+        self.err = err | (self.fl != 0)
+        return x
+
+    def logits(self, h):
+        """Final residual rows [M, D] -> logits int64 [M, V] at FR (exact_run.py:157-175)."""
+        q, sh, err = ops.norm_quant(h, *self.gf, self.err)
+        y = self.fused["lm"](q, sh, self.fl, True)
+        self.err = err | (self.fl != 0)
+        return y
+
+    def greedy(self, logits):
+        """The greedy token of each logits row: its first maximum."""
+        return first_argmax(logits)
+
+    def check(self):
+        if bool(self.err):
+            raise OverflowError("integer bound violated (exact/model.py)")

@@ -1,5 +1,6 @@
 // Row-wise integer stages around the GEMMs and the attention, one 256-thread block per row with wavefront
-// int64 reductions: RMSNorm + per-row quantization (segs.norm_quant), the masked softmax weights
+// int64 reductions: RMSNorm + per-row quantization (segs.norm_quant, optionally after the residual add or the
+// embedding gather), SiLU gating + quantization (segs.silu_y + quant_silu), the masked softmax weights
 // (segs.softmax), and the attention output rule (segs.attn_out = div_round + regroup + quant).
 #include "bx_common.h"
 
@@ -60,43 +61,153 @@ __device__ __forceinline__ int64_t div_round64(int64_t a, int64_t p, int64_t r) 
 }
 
 // ---- segs.norm_quant (src/bitexact/exact/segs.py:59-63) over ops.rms (src/bitexact/exact/ops.py:92-105) and
-// ops.quant (src/bitexact/exact/ops.py:82-89). P rows are kept in LDS between the two passes. ----
-__global__ __launch_bounds__(256) void norm_quant_kernel(const int64_t* x, int64_t ldx, const int64_t* gm,
-                                                         const int64_t* ge, int32_t* q, int64_t ldq, int64_t* sh, int D,
-                                                         int lg, int FR, int FN, int32_t* err) {
+// ops.quant (src/bitexact/exact/ops.py:82-89), on the residual row the block first forms:
+//   SRC_X    the row of x as it is;
+//   SRC_ADD  x + y (segs.add_y, src/bitexact/exact/segs.py:40-41), written back to x;
+//   SRC_EMB  emb[ids[row]] widened to int64 (the model's `emb[ids].long()`, exact/model.py:130), written to x.
+// With gm null only the residual row is formed and bound-checked (the last layer's add). The row and P stay in LDS between the
+// passes. ----
+enum RowSrc { SRC_X = 0, SRC_ADD = 1, SRC_EMB = 2 };
+
+struct NormArgs {
+  int64_t* x;
+  int64_t ldx;
+  const int64_t* y;
+  int64_t ldy;
+  const int32_t* emb;
+  const int64_t* ids;
+  const int64_t* gm;
+  const int64_t* ge;
+  int32_t* q;
+  int64_t ldq;
+  int64_t* sh;
+  int D, lg, FR, FN;
+  int32_t* err;
+};
+
+template <int SRC>
+__global__ __launch_bounds__(256) void norm_quant_kernel(NormArgs p) {
   extern __shared__ __align__(16) char smem[];
-  int64_t* Ps = (int64_t*)smem;
+  int64_t* Xs = (int64_t*)smem;
+  int64_t* Ps = Xs + p.D;
   __shared__ int64_t sbuf[8];
-  const int64_t* xr = x + (int64_t)blockIdx.x * ldx;
+  const int D = p.D;
+  int64_t* xr = p.x + (int64_t)blockIdx.x * p.ldx;
+  const int32_t* er_row = nullptr;
+  if (SRC == SRC_EMB) er_row = p.emb + p.ids[blockIdx.x] * (int64_t)D;
   int64_t amax = 0;
   for (int i = threadIdx.x; i < D; i += 256) {
-    const int64_t v = xr[i];
+    int64_t v;
+    if (SRC == SRC_EMB) v = er_row[i];
+    else if (SRC == SRC_ADD) v = add_wrap(xr[i], p.y[(int64_t)blockIdx.x * p.ldy + i]);
+    else v = xr[i];
+    if (SRC != SRC_X) xr[i] = v;
+    Xs[i] = v;
     amax = imax(amax, v < 0 ? -v : v);
   }
   amax = block_max64(amax, sbuf);
-  if (threadIdx.x == 0 && amax >= (1LL << 40)) err[0] = 1;
+  if (threadIdx.x == 0 && amax >= (1LL << 40)) p.err[0] = 1;
+  if (p.gm == nullptr) return;
   const int64_t shx = imax(bitlen(imax(amax, 1)) - 25, -6);
   int64_t S = 0;
   for (int i = threadIdx.x; i < D; i += 256) {
-    const int64_t xs = rshc(xr[i], shx);
+    const int64_t xs = rshc(Xs[i], shx);
     S = add_wrap(S, mul_wrap(xs, xs));
   }
   S = block_sum64(S, sbuf);
-  const int64_t T = add_wrap(S, rshc(kEps60 * (int64_t)D, 60 - 2 * (FR - shx)));
-  const int64_t m = fdiv(62 + lg - bitlen(T), 2);
-  const int64_t s = 2 * m - lg;
+  const int64_t T = add_wrap(S, rshc(kEps60 * (int64_t)D, 60 - 2 * (p.FR - shx)));
+  const int64_t m = fdiv(62 + p.lg - bitlen(T), 2);
+  const int64_t s = 2 * m - p.lg;
   const int64_t V = s >= 0 ? shl(T, s) : sar(T, -s);
-  const int64_t r = isqrt64(V), er = shx - FR - m;
+  const int64_t r = isqrt64(V), er = shx - p.FR - m;
   int64_t emax = kNegBig;
   for (int i = threadIdx.x; i < D; i += 256) {
-    const int64_t P = div_round64(mul_wrap(xr[i], gm[i]), ge[i] - FR - er + FN, r);
+    const int64_t P = div_round64(mul_wrap(Xs[i], p.gm[i]), p.ge[i] - p.FR - er + p.FN, r);
     Ps[i] = P;
-    if (P != 0) emax = imax(emax, bitlen(P < 0 ? -P : P) - FN);
+    if (P != 0) emax = imax(emax, bitlen(P < 0 ? -P : P) - p.FN);
   }
   emax = block_max64(emax, sbuf);
   const int64_t shr = imax(emax - kQB, kNegBig);
-  for (int i = threadIdx.x; i < D; i += 256) q[(int64_t)blockIdx.x * ldq + i] = (int32_t)rshc(Ps[i], shr + FN);
+  for (int i = threadIdx.x; i < D; i += 256) p.q[(int64_t)blockIdx.x * p.ldq + i] = (int32_t)rshc(Ps[i], shr + p.FN);
+  if (threadIdx.x == 0) p.sh[blockIdx.x] = shr;
+}
+
+// ---- segs.silu_y + segs.quant_silu (src/bitexact/exact/segs.py:120-128) over ops.silu_mul
+// (src/bitexact/exact/ops.py:119-130): per row of gu = [gate | up] at FR, P = silu(gate) up at 2 FR exactly,
+// then the row quantization at eps = -2 FR. err[0] = 1 where silu_mul's ok is false (|g| > 2^32, or an element
+// with bitlen(|s|) + bitlen(|u|) > 62). ----
+constexpr int64_t kL2E30 = 1549082005LL;   // round(log2(e) 2^30) (ops.L2E30)
+
+__device__ __forceinline__ int64_t exp2neg30(int64_t t, const int64_t* lut) {   // ops.exp2neg_lut(t, lut, 30)
+  const int64_t n = t >> 26, f = t & ((1LL << 26) - 1);
+  const int64_t idx = f >> 12, rr = f & 4095;
+  const int64_t a = lut[idx];
+  const int64_t v = add_wrap(a, rshc(mul_wrap(lut[idx + 1] - a, rr), 12));
+  return rshc(v, 30 + n);
+}
+
+__global__ __launch_bounds__(256) void silu_quant_kernel(const int64_t* gu, int64_t ldgu, int ff, const int64_t* lut,
+                                                         int FR, int32_t* q, int64_t ldq, int64_t* sh, int32_t* err) {
+  extern __shared__ __align__(16) char smem[];
+  int64_t* Ps = (int64_t*)smem;
+  __shared__ int64_t sbuf[8];
+  const int64_t* row = gu + (int64_t)blockIdx.x * ldgu;
+  const int eps = -2 * FR;
+  int64_t emax = kNegBig;
+  int bad = 0;
+  for (int i = threadIdx.x; i < ff; i += 256) {
+    const int64_t g = row[i], u = row[ff + i];
+    const int64_t ga = g < 0 ? (int64_t)(0 - (uint64_t)g) : g;
+    const int64_t a = imin(ga, 64LL << FR);
+    const int64_t t = rshc(a * kL2E30, FR + 4);              // FR + 30 - FT2
+    const int64_t E = exp2neg30(t, lut);
+    const int64_t den = (1LL << 30) + E;
+    const int64_t sig = g >= 0 ? fdiv((1LL << 61) + den, 2 * den) : fdiv(2 * (E << 30) + den, 2 * den);
+    const int64_t gc = imin(imax(g, -(1LL << 32)), 1LL << 32);
+    const int64_t sv = rshc(mul_wrap(gc, sig), 30);
+    const int64_t ua = u < 0 ? (int64_t)(0 - (uint64_t)u) : u;
+    const int64_t sa = sv < 0 ? -sv : sv;
+    bad |= (bitlen(sa) + bitlen(ua) > 62) | (ga > (1LL << 32));
+    const int64_t P = mul_wrap(sv, u);
+    Ps[i] = P;
+    if (P != 0) emax = imax(emax, bitlen(P < 0 ? (int64_t)(0 - (uint64_t)P) : P) + eps);
+  }
+  if (bad) err[0] = 1;
+  emax = block_max64(emax, sbuf);
+  const int64_t shr = imax(emax - kQB, kNegBig);
+  for (int i = threadIdx.x; i < ff; i += 256) q[(int64_t)blockIdx.x * ldq + i] = (int32_t)rshc(Ps[i], shr - eps);
   if (threadIdx.x == 0) sh[blockIdx.x] = shr;
+}
+
+// ---- intops.first_argmax (src/bitexact/intops.py:55-59): index of the first maximum of each int64 row. A lane
+// keeps its first maximum (columns rise along its loop, only a strictly larger value replaces it); the block
+// then takes the row maximum and the smallest index holding it. Integer max / min: no order dependence. ----
+__global__ __launch_bounds__(1024) void first_argmax_kernel(const int64_t* v, int64_t ldv, int N, int64_t* out) {
+  __shared__ int64_t smax[16], sidx[16];
+  const int64_t* row = v + (int64_t)blockIdx.x * ldv;
+  int64_t best = INT64_MIN, idx = N;
+  for (int i = threadIdx.x; i < N; i += 1024) {
+    const int64_t x = row[i];
+    if (x > best || idx == N) { best = x; idx = i; }
+  }
+  int64_t m = best;
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) m = imax(m, __shfl_xor(m, o, 64));
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  if (lane == 0) smax[wave] = m;
+  __syncthreads();
+  int64_t rm = smax[0];
+  for (int w = 1; w < 16; ++w) rm = imax(rm, smax[w]);
+  int64_t cand = (best == rm) ? idx : N;
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) cand = imin(cand, __shfl_xor(cand, o, 64));
+  if (lane == 0) sidx[wave] = cand;
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    int64_t r = sidx[0];
+    for (int w = 1; w < 16; ++w) r = imin(r, sidx[w]);
+    out[blockIdx.x] = r;
+  }
 }
 
 // ---- segs.softmax (src/bitexact/exact/segs.py:102-105) over ops.softmax_w: key s visible iff s <= qpos ----
@@ -166,19 +277,69 @@ static void allow_lds_rows(const void* k, size_t lds) {
   if (lds > 64 * 1024) hipFuncSetAttribute(k, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
 }
 
+static int launch_norm(NormArgs& p, int src, int32_t M, bx_stream_t stream) {
+  int lg = 0;
+  while ((1 << lg) < p.D) ++lg;
+  BX_REQUIRE(p.D > 0 && (1 << lg) == p.D && lg <= 12, "row length a power of two <= 4096");
+  BX_REQUIRE(M >= 0 && p.ldx >= p.D, "bad sizes");
+  BX_REQUIRE(p.x && p.err, "null pointer");
+  BX_REQUIRE(!p.gm || (p.ge && p.q && p.sh && p.ldq >= p.D), "gamma given without the quantized outputs");
+  if (M == 0) return BX_OK;
+  p.lg = lg;
+  const size_t lds = (size_t)p.D * 16;
+  const void* k = src == SRC_ADD ? (const void*)norm_quant_kernel<SRC_ADD>
+                  : src == SRC_EMB ? (const void*)norm_quant_kernel<SRC_EMB> : (const void*)norm_quant_kernel<SRC_X>;
+  allow_lds_rows(k, lds);
+  hipStream_t st = (hipStream_t)stream;
+  if (src == SRC_ADD) norm_quant_kernel<SRC_ADD><<<M, 256, lds, st>>>(p);
+  else if (src == SRC_EMB) norm_quant_kernel<SRC_EMB><<<M, 256, lds, st>>>(p);
+  else norm_quant_kernel<SRC_X><<<M, 256, lds, st>>>(p);
+  return check_launch("norm_quant_kernel");
+}
+
 extern "C" int bx_rmsnorm_quant(const int64_t* x, int64_t ldx, const int64_t* gm, const int64_t* ge, int32_t* q,
                                 int64_t ldq, int64_t* sh, int32_t M, int32_t D, int32_t FR, int32_t FN, int32_t* err,
                                 bx_stream_t stream) {
-  int lg = 0;
-  while ((1 << lg) < D) ++lg;
-  BX_REQUIRE(D > 0 && (1 << lg) == D && lg <= 12, "row length a power of two <= 4096");
-  BX_REQUIRE(M >= 0 && ldx >= D && ldq >= D, "bad sizes");
-  BX_REQUIRE(x && gm && ge && q && sh && err, "null pointer");
+  BX_REQUIRE(gm && ge && q && sh, "null pointer");
+  NormArgs p = {const_cast<int64_t*>(x), ldx, nullptr, 0, nullptr, nullptr, gm, ge, q, ldq, sh, D, 0, FR, FN, err};
+  return launch_norm(p, SRC_X, M, stream);
+}
+
+extern "C" int bx_add_rmsnorm_quant(int64_t* x, int64_t ldx, const int64_t* y, int64_t ldy, const int64_t* gm,
+                                    const int64_t* ge, int32_t* q, int64_t ldq, int64_t* sh, int32_t M, int32_t D,
+                                    int32_t FR, int32_t FN, int32_t* err, bx_stream_t stream) {
+  BX_REQUIRE(y && ldy >= D, "y: null or ldy too small");
+  NormArgs p = {x, ldx, y, ldy, nullptr, nullptr, gm, ge, q, ldq, sh, D, 0, FR, FN, err};
+  return launch_norm(p, SRC_ADD, M, stream);
+}
+
+extern "C" int bx_embed_rmsnorm_quant(const int32_t* emb, const int64_t* ids, int64_t* x, int64_t ldx,
+                                      const int64_t* gm, const int64_t* ge, int32_t* q, int64_t ldq, int64_t* sh,
+                                      int32_t M, int32_t D, int32_t FR, int32_t FN, int32_t* err, bx_stream_t stream) {
+  BX_REQUIRE(emb && ids, "null pointer");
+  NormArgs p = {x, ldx, nullptr, 0, emb, ids, gm, ge, q, ldq, sh, D, 0, FR, FN, err};
+  return launch_norm(p, SRC_EMB, M, stream);
+}
+
+extern "C" int bx_silu_quant(const int64_t* gu, int64_t ldgu, int32_t ff, const int64_t* lut, int32_t FR, int32_t* q,
+                             int64_t ldq, int64_t* sh, int32_t M, int32_t* err, bx_stream_t stream) {
+  BX_REQUIRE(M >= 0 && ff > 0 && ldgu >= 2 * (int64_t)ff && ldq >= ff, "bad sizes");
+  BX_REQUIRE(ff <= 16384, "ff > 16384 (row kept in LDS)");
+  BX_REQUIRE(FR >= 0 && FR <= 24, "FR outside [0, 24]");
+  BX_REQUIRE(gu && lut && q && sh && err, "null pointer");
   if (M == 0) return BX_OK;
-  const size_t lds = (size_t)D * 8;
-  allow_lds_rows((const void*)norm_quant_kernel, lds);
-  norm_quant_kernel<<<M, 256, lds, (hipStream_t)stream>>>(x, ldx, gm, ge, q, ldq, sh, D, lg, FR, FN, err);
-  return check_launch("norm_quant_kernel");
+  const size_t lds = (size_t)ff * 8;
+  allow_lds_rows((const void*)silu_quant_kernel, lds);
+  silu_quant_kernel<<<M, 256, lds, (hipStream_t)stream>>>(gu, ldgu, ff, lut, FR, q, ldq, sh, err);
+  return check_launch("silu_quant_kernel");
+}
+
+extern "C" int bx_first_argmax(const int64_t* v, int64_t ldv, int32_t M, int32_t N, int64_t* out, bx_stream_t stream) {
+  BX_REQUIRE(M >= 0 && N > 0 && ldv >= N, "bad sizes");
+  BX_REQUIRE(v && out, "null pointer");
+  if (M == 0) return BX_OK;
+  first_argmax_kernel<<<M, 1024, 0, (hipStream_t)stream>>>(v, ldv, N, out);
+  return check_launch("first_argmax_kernel");
 }
 
 extern "C" int bx_softmax_w(const int64_t* raw, int64_t ldr, const int64_t* qpos, const int64_t* sh, int32_t rows,

@@ -134,6 +134,31 @@ int bx_limb_bmm(const void* a, int32_t a_bytes, int64_t saz, int64_t sam, int64_
 int bx_rmsnorm_quant(const int64_t* x, int64_t ldx, const int64_t* gm, const int64_t* ge, int32_t* q, int64_t ldq,
                      int64_t* sh, int32_t M, int32_t D, int32_t FR, int32_t FN, int32_t* err, bx_stream_t stream);
 
+/* Replaces Segs.add_norm_y = segs.add_y + norm_q (src/bitexact/exact/segs.py:40-41, 175-178; exact_fuse.add_norm,
+ * src/bitexact/vllm_plugin/exact_fuse.py:361-364): x += y in place (x, y int64 [M, D] at FR), then with gm non-null
+ * bx_rmsnorm_quant's rule on the new x. gm null: the add and its bound check alone (the engine's last layer). */
+int bx_add_rmsnorm_quant(int64_t* x, int64_t ldx, const int64_t* y, int64_t ldy, const int64_t* gm, const int64_t* ge,
+                         int32_t* q, int64_t ldq, int64_t* sh, int32_t M, int32_t D, int32_t FR, int32_t FN, int32_t* err,
+                         bx_stream_t stream);
+
+/* Replaces the model's `emb[ids].long()` + pre_norm (src/bitexact/exact/model.py:130-132; exact_fuse.embed_norm,
+ * src/bitexact/vllm_plugin/exact_fuse.py:356-358): x[m] = emb[ids[m]] (emb int32 [V, D] at FR, widened to int64),
+ * then bx_rmsnorm_quant's rule (skipped when gm is null). ids are not range-checked. */
+int bx_embed_rmsnorm_quant(const int32_t* emb, const int64_t* ids, int64_t* x, int64_t ldx, const int64_t* gm,
+                           const int64_t* ge, int32_t* q, int64_t ldq, int64_t* sh, int32_t M, int32_t D, int32_t FR,
+                           int32_t FN, int32_t* err, bx_stream_t stream);
+
+/* Replaces Segs.gu_silu_y = segs.silu_y + quant_silu (src/bitexact/exact/segs.py:120-128, 180-182) over
+ * ops.silu_mul (src/bitexact/exact/ops.py:119-130): gu int64 [M, 2 ff] = [gate | up] at FR; q int32 [M, ff],
+ * sh int64 [M] the row quantization of silu(gate) up at eps = -2 FR; err[0] = 1 where silu_mul's ok is false.
+ * lut: the 2^-f table (exp2, 16385 entries at 2^60). ff <= 16384. */
+int bx_silu_quant(const int64_t* gu, int64_t ldgu, int32_t ff, const int64_t* lut, int32_t FR, int32_t* q, int64_t ldq,
+                  int64_t* sh, int32_t M, int32_t* err, bx_stream_t stream);
+
+/* Replaces intops.first_argmax (src/bitexact/intops.py:55-59), the greedy token of tri_logits
+ * (src/bitexact/vllm_plugin/tri_logits.py:1-20): out[m] = the first index of the maximum of row m of v int64 [M, N]. */
+int bx_first_argmax(const int64_t* v, int64_t ldv, int32_t M, int32_t N, int64_t* out, bx_stream_t stream);
+
 /* Replaces segs.softmax (src/bitexact/exact/segs.py:102-105, ops.softmax_w): weights p int32 [rows, S] at fp bits of
  * the scores raw int64 [rows, S] (key s visible iff s <= qpos[row]; hidden keys weigh 0) and den int64 [rows]. */
 int bx_softmax_w(const int64_t* raw, int64_t ldr, const int64_t* qpos, const int64_t* sh, int32_t rows, int32_t S,

@@ -19,8 +19,8 @@ How each function is pinned (tests/test_oracle.py):
   epilogue(checked) flag             the big-integer rule |y| >= 2^62 (reference tests/test_model_bounds.py)
   quant_rows / rdiv32 / bitlen32     closed forms and rdiv equality near ties
   imm / bmm / int8 GEMM              brute-force Python-int matmul
-  exp2neg_lut / softmax_w / rms      golden vectors written from the reference (tests/golden/) plus
-                                     the precision bounds of the reference's own tests
+  exp2neg_lut / softmax_w / rms /    golden vectors written from the reference (tests/golden/) plus
+  silu_mul / gu_silu_y               the precision bounds of the reference's own tests
   paged attention                    softmax_w + exact matmuls (the reference's own test formulation,
                                      tests/test_vllm_exact_attn.py:38-41)
 """
@@ -242,8 +242,9 @@ def norm_quant(x, gm, ge):
 
 def exp2_table():
     """2^-f at 2^60 for f = i / 2^14, i = 0 .. 2^14 (src/bitexact/exact/consts.py:110-115)."""
-    f = np.arange((1 << EXP2_BITS) + 1, dtype=np.float64) / (1 << EXP2_BITS)
-    return np.round(np.power(2.0, -f) * 2.0 ** EXP2_ONE).astype(I64)
+    import torch                                   # the reference's float64 pow (CPU): its rounding, bit for bit
+    f = torch.arange((1 << EXP2_BITS) + 1, dtype=torch.float64) / (1 << EXP2_BITS)
+    return torch.round(torch.pow(2.0, -f) * 2.0 ** EXP2_ONE).long().numpy()
 
 
 def exp2neg_lut(t, lut, out_bits):
@@ -272,6 +273,39 @@ def softmax_w(raw, ok, sh, kbits, lut, fp, l2e=None):
 def attn_div(num, den):
     """o = round(num 2^(FR-FV) / den) (src/bitexact/exact/segs.py:108-113, before the regroup)."""
     return div_round(_a(num), FR - FV, _a(den))
+
+
+def silu_mul(g, u, lut):
+    """silu(g) u for g, u at FR -> (P, eps, ok): P 2^eps the product, ok when every |s| |u| < 2^62 by bit
+    lengths and |g| <= 2^32 (src/bitexact/exact/ops.py:119-130)."""
+    g, u = np.broadcast_arrays(_a(g), _a(u))
+    a = np.minimum(np.abs(g), I64(64 << FR))
+    t = rshc(a * I64(L2E30), FR + 30 - FT2)
+    E = exp2neg_lut(t, lut, 30)                                  # e^-|g| at 2^30
+    den = I64(1 << 30) + E
+    sig = np.where(g >= 0, rdiv(np.full_like(E, 1 << 60), den), rdiv(E << I64(30), den))
+    gc = np.clip(g, -(1 << 32), 1 << 32)
+    s = rshc(gc * sig, 30)
+    ok = bool(((bitlen(np.abs(s)) + bitlen(np.abs(u))) <= 62).all()) and int(np.abs(g).max(initial=0)) <= 1 << 32
+    return s * u, -2 * FR, ok
+
+
+def gu_silu_y(y, lut):
+    """Segs.gu_silu_y = silu_y + quant_silu (src/bitexact/exact/segs.py:120-128, 180-182): y int64 [M, 2 ff]
+    (gate | up) at FR -> (q int32, sh, flag) with flag = not ok."""
+    y = _a(y)
+    ff = y.shape[1] // 2
+    P, eps, ok = silu_mul(y[:, :ff], y[:, ff:], lut)
+    q, sh = quant(P, eps)
+    return q.astype(np.int32), sh, not ok
+
+
+def add_norm_y(y, x, gm, ge):
+    """Segs.add_norm_y = add_y + norm_q (src/bitexact/exact/segs.py:40-41, 175-178): x + y, then norm_quant.
+    Returns (x + y, q, sh, flag)."""
+    x = _a(x) + _a(y).reshape(np.shape(x))
+    q, sh, flag = norm_quant(x, gm, ge)
+    return x, q, sh, flag
 
 
 # ---- src/bitexact/exact/consts.py ----
@@ -515,20 +549,28 @@ def attention_prefill(qg, shg, K, V, qpos, lut, l2e):
 
 # ---- RoPE tables (src/bitexact/llama.py:52-68): llama3 inverse frequencies in closed form ----
 def llama3_inv_freq(hd=64, theta=500000.0, factor=32.0, low=1.0, high=4.0, orig=8192):
-    """transformers' llama3 rope rule (the function src/bitexact/llama.py:57-60 calls), float64."""
-    inv = 1.0 / theta ** (np.arange(0, hd, 2, dtype=np.float64) / hd)
-    low_wl, high_wl = orig / low, orig / high
-    wl = 2 * math.pi / inv
-    out = np.where(wl > low_wl, inv / factor, inv)
-    smooth = (orig / wl - low) / (high - low)
-    mid = (1 - smooth) * out / factor + smooth * out
-    is_mid = (wl >= high_wl) & (wl <= low_wl)
-    return np.where(is_mid, mid, out)
+    """transformers' llama3 rope rule (the function src/bitexact/llama.py:57-62 calls; transformers 5.x
+    modeling_rope_utils._compute_llama3_parameters), restated: float32 throughout, the power correctly rounded
+    (float64 pow of the float32 exponent, rounded to float32, which is what torch's CPU float32 pow returns);
+    returned widened to float64 as the reference's `.double()`."""
+    f = np.float32
+    e = np.arange(0, hd, 2).astype(f) / f(hd)
+    inv = f(1.0) / np.power(np.float64(f(theta)), e.astype(np.float64)).astype(f)
+    wl = f(2 * math.pi) / inv
+    out = np.where(wl > f(orig / low), inv / f(factor), inv)
+    smooth = (f(orig) / wl - f(low)) / (f(high) - f(low))
+    mid = (f(1) - smooth) * out / f(factor) + smooth * out
+    is_mid = ~(wl < f(orig / high)) & ~(wl > f(orig / low))
+    return np.where(is_mid, mid, out).astype(np.float32).astype(np.float64)
 
 
 def rope_tables(n_pos, bits, inv_freq):
-    ang = np.arange(n_pos, dtype=np.float64)[:, None] * inv_freq[None, :]
-    return np.round(np.cos(ang) * 2.0 ** bits).astype(I64), np.round(np.sin(ang) * 2.0 ** bits).astype(I64)
+    """Integer cos / sin at `bits` (src/bitexact/llama.py:65-68), with torch's float64 cos / sin on the CPU as the
+    reference calls them."""
+    import torch
+    ang = torch.arange(n_pos, dtype=torch.float64)[:, None] * torch.from_numpy(np.asarray(inv_freq, np.float64))[None, :]
+    return (torch.round(torch.cos(ang) * 2.0 ** bits).long().numpy(),
+            torch.round(torch.sin(ang) * 2.0 ** bits).long().numpy())
 
 # ---- RoPE + q quantization + regroup (src/bitexact/exact/segs.py:66-99) ----
 FT_ROPE = 30                                    # cos / sin fractional bits (src/bitexact/exact/consts.py:24)
@@ -637,3 +679,69 @@ def paged_attend_int8(q, qpos, c32, bt, expt):
             den[r, h] = dn
     return num, den
 
+
+
+# ---- the exact decode engine (src/bitexact/vllm_plugin/exact_run.py:60-128, src/bitexact/exact/model.py:95-148) ----
+def engine_constants(emb_bits, lin_bits, gammas, cos, sin, L):
+    """Oracle-side model from raw bf16 bits: emb_bits [V, D], lin_bits {(i, name) or "lm": bits [N, K]},
+    gammas {"0.ga": (m, e), ..., "gf": (m, e)}. Every linear is decomposed here (decompose above) and the
+    embedding rounded to 2^-FR (src/bitexact/exact/consts.py:131-135)."""
+    sm, ex = bf16_parts(emb_bits)
+    s = ex + FR
+    e = np.where(s >= 0, _shl(sm, np.maximum(s, 0)),
+                 _sar(sm + _shl(np.ones_like(s), np.clip(-s - 1, 0, 62)), np.clip(-s, 0, 63)))
+    return {"emb": e.astype(np.int32), "dec": {k: decompose(b) for k, b in lin_bits.items()}, "gam": dict(gammas),
+            "cos": _a(cos), "sin": _a(sin), "lut": exp2_table(), "L": L}
+
+
+def engine_forward(m, c32, ids, pos, slot, bt, rmap, dm):
+    """ExactEngine.forward (src/bitexact/vllm_plugin/exact_run.py:60-128): one step over token rows. c32: per layer
+    int32 caches [nb, HKV, bs, 2 HD] (K | V), updated in place. Returns (x [N, D] int64 at FR, err)."""
+    H, HKV, HD = dm
+    G = H // HKV
+    ids, pos, bt, rmap = _a(ids), _a(pos), _a(bt), _a(rmap)
+    slot = np.where(_a(slot) < 0, 0, _a(slot))
+    N = ids.shape[0]
+    qpos = np.repeat(pos[:, None], G, 1)
+    lut, l2e = m["lut"], L2E28_HD[HD]
+    err = False
+    x = m["emb"][ids].astype(I64)
+    q, sh, f = norm_quant(x, *m["gam"]["0.ga"])
+    err |= f
+    for i in range(m["L"]):
+        dec = lambda n: m["dec"][(i, n)]
+        y, _ = exact_linear(q, dec("wqkv"), sh, checked=False)
+        Pq, k, v = rope_y(y, pos[:, None], m["cos"], m["sin"], N, 1, dm)
+        qg, shg, e = q_group(Pq, k, v, y)
+        err |= e
+        c = c32[i]
+        bs = c.shape[2]
+        for n in range(N):
+            c[slot[n] // bs, :, slot[n] % bs, :HD] = k[n, 0]
+            c[slot[n] // bs, :, slot[n] % bs, HD:] = v[n, 0]
+        num, den = paged_attend(qg.reshape(N, HKV, G, HD), shg.reshape(N, HKV, G), qpos, c, bt, rmap, lut, l2e)
+        o = attn_div(num, den).reshape(N, H * HD)             # Segs.attn_out at T = 1: the regroup is a reshape
+        qo, sho = quant(o, -FR)
+        y, f = exact_linear(qo.astype(np.int32), dec("wo"), sho, checked=True)
+        err |= f
+        x, q, sh, f = add_norm_y(y, x, *m["gam"][f"{i}.gm"])
+        err |= f
+        y, _ = exact_linear(q, dec("wgu"), sh, checked=False)
+        q, sh, f = gu_silu_y(y, lut)
+        err |= f
+        y, f = exact_linear(q, dec("wd"), sh, checked=True)
+        err |= f
+        if i + 1 < m["L"]:
+            x, q, sh, f = add_norm_y(y, x, *m["gam"][f"{i + 1}.ga"])
+            err |= f
+        else:
+            x = x + y
+            err |= bool((np.abs(x) >= 1 << 40).any())
+    return x, err
+
+
+def engine_logits(m, h):
+    """ExactEngine.logits (src/bitexact/vllm_plugin/exact_run.py:157-175): final norm + tied lm_head."""
+    q, sh, f = norm_quant(h, *m["gam"]["gf"])
+    y, f2 = exact_linear(q, m["dec"]["lm"], sh, checked=True)
+    return y, f or f2

@@ -1,11 +1,11 @@
 """Writes tests/golden/reference_vectors.npz: input/output vectors of the reference's CPU integer rules that
 closed forms do not pin bit for bit (ops.rms, ops.exp2neg_lut, ops.softmax_w, segs.norm_quant, ops.div_round,
-int8 ops.quant_rows, int8 segs.softmax). Run in the development container only, where the reference checkout is present:
+int8 ops.quant_rows, int8 segs.softmax, ops.silu_mul, segs.silu_y + quant_silu). Run in the development container only, where the reference checkout is present:
 
     python tests/golden/make_golden.py /root/reference
 
 The reference's own functions compute the expected outputs (src/bitexact/exact/ops.py:92-143,
-src/bitexact/exact/segs.py:59-63, src/bitexact/int8/ops.py:24-35); the inputs are seeded here. Only the
+src/bitexact/exact/segs.py:59-63, 120-128, src/bitexact/int8/ops.py:24-35); the inputs are seeded here. Only the
 resulting arrays are committed; nothing from the reference is copied.
 """
 
@@ -94,6 +94,23 @@ def main(ref_root):
         p, den = isegs.softmax(raw, qpos, expt, hd)
         out[f"i8sm{hd}_raw"], out[f"i8sm{hd}_qpos"] = raw.numpy(), qpos.numpy()
         out[f"i8sm{hd}_p"], out[f"i8sm{hd}_den"] = p.numpy(), den.numpy()
+
+    # silu_mul and the gate/up stage (silu_y + quant_silu) over magnitudes up to and beyond the table clamp
+    gate = torch.randint(-(1 << 31), 1 << 31, (6, 512), generator=g)
+    gate[1] >>= 16
+    gate[2] = torch.randint(-(80 << 24), 80 << 24, (512,), generator=g)      # beyond 64 at FR: clamped argument
+    gate[3, :5] = torch.tensor([0, 1, -1, 1 << 32, -(1 << 32)])
+    gate[4] = 0
+    up = torch.randint(-(1 << 30), 1 << 30, (6, 512), generator=g)
+    up[3] >>= 12
+    P, eps, ok = ops.silu_mul(gate, up, lut)
+    out["silu_g"], out["silu_u"], out["silu_P"], out["silu_ok"] = gate.numpy(), up.numpy(), P.numpy(), np.array(bool(ok))
+    bad = gate.clone()
+    bad[0, 0] = (1 << 32) + 1                                                # |g| > 2^32: not ok
+    out["silu_bad_ok"] = np.array(bool(ops.silu_mul(bad, up, lut)[2]))
+    gu = torch.cat([gate, up], 1)
+    q, sh, err = segs.quant_silu(*segs.silu_y(gu, lut), torch.zeros((), dtype=torch.bool))
+    out["gus_q"], out["gus_sh"], out["gus_err"] = q.numpy(), sh.numpy(), np.array(bool(err))
 
     path = os.path.join(os.path.dirname(os.path.abspath(__file__)), "reference_vectors.npz")
     np.savez_compressed(path, **out)

@@ -6,6 +6,8 @@ import glob
 import os
 import re
 
+import numpy as np
+
 ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 LIB = os.path.join(ROOT, "bitexact-llm_amd", "bitexact", "_lib", "libbitexact_hip.so")
 
@@ -36,3 +38,20 @@ def test_product_never_imports_oracle():
     for f in glob.glob(os.path.join(ROOT, "bitexact-llm_amd", "**", "*.py"), recursive=True):
         src = open(f).read()
         assert "oracle" not in re.findall(r"^\s*(?:from|import)\s+(\w+)", src, flags=re.M), f
+
+
+def test_host_tables_match_oracle():
+    """The product's RoPE tables, 2^-f table and embedding rounding are the oracle's (host float64 constants)."""
+    import torch
+    from bitexact.exact import consts
+    from oracle import bxref as R
+    inv = consts.llama3_inv_freq(64)
+    assert np.array_equal(inv.numpy(), R.llama3_inv_freq(64))
+    c, s = consts.rope_tables(4096, 30, inv)
+    rc, rs = R.rope_tables(4096, 30, R.llama3_inv_freq(64))
+    assert np.array_equal(c.numpy(), rc) and np.array_equal(s.numpy(), rs)
+    assert np.array_equal(consts.exp2_table().numpy(), R.exp2_table())
+    w = (torch.randn(64, 300, generator=torch.Generator().manual_seed(1)) * 0.02).to(torch.bfloat16)
+    w[0, :4] = torch.tensor([0.0, -0.0, 1e-30, -3e-8])
+    m = R.engine_constants(w.view(torch.int16).numpy(), {}, {}, c, s, 0)
+    assert np.array_equal(consts.emb_fixed(w).numpy(), m["emb"])

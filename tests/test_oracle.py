@@ -277,9 +277,27 @@ def test_paged_layout_roundtrip():
 
 
 def test_rope_inv_freq_llama3():
+    """Pinned against transformers' own llama3 rule (the reference's dependency) where it imports."""
+    try:
+        import torch
+        from transformers import LlamaConfig
+        from transformers.modeling_rope_utils import ROPE_INIT_FUNCTIONS
+    except ImportError:
+        ROPE_INIT_FUNCTIONS = None
+    if ROPE_INIT_FUNCTIONS is not None:
+        for hd in (64, 128):
+            cfg = LlamaConfig(hidden_size=hd * 32, num_attention_heads=32, num_key_value_heads=8, head_dim=hd,
+                              rope_theta=500000.0, max_position_embeddings=131072,
+                              rope_scaling={"rope_type": "llama3", "factor": 32.0, "low_freq_factor": 1.0,
+                                            "high_freq_factor": 4.0, "original_max_position_embeddings": 8192})
+            try:
+                want = ROPE_INIT_FUNCTIONS["llama3"](cfg, "cpu")[0]
+            except TypeError:
+                want = ROPE_INIT_FUNCTIONS["llama3"](cfg, torch.device("cpu"), None)[0]
+            assert np.array_equal(R.llama3_inv_freq(hd), want.double().numpy())
     inv = R.llama3_inv_freq()
     base = 1.0 / 500000.0 ** (np.arange(0, 64, 2) / 64)
-    assert inv[0] == base[0]                       # high frequency: unscaled
+    assert inv[0] == np.float32(base[0])           # high frequency: unscaled
     assert np.isclose(inv[-1], base[-1] / 32)      # low frequency: divided by the factor
     c, s = R.rope_tables(16, R.FT, inv)
     assert (c[0] == 1 << 30).all() and (s[0] == 0).all()
@@ -335,3 +353,41 @@ def test_norm24_and_int8_post_closed_forms():
         for j in range(50):
             t = rnd(int(acc[i, j]) * int(m[j]), 40)
             assert int(y[i, j]) == rnd(t * int(mant[i]), 24 - R.FR8 - int(e[i]))
+
+
+def test_silu_mul_closed_forms():
+    """silu(g) u: the sigmoid is within a few units of 2^30 / (1 + e^-g), sig(g) + sig(-g) = 2^30 +- 1, and
+    s = silu(g) at FR is within 2^-20 relative (plus 1 unit) of the real value; P = s u exactly."""
+    import math
+    lut = R.exp2_table()
+    rng = np.random.default_rng(7)
+    g = np.concatenate([rng.integers(-(20 << 24), 20 << 24, 4000), np.array([0, 1, -1, 64 << 24, -(64 << 24)])])
+    u = rng.integers(-(1 << 28), 1 << 28, g.shape[0])
+    P, eps, ok = R.silu_mul(g, u, lut)
+    assert ok and eps == -2 * R.FR
+    Pp, _, _ = R.silu_mul(g, np.ones_like(g), lut)
+    Pn, _, _ = R.silu_mul(-g, np.ones_like(g), lut)
+    assert np.array_equal(P, Pp * u)                        # s u exactly
+    # silu(g) - silu(-g) = g exactly in the reals; the integer rule keeps it within 2 units + g 2^-29
+    assert np.all(np.abs(Pp - Pn - g) <= 2 + np.abs(g) // (1 << 29))
+    for gi, si in zip(g[:500].tolist(), Pp[:500].tolist()):
+        x = gi / 2.0 ** 24
+        want = x / (1.0 + math.exp(-x)) * 2.0 ** 24
+        assert abs(si - want) <= 1 + abs(want) * 2.0 ** -20, (gi, si, want)
+    assert Pp[g.shape[0] - 5] == 0                          # silu(0) = 0
+    # a gate beyond 2^32 or a product beyond 2^62 bits is flagged
+    assert not R.silu_mul(np.array([(1 << 32) + 1]), np.array([1]), lut)[2]
+    assert not R.silu_mul(np.array([1 << 32]), np.array([1 << 31]), lut)[2]
+
+
+def test_exp2_table_accuracy():
+    """Every entry of the 2^-f table is within 2 float64 units (256 at 2^59..2^60) of the exact 2^(60 - i / 2^14)
+    (50-digit decimal arithmetic): a wrong index, sign or scale misses by far more. End points are exact."""
+    from decimal import Decimal, getcontext
+    getcontext().prec = 50
+    t = R.exp2_table()
+    assert t.shape == ((1 << 14) + 1,) and t[0] == 1 << 60 and t[-1] == 1 << 59
+    ln2 = Decimal(2).ln()
+    for i in range(0, (1 << 14) + 1, 7):
+        exact = (Decimal(2) ** 60) * (-(Decimal(i) * ln2) / (1 << 14)).exp()
+        assert abs(Decimal(int(t[i])) - exact) <= 256, i

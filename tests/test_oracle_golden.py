@@ -1,6 +1,6 @@
 """The oracle against vectors the reference's own CPU rules produced (tests/golden/make_golden.py):
 ops.rms, segs.norm_quant, ops.exp2neg_lut, ops.softmax_w (head_dim 64 and 128), ops.div_round, int8 quant_rows,
-int8 segs.softmax (head_dim 64 and 128)."""
+int8 segs.softmax (head_dim 64 and 128), ops.silu_mul and the gate/up stage (segs.silu_y + quant_silu)."""
 
 import os
 
@@ -55,3 +55,14 @@ def test_int8_exp_table_and_softmax():
         ok = np.arange(raw.shape[-1]) <= qpos
         p, den = R.int8_softmax(raw, ok, expt, hd)
         assert np.array_equal(p, GOLD[f"i8sm{hd}_p"]) and np.array_equal(den, GOLD[f"i8sm{hd}_den"])
+
+
+def test_silu_mul_and_gate_up_stage():
+    lut = R.exp2_table()
+    P, eps, ok = R.silu_mul(GOLD["silu_g"], GOLD["silu_u"], lut)
+    assert np.array_equal(P, GOLD["silu_P"]) and eps == -2 * R.FR and ok == bool(GOLD["silu_ok"])
+    bad = GOLD["silu_g"].copy()
+    bad[0, 0] = (1 << 32) + 1
+    assert R.silu_mul(bad, GOLD["silu_u"], lut)[2] == bool(GOLD["silu_bad_ok"])
+    q, sh, err = R.gu_silu_y(np.concatenate([GOLD["silu_g"], GOLD["silu_u"]], 1), lut)
+    assert np.array_equal(q, GOLD["gus_q"]) and np.array_equal(sh, GOLD["gus_sh"]) and err == bool(GOLD["gus_err"])
