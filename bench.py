@@ -16,7 +16,11 @@ Config 4 (integer attention, B=4, H=32, HKV=8, HD=64, causal, S=2048) is measure
 (HBM bytes B HKV S 6 HD of limb planes per call, caches rotated over >= 1 GiB) and the fused prefill attention
 (effective limb-op TOPS, 2 x 9 x 2 HD B H T(T+1)/2 per call).
 
-Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-prefill] [--no-attn] [--no-cpu]
+Config 5 (random-init Llama-3.2-1B in exact mode, greedy decode at batch 32, context 1024, paged KV block 16) is
+measured end to end through the decode engine: tokens/s over graph-replayed steps, and the check that a
+sequence's logits hash does not depend on the batch size (1, 8, 32).
+
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-prefill] [--no-attn] [--no-engine] [--no-cpu]
        python bench.py --eager ...        launches without graphs (for counter collection)
        python bench.py --copy-calibrate   only a 1 GiB device copy, 20 times (HBM counter scale)
 """
@@ -260,6 +264,82 @@ def bench_attention(dev, reps=20):
             "prefill_frac_int8_peak": round(ops / s_pre / 1e12 / INT8_PEAK_TOPS, 4)}
 
 
+def bench_engine(dev, steps, warmup, B=32, ctx=1024, bs=16):
+    """Config 5: a random-init Llama-3.2-1B (16 layers, bf16 N(0,0.02) weights decomposed on the device) in exact
+    mode. Prefill B sequences of ctx seeded random token ids into the paged block-16 KV cache, then time greedy
+    decode steps at batch B (forward + logits + first-max + next-step inputs, one HIP graph per step replayed
+    `steps` times). Also checks that sequence 0's first decode logits hash is the same at batch 1, 8 and B."""
+    import torch
+    from bitexact.exact.consts import random_constants
+    from bitexact.generate import logits_sha
+    from bitexact.vllm_plugin.exact_run import ExactEngine
+    t0 = time.time()
+    eng = ExactEngine(random_constants(None, seed=0, device=dev), dev)
+    torch.cuda.synchronize()
+    t_build = time.time() - t0
+    nblk = -(-(ctx + warmup + steps + 2) // bs)
+    bt = (1 + torch.arange(B * nblk, device=dev, dtype=torch.int32)).view(B, nblk)
+    kvs = eng.new_cache(1 + B * nblk, bs)
+    g = torch.Generator().manual_seed(5)
+    prompts = torch.randint(0, eng.V, (B, ctx), generator=g).to(dev)
+    # prefill in chunks of whole sequences
+    t0 = time.time()
+    first = torch.empty(B, dtype=torch.long, device=dev)
+    chunk = max(1, 4096 // ctx)
+    for s0 in range(0, B, chunk):
+        seqs = torch.arange(s0, min(B, s0 + chunk), device=dev)
+        n = seqs.numel()
+        pos = torch.arange(ctx, device=dev).repeat(n)
+        rmap = seqs.repeat_interleave(ctx)
+        slot = bt[rmap, pos // bs].long() * bs + pos % bs
+        x = eng.forward(kvs, prompts[s0:s0 + n].reshape(-1), pos, slot, bt, rmap)
+        first[s0:s0 + n] = eng.greedy(eng.logits(x.view(n, ctx, -1)[:, -1].contiguous()))
+    torch.cuda.synchronize()
+    t_prefill = time.time() - t0
+    # batch invariance: sequence 0's first decode step at batch 1, 8 and B (row-local rules: same bits)
+    shas = {}
+    for b in (1, 8, B):
+        pos = torch.full((b,), ctx, device=dev, dtype=torch.long)
+        rmap = torch.arange(b, device=dev)
+        slot = bt[rmap, pos // bs].long() * bs + pos % bs
+        x = eng.forward(kvs, first[:b], pos, slot, bt, rmap)
+        shas[b] = logits_sha(eng.logits(x)[0])
+    # timed decode: static inputs updated on the device by each step
+    ids = first.clone()
+    pos = torch.full((B,), ctx, device=dev, dtype=torch.long)
+    rmap = torch.arange(B, device=dev)
+    slot = bt[rmap, pos // bs].long() * bs + pos % bs
+
+    def step(i):
+        x = eng.forward(kvs, ids, pos, slot, bt, rmap)
+        ids.copy_(eng.greedy(eng.logits(x)))
+        pos.add_(1)
+        slot.copy_(bt[rmap, pos // bs].long() * bs + pos % bs)
+
+    stream = torch.cuda.Stream(dev)
+    with torch.cuda.stream(stream):
+        step(0)                                          # allocations and workspaces before capture
+    torch.cuda.synchronize()
+    pos.fill_(ctx)
+    slot.copy_(bt[rmap, pos // bs].long() * bs + pos % bs)
+    ids.copy_(first)
+    sec = time_graph(step, warmup, steps, stream)
+    overflow = bool(eng.err)
+    tok_s = B * steps / sec
+    return {"workload": "config 5: random-init Llama-3.2-1B exact mode (16 layers, D 2048, FF 8192, V 128256, "
+                        "bf16 N(0,0.02) weights), greedy decode at batch %d, context %d, paged KV block %d" % (B, ctx, bs),
+            "tokens_per_s": round(tok_s, 1), "ms_per_step": round(sec / steps * 1e3, 4), "batch": B, "context": ctx,
+            "steps": steps, "warmup": warmup, "weight_bytes_per_step": eng_weight_bytes(eng),
+            "weight_GBps": round(eng_weight_bytes(eng) * steps / sec / 1e9, 1),
+            "logits_sha_batch_1_8_%d_equal" % B: len(set(shas.values())) == 1, "logits_sha_seq0": shas[1][:16],
+            "overflow_flag": overflow, "build_s": round(t_build, 1), "prefill_s": round(t_prefill, 2)}
+
+
+def eng_weight_bytes(eng):
+    """Limb-plane bytes one decode step streams: every linear's 3 int8 planes."""
+    return sum(int(f.limbs.numel()) for f in eng.fused.values())
+
+
 def copy_calibrate(dev):
     """A plain 1 GiB device copy, 20 times: the HBM counters read for it scale the bench's counters."""
     import torch
@@ -307,6 +387,8 @@ def main():
     ap.add_argument("--no-prefill", action="store_true")
     ap.add_argument("--no-attn", action="store_true")
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--no-engine", action="store_true")
+    ap.add_argument("--engine-steps", type=int, default=20)
     ap.add_argument("--eager", action="store_true")
     ap.add_argument("--copy-calibrate", action="store_true")
     args = ap.parse_args()
@@ -361,6 +443,9 @@ def main():
     if not args.no_attn:
         log("attention ...")
         out["exact_attention"] = bench_attention(dev)
+    if not args.no_engine:
+        log("exact decode engine (config 5) ...")
+        out["exact_engine"] = bench_engine(dev, args.engine_steps, 3)
     if not args.no_cpu:
         log("cpu baseline ...")
         out["cpu_baseline"] = cpu_baseline()

@@ -1,5 +1,9 @@
 """Exact-mode row stages on HIP (src/bitexact/exact/segs.py, src/bitexact/exact/ops.py).
 
+Stages with a bound check return err (a bool tensor, or'ed into the caller's `err`); with flag= (an int32 [1]
+device tensor) they set that flag instead and pass err through, so a caller chaining many stages keeps one flag
+and launches no extra kernels.
+
 norm_quant(x, gm, ge, err)      segs.norm_quant: RMSNorm + quantization at -FN -> (q int32, sh, err)
 softmax(raw, qpos, shg, lut, l2e) segs.softmax: masked weights at FP -> (p int32, den)
 attn_out(num, den, T, hkv)      Segs.attn_out: div_round + regroup + quantization at -FR -> (q int32, sh)
@@ -22,18 +26,34 @@ L2E28 = 387270501
 L2E28_HD = {64: L2E28, 128: 273841598}
 
 
-def norm_quant(x, gm, ge, err=None):
+def _flag(dev, flag):
+    """The stage's bound flag: the caller's int32 [1] device tensor (set to 1 by the kernel, never cleared), or a
+    fresh zero one."""
+    if flag is not None:
+        assert flag.dtype == torch.int32 and flag.is_cuda
+        return flag
+    return torch.zeros(1, dtype=torch.int32, device=dev)
+
+
+def _or(err, flag, given):
+    """err | flag as a bool tensor; with a caller's flag the flag itself carries it and err passes through."""
+    if given is not None:
+        return err
+    e = flag[0].bool()
+    return e if err is None else (err | e)
+
+
+def norm_quant(x, gm, ge, err=None, flag=None):
     _hip.require_cuda(x, gm, ge)
     assert x.dtype == torch.int64 and x.stride(-1) == 1
     M, D = x.shape
     q = torch.empty(M, D, dtype=torch.int32, device=x.device)
     sh = torch.empty(M, dtype=torch.long, device=x.device)
-    flag = torch.zeros(1, dtype=torch.int32, device=x.device)
+    fl = _flag(x.device, flag)
     gm, ge = gm.contiguous().long(), ge.contiguous().long()     # kept alive until the launch is queued
     _hip.call("bx_rmsnorm_quant", _hip.ptr(x), x.stride(0), _hip.ptr(gm), _hip.ptr(ge), _hip.ptr(q), D, _hip.ptr(sh),
-              M, D, FR, FN, _hip.ptr(flag), _hip.stream_of(x))
-    e = flag[0].bool()
-    return q, sh, e if err is None else (err | e)
+              M, D, FR, FN, _hip.ptr(fl), _hip.stream_of(x))
+    return q, sh, _or(err, fl, flag)
 
 
 def softmax(raw, qpos, shg, lut, l2e, kbits=FK, fp=FP):
@@ -71,7 +91,7 @@ def attn_out(num, den, T, hkv):
     return q, sh
 
 
-def qkv_y(y, pos, cos, sin, B, T, dm, err=None):
+def qkv_y(y, pos, cos, sin, B, T, dm, err=None, flag=None):
     """Segs.qkv_y (src/bitexact/exact/segs.py:170-173): y int64 [B T, (H + 2 HKV) HD] at FR, pos int64 [B, T],
     cos / sin int64 [n_pos, HD / 2] at FT, dm = (H, HKV, HD) -> qg int32 [B HKV, g T, HD], shg int64
     [B HKV, g T, 1], k / v int64 [B, T, HKV, HD], err (bool tensor, or'ed into `err`)."""
@@ -88,44 +108,36 @@ def qkv_y(y, pos, cos, sin, B, T, dm, err=None):
     shg = torch.empty(B * HKV, g * T, 1, dtype=torch.long, device=dev)
     k = torch.empty(B, T, HKV, HD, dtype=torch.long, device=dev)
     v = torch.empty(B, T, HKV, HD, dtype=torch.long, device=dev)
-    flag = torch.zeros(1, dtype=torch.int32, device=dev)
+    fl = _flag(dev, flag)
     _hip.call("bx_rope_qgroup", _hip.ptr(y), y.stride(0), _hip.ptr(pos), pos.stride(0), pos.stride(1),
               _hip.ptr(cos), _hip.ptr(sin), cos.shape[0], B, T, H, HKV, HD, FR, FT, FK, FV, FZ, _hip.ptr(qg),
-              _hip.ptr(shg), _hip.ptr(k), _hip.ptr(v), _hip.ptr(flag), _hip.stream_of(y))
-    e = flag[0].bool()
-    return qg, shg, k, v, e if err is None else (err | e)
+              _hip.ptr(shg), _hip.ptr(k), _hip.ptr(v), _hip.ptr(fl), _hip.stream_of(y))
+    return qg, shg, k, v, _or(err, fl, flag)
 
 
-def _flag(dev):
-    return torch.zeros(1, dtype=torch.int32, device=dev)
 
 
-def _or(err, flag):
-    e = flag[0].bool()
-    return e if err is None else (err | e)
-
-
-def add_norm_y(y, x, gm, ge, err=None):
+def add_norm_y(y, x, gm, ge, err=None, flag=None):
     """Segs.add_norm_y (src/bitexact/exact/segs.py:175-178): x int64 [M, D] += y (in place, as exact_fuse.add_norm's
     store), then norm_quant of the sum. gm None: the add alone (returns q = sh = None)."""
     _hip.require_cuda(x, y)
     assert x.dtype == torch.int64 and y.dtype == torch.int64 and x.stride(-1) == 1 and y.stride(-1) == 1
     M, D = x.shape
     y = y.view(M, D) if y.dim() != 2 else y
-    flag = _flag(x.device)
+    fl = _flag(x.device, flag)
     if gm is None:
         _hip.call("bx_add_rmsnorm_quant", _hip.ptr(x), x.stride(0), _hip.ptr(y), y.stride(0), None, None, None, D, None,
-                  M, D, FR, FN, _hip.ptr(flag), _hip.stream_of(x))
-        return x, None, None, _or(err, flag)
+                  M, D, FR, FN, _hip.ptr(fl), _hip.stream_of(x))
+        return x, None, None, _or(err, fl, flag)
     q = torch.empty(M, D, dtype=torch.int32, device=x.device)
     sh = torch.empty(M, dtype=torch.long, device=x.device)
     gm, ge = gm.contiguous().long(), ge.contiguous().long()
     _hip.call("bx_add_rmsnorm_quant", _hip.ptr(x), x.stride(0), _hip.ptr(y), y.stride(0), _hip.ptr(gm), _hip.ptr(ge),
-              _hip.ptr(q), D, _hip.ptr(sh), M, D, FR, FN, _hip.ptr(flag), _hip.stream_of(x))
-    return x, q, sh, _or(err, flag)
+              _hip.ptr(q), D, _hip.ptr(sh), M, D, FR, FN, _hip.ptr(fl), _hip.stream_of(x))
+    return x, q, sh, _or(err, fl, flag)
 
 
-def embed_norm(emb, ids, gm, ge, err=None):
+def embed_norm(emb, ids, gm, ge, err=None, flag=None):
     """x = emb[ids].long() (emb int32 [V, D]) and its pre_norm (src/bitexact/exact/model.py:130-132) -> (x, q, sh, err)."""
     _hip.require_cuda(emb, ids, gm, ge)
     assert emb.dtype == torch.int32 and emb.is_contiguous()
@@ -134,14 +146,14 @@ def embed_norm(emb, ids, gm, ge, err=None):
     x = torch.empty(M, D, dtype=torch.long, device=emb.device)
     q = torch.empty(M, D, dtype=torch.int32, device=emb.device)
     sh = torch.empty(M, dtype=torch.long, device=emb.device)
-    flag = _flag(emb.device)
+    fl = _flag(emb.device, flag)
     gm, ge = gm.contiguous().long(), ge.contiguous().long()
     _hip.call("bx_embed_rmsnorm_quant", _hip.ptr(emb), _hip.ptr(ids), _hip.ptr(x), D, _hip.ptr(gm), _hip.ptr(ge),
-              _hip.ptr(q), D, _hip.ptr(sh), M, D, FR, FN, _hip.ptr(flag), _hip.stream_of(emb))
-    return x, q, sh, _or(err, flag)
+              _hip.ptr(q), D, _hip.ptr(sh), M, D, FR, FN, _hip.ptr(fl), _hip.stream_of(emb))
+    return x, q, sh, _or(err, fl, flag)
 
 
-def gu_silu_y(y, lut, err=None):
+def gu_silu_y(y, lut, err=None, flag=None):
     """Segs.gu_silu_y (src/bitexact/exact/segs.py:180-182): y int64 [M, 2 ff] (gate | up) at FR ->
     (q int32 [M, ff], sh int64 [M], err | not ok)."""
     _hip.require_cuda(y, lut)
@@ -149,8 +161,8 @@ def gu_silu_y(y, lut, err=None):
     M, ff = y.shape[0], y.shape[1] // 2
     q = torch.empty(M, ff, dtype=torch.int32, device=y.device)
     sh = torch.empty(M, dtype=torch.long, device=y.device)
-    flag = _flag(y.device)
+    fl = _flag(y.device, flag)
     lut = lut.contiguous().long()
     _hip.call("bx_silu_quant", _hip.ptr(y), y.stride(0), ff, _hip.ptr(lut), FR, _hip.ptr(q), ff, _hip.ptr(sh), M,
-              _hip.ptr(flag), _hip.stream_of(y))
-    return q, sh, _or(err, flag)
+              _hip.ptr(fl), _hip.stream_of(y))
+    return q, sh, _or(err, fl, flag)

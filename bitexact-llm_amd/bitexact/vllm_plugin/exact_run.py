@@ -44,8 +44,13 @@ class ExactEngine:
         self.gm = [gam(f"{i}.gm") for i in range(self.L)]
         self.gf = gam("gf")
         self.cos, self.sin, self.exp2 = t("cos").long(), t("sin").long(), t("exp2").long()
-        self.fl = torch.zeros(1, dtype=torch.int32, device=dev)  # flags of the checked linears
-        self.err = torch.zeros((), dtype=torch.bool, device=dev)
+        # one sticky int32 flag for every bound check of every stage (the reference's fl and err together)
+        self.fl = torch.zeros(1, dtype=torch.int32, device=dev)
+
+    @property
+    def err(self):
+        """The bound flag as a bool tensor (no host sync)."""
+        return self.fl[0] != 0
 
     def new_cache(self, nblocks, bs=16):
         """One limb-plane cache per layer: int8 [nblocks, HKV, bs, 8 HD] (block 0 is the null block)."""
@@ -60,28 +65,25 @@ class ExactEngine:
         pos = pos.long().contiguous()
         slot = torch.where(slot < 0, torch.zeros_like(slot), slot).long()
         qpos = pos.view(-1, 1).expand(-1, G).contiguous()
-        err = self.err
-        x, q, sh, err = ops.embed_norm(self.emb, ids, *self.ga[0], err)
+        fl = self.fl
+        x, q, sh, _ = ops.embed_norm(self.emb, ids, *self.ga[0], flag=fl)
         for i in range(self.L):
-            y = self.fused[i, "wqkv"](q, sh, self.fl, False)
-            qg, shg, k, v, err = ops.qkv_y(y, pos.view(N, 1), self.cos, self.sin, N, 1, (self.H, HKV, HD), err)
+            y = self.fused[i, "wqkv"](q, sh, fl, False)
+            qg, shg, k, v, _ = ops.qkv_y(y, pos.view(N, 1), self.cos, self.sin, N, 1, (self.H, HKV, HD), flag=fl)
             tri_paged.store(kvs[i], slot, k[:, 0], v[:, 0])
             num, den = tri_exact_attn.attend(qg.view(N, HKV, G, HD), shg.view(N, HKV, G), qpos, kvs[i], bt, rmap,
                                              self.exp2, self.l2e)
             qo, sho = ops.attn_out(num.view(N * HKV, G, HD), den.view(N * HKV, G, 1), 1, HKV)
-            x, q, sh, err = ops.add_norm_y(self.fused[i, "wo"](qo, sho, self.fl, True), x, *self.gm[i], err)
-            q, sh, err = ops.gu_silu_y(self.fused[i, "wgu"](q, sh, self.fl, False), self.exp2, err)
+            x, q, sh, _ = ops.add_norm_y(self.fused[i, "wo"](qo, sho, fl, True), x, *self.gm[i], flag=fl)
+            q, sh, _ = ops.gu_silu_y(self.fused[i, "wgu"](q, sh, fl, False), self.exp2, flag=fl)
             nxt = self.ga[i + 1] if i + 1 < self.L else (None, None)
-            x, q, sh, err = ops.add_norm_y(self.fused[i, "wd"](q, sh, self.fl, True), x, *nxt, err)
-        self.err = err | (self.fl != 0)
+            x, q, sh, _ = ops.add_norm_y(self.fused[i, "wd"](q, sh, fl, True), x, *nxt, flag=fl)
         return x
 
     def logits(self, h):
         """Final residual rows [M, D] -> logits int64 [M, V] at FR (exact_run.py:157-175)."""
-        q, sh, err = ops.norm_quant(h, *self.gf, self.err)
-        y = self.fused["lm"](q, sh, self.fl, True)
-        self.err = err | (self.fl != 0)
-        return y
+        q, sh, _ = ops.norm_quant(h, *self.gf, flag=self.fl)
+        return self.fused["lm"](q, sh, self.fl, True)
 
     def greedy(self, logits):
         """The greedy token of each logits row: its first maximum."""

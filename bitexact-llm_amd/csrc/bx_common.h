@@ -64,6 +64,19 @@ __device__ __forceinline__ int64_t fdiv(int64_t a, int64_t b) {
   return (a - q * b < 0) ? q - 1 : q;
 }
 
+// floor(a / b) for b > 0 from a float64 estimate and exact integer corrections (the same value as fdiv). The
+// estimate is used when |a / b| <= 2^52: its error is then at most a few units, so a - q b cannot overflow for
+// |a| < 2^62 and b < 2^60, and the loops bring q to the floor quotient. Larger quotients take fdiv.
+__device__ __forceinline__ int64_t fdiv_fast(int64_t a, int64_t b) {
+  const double qd = (double)a / (double)b;
+  if (!(qd < 4503599627370496.0 && qd > -4503599627370496.0)) return fdiv(a, b);
+  int64_t q = (int64_t)qd;
+  int64_t r = a - q * b;
+  while (r < 0) { --q; r += b; }
+  while (r >= b) { ++q; r -= b; }
+  return q;
+}
+
 // Signed base-256 digit and remainder (intops.split_limbs, src/bitexact/intops.py:62-70).
 __device__ __forceinline__ int32_t limb_lo(int32_t r) { return ((r + 128) & 255) - 128; }
 __device__ __forceinline__ int64_t limb_lo64(int64_t r) { return ((r + 128) & 255) - 128; }

@@ -1,4 +1,5 @@
-// Row-wise integer stages around the GEMMs and the attention, one 256-thread block per row with wavefront
+// Row-wise integer stages around the GEMMs and the attention, one block per row (1024 threads: a decode step has
+// few rows, so each row spreads over a whole CU; softmax rows use 256) with wavefront
 // int64 reductions: RMSNorm + per-row quantization (segs.norm_quant, optionally after the residual add or the
 // embedding gather), SiLU gating + quantization (segs.silu_y + quant_silu), the masked softmax weights
 // (segs.softmax), and the attention output rule (segs.attn_out = div_round + regroup + quant).
@@ -9,6 +10,8 @@ namespace bx {
 constexpr int64_t kEps60 = 11529215046068LL;   // round(1e-5 2^60) (src/bitexact/exact/ops.py:21)
 constexpr int64_t kNegBig = -(1LL << 20);      // ops.NEG_BIG
 constexpr int kQB = 22;                        // |q| <= 2^22
+
+constexpr int kRowThreads = 1024;
 
 __device__ __forceinline__ int64_t block_max64(int64_t v, int64_t* sbuf) {
   v = wave_max64(v);
@@ -42,14 +45,14 @@ __device__ __forceinline__ int64_t isqrt64(int64_t x) {
 
 // ops.div_round (src/bitexact/exact/ops.py:37-57): round(a 2^p / r) by 28-bit long division, r > 0
 __device__ __forceinline__ int64_t div_round64(int64_t a, int64_t p, int64_t r) {
-  int64_t Q = fdiv(a, r);
+  int64_t Q = fdiv_fast(a, r);
   int64_t R = a - Q * r;
   int64_t left = imax(p, 0);
 #pragma unroll
   for (int it = 0; it < 3; ++it) {
     const int64_t c = imin(left, 28);
     const int64_t X = shl(R, c);
-    const int64_t q1 = fdiv(X, r);
+    const int64_t q1 = fdiv_fast(X, r);
     Q = add_wrap(shl(Q, c), q1);
     R = X - q1 * r;
     left -= c;
@@ -86,17 +89,17 @@ struct NormArgs {
 };
 
 template <int SRC>
-__global__ __launch_bounds__(256) void norm_quant_kernel(NormArgs p) {
+__global__ __launch_bounds__(kRowThreads) void norm_quant_kernel(NormArgs p) {
   extern __shared__ __align__(16) char smem[];
   int64_t* Xs = (int64_t*)smem;
   int64_t* Ps = Xs + p.D;
-  __shared__ int64_t sbuf[8];
+  __shared__ int64_t sbuf[16];
   const int D = p.D;
   int64_t* xr = p.x + (int64_t)blockIdx.x * p.ldx;
   const int32_t* er_row = nullptr;
   if (SRC == SRC_EMB) er_row = p.emb + p.ids[blockIdx.x] * (int64_t)D;
   int64_t amax = 0;
-  for (int i = threadIdx.x; i < D; i += 256) {
+  for (int i = threadIdx.x; i < D; i += kRowThreads) {
     int64_t v;
     if (SRC == SRC_EMB) v = er_row[i];
     else if (SRC == SRC_ADD) v = add_wrap(xr[i], p.y[(int64_t)blockIdx.x * p.ldy + i]);
@@ -110,7 +113,7 @@ __global__ __launch_bounds__(256) void norm_quant_kernel(NormArgs p) {
   if (p.gm == nullptr) return;
   const int64_t shx = imax(bitlen(imax(amax, 1)) - 25, -6);
   int64_t S = 0;
-  for (int i = threadIdx.x; i < D; i += 256) {
+  for (int i = threadIdx.x; i < D; i += kRowThreads) {
     const int64_t xs = rshc(Xs[i], shx);
     S = add_wrap(S, mul_wrap(xs, xs));
   }
@@ -121,14 +124,14 @@ __global__ __launch_bounds__(256) void norm_quant_kernel(NormArgs p) {
   const int64_t V = s >= 0 ? shl(T, s) : sar(T, -s);
   const int64_t r = isqrt64(V), er = shx - p.FR - m;
   int64_t emax = kNegBig;
-  for (int i = threadIdx.x; i < D; i += 256) {
+  for (int i = threadIdx.x; i < D; i += kRowThreads) {
     const int64_t P = div_round64(mul_wrap(Xs[i], p.gm[i]), p.ge[i] - p.FR - er + p.FN, r);
     Ps[i] = P;
     if (P != 0) emax = imax(emax, bitlen(P < 0 ? -P : P) - p.FN);
   }
   emax = block_max64(emax, sbuf);
   const int64_t shr = imax(emax - kQB, kNegBig);
-  for (int i = threadIdx.x; i < D; i += 256) p.q[(int64_t)blockIdx.x * p.ldq + i] = (int32_t)rshc(Ps[i], shr + p.FN);
+  for (int i = threadIdx.x; i < D; i += kRowThreads) p.q[(int64_t)blockIdx.x * p.ldq + i] = (int32_t)rshc(Ps[i], shr + p.FN);
   if (threadIdx.x == 0) p.sh[blockIdx.x] = shr;
 }
 
@@ -146,23 +149,23 @@ __device__ __forceinline__ int64_t exp2neg30(int64_t t, const int64_t* lut) {   
   return rshc(v, 30 + n);
 }
 
-__global__ __launch_bounds__(256) void silu_quant_kernel(const int64_t* gu, int64_t ldgu, int ff, const int64_t* lut,
+__global__ __launch_bounds__(kRowThreads) void silu_quant_kernel(const int64_t* gu, int64_t ldgu, int ff, const int64_t* lut,
                                                          int FR, int32_t* q, int64_t ldq, int64_t* sh, int32_t* err) {
   extern __shared__ __align__(16) char smem[];
   int64_t* Ps = (int64_t*)smem;
-  __shared__ int64_t sbuf[8];
+  __shared__ int64_t sbuf[16];
   const int64_t* row = gu + (int64_t)blockIdx.x * ldgu;
   const int eps = -2 * FR;
   int64_t emax = kNegBig;
   int bad = 0;
-  for (int i = threadIdx.x; i < ff; i += 256) {
+  for (int i = threadIdx.x; i < ff; i += kRowThreads) {
     const int64_t g = row[i], u = row[ff + i];
     const int64_t ga = g < 0 ? (int64_t)(0 - (uint64_t)g) : g;
     const int64_t a = imin(ga, 64LL << FR);
     const int64_t t = rshc(a * kL2E30, FR + 4);              // FR + 30 - FT2
     const int64_t E = exp2neg30(t, lut);
     const int64_t den = (1LL << 30) + E;
-    const int64_t sig = g >= 0 ? fdiv((1LL << 61) + den, 2 * den) : fdiv(2 * (E << 30) + den, 2 * den);
+    const int64_t sig = g >= 0 ? fdiv_fast((1LL << 61) + den, 2 * den) : fdiv_fast(2 * (E << 30) + den, 2 * den);
     const int64_t gc = imin(imax(g, -(1LL << 32)), 1LL << 32);
     const int64_t sv = rshc(mul_wrap(gc, sig), 30);
     const int64_t ua = u < 0 ? (int64_t)(0 - (uint64_t)u) : u;
@@ -175,7 +178,7 @@ __global__ __launch_bounds__(256) void silu_quant_kernel(const int64_t* gu, int6
   if (bad) err[0] = 1;
   emax = block_max64(emax, sbuf);
   const int64_t shr = imax(emax - kQB, kNegBig);
-  for (int i = threadIdx.x; i < ff; i += 256) q[(int64_t)blockIdx.x * ldq + i] = (int32_t)rshc(Ps[i], shr - eps);
+  for (int i = threadIdx.x; i < ff; i += kRowThreads) q[(int64_t)blockIdx.x * ldq + i] = (int32_t)rshc(Ps[i], shr - eps);
   if (threadIdx.x == 0) sh[blockIdx.x] = shr;
 }
 
@@ -224,7 +227,7 @@ __device__ __forceinline__ int64_t weight64(int64_t z, int64_t zshift, const int
 __global__ __launch_bounds__(256) void softmax_kernel(const int64_t* raw, int64_t ldr, const int64_t* qpos,
                                                       const int64_t* sh, int S, int kbits, const int64_t* lut,
                                                       int64_t l2e, int fp, int32_t* p, int64_t ldp, int64_t* den) {
-  __shared__ int64_t sbuf[8];
+  __shared__ int64_t sbuf[16];
   const int64_t row = blockIdx.x;
   const int64_t* rr = raw + row * ldr;
   const int64_t qp = qpos[row];
@@ -246,16 +249,16 @@ __global__ __launch_bounds__(256) void softmax_kernel(const int64_t* raw, int64_
 // ---- segs.attn_out (src/bitexact/exact/segs.py:108-113, 187-188): o = div_round(num, FR - FV, den), regrouped to
 // one row of H HD values per token, then quantized per row with eps = -FR. Output row o, head hh:
 // group = (o / T) HKV + hh / g, query = (hh % g) T + o % T, with g = H / HKV. ----
-__global__ __launch_bounds__(256) void attn_out_kernel(const int64_t* num, int64_t sn_group, int64_t sn_query,
+__global__ __launch_bounds__(kRowThreads) void attn_out_kernel(const int64_t* num, int64_t sn_group, int64_t sn_query,
                                                        const int64_t* den, int64_t sd_group, int T, int HKV, int g,
                                                        int HD, int FR, int FV, int32_t* q, int64_t ldq, int64_t* sh) {
   extern __shared__ __align__(16) char smem[];
   int64_t* Os = (int64_t*)smem;
-  __shared__ int64_t sbuf[8];
+  __shared__ int64_t sbuf[16];
   const int o = blockIdx.x;
   const int W = HKV * g * HD;
   int64_t emax = kNegBig;
-  for (int c = threadIdx.x; c < W; c += 256) {
+  for (int c = threadIdx.x; c < W; c += kRowThreads) {
     const int hh = c / HD, d = c % HD;
     const int64_t group = (int64_t)(o / T) * HKV + hh / g, query = (int64_t)(hh % g) * T + o % T;
     const int64_t dn = den[group * sd_group + query];   // >= 1 whenever the query sees a key (itself)
@@ -265,7 +268,7 @@ __global__ __launch_bounds__(256) void attn_out_kernel(const int64_t* num, int64
   }
   emax = block_max64(emax, sbuf);
   const int64_t shr = imax(emax - kQB, kNegBig);
-  for (int c = threadIdx.x; c < W; c += 256) q[(int64_t)o * ldq + c] = (int32_t)rshc(Os[c], shr + FR);
+  for (int c = threadIdx.x; c < W; c += kRowThreads) q[(int64_t)o * ldq + c] = (int32_t)rshc(Os[c], shr + FR);
   if (threadIdx.x == 0) sh[o] = shr;
 }
 
@@ -291,9 +294,9 @@ static int launch_norm(NormArgs& p, int src, int32_t M, bx_stream_t stream) {
                   : src == SRC_EMB ? (const void*)norm_quant_kernel<SRC_EMB> : (const void*)norm_quant_kernel<SRC_X>;
   allow_lds_rows(k, lds);
   hipStream_t st = (hipStream_t)stream;
-  if (src == SRC_ADD) norm_quant_kernel<SRC_ADD><<<M, 256, lds, st>>>(p);
-  else if (src == SRC_EMB) norm_quant_kernel<SRC_EMB><<<M, 256, lds, st>>>(p);
-  else norm_quant_kernel<SRC_X><<<M, 256, lds, st>>>(p);
+  if (src == SRC_ADD) norm_quant_kernel<SRC_ADD><<<M, kRowThreads, lds, st>>>(p);
+  else if (src == SRC_EMB) norm_quant_kernel<SRC_EMB><<<M, kRowThreads, lds, st>>>(p);
+  else norm_quant_kernel<SRC_X><<<M, kRowThreads, lds, st>>>(p);
   return check_launch("norm_quant_kernel");
 }
 
@@ -330,7 +333,7 @@ extern "C" int bx_silu_quant(const int64_t* gu, int64_t ldgu, int32_t ff, const 
   if (M == 0) return BX_OK;
   const size_t lds = (size_t)ff * 8;
   allow_lds_rows((const void*)silu_quant_kernel, lds);
-  silu_quant_kernel<<<M, 256, lds, (hipStream_t)stream>>>(gu, ldgu, ff, lut, FR, q, ldq, sh, err);
+  silu_quant_kernel<<<M, kRowThreads, lds, (hipStream_t)stream>>>(gu, ldgu, ff, lut, FR, q, ldq, sh, err);
   return check_launch("silu_quant_kernel");
 }
 
@@ -361,7 +364,7 @@ extern "C" int bx_attn_out(const int64_t* num, int64_t sn_group, int64_t sn_quer
   if (rows == 0) return BX_OK;
   const size_t lds = (size_t)HKV * g * HD * 8;
   allow_lds_rows((const void*)attn_out_kernel, lds);
-  attn_out_kernel<<<rows, 256, lds, (hipStream_t)stream>>>(num, sn_group, sn_query, den, sd_group, T, HKV, g, HD, FR,
+  attn_out_kernel<<<rows, kRowThreads, lds, (hipStream_t)stream>>>(num, sn_group, sn_query, den, sd_group, T, HKV, g, HD, FR,
                                                           FV, q, ldq, sh);
   return check_launch("attn_out_kernel");
 }
