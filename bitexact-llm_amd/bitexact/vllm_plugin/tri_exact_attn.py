@@ -11,14 +11,17 @@ import torch
 from bitexact import _hip
 
 BQ = 4
-BLOCK_TARGET = 512          # blocks to aim for: 2 per MI355X compute unit
+BLOCK_TARGET = 256          # blocks (of 8 waves) to aim for: 1 per MI355X compute unit
 
 
 def default_nsplit(R, HKV, nblk, bs):
-    """Key splits: enough blocks to fill the device, at least 128 keys per split."""
+    """Key splits: none once the (row, KV head) tiles alone cover half the device (one launch, K read once);
+    otherwise enough blocks to fill it, at least 128 keys per split."""
     tiles = max(1, R * HKV)
     keys = max(1, nblk * bs)
-    return max(1, min(64, BLOCK_TARGET // tiles, (keys + 127) // 128))
+    if tiles >= 128:
+        return 1
+    return max(1, min(64, BLOCK_TARGET // tiles, keys // 128))
 
 
 def attend(q, sh, qpos, cache, bt, rmap, lut, l2e, nsplit=None, bn=64, warps=4):

@@ -38,7 +38,7 @@ def to_limbs(c):
 
 
 FE, FP = 30, 20                 # exp table values, int8 attention weights (src/bitexact/int8/segs.py:22)
-SM_TARGET = 512                 # blocks to aim for: 2 per MI355X compute unit
+SM_TARGET = 256                 # blocks (of 8 waves) to aim for: 1 per MI355X compute unit
 
 
 def weight_table(lut):
@@ -60,7 +60,7 @@ def attend(q, qpos, cache, bt, ptab, nsplit=None, bm=None, bn=None, warps=4):
     if nsplit is None:
         tiles = max(1, R * HKV * ((M + 3) // 4))
         keys = max(1, bt.shape[1] * cache.shape[2])
-        nsplit = max(1, min(64, SM_TARGET // tiles, (keys + 127) // 128))
+        nsplit = 1 if tiles >= 128 else max(1, min(64, SM_TARGET // tiles, keys // 128))
     num = torch.empty(R, HKV, M, HD, dtype=torch.long, device=q.device)
     den = torch.empty(R, HKV, M, 1, dtype=torch.long, device=q.device)
     ws, wsb = _hip.workspace(q.device, _hip.lib().bx_attn_paged_workspace(R, HKV, M, HD) if nsplit > 1 else 0)

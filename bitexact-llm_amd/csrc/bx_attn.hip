@@ -18,6 +18,8 @@
 // hit distinct banks (rows padded by one word).
 #include "bx_common.h"
 
+#include <algorithm>
+
 namespace bx {
 
 constexpr int kFK = 17, kFZ = 26, kFP = 22, kFT2 = 26, kExp2Bits = 14, kExp2One = 60;
@@ -357,6 +359,297 @@ __global__ __launch_bounds__(256) void attn_kernel(AttnArgs p) {
   }
 }
 
+// ---- paged decode attention on MFMA ----
+// Grid (query tiles of <= 4 queries, key splits); a block is 8 independent waves, wave w taking the 16-key blocks
+// w, w + 8, ... of the block's key range, with the next block's limb loads in flight while one is used.
+// Scores: v_mfma_i32_16x16x64_i8 with the queries' limbs as A (row m = 4 query + limb; the fourth row of each
+// query is zero) and one K limb plane as B straight from the cache (lane: key lane & 15, dims of chunk
+// lane >> 4 -- the key row is contiguous along the MFMA depth). Lane l receives query l >> 4's limb rows for key
+// l & 15 and joins them in int64: raw = sum_j sum_i acc_j[i] 2^(8 (i + j)) (|acc| <= HD 2^14, exact in int32).
+// Sweep 1 keeps per-lane maxima. Sweep 2 turns scores into weights, puts the block's weights and joined V rows
+// in the wave's own LDS slice and accumulates p V in int64 with one lane per dimension. Waves, then splits,
+// are summed in a fixed order: partial maxima and sums go to per-split workspace slots with plain stores and the
+// last block of a tile (counter) combines them, so no value is accumulated with atomics.
+constexpr int kDecWaves = 8;
+constexpr int kDecMaxSplit = 64;
+constexpr int64_t kDecWsSplitBudget = 4096;   // the workspace query sizes for min(64, 4096 / tiles) splits
+
+template <int HD>
+struct DecSmem {
+  union {
+    int32_t Vs[kDecWaves][16][HD + 1];   // sweep 2: each wave's joined V rows
+    int64_t red[kDecWaves][4][HD];        // after it: each wave's p V sums
+  };
+  int32_t Ps[kDecWaves][4][16];
+  int64_t qpos[4];
+  int64_t shift[4];
+  int64_t mx[4];
+  int64_t den[kDecWaves][4];
+  int s_last;
+};
+
+template <int HD>
+struct KvRegs {
+  v4i k[3][HD / 64];
+  v4i v[3][HD / 64];
+};
+
+template <int HD, bool WANT_K, bool WANT_V>
+__device__ __forceinline__ void dec_load(const AttnArgs& p, int64_t brow, int h, int s, KvRegs<HD>& r) {
+  const int c = (threadIdx.x & 63) >> 4;
+  const int blk = p.bt[brow * p.sbt + s / p.bs];
+  const int8_t* row = p.cache + (int64_t)blk * p.sc_nb + (int64_t)h * p.sc_h + (int64_t)(s % p.bs) * p.sc_bs + c * 16;
+#pragma unroll
+  for (int j = 0; j < 3; ++j)
+#pragma unroll
+    for (int kk = 0; kk < HD / 64; ++kk) {
+      if (WANT_K) r.k[j][kk] = *(const v4i*)(row + j * HD + kk * 64);
+      if (WANT_V) r.v[j][kk] = *(const v4i*)(row + (3 + j) * HD + kk * 64);
+    }
+}
+
+template <int HD>
+__device__ __forceinline__ int64_t dec_score(const v4i (&qa)[HD / 64], const KvRegs<HD>& r) {
+  int64_t raw = 0;
+#pragma unroll
+  for (int j = 0; j < 3; ++j) {
+    v4i acc = {0, 0, 0, 0};
+#pragma unroll
+    for (int kk = 0; kk < HD / 64; ++kk) acc = __builtin_amdgcn_mfma_i32_16x16x64_i8(qa[kk], r.k[j][kk], acc, 0, 0, 0);
+    const int64_t t = (int64_t)acc[0] + ((int64_t)acc[1] << 8) + ((int64_t)acc[2] << 16);
+    raw += t << (8 * j);
+  }
+  return raw;
+}
+
+// workspace slots of tile t (per split sp): maxima (stored as mx - kNeg), p V sums, weight sums; then counters
+struct DecWs {
+  int64_t* mx;    // [T][NS][4]
+  int64_t* num;   // [T][NS][4][HD]
+  int64_t* den;   // [T][NS][4]
+  int32_t* sem;   // [T]
+};
+__host__ __device__ __forceinline__ int64_t dec_ws_bytes(int64_t T, int64_t NS, int HD) {
+  return T * NS * 4 * 8 * (2 + HD) + T * 4 + 256;
+}
+// Workspace slots are written by one block and read by another, possibly on another XCD (whose L2 is its own):
+// agent-scope relaxed atomic stores and loads keep them coherent without a cache-wide fence.
+__device__ __forceinline__ void ws_store(int64_t* a, int64_t v) {
+  __hip_atomic_store(a, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ int64_t ws_load(int64_t* a) {
+  return __hip_atomic_load(a, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+__device__ __forceinline__ DecWs dec_ws(const AttnArgs& p, int T, int NS, int HD) {
+  const int64_t slots = (int64_t)T * NS * 4;
+  char* b = (char*)p.mx_ws;
+  DecWs w;
+  w.mx = (int64_t*)b;
+  w.num = (int64_t*)(b + slots * 8);
+  w.den = (int64_t*)(b + slots * 8 * (1 + HD));
+  w.sem = (int32_t*)(b + slots * 8 * (2 + HD));
+  return w;
+}
+
+// RAW (single launch only): sweep 1 keeps every score of the block's key range (p.S >= hi - lo of them per
+// query) in dynamic LDS and sweep 2 reads them back, so K is read once.
+template <int HD, int PHASE, bool RAW>
+__global__ __launch_bounds__(kDecWaves * 64) void attn_dec_kernel(AttnArgs p) {
+  __shared__ DecSmem<HD> sm;
+  extern __shared__ __align__(16) int64_t raw_cache[];
+  constexpr int KK = HD / 64;
+  const int tiles = (p.nq + 3) / 4;
+  const int tile = blockIdx.x, T = gridDim.x, sp = blockIdx.y, NS = gridDim.y;
+  const int group = tile / tiles, q0 = (tile % tiles) * 4;
+  const int nvalid = min(4, p.nq - q0);
+  const int h = group % p.hkv;
+  const int64_t brow = p.rmap ? p.rmap[group / p.hkv] : group / p.hkv;
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  const int kl = lane & 15, qo = lane >> 4;
+  const DecWs ws = dec_ws(p, T, NS, HD);
+
+  if (threadIdx.x < 4) {
+    const int i = threadIdx.x;
+    const bool ok = i < nvalid;
+    sm.qpos[i] = ok ? p.qpos[(group / p.qpos_div) * p.qpos_tile + (int64_t)(q0 + i) * p.qpos_row] : -1;
+    sm.shift[i] = ok && p.sh ? (int64_t)(kFK + 3 - kFZ) - p.sh[group * p.sh_tile + q0 + i] : 0;
+    sm.mx[i] = kNeg;
+  }
+  // A operand: limb (m & 3) of query (m >> 2), m = lane & 15, dims kk 64 + (lane >> 4) 16 + [0, 16)
+  v4i qa[KK];
+  {
+    const int m = lane & 15, qi = m >> 2, li = m & 3, c = lane >> 4;
+    const bool live = qi < nvalid && li < 3;
+#pragma unroll
+    for (int kk = 0; kk < KK; ++kk) {
+      int32_t word[4];
+#pragma unroll
+      for (int e4 = 0; e4 < 4; ++e4) {
+        uint32_t wv = 0;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const int64_t qidx = group * p.sq_tile + (int64_t)(q0 + qi) * p.sq_row + kk * 64 + c * 16 + e4 * 4 + e;
+          int32_t x = live ? (p.q64 ? (int32_t)p.q64[qidx] : p.q[qidx]) : 0;
+          const int32_t a0 = limb_lo(x);
+          x = (x - a0) >> 8;
+          const int32_t a1 = limb_lo(x);
+          x = (x - a1) >> 8;
+          const int32_t a2 = limb_lo(x);
+          const int32_t v = li == 0 ? a0 : li == 1 ? a1 : a2;
+          wv |= (uint32_t)(v & 255) << (8 * e);
+        }
+        word[e4] = (int32_t)wv;
+      }
+      qa[kk] = v4i{word[0], word[1], word[2], word[3]};
+    }
+  }
+  __syncthreads();
+  int64_t kend = 0;
+  for (int i = 0; i < 4; ++i) kend = imax(kend, sm.qpos[i] + 1);
+  int64_t lo64, hi64;
+  split_range(kend, NS, sp, lo64, hi64);
+  const int lo = (int)lo64, hi = (int)hi64;
+  const int64_t my_qpos = sm.qpos[qo];
+  const int nb16 = (hi - lo + 15) / 16;
+
+  // ---- sweep 1: maxima over visible keys ----
+  if (PHASE == 0 || NS == 1) {
+    int64_t best = kNeg;
+    KvRegs<HD> cur, nxt;
+    if (w < nb16) dec_load<HD, true, false>(p, brow, h, min(lo + w * 16 + kl, hi - 1), cur);
+    for (int b = w; b < nb16; b += kDecWaves) {
+      const int s = lo + b * 16 + kl;
+      if (b + kDecWaves < nb16) dec_load<HD, true, false>(p, brow, h, min(s + 16 * kDecWaves, hi - 1), nxt);
+      const int64_t raw = dec_score<HD>(qa, cur);
+      if (RAW && s < hi && s - lo < p.S) raw_cache[qo * p.S + (s - lo)] = raw;
+      if (s < hi && s <= my_qpos) best = imax(best, raw);
+      cur = nxt;
+    }
+#pragma unroll
+    for (int o = 1; o < 16; o <<= 1) best = imax(best, __shfl_xor(best, o, 64));
+    if (kl == 0) atomicMax((long long*)&sm.mx[qo], (long long)best);
+    __syncthreads();
+    if (NS > 1) {                       // PHASE 0: this split's maxima (kNeg: none) into its slot
+      if (threadIdx.x < 4) ws_store(&ws.mx[((int64_t)tile * NS + sp) * 4 + threadIdx.x], sm.mx[threadIdx.x] - kNeg);
+      return;
+    }
+  } else {                              // PHASE 1 of a split launch: the maxima over every split
+    __syncthreads();                    // sm.mx holds kNeg
+    for (int u = threadIdx.x; u < NS * 4; u += kDecWaves * 64)      // every split's slot at once
+      atomicMax((long long*)&sm.mx[u & 3], (long long)(ws_load(&ws.mx[(int64_t)tile * NS * 4 + u]) + kNeg));
+    __syncthreads();
+  }
+
+  // ---- sweep 2: weights, den, num ----
+  const int64_t mx = sm.mx[qo];
+  const int64_t shift = sm.shift[qo];
+  int64_t den = 0;
+  int64_t num[4][KK];
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+#pragma unroll
+    for (int kk = 0; kk < KK; ++kk) num[i][kk] = 0;
+  KvRegs<HD> cur, nxt;
+  if (w < nb16) dec_load<HD, !RAW, true>(p, brow, h, min(lo + w * 16 + kl, hi - 1), cur);
+  for (int b = w; b < nb16; b += kDecWaves) {
+    const int s = lo + b * 16 + kl;
+    if (b + kDecWaves < nb16) dec_load<HD, !RAW, true>(p, brow, h, min(s + 16 * kDecWaves, hi - 1), nxt);
+    const int64_t raw = RAW ? (s < hi && s - lo < p.S ? raw_cache[qo * p.S + (s - lo)] : 0) : dec_score<HD>(qa, cur);
+    int64_t pw = 0;
+    if (qo < nvalid && s < hi && s <= my_qpos)
+      pw = p.wrule == 0 ? attn_weight(mx - raw, shift, p.lut, p.l2e) : int8_weight(raw - mx, p.zsh, p.zmul, p.ptab);
+    den += pw;
+    sm.Ps[w][qo][kl] = (int32_t)pw;
+    const int c = lane >> 4;
+#pragma unroll
+    for (int kk = 0; kk < KK; ++kk) {
+#pragma unroll
+      for (int e4 = 0; e4 < 4; ++e4) {
+        const int32_t w0 = cur.v[0][kk][e4], w1 = cur.v[1][kk][e4], w2 = cur.v[2][kk][e4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const int32_t b0 = (w0 << (24 - 8 * e)) >> 24, b1 = (w1 << (24 - 8 * e)) >> 24, b2 = (w2 << (24 - 8 * e)) >> 24;
+          sm.Vs[w][kl][kk * 64 + c * 16 + e4 * 4 + e] = b0 + b1 * 256 + b2 * 65536;
+        }
+      }
+    }
+    __builtin_amdgcn_s_waitcnt(0xc07f);           // lgkmcnt(0): this wave's LDS writes are done
+    __builtin_amdgcn_wave_barrier();
+#pragma unroll
+    for (int k = 0; k < 16; ++k) {
+      int64_t vd[KK];
+#pragma unroll
+      for (int kk = 0; kk < KK; ++kk) vd[kk] = sm.Vs[w][k][lane + 64 * kk];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int64_t pv = sm.Ps[w][i][k];
+#pragma unroll
+        for (int kk = 0; kk < KK; ++kk) num[i][kk] += pv * vd[kk];
+      }
+    }
+    __builtin_amdgcn_s_waitcnt(0xc07f);
+    __builtin_amdgcn_wave_barrier();
+    cur = nxt;
+  }
+#pragma unroll
+  for (int o = 1; o < 16; o <<= 1) den += __shfl_xor(den, o, 64);
+  if (kl == 0) sm.den[w][qo] = den;
+  __syncthreads();                                 // red overlays the waves' V rows
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+#pragma unroll
+    for (int kk = 0; kk < KK; ++kk) sm.red[w][i][lane + 64 * kk] = num[i][kk];
+  __syncthreads();
+  // the block's sums, waves in order: thread u -> (query u / HD, dim u % HD)
+  for (int u = threadIdx.x; u < 4 * HD + 4; u += kDecWaves * 64) {
+    int64_t t = 0;
+    if (u < 4 * HD) {
+      for (int ww = 0; ww < kDecWaves; ++ww) t += sm.red[ww][u / HD][u % HD];
+    } else {
+      for (int ww = 0; ww < kDecWaves; ++ww) t += sm.den[ww][u - 4 * HD];
+    }
+    const int i = u < 4 * HD ? u / HD : u - 4 * HD;
+    if (i >= nvalid) continue;
+    if (NS == 1) {
+      if (u < 4 * HD) p.num[group * p.snum_tile + (int64_t)(q0 + i) * p.snum_row + u % HD] = t;
+      else p.den[group * p.sden_tile + q0 + i] = t;
+    } else {
+      const int64_t slot = (int64_t)tile * NS + sp;
+      if (u < 4 * HD) ws_store(&ws.num[(slot * 4 + i) * HD + u % HD], t);
+      else ws_store(&ws.den[slot * 4 + i], t);
+    }
+  }
+  if (NS == 1) return;
+  // every split arrives (its slot stores complete first); the last one adds the slots in split order
+  __builtin_amdgcn_s_waitcnt(0);
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    const bool last = atomicAdd(&ws.sem[tile], 1) == NS - 1;
+    if (last) atomicExch(&ws.sem[tile], 0);
+    sm.s_last = last;
+  }
+  __syncthreads();
+  if (!sm.s_last) return;
+  // every (split, entry) slot is read at once and added into LDS (exact in any order); the slots go back to
+  // zero, so the workspace is left as it was found
+  int64_t* fin = &sm.red[0][0][0];                 // 4 HD + 4 sums
+  for (int u = threadIdx.x; u < 4 * HD + 4; u += kDecWaves * 64) fin[u] = 0;
+  __syncthreads();
+  for (int u = threadIdx.x; u < NS * (4 * HD + 4); u += kDecWaves * 64) {
+    const int k = u / (4 * HD + 4), e = u % (4 * HD + 4);
+    const int64_t slot = (int64_t)tile * NS + k;
+    int64_t* src = e < 4 * HD ? &ws.num[slot * 4 * HD + e] : &ws.den[slot * 4 + (e - 4 * HD)];
+    atomicAdd((unsigned long long*)&fin[e], (unsigned long long)ws_load(src));
+    ws_store(src, 0);
+  }
+  for (int u = threadIdx.x; u < NS * 4; u += kDecWaves * 64) ws_store(&ws.mx[(int64_t)tile * NS * 4 + u], 0);
+  __syncthreads();
+  for (int u = threadIdx.x; u < nvalid * HD; u += kDecWaves * 64)
+    p.num[group * p.snum_tile + (int64_t)(q0 + u / HD) * p.snum_row + u % HD] = fin[u];
+  if (threadIdx.x < nvalid) p.den[group * p.sden_tile + q0 + threadIdx.x] = fin[4 * HD + threadIdx.x];
+}
+
 // ---- KV store into the limb-plane cache (tri_paged.store, src/bitexact/vllm_plugin/tri_paged.py:311-335) ----
 template <typename T>
 __global__ __launch_bounds__(128) void kv_store_kernel(int8_t* cache, int64_t sc_nb, int64_t sc_h, int64_t sc_bs,
@@ -402,6 +695,30 @@ static int launch_attn(AttnArgs& p, int groups, hipStream_t st) {
   return check_launch("attn_kernel");
 }
 
+constexpr int kDecRawKeys = 2048;               // single-launch score cache: 4 x 2048 x 8 B of LDS
+
+template <int HD>
+static int launch_dec(AttnArgs& p, int groups, int64_t max_keys, hipStream_t st) {
+  const int tiles = (p.nq + 3) / 4;
+  dim3 grid(groups * tiles, p.nsplit);
+  if (p.nsplit > 1) {
+    attn_dec_kernel<HD, 0, false><<<grid, kDecWaves * 64, 0, st>>>(p);
+    if (int rc = check_launch("attn_dec_kernel(max)")) return rc;
+    attn_dec_kernel<HD, 1, false><<<grid, kDecWaves * 64, 0, st>>>(p);
+    return check_launch("attn_dec_kernel");
+  }
+  if (max_keys <= kDecRawKeys) {
+    p.S = (int)((max_keys + 15) / 16 * 16);
+    const size_t lds = (size_t)4 * p.S * 8;
+    hipFuncSetAttribute((const void*)attn_dec_kernel<HD, 1, true>, hipFuncAttributeMaxDynamicSharedMemorySize,
+                        (int)(4 * kDecRawKeys * 8));
+    attn_dec_kernel<HD, 1, true><<<grid, kDecWaves * 64, lds, st>>>(p);
+    return check_launch("attn_dec_kernel(raw)");
+  }
+  attn_dec_kernel<HD, 1, false><<<grid, kDecWaves * 64, 0, st>>>(p);
+  return check_launch("attn_dec_kernel");
+}
+
 // split-KV workspace: mx [Gq] + num [Gq, HD] + den [Gq] + counters [tiles]; zero-filled = idle
 static int64_t attn_ws_bytes(int64_t gq, int64_t tiles, int HD) { return gq * 8 * (2 + HD) + tiles * 4 + 256; }
 
@@ -413,8 +730,11 @@ static void bind_attn_ws(AttnArgs& p, void* ws, int64_t gq, int HD) {
   p.sem = (int32_t*)(b + gq * 8 * (2 + HD));
 }
 
+static int64_t dec_split_cap(int64_t T) { return std::max<int64_t>(1, std::min<int64_t>(kDecMaxSplit, kDecWsSplitBudget / std::max<int64_t>(T, 1))); }
+
 extern "C" int64_t bx_attn_paged_workspace(int32_t R, int32_t HKV, int32_t M, int32_t HD) {
-  return attn_ws_bytes((int64_t)R * HKV * M, (int64_t)R * HKV * ((M + 3) / 4), HD);   // counters per query tile
+  const int64_t T = (int64_t)R * HKV * ((M + 3) / 4);                                  // query tiles
+  return dec_ws_bytes(T, dec_split_cap(T), HD);
 }
 
 extern "C" int bx_exact_attn_paged(const int32_t* q, const int64_t* sh, const int64_t* qpos, int64_t sqpos_r,
@@ -440,13 +760,16 @@ extern "C" int bx_exact_attn_paged(const int32_t* q, const int64_t* sh, const in
   p.num = num; p.den = den; p.snum_tile = (int64_t)M * HD; p.snum_row = HD; p.sden_tile = M;
   p.nsplit = nsplit;
   if (nsplit > 1) {
-    const int64_t need = attn_ws_bytes((int64_t)R * HKV * M, (int64_t)R * HKV, HD);
-    BX_REQUIRE(ws != nullptr && ws_bytes >= need, "workspace too small (%lld < %lld)", (long long)ws_bytes,
-               (long long)need);
-    bind_attn_ws(p, ws, (int64_t)R * HKV * M, HD);
+    const int64_t T = (int64_t)R * HKV * ((M + 3) / 4);
+    const int64_t need = dec_ws_bytes(T, nsplit, HD);
+    BX_REQUIRE(ws != nullptr && ws_bytes >= need, "workspace too small for %d splits (%lld < %lld)", nsplit,
+               (long long)ws_bytes, (long long)need);
+    BX_REQUIRE(((uintptr_t)ws & 7) == 0, "workspace must be 8-byte aligned");
+    p.mx_ws = (int64_t*)ws;
   }
-  return HD == 64 ? launch_attn<4, 64, true>(p, R * HKV, (hipStream_t)stream)
-                  : launch_attn<4, 128, true>(p, R * HKV, (hipStream_t)stream);
+  const int64_t max_keys = (int64_t)nblk * bs;     // qpos < nblk bs: the block table's reach
+  return HD == 64 ? launch_dec<64>(p, R * HKV, max_keys, (hipStream_t)stream)
+                  : launch_dec<128>(p, R * HKV, max_keys, (hipStream_t)stream);
 }
 
 extern "C" int bx_int8_attn_paged(const int64_t* q, const int64_t* qpos, int64_t sqpos_r, const int8_t* cache,
@@ -475,13 +798,16 @@ extern "C" int bx_int8_attn_paged(const int64_t* q, const int64_t* qpos, int64_t
   p.num = num; p.den = den; p.snum_tile = (int64_t)M * HD; p.snum_row = HD; p.sden_tile = M;
   p.nsplit = nsplit;
   if (nsplit > 1) {
-    const int64_t need = attn_ws_bytes((int64_t)R * HKV * M, (int64_t)R * HKV * ((M + 3) / 4), HD);
-    BX_REQUIRE(ws != nullptr && ws_bytes >= need, "workspace too small (%lld < %lld)", (long long)ws_bytes,
-               (long long)need);
-    bind_attn_ws(p, ws, (int64_t)R * HKV * M, HD);
+    const int64_t T = (int64_t)R * HKV * ((M + 3) / 4);
+    const int64_t need = dec_ws_bytes(T, nsplit, HD);
+    BX_REQUIRE(ws != nullptr && ws_bytes >= need, "workspace too small for %d splits (%lld < %lld)", nsplit,
+               (long long)ws_bytes, (long long)need);
+    BX_REQUIRE(((uintptr_t)ws & 7) == 0, "workspace must be 8-byte aligned");
+    p.mx_ws = (int64_t*)ws;
   }
-  return HD == 64 ? launch_attn<4, 64, true>(p, R * HKV, (hipStream_t)stream)
-                  : launch_attn<4, 128, true>(p, R * HKV, (hipStream_t)stream);
+  const int64_t max_keys = (int64_t)nblk * bs;     // qpos < nblk bs: the block table's reach
+  return HD == 64 ? launch_dec<64>(p, R * HKV, max_keys, (hipStream_t)stream)
+                  : launch_dec<128>(p, R * HKV, max_keys, (hipStream_t)stream);
 }
 
 extern "C" int bx_exact_attn_prefill(const int32_t* qg, int64_t sq_z, int64_t sq_row, const int64_t* shg,

@@ -93,6 +93,8 @@ int bx_exact_attn_paged(const int32_t* q, const int64_t* sh, const int64_t* qpos
                         int32_t nblk, const int64_t* rmap, const int64_t* lut, int64_t l2e, int64_t* num, int64_t* den,
                         int32_t R, int32_t HKV, int32_t M, int32_t HD, int32_t nsplit, void* ws, int64_t ws_bytes,
                         bx_stream_t stream);
+/* Workspace bytes of the paged attentions (exact and int8) for up to min(64, 4096 / T) key splits, T = R HKV
+ * ceil(M / 4) query tiles; a call with more splits than the workspace holds is rejected. */
 int64_t bx_attn_paged_workspace(int32_t R, int32_t HKV, int32_t M, int32_t HD);
 
 /* Replaces tri_paged.attend (src/bitexact/vllm_plugin/tri_paged.py:363-430), the int8-mode paged attention: q int64
