@@ -1,9 +1,10 @@
 """bench.py -- the hot path on one MI355X: int8-mode decode GEMMs (HBM GB/s) and exact-mode prefill limb GEMMs
 (effective limb-op TOPS against the dense int8 MFMA peak).
 
-One step = one pass over BASELINE config 2's decode GEMMs: batch M in {1, 8, 64} x {gate K=2048 N=8192,
-up K=2048 N=8192, down K=8192 N=2048}, int8 weights uniform in [-127, 127], activations N(0,1) quantized per
-row into 2 int8 limbs, int64 joined output (bitexact.int8.gemm_skinny.int_mm_join). Weights rotate over
+One step = one pass over BASELINE config 2's decode GEMMs as the reference's int8 MLP issues them: batch M in
+{1, 8, 64} x {gate|up fused (wgu = cat(gate, up): K=2048, N=2 x 8192), down K=8192 N=2048}, int8 weights uniform
+in [-127, 127], activations N(0,1) quantized per row into 2 int8 limbs, int64 joined output
+(bitexact.int8.gemm_skinny.int_mm_join). Separate gate / up GEMMs are timed too (per_gemm). Weights rotate over
 >= 1 GiB of copies per shape (4x the 256 MB MALL) so every launch reads them from HBM. The steps are captured
 in a HIP graph and timed with HIP events on the launch stream.
 value = sum of algorithmic bytes (N K + 2 M K + 8 M N per GEMM) / time, in GB/s.
@@ -40,7 +41,10 @@ HBM_PEAK_GBS = 8000.0
 # plain 1 GiB device copy (profiles/decode_gemv_config2_hbm_traffic.txt).
 DECODE_TRAFFIC_PER_LAUNCH = 20356654
 INT8_PEAK_TOPS = 5000.0
-DECODE_SHAPES = [("gate", 8192, 2048), ("up", 8192, 2048), ("down", 2048, 8192)]
+# The reference's int8 MLP issues gate and up as one GEMM over wgu = cat(gate, up) [2 x 8192, 2048]
+# (src/bitexact/int8/consts.py:68, src/bitexact/int8/model.py:106), then down; the step follows that call pattern.
+DECODE_SHAPES = [("gate_up", 16384, 2048), ("down", 2048, 8192)]
+SEPARATE_SHAPES = [("gate", 8192, 2048), ("up", 8192, 2048), ("down", 2048, 8192)]
 DECODE_M = (1, 8, 64)
 PREFILL_SHAPES = [("q_o", 2048, 2048), ("k_v", 512, 2048), ("gate_up_each", 8192, 2048), ("down", 2048, 8192),
                   ("qkv_fused", 3072, 2048), ("gate_up_fused", 16384, 2048), ("lm_head", 128256, 2048)]
@@ -165,7 +169,11 @@ def bench_decode(dev, steps, warmup):
     stream = torch.cuda.Stream(dev)
     sec = time_graph(step, warmup, steps, stream)
     per = []
-    for M, name, N, K in plan:          # per-GEMM figures, each on its own graph (rotation as above)
+    for M, name, N, K in plan + [(M, nm, N, K) for M in DECODE_M for nm, N, K in SEPARATE_SHAPES if nm != "down"]:
+        if (N, K) not in copies:        # per-GEMM figures, each on its own graph (rotation as above)
+            n = max(4, -(-(1 << 30) // (N * K)))
+            copies[(N, K)] = [torch.randint(-127, 128, (N, K), dtype=torch.int8, device=dev, generator=g)
+                              for _ in range(n)]
         cs = copies[(N, K)]
         reps = 64
         s = time_graph(lambda i: int_mm_join(acts[(M, K)], cs[i % len(cs)], M, 2), 8, reps, stream)
@@ -424,8 +432,9 @@ def main():
            "value": r(value, 1), "unit": "GB/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
            "ms_per_step": round(sec / args.steps * 1e3, 4), "higher_is_better": True, "scaling": "weak",
            "vs_baseline": None, "dtype": "int8 (int32 accumulate, int64 join)", "data": "synthetic",
-           "config": {"workload": "config 2: int8-mode decode GEMMs, M in {1,8,64} x gate/up (K=2048, N=8192), "
-                                  "down (K=8192, N=2048), 2 activation limbs, int64 joined output",
+           "config": {"workload": "config 2: int8-mode decode GEMMs, M in {1,8,64} x gate|up as the reference's fused "
+                                  "wgu (K=2048, N=2x8192), down (K=8192, N=2048), 2 activation limbs, int64 joined "
+                                  "output",
                       "gemms_per_step": launches, "bytes_per_step": step_bytes, "weight_rotation": ">=1 GiB/shape"},
            "roofline": {"bound": "hbm", "kernel": "gemv_kernel (each of the step's decode GEMMs is one launch)",
                         "achieved": r(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",

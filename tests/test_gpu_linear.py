@@ -92,6 +92,29 @@ def test_exact_linear_matches_oracle(dev, M):
         assert bool(flag.item()) == rflag, (M, lim)
 
 
+@pytest.mark.parametrize("M,N", [(22, 16384), (32, 16400), (42, 16384)])
+def test_exact_linear_wide_rows(dev, M, N):
+    """65..128 stacked limb rows over a wide N (the every-row strip path; N = 16400 leaves a partial column tile)."""
+    from bitexact.vllm_plugin.exact_gemm import exact_linear
+    K = 512
+    w = _bf16(N, K, 5)
+    dec = _dec(w)
+    limbs = torch.from_numpy(dec["limbs"]).to(dev)
+    d, gg = torch.from_numpy(dec["d"]).to(dev), torch.from_numpy(dec["g"]).to(dev)
+    cnt, ec, ev, Rr = _ell(dec, N, dev)
+    g = np.random.default_rng(M + N)
+    for lim, shr in ((1 << 22, (-30, -20)), (3, (-70, 10))):
+        q = g.integers(-lim, lim + 1, (M, K))
+        sh = g.integers(shr[0], shr[1], M)
+        ref, rflag, _ = R.epilogue(R.wmm_f64(q, dec["W"]), R.residual(q, dec["rr"], dec["rc"], dec["rv"], N),
+                                   dec["d"], dec["g"], sh, R.FR, True)
+        flag = torch.zeros(1, dtype=torch.int32, device=dev)
+        y = exact_linear(torch.from_numpy(q).to(torch.int32).to(dev), torch.from_numpy(sh).to(dev), limbs, d, gg,
+                         cnt, ec, ev, Rr, flag, True)
+        assert np.array_equal(y.cpu().numpy(), ref), (M, N, lim)
+        assert bool(flag.item()) == rflag, (M, N, lim)
+
+
 def test_exact_linear_flag_cases(dev):
     """The checked epilogue's loss / range flag, per element (reference tests/test_model_bounds.py)."""
     from bitexact.vllm_plugin.exact_gemm import exact_linear
@@ -166,8 +189,8 @@ def test_int_mm_join(dev, M, nl):
     assert np.array_equal(y.cpu().numpy(), ref)
 
 
-@pytest.mark.parametrize("M", [1, 8, 64])
-@pytest.mark.parametrize("N,K", [(8192, 2048), (2048, 8192)])
+@pytest.mark.parametrize("M", [1, 8, 33, 64])
+@pytest.mark.parametrize("N,K", [(8192, 2048), (2048, 8192), (16384, 2048)])
 def test_config2_int8_decode(dev, M, N, K):
     """Config 2 shapes at full size: int8 uniform weights, N(0,1) activations in 2 limbs."""
     from bitexact.int8.gemm_skinny import int_mm_join
