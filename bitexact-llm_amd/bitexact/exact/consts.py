@@ -116,10 +116,11 @@ def dims(cfg):
             cfg.get("intermediate_size", c["intermediate_size"]))
 
 
-def random_constants(cfg=None, n_layers=None, seed=0, device="cuda", keep_bf16=False):
+def random_constants(cfg=None, n_layers=None, seed=0, device="cuda", keep_bf16=False, with_sha=False):
     """Constants dict (the reference's keys) of a random-init Llama: every linear weight bf16 N(0, 0.02) drawn on
     `device` from `seed`, decomposed there; norm gammas 1.0; lm_head tied to the embedding. keep_bf16 also keeps
-    each weight's bf16 tensor under f"{name}.bf16" (checkers rebuild the decomposition from it)."""
+    each weight's bf16 tensor under f"{name}.bf16" (checkers rebuild the decomposition from it). with_sha stores
+    the model's identity under "sha256", as the reference's build does (it hashes every plane on the host)."""
     cfg = dict(LLAMA_3_2_1B if cfg is None else cfg)
     H, HKV, HD, D, FF = dims(cfg)
     V = cfg.get("vocab_size", LLAMA_3_2_1B["vocab_size"])
@@ -157,4 +158,56 @@ def random_constants(cfg=None, n_layers=None, seed=0, device="cuda", keep_bf16=F
                           rs.get("high_freq_factor", 4.0), rs.get("original_max_position_embeddings", 8192))
     c["cos"], c["sin"] = (t.to(dev) for t in rope_tables(MAX_POS, FT, inv))
     c["exp2"] = exp2_table(dev)
+    if with_sha:
+        c["sha256"] = sha256(c)
+    return c
+
+
+# keys this build adds to a constants dict (device-side ELL form, kept bf16 sources); they are derived data and
+# stay out of the model's identity
+_DERIVED = (".ell_cnt", ".ell_col", ".ell_val", ".R", ".bf16")
+
+
+def sha256(c, skip=("cfg", "stats", "sha256")):
+    """The model's identity: SHA-256 over every tensor and scalar of the constants dict in key order -- per key its
+    name, then a tensor's dtype name and bytes or a scalar's repr (src/bitexact/llama.py:77-92 via
+    src/bitexact/exact/consts.py:152-154). Keys in `skip` and this build's derived keys are left out."""
+    import hashlib
+    h = hashlib.sha256()
+    for k in sorted(c):
+        if k in skip or k.endswith(_DERIVED):
+            continue
+        v = c[k]
+        h.update(k.encode())
+        if torch.is_tensor(v):
+            h.update(str(v.dtype).encode())
+            h.update(v.detach().contiguous().cpu().numpy().tobytes())
+        else:
+            h.update(repr(v).encode())
+    return h.hexdigest()
+
+
+def save(c, path):
+    """Write a constants dict as one safetensors file: every tensor under its key, every other entry (layer count,
+    config, residual widths) as JSON in the file's metadata. Replaces the reference's pickle (torch.save) with a
+    format that loads without executing anything."""
+    import json
+
+    from safetensors.torch import save_file
+    tensors = {k: v.detach().contiguous().cpu() for k, v in c.items() if torch.is_tensor(v)}
+    other = {k: v for k, v in c.items() if not torch.is_tensor(v)}
+    save_file(tensors, path, metadata={"bitexact": json.dumps(other, sort_keys=True)})
+
+
+def load(path, device="cpu"):
+    """Read a constants dict written by save() (tensors moved to `device`)."""
+    import json
+
+    from safetensors import safe_open
+    c = {}
+    with safe_open(path, framework="pt", device="cpu") as f:
+        meta = f.metadata() or {}
+        for k in f.keys():
+            c[k] = f.get_tensor(k).to(device)
+    c.update(json.loads(meta.get("bitexact", "{}")))
     return c

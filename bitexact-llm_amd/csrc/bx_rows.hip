@@ -189,7 +189,17 @@ __global__ __launch_bounds__(1024) void first_argmax_kernel(const int64_t* v, in
   __shared__ int64_t smax[16], sidx[16];
   const int64_t* row = v + (int64_t)blockIdx.x * ldv;
   int64_t best = INT64_MIN, idx = N;
-  for (int i = threadIdx.x; i < N; i += 1024) {
+  constexpr int U = 8;                             // loads in flight per thread
+  int i0 = threadIdx.x;
+  for (; i0 + (U - 1) * 1024 < N; i0 += U * 1024) {
+    int64_t x[U];
+#pragma unroll
+    for (int u = 0; u < U; ++u) x[u] = __builtin_nontemporal_load(row + i0 + u * 1024);
+#pragma unroll
+    for (int u = 0; u < U; ++u)
+      if (x[u] > best || idx == N) { best = x[u]; idx = i0 + u * 1024; }
+  }
+  for (int i = i0; i < N; i += 1024) {
     const int64_t x = row[i];
     if (x > best || idx == N) { best = x; idx = i; }
   }

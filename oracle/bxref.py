@@ -23,6 +23,12 @@ How each function is pinned (tests/test_oracle.py):
   silu_mul / gu_silu_y               the precision bounds of the reference's own tests
   paged attention                    softmax_w + exact matmuls (the reference's own test formulation,
                                      tests/test_vllm_exact_attn.py:38-41)
+  rope_y / q_group                   position-0 scale and exact-rotation closed forms; quant (pinned) + permutation
+  llama3_inv_freq                    transformers' own llama3 rule, element for element
+  exp2_table                         every entry within 2 float64 units of 2^(60 - i/2^14) (50-digit decimal)
+  first_argmax                       numpy argmax (documented: the first occurrence of the maximum)
+  engine_forward / engine_logits     a composition of the pinned functions above, in the order of the
+                                     reference's engine; checked further on the GPU by batch invariance
 """
 
 import math

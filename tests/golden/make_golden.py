@@ -1,6 +1,6 @@
 """Writes tests/golden/reference_vectors.npz: input/output vectors of the reference's CPU integer rules that
 closed forms do not pin bit for bit (ops.rms, ops.exp2neg_lut, ops.softmax_w, segs.norm_quant, ops.div_round,
-int8 ops.quant_rows, int8 segs.softmax, ops.silu_mul, segs.silu_y + quant_silu). Run in the development container only, where the reference checkout is present:
+int8 ops.quant_rows, int8 segs.softmax, ops.silu_mul, segs.silu_y + quant_silu, llama.digest). Run in the development container only, where the reference checkout is present:
 
     python tests/golden/make_golden.py /root/reference
 
@@ -111,6 +111,19 @@ def main(ref_root):
     gu = torch.cat([gate, up], 1)
     q, sh, err = segs.quant_silu(*segs.silu_y(gu, lut), torch.zeros((), dtype=torch.bool))
     out["gus_q"], out["gus_sh"], out["gus_err"] = q.numpy(), sh.numpy(), np.array(bool(err))
+
+    # llama.digest: the constants dict's SHA-256 over sorted keys (tensors: name, dtype, bytes; scalars: repr)
+    from bitexact.llama import digest                     # noqa: E402
+    gd = torch.Generator().manual_seed(3)
+    cdict = {"n_layers": 2, "cfg": {"hidden_size": 64}, "stats": {"x": 1},
+             "0.wo.limbs": torch.randint(-128, 128, (3, 4, 8), dtype=torch.int8, generator=gd),
+             "0.wo.g": torch.randint(-40, 0, (4,), generator=gd), "emb": torch.randint(-9, 9, (5, 8), dtype=torch.int32,
+                                                                                       generator=gd),
+             "gf.m": torch.randint(-255, 256, (8,), generator=gd)}
+    for k, v in cdict.items():
+        if torch.is_tensor(v):
+            out["dg_" + k] = v.numpy()
+    out["dg_sha"] = np.frombuffer(bytes.fromhex(digest(cdict)), np.uint8)
 
     path = os.path.join(os.path.dirname(os.path.abspath(__file__)), "reference_vectors.npz")
     np.savez_compressed(path, **out)

@@ -55,3 +55,26 @@ def test_host_tables_match_oracle():
     w[0, :4] = torch.tensor([0.0, -0.0, 1e-30, -3e-8])
     m = R.engine_constants(w.view(torch.int16).numpy(), {}, {}, c, s, 0)
     assert np.array_equal(consts.emb_fixed(w).numpy(), m["emb"])
+
+
+def test_constants_digest_and_file_roundtrip(tmp_path):
+    """sha256 equals the reference's llama.digest on the golden dict; save / load round-trips every entry and the
+    digest; this build's derived keys do not change the identity."""
+    import torch
+    from bitexact.exact import consts
+    gold = np.load(os.path.join(os.path.dirname(__file__), "golden", "reference_vectors.npz"))
+    c = {"n_layers": 2, "cfg": {"hidden_size": 64}, "stats": {"x": 1}}
+    for k in gold.files:
+        if k.startswith("dg_") and k != "dg_sha":
+            c[k[3:]] = torch.from_numpy(gold[k])
+    assert bytes.fromhex(consts.sha256(c)) == gold["dg_sha"].tobytes()
+    c2 = dict(c)
+    c2["0.wo.ell_cnt"] = torch.zeros(4, dtype=torch.int32)
+    c2["0.wo.R"] = 0
+    assert consts.sha256(c2) == consts.sha256(c)
+    f = str(tmp_path / "c.safetensors")
+    consts.save(c, f)
+    d = consts.load(f)
+    assert set(d) == set(c) and d["n_layers"] == 2 and d["cfg"] == {"hidden_size": 64}
+    assert all(torch.equal(d[k], c[k]) for k in c if torch.is_tensor(c[k]))
+    assert consts.sha256(d) == consts.sha256(c)

@@ -115,3 +115,26 @@ def test_batch_invariance(dev, model):
     alone = run([prompt])
     batched = run([prompt] + others)
     assert alone == batched
+
+
+def test_constants_file_roundtrip(dev, tmp_path):
+    """A random-init constants dict saved to a safetensors file and loaded back gives the same identity and the
+    same logits."""
+    from bitexact.exact import consts
+    from bitexact.vllm_plugin.exact_run import ExactEngine
+    c = consts.random_constants(CFG, n_layers=1, seed=4, device=dev, with_sha=True)
+    f = str(tmp_path / "m.safetensors")
+    consts.save(c, f)
+    c2 = consts.load(f, dev)
+    assert c2["sha256"] == c["sha256"] == consts.sha256(c2)
+    ids = torch.tensor([5, 7, 11], device=dev)
+    pos = torch.arange(3, device=dev)
+    bt = torch.arange(1, 1 + NBLK, dtype=torch.int32, device=dev).view(1, NBLK)
+    slot = bt[0, pos // BS].long() * BS + pos % BS
+    rmap = torch.zeros(3, dtype=torch.long, device=dev)
+    out = []
+    for cc in (c, c2):
+        eng = ExactEngine(cc, dev)
+        kvs = eng.new_cache(1 + NBLK, BS)
+        out.append(eng.logits(eng.forward(kvs, ids, pos, slot, bt, rmap)).cpu())
+    assert torch.equal(out[0], out[1])

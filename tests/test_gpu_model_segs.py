@@ -94,3 +94,19 @@ def test_gu_silu(dev, M, ff):
     bad = gu.clone()
     bad[0, 0], bad[0, ff] = 1 << 32, 1 << 31           # bitlen(s) + bitlen(u) > 62
     assert bool(ops.gu_silu_y(bad.to(dev), torch.from_numpy(lut).to(dev))[2]) and R.gu_silu_y(bad.numpy(), lut)[2]
+
+
+@pytest.mark.parametrize("M,N", [(1, 128256), (5, 1000), (3, 7)])
+def test_first_argmax(dev, M, N):
+    """First index of the row maximum, ties included; a row of int64 minima gives 0."""
+    from bitexact.intops import first_argmax
+    g = torch.Generator().manual_seed(N)
+    v = torch.randint(-(1 << 40), 1 << 40, (M, N), generator=g)
+    v[0, N // 3] = v[0, N - 1] = v[0, N // 2] = 1 << 50          # ties: the first one wins
+    if M > 1:
+        v[1] = -(1 << 63)
+    if M > 2:
+        v[2] = 5
+    want = [R.first_argmax(r) for r in v.numpy()]
+    assert first_argmax(v.to(dev)).cpu().tolist() == want
+    assert want[0] == N // 3 and (M < 2 or want[1] == 0) and (M < 3 or want[2] == 0)
