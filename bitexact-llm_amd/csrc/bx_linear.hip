@@ -712,6 +712,142 @@ __global__ __launch_bounds__(WM * WN * 64) void tile_kernel(LinArgs p) {
 }
 
 // =====================================================================================================
+// wide kernel (exact-mode decode with 65..96 limb rows, wide N)
+// =====================================================================================================
+// A block owns BNC = 16 CG output columns and every limb row of q (RA = 16 RBW WR >= 3 M), so each weight byte
+// is read once and no row part re-reads it (the gemv splits 96 limb rows into two parts, and the second part
+// re-reads the weights). The K range is walked in CK-byte chunks. The limb rows of a chunk (the planes of q
+// written by split_q_kernel) go through an S = 3 stage LDS ring filled by asynchronous global_load_lds_dwordx4
+// (1 KiB per wave instruction = 1024 / CK rows; chunk slots XOR-swizzled by row so the MFMA operand reads hit
+// distinct banks); rows past the activations repeat the last row and only feed output rows that are never
+// read. Waves are CG column groups x WR row groups; each streams its 16 weight rows from HBM straight into
+// v_mfma_i32_16x16x64_i8 B operands. A chunk's weight and limb-row loads form one group, issued two chunks
+// ahead. Limb products accumulate in int32 (exact: |sum| <= K 2^14 < 2^31), meet in LDS and are joined in
+// int64 per output (sum C_j[i M + m] 2^(8 (i + j))).
+constexpr int kWideCK = 256;   // K granularity of the wide plan (chunks are 128 bytes)
+
+template <int NB, int RBW, int WR, int CG, int S, int CK, int MODE>
+__global__ __launch_bounds__(64 * WR * CG) void wide_kernel(LinArgs p) {
+  constexpr int NW = WR * CG, NT = 64 * NW, RA = 16 * RBW * WR, BNC = 16 * CG, NSTEP = CK / 64;
+  constexpr int RPI = 1024 / CK, CHN = CK / 16;                    // rows per 1 KiB load instruction, chunks per row
+  constexpr int STAGE = RA * CK, NI = RA / RPI;                    // bytes and load instructions per stage
+  constexpr int IPW = (NI + NW - 1) / NW;                          // load instructions per wave per stage (bound)
+  static_assert(RA % RPI == 0 && (CK == 128 || CK == 256), "chunk shape");
+  extern __shared__ __align__(16) char smem[];
+  int32_t* Cs = (int32_t*)smem;                                    // after the K loop: [NB][RA][BNC]
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int cg = wave % CG, wr = wave / CG;
+  const int n0 = blockIdx.x * BNC;
+  const int M = p.M, rows = p.rows_a;
+  const int nchunk = p.K / CK;
+
+  // asynchronous activation loads: instruction i of a stage covers rows RPI i .. RPI i + RPI - 1; lane L -> row
+  // RPI i + L / CHN, LDS slot L % CHN, global chunk slot ^ (row % CHN)
+  const int8_t* abase = p.a;
+  auto a_issue = [&](int ch) {
+    char* stage = smem + (ch % S) * STAGE;
+#pragma unroll
+    for (int t = 0; t < IPW; ++t) {
+      const int i = wave + t * NW;
+      if (i < NI) {
+        const int row = RPI * i + lane / CHN;
+        const int gc = (lane % CHN) ^ (row % CHN);
+        const int8_t* src = abase + (int64_t)min(row, rows - 1) * p.K + ch * CK + gc * 16;
+        async16(src, stage + i * 1024);
+      }
+    }
+  };
+  // weights: this wave's 16 columns, NB planes, NSTEP k steps of a chunk
+  const __amdgpu_buffer_rsrc_t wres = buf_rsrc(p.w + (int64_t)n0 * p.ld_row);
+  const int wrow = (min(n0 + cg * 16 + (lane & 15), p.N - 1) - n0) * (int)p.ld_row;
+  const int kl = (lane >> 4) * 16;
+  auto w_issue = [&](v4i(&b)[NSTEP][NB], int ch) {
+#pragma unroll
+    for (int u = 0; u < NSTEP; ++u)
+#pragma unroll
+      for (int j = 0; j < NB; ++j)
+        b[u][j] = buf_load16(wres, wrow + j * (int)p.ld_plane + ch * CK + u * 64 + kl);
+  };
+  v4i acc[RBW][NB];
+#pragma unroll
+  for (int r = 0; r < RBW; ++r)
+#pragma unroll
+    for (int j = 0; j < NB; ++j) acc[r][j] = v4i{0, 0, 0, 0};
+  auto compute = [&](const v4i(&b)[NSTEP][NB], int ch) {
+    const char* stage = smem + (ch % S) * STAGE;
+#pragma unroll
+    for (int u = 0; u < NSTEP; ++u)
+#pragma unroll
+      for (int r = 0; r < RBW; ++r) {
+        const int row = (wr * RBW + r) * 16 + (lane & 15);
+        const int slot = (u * 4 + (lane >> 4)) ^ (row % CHN);
+        const v4i a = *(const v4i*)(stage + row * CK + slot * 16);
+#pragma unroll
+        for (int j = 0; j < NB; ++j) acc[r][j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a, b[u][j], acc[r][j], 0, 0, 0);
+      }
+  };
+
+  // Group g = chunk g's weight loads, then its activation loads; groups are issued S - 1 = 2 chunks ahead and
+  // vector memory operations complete in order, so before chunk c is read this wave waits until at most the
+  // group issued after it (c + 1) is outstanding, and for everything on the last chunk. LDS reads of the
+  // previous chunk are drained too (lgkmcnt 0) before the barrier lets any wave refill that stage.
+  static_assert(S == 3, "three register sets and three ring stages");
+  // vector memory operations per group: the weights, then IPW activation loads (IPW - 1 for the waves past
+  // NI % NW when the instructions do not divide evenly)
+  constexpr int NG_HI = NSTEP * NB + IPW, NG_LO = NI % NW == 0 ? NG_HI : NG_HI - 1;
+  const bool hi_wave = NI % NW == 0 || wave < NI % NW;
+  v4i ws0[NSTEP][NB], ws1[NSTEP][NB], ws2[NSTEP][NB];
+  if (0 < nchunk) { w_issue(ws0, 0); a_issue(0); }
+  if (1 < nchunk) { w_issue(ws1, 1); a_issue(1); }
+  auto step = [&](int c, v4i(&cur)[NSTEP][NB], v4i(&nxt)[NSTEP][NB]) {
+    if (c + 1 >= nchunk)
+      ring_barrier<0>();
+    else if (hi_wave)
+      ring_barrier<NG_HI>();
+    else
+      ring_barrier<NG_LO>();
+    if (c + 2 < nchunk) { w_issue(nxt, c + 2); a_issue(c + 2); }
+    compute(cur, c);
+  };
+  for (int ch = 0; ch < nchunk; ch += 3) {
+    step(ch, ws0, ws2);
+    if (ch + 1 >= nchunk) break;
+    step(ch + 1, ws1, ws0);
+    if (ch + 2 >= nchunk) break;
+    step(ch + 2, ws2, ws1);
+  }
+  __syncthreads();                              // Cs overlays the activation ring
+#pragma unroll
+  for (int r = 0; r < RBW; ++r)
+#pragma unroll
+    for (int j = 0; j < NB; ++j)
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const int row = (wr * RBW + r) * 16 + (lane >> 4) * 4 + e, col = cg * 16 + (lane & 15);
+        Cs[(j * RA + row) * BNC + col] = acc[r][j][e];
+      }
+  __syncthreads();
+  bool bad = false;
+  for (int e = tid; e < M * BNC; e += NT) {
+    const int m = e / BNC, c = e - m * BNC, n = n0 + c;
+    if (n >= p.N) continue;
+    int64_t v = 0;
+    if (MODE == RAW32) {
+      v = Cs[m * BNC + c];
+    } else if (MODE == JOIN) {
+      for (int i = 0; i < p.nl; ++i) v += (int64_t)Cs[(i * M + m) * BNC + c] << (8 * i);
+    } else {
+#pragma unroll
+      for (int i = 0; i < 3; ++i)
+#pragma unroll
+        for (int j = 0; j < NB; ++j) v += (int64_t)Cs[(j * RA + i * M + m) * BNC + c] << (8 * (i + j));
+    }
+    finalize<MODE>(p, m, n, v, bad);
+  }
+  if (MODE == EXACT && p.checked && bad) p.flag[0] = 1;
+}
+
+// =====================================================================================================
 // host planning and dispatch
 // =====================================================================================================
 // tile configurations: (WM, WN, TM, TN, S)
@@ -725,6 +861,7 @@ static const TileShape kTiles[3] = {{2, 2, 2, 2, 64, 3},    // 128 x 128, 64x64 
 static const TileShape kTileExact = {4, 2, 1, 2, 64, 3};   // 5 accumulator sets: 32x64 wave tiles
 
 struct Plan {
+  int wide;                       // wide kernel configuration (0: none)
   bool gemv;
   int rb, cg, ks_waves, u, spw;   // gemv
   int parts, mp;                  // gemv row parts, output rows per part
@@ -796,10 +933,28 @@ static bool gemv_shape(int na, int M, int N, int K, int nb, bool exact, int cus,
 // rows_a: stacked activation rows; nb: weight planes (exact 3, int8 1); na: activation planes on the tile path
 static bool gemv_shape(int na, int M, int N, int K, int nb, bool exact, int cus, Plan& best);
 
+// wide configuration (exact mode: 65..96 limb rows, N / 64 >= 128 column tiles, K a multiple of 256)
+enum WideCfg { W_NONE = 0, W_E96 = 1 };
+
+static int wide_cfg(int rows_a, int N, int K, bool exact) {
+  // int8 (one weight plane) stays on the gemv: its row parts measured as fast or faster (11.5 vs 22 us at
+  // M = 64, N = 8192); with three weight planes the wide kernel wins (37 vs 53 us at M = 32, N = 16384)
+  if (!exact || rows_a <= 64 || rows_a > 96 || K % kWideCK != 0 || (N + 63) / 64 < 128) return W_NONE;
+  return W_E96;
+}
+
 static Plan make_plan(int rows_a, int M_out, int N, int K, int nb, int na, bool exact) {
   Plan s = {};
   const int cus = device_cus();
   const int nst = (K + 63) / 64;
+  s.wide = wide_cfg(rows_a, N, K, exact);
+  if (s.wide != W_NONE) {
+    s.tiles_x = (N + 63) / 64;
+    s.tiles_y = 1;
+    s.split = 1;
+    s.tmp_bytes = exact ? 3LL * M_out * K : 0;   // exact: q limb planes
+    return s;
+  }
   if (rows_a <= 128 && gemv_shape(na, M_out, N, K, nb, exact, cus, s)) {
     s.gemv = true;
     const int RA = 16 * s.rb, BNC = 16 * s.cg;
@@ -934,6 +1089,23 @@ static int launch_tile(LinArgs& p, const Plan& s, hipStream_t st) {
   return launch_tile_cfg<NA, NB, MODE, 2, 1, 1, 1, 64, 8>(p, s, st);
 }
 
+template <int NB, int RBW, int WR, int CG, int CK, int MODE>
+static int launch_wide_cfg(LinArgs& p, const Plan& s, hipStream_t st) {
+  constexpr int S = 3, RA = 16 * RBW * WR, BNC = 16 * CG;
+  const size_t lds = std::max<size_t>((size_t)S * RA * CK, (size_t)NB * RA * BNC * 4);
+  BX_REQUIRE(p.rows_a <= RA && p.K % CK == 0, "wide plan shape");
+  allow_lds(wide_kernel<NB, RBW, WR, CG, S, CK, MODE>, lds);
+  wide_kernel<NB, RBW, WR, CG, S, CK, MODE><<<s.tiles_x, 64 * WR * CG, lds, st>>>(p);
+  return check_launch("wide_kernel");
+}
+
+template <int MODE>
+static int launch_wide(LinArgs& p, const Plan& s, hipStream_t st) {
+  // weight offsets of a block are 32-bit buffer offsets
+  BX_REQUIRE((int64_t)p.ld_plane * 2 + (int64_t)64 * p.ld_row + p.K < (1LL << 31), "weight span exceeds 2^31 bytes");
+  return launch_wide_cfg<3, 3, 2, 4, 128, MODE>(p, s, st);        // 96 limb rows: q of up to 32 tokens
+}
+
 static bool aligned16(const void* x) { return ((uintptr_t)x & 15) == 0; }
 
 static int need_ws(const LinArgs& p, const Plan& s, int64_t ws_bytes, const void* tmp, int64_t tmp_bytes) {
@@ -969,6 +1141,7 @@ static int exact_common(LinArgs& p, int mode, int64_t ws_bytes, void* tmp, int64
   split_q_kernel<<<blocks, 256, 0, st>>>(p.q, p.ldq, p.M, p.K, planes);
   if (int rc = check_launch("split_q_kernel")) return rc;
   p.a = planes;
+  if (s.wide) return mode == EXACT ? launch_wide<EXACT>(p, s, st) : launch_wide<WMM_T>(p, s, st);
   return mode == EXACT ? launch_tile<3, 3, EXACT>(p, s, st) : launch_tile<3, 3, WMM_T>(p, s, st);
 }
 
