@@ -851,13 +851,14 @@ __global__ __launch_bounds__(64 * WR * CG) void wide_kernel(LinArgs p) {
 // host planning and dispatch
 // =====================================================================================================
 // tile configurations: (WM, WN, TM, TN, S)
-enum TileCfg { T_BIG = 0, T_MID = 1, T_NARROW = 2 };
+enum TileCfg { T_BIG = 0, T_MID = 1, T_NARROW = 2, T_DEC = 3 };
 struct TileShape {
   int wm, wn, tm, tn, bk, stages;
 };
-static const TileShape kTiles[3] = {{2, 2, 2, 2, 64, 3},    // 128 x 128, 64x64 wave tiles (prefill)
+static const TileShape kTiles[4] = {{2, 2, 2, 2, 64, 3},    // 128 x 128, 64x64 wave tiles (prefill)
                                     {2, 2, 1, 2, 64, 3},    // 64 x 128 (few tiles)
-                                    {2, 1, 1, 1, 64, 8}};   // 64 x 32, deep ring (<= 64 output rows, decode)
+                                    {2, 1, 1, 1, 64, 8},    // 64 x 32, deep ring (<= 64 output rows, decode)
+                                    {2, 2, 1, 1, 64, 8}};   // 64 x 64, deep ring (int8 decode, 65..128 limb rows)
 static const TileShape kTileExact = {4, 2, 1, 2, 64, 3};   // 5 accumulator sets: 32x64 wave tiles
 
 struct Plan {
@@ -948,6 +949,10 @@ static Plan make_plan(int rows_a, int M_out, int N, int K, int nb, int na, bool 
   const int cus = device_cus();
   const int nst = (K + 63) / 64;
   s.wide = wide_cfg(rows_a, N, K, exact);
+  // int8 decode with 65..128 stacked rows over a wide N (>= one 64-column tile per CU): 64 x 64 tiles with an
+  // 8-stage ring read each weight once (17.2 vs 22.3 us for the gemv's two row parts at M = 64, N = 16384); at
+  // N = 8192 the tiles would fill half the chip and the gemv stays faster
+  const bool dec_tile = !exact && rows_a > 64 && M_out <= 64 && (N + 63) / 64 >= cus;
   if (s.wide != W_NONE) {
     s.tiles_x = (N + 63) / 64;
     s.tiles_y = 1;
@@ -955,7 +960,7 @@ static Plan make_plan(int rows_a, int M_out, int N, int K, int nb, int na, bool 
     s.tmp_bytes = exact ? 3LL * M_out * K : 0;   // exact: q limb planes
     return s;
   }
-  if (rows_a <= 128 && gemv_shape(na, M_out, N, K, nb, exact, cus, s)) {
+  if (!dec_tile && rows_a <= 128 && gemv_shape(na, M_out, N, K, nb, exact, cus, s)) {
     s.gemv = true;
     const int RA = 16 * s.rb, BNC = 16 * s.cg;
     const int steps = (nst + s.split - 1) / s.split;
@@ -978,7 +983,9 @@ static Plan make_plan(int rows_a, int M_out, int N, int K, int nb, int na, bool 
   } else {
     s.gemv = false;
     const int64_t big = (int64_t)((M_out + 127) / 128) * ((N + 127) / 128);
-    if (M_out <= 64 && 2 * ((N + 31) / 32) >= cus)
+    if (dec_tile)
+      s.tile = T_DEC;
+    else if (M_out <= 64 && 2 * ((N + 31) / 32) >= cus)
       s.tile = T_NARROW;
     else
       s.tile = big >= cus ? T_BIG : T_MID;
@@ -1086,6 +1093,9 @@ static int launch_tile(LinArgs& p, const Plan& s, hipStream_t st) {
       return launch_tile_cfg<NA, NB, MODE, 2, 2, 2, 2, 64, 3>(p, s, st);
   }
   if (s.tile == T_MID) return launch_tile_cfg<NA, NB, MODE, 2, 2, 1, 2, 64, 3>(p, s, st);
+  if constexpr (NB == 1) {
+    if (s.tile == T_DEC) return launch_tile_cfg<NA, NB, MODE, 2, 2, 1, 1, 64, 8>(p, s, st);
+  }
   return launch_tile_cfg<NA, NB, MODE, 2, 1, 1, 1, 64, 8>(p, s, st);
 }
 
