@@ -12,6 +12,12 @@ import torch
 from bitexact import _hip
 
 
+def _aligned_rows(t):
+    """The kernel reads 16-byte row pieces: rows must start 16-byte aligned (else a contiguous copy)."""
+    ok = t.data_ptr() % 16 == 0 and t.stride(0) % 4 == 0 and t.stride(1) % 4 == 0
+    return t if ok else t.contiguous()
+
+
 def prefill(qg, shg, K, V, qpos, lut, l2e):
     _hip.require_cuda(qg, shg, K, V, qpos, lut)
     Z, gT, HD = qg.shape
@@ -19,6 +25,7 @@ def prefill(qg, shg, K, V, qpos, lut, l2e):
     assert K.shape == V.shape and K.shape[0] == Z and K.shape[2] == HD
     assert qg.dtype == torch.int32 and K.dtype == torch.int32 and V.dtype == torch.int32
     assert qg.stride(2) == 1 and K.stride(2) == 1 and V.stride(2) == 1
+    qg, K, V = (_aligned_rows(t) for t in (qg, K, V))
     shg = shg.reshape(Z, gT).contiguous().long()
     qpos = qpos.reshape(Z, gT).long()
     lut = lut.contiguous().long()

@@ -650,6 +650,211 @@ __global__ __launch_bounds__(kDecWaves * 64) void attn_dec_kernel(AttnArgs p) {
   if (threadIdx.x < nvalid) p.den[group * p.sden_tile + q0 + threadIdx.x] = fin[4 * HD + threadIdx.x];
 }
 
+// ---- fused prefill attention on MFMA (contiguous int32 K / V) ----
+// A block (4 waves) owns 64 consecutive query rows of one group z; wave w owns rows 16 w .. 16 w + 15. Keys go
+// in 64-key tiles staged in LDS as int8 limb planes: K row-major (Ks[j][key][dim], the QK B operand: a lane's
+// 16 bytes are 16 dims of one key) and V transposed (Vt[j][dim][key], the PV B operand: 16 keys of one dim).
+// QK: for each 16-key block, A = limb i of the wave's 16 queries (registers), B = K limb plane j; the nine limb
+// products accumulate by weight i + j in five int32 sets, joined in int64 per score (lane: query rows
+// 4 (lane >> 4) + e, key lane & 15). Sweep 1 keeps per-row maxima; sweep 2 turns scores into weights p, writes
+// p's three limbs to the wave's LDS slice (Pl[i][query][key]) and runs PV on MFMA: A = limb i of p (16
+// queries x 64 keys), B = V limb plane j (64 keys x 16 dims), five int32 sets per 16-dim block, exact while
+// S 3 2^14 < 2^31 (S < 43690), joined in int64 at the end.
+template <int HD>
+struct PreSmem {
+  int8_t Ks[3][64][HD + 16];
+  int8_t Vt[3][HD][64 + 16];
+  int8_t Pl[4][3][16][64 + 16];
+};
+
+template <int HD>
+__device__ __forceinline__ void pre_stage(const AttnArgs& p, PreSmem<HD>& sm, int z, int key0, int kend, bool want_v) {
+  // K: thread -> (key, 16-dim chunk); V: thread -> (4 keys, 4 dims), packed 4 keys per dword
+  for (int u = threadIdx.x; u < 64 * (HD / 16); u += 256) {
+    const int kk = u / (HD / 16), c = u % (HD / 16);
+    const int s = min(key0 + kk, kend - 1);
+    const int32_t* kr = p.K + (int64_t)z * p.sk_z + (int64_t)s * p.sk_s + c * 16;
+    uint32_t w0[4], w1[4], w2[4];
+#pragma unroll
+    for (int e4 = 0; e4 < 4; ++e4) split3(*(const v4i*)(kr + e4 * 4), w0[e4], w1[e4], w2[e4]);
+    *(v4i*)&sm.Ks[0][kk][c * 16] = v4i{(int)w0[0], (int)w0[1], (int)w0[2], (int)w0[3]};
+    *(v4i*)&sm.Ks[1][kk][c * 16] = v4i{(int)w1[0], (int)w1[1], (int)w1[2], (int)w1[3]};
+    *(v4i*)&sm.Ks[2][kk][c * 16] = v4i{(int)w2[0], (int)w2[1], (int)w2[2], (int)w2[3]};
+  }
+  if (!want_v) return;
+  for (int u = threadIdx.x; u < 16 * (HD / 4); u += 256) {
+    const int kq = u % 16, dq = u / 16;
+    uint32_t l[4][3];                                   // key quad member t: limb words of dims 4 dq .. + 3
+#pragma unroll
+    for (int t = 0; t < 4; ++t) {
+      const int s = min(key0 + 4 * kq + t, kend - 1);
+      split3(*(const v4i*)(p.V + (int64_t)z * p.sv_z + (int64_t)s * p.sv_s + dq * 4), l[t][0], l[t][1], l[t][2]);
+    }
+#pragma unroll
+    for (int j = 0; j < 3; ++j)
+#pragma unroll
+      for (int d = 0; d < 4; ++d) {
+        const uint32_t word = ((l[0][j] >> (8 * d)) & 255) | (((l[1][j] >> (8 * d)) & 255) << 8) |
+                              (((l[2][j] >> (8 * d)) & 255) << 16) | (((l[3][j] >> (8 * d)) & 255) << 24);
+        *(uint32_t*)&sm.Vt[j][dq * 4 + d][kq * 4] = word;
+      }
+  }
+}
+
+template <int HD>
+__device__ __forceinline__ void pre_scores(const PreSmem<HD>& sm, const v4i (&qa)[3][HD / 64], int kb, int64_t (&raw)[4]) {
+  const int lane = threadIdx.x & 63;
+  v4i acc[5];
+#pragma unroll
+  for (int w = 0; w < 5; ++w) acc[w] = v4i{0, 0, 0, 0};
+#pragma unroll
+  for (int kk = 0; kk < HD / 64; ++kk)
+#pragma unroll
+    for (int j = 0; j < 3; ++j) {
+      const v4i b = *(const v4i*)&sm.Ks[j][kb * 16 + (lane & 15)][kk * 64 + (lane >> 4) * 16];
+#pragma unroll
+      for (int i = 0; i < 3; ++i) acc[i + j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(qa[i][kk], b, acc[i + j], 0, 0, 0);
+    }
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    int64_t r = 0;
+#pragma unroll
+    for (int w = 0; w < 5; ++w) r += (int64_t)acc[w][e] << (8 * w);
+    raw[e] = r;
+  }
+}
+
+template <int HD>
+__global__ __launch_bounds__(256) void attn_pre_kernel(AttnArgs p) {
+  extern __shared__ __align__(16) char smem_raw[];
+  PreSmem<HD>& sm = *(PreSmem<HD>*)smem_raw;
+  constexpr int KK = HD / 64, DB = HD / 16;
+  const int tiles = (p.nq + 63) / 64;
+  const int z = blockIdx.x / tiles, q0 = (blockIdx.x % tiles) * 64;
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  // A operands: limb i of query q0 + 16 w + (lane & 15), dims kk 64 + (lane >> 4) 16 + [0, 16)
+  v4i qa[3][KK];
+  {
+    const int qr = min(q0 + 16 * w + (lane & 15), p.nq - 1);
+    const int32_t* qp = p.q + (int64_t)z * p.sq_tile + (int64_t)qr * p.sq_row;
+#pragma unroll
+    for (int kk = 0; kk < KK; ++kk) {
+      uint32_t l[3][4];
+#pragma unroll
+      for (int e4 = 0; e4 < 4; ++e4) {
+        split3(*(const v4i*)(qp + kk * 64 + (lane >> 4) * 16 + e4 * 4), l[0][e4], l[1][e4], l[2][e4]);
+      }
+#pragma unroll
+      for (int i = 0; i < 3; ++i) qa[i][kk] = v4i{(int)l[i][0], (int)l[i][1], (int)l[i][2], (int)l[i][3]};
+    }
+  }
+  // this lane's output rows: 16 w + 4 (lane >> 4) + e
+  int64_t qpos[4], shift[4], mx[4];
+  int64_t kend = 0;
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    const int r = q0 + 16 * w + 4 * (lane >> 4) + e;
+    const bool ok = r < p.nq;
+    qpos[e] = ok ? p.qpos[(z / p.qpos_div) * p.qpos_tile + (int64_t)r * p.qpos_row] : -1;
+    shift[e] = ok ? (int64_t)(kFK + 3 - kFZ) - p.sh[z * p.sh_tile + r] : 0;
+    mx[e] = kNeg;
+    kend = imax(kend, qpos[e] + 1);
+  }
+  // the block's key range: the largest visible key of its rows (bounded by the cache)
+  __shared__ int64_t s_kend;
+  if (threadIdx.x == 0) s_kend = 0;
+  __syncthreads();
+  atomicMax((long long*)&s_kend, (long long)kend);
+  __syncthreads();
+  const int kb_end = (int)imin(s_kend, (int64_t)p.S);
+  const int ntile = (kb_end + 63) / 64;
+
+  // ---- sweep 1: row maxima ----
+  for (int t = 0; t < ntile; ++t) {
+    __syncthreads();
+    pre_stage<HD>(p, sm, z, t * 64, kb_end, false);
+    __syncthreads();
+#pragma unroll
+    for (int kb = 0; kb < 4; ++kb) {
+      int64_t raw[4];
+      pre_scores<HD>(sm, qa, kb, raw);
+      const int s = t * 64 + kb * 16 + (lane & 15);
+#pragma unroll
+      for (int e = 0; e < 4; ++e)
+        if (s < kb_end && s <= qpos[e]) mx[e] = imax(mx[e], raw[e]);
+    }
+  }
+#pragma unroll
+  for (int e = 0; e < 4; ++e)
+#pragma unroll
+    for (int o = 1; o < 16; o <<= 1) mx[e] = imax(mx[e], __shfl_xor(mx[e], o, 64));
+
+  // ---- sweep 2: weights, den, PV ----
+  int64_t den[4] = {0, 0, 0, 0};
+  v4i pacc[DB][5];
+#pragma unroll
+  for (int d = 0; d < DB; ++d)
+#pragma unroll
+    for (int ww = 0; ww < 5; ++ww) pacc[d][ww] = v4i{0, 0, 0, 0};
+  for (int t = 0; t < ntile; ++t) {
+    __syncthreads();
+    pre_stage<HD>(p, sm, z, t * 64, kb_end, true);
+    __syncthreads();
+#pragma unroll
+    for (int kb = 0; kb < 4; ++kb) {
+      int64_t raw[4];
+      pre_scores<HD>(sm, qa, kb, raw);
+      const int s = t * 64 + kb * 16 + (lane & 15);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        int64_t pw = 0;
+        if (s < kb_end && s <= qpos[e]) pw = attn_weight(mx[e] - raw[e], shift[e], p.lut, p.l2e);
+        den[e] += pw;
+        int32_t x = (int32_t)pw;                         // 0 <= p <= 2^22: three limbs
+        const int32_t a0 = limb_lo(x);
+        x = (x - a0) >> 8;
+        const int32_t a1 = limb_lo(x);
+        x = (x - a1) >> 8;
+        const int row = 4 * (lane >> 4) + e, col = kb * 16 + (lane & 15);
+        sm.Pl[w][0][row][col] = (int8_t)a0;
+        sm.Pl[w][1][row][col] = (int8_t)a1;
+        sm.Pl[w][2][row][col] = (int8_t)limb_lo(x);
+      }
+    }
+    __builtin_amdgcn_s_waitcnt(0xc07f);                  // this wave's LDS writes are done
+    __builtin_amdgcn_wave_barrier();
+    v4i pa[3];
+#pragma unroll
+    for (int i = 0; i < 3; ++i) pa[i] = *(const v4i*)&sm.Pl[w][i][lane & 15][(lane >> 4) * 16];
+#pragma unroll
+    for (int d = 0; d < DB; ++d)
+#pragma unroll
+      for (int j = 0; j < 3; ++j) {
+        const v4i b = *(const v4i*)&sm.Vt[j][d * 16 + (lane & 15)][(lane >> 4) * 16];
+#pragma unroll
+        for (int i = 0; i < 3; ++i) pacc[d][i + j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(pa[i], b, pacc[d][i + j], 0, 0, 0);
+      }
+  }
+#pragma unroll
+  for (int e = 0; e < 4; ++e)
+#pragma unroll
+    for (int o = 1; o < 16; o <<= 1) den[e] += __shfl_xor(den[e], o, 64);
+  // outputs: lane holds rows 4 (lane >> 4) + e of the wave, dims d 16 + (lane & 15)
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    const int r = q0 + 16 * w + 4 * (lane >> 4) + e;
+    if (r >= p.nq) continue;
+#pragma unroll
+    for (int d = 0; d < DB; ++d) {
+      int64_t v = 0;
+#pragma unroll
+      for (int ww = 0; ww < 5; ++ww) v += (int64_t)pacc[d][ww][e] << (8 * ww);
+      p.num[z * p.snum_tile + (int64_t)r * p.snum_row + d * 16 + (lane & 15)] = v;
+    }
+    if ((lane & 15) == 0) p.den[z * p.sden_tile + r] = den[e];
+  }
+}
+
 // ---- KV store into the limb-plane cache (tri_paged.store, src/bitexact/vllm_plugin/tri_paged.py:311-335) ----
 template <typename T>
 __global__ __launch_bounds__(128) void kv_store_kernel(int8_t* cache, int64_t sc_nb, int64_t sc_h, int64_t sc_bs,
@@ -677,6 +882,10 @@ __global__ __launch_bounds__(128) void kv_store_kernel(int8_t* cache, int64_t sc
 using namespace bx;
 
 // ======================================== C ABI ========================================
+
+static void allow_lds_attn(const void* k, size_t lds) {
+  if (lds > 64 * 1024) hipFuncSetAttribute(k, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+}
 
 template <int QT, int HD, bool PAGED>
 static int launch_attn(AttnArgs& p, int groups, hipStream_t st) {
@@ -820,6 +1029,9 @@ extern "C" int bx_exact_attn_prefill(const int32_t* qg, int64_t sq_z, int64_t sq
   BX_REQUIRE(S < 43690, "keys must stay below 43690");
   BX_REQUIRE(qg && shg && qpos && K && V && lut && num && den, "null pointer");
   BX_REQUIRE(ssh_z == gT, "shg must be [Z, gT, 1] contiguous");
+  BX_REQUIRE(((uintptr_t)qg & 15) == 0 && ((uintptr_t)K & 15) == 0 && ((uintptr_t)V & 15) == 0 && sq_z % 4 == 0 &&
+                 sq_row % 4 == 0 && sk_z % 4 == 0 && sk_s % 4 == 0 && sv_z % 4 == 0 && sv_s % 4 == 0,
+             "qg, K, V: 16-byte aligned rows (base and strides multiples of 4 elements)");
   if (Z == 0 || gT == 0) return BX_OK;
   AttnArgs p = {};
   p.q = qg; p.sq_tile = sq_z; p.sq_row = sq_row;
@@ -830,8 +1042,16 @@ extern "C" int bx_exact_attn_prefill(const int32_t* qg, int64_t sq_z, int64_t sq
   p.num = num; p.den = den; p.snum_tile = (int64_t)gT * HD; p.snum_row = HD; p.sden_tile = gT;
   p.nsplit = 1;
   // keys visible to a query never exceed the cache length S: qpos beyond S - 1 is the caller's contract
-  return HD == 64 ? launch_attn<64, 64, false>(p, Z, (hipStream_t)stream)
-                  : launch_attn<64, 128, false>(p, Z, (hipStream_t)stream);
+  const int tiles = (gT + 63) / 64;
+  hipStream_t st = (hipStream_t)stream;
+  if (HD == 64) {
+    allow_lds_attn((const void*)attn_pre_kernel<64>, sizeof(PreSmem<64>));
+    attn_pre_kernel<64><<<Z * tiles, 256, sizeof(PreSmem<64>), st>>>(p);
+  } else {
+    allow_lds_attn((const void*)attn_pre_kernel<128>, sizeof(PreSmem<128>));
+    attn_pre_kernel<128><<<Z * tiles, 256, sizeof(PreSmem<128>), st>>>(p);
+  }
+  return check_launch("attn_pre_kernel");
 }
 
 extern "C" int bx_kv_store(int8_t* cache, int64_t sc_nb, int64_t sc_h, int64_t sc_bs, int32_t bs, const int64_t* slot,

@@ -126,6 +126,27 @@ __device__ __forceinline__ int64_t exact_round_fast(int64_t T, int64_t B, int64_
   return exact_round(T, B, d, p, bad);
 }
 
+__device__ __forceinline__ uint32_t pack4(int32_t a, int32_t b, int32_t c, int32_t d) {
+  return (uint32_t)(a & 255) | ((uint32_t)(b & 255) << 8) | ((uint32_t)(c & 255) << 16) | ((uint32_t)(d & 255) << 24);
+}
+
+// Three int8 limb words (4 values each) of 4 int32 values (intops.split_limbs, src/bitexact/intops.py:62-70).
+__device__ __forceinline__ void split3(v4i v, uint32_t& l0, uint32_t& l1, uint32_t& l2) {
+  int32_t a0[4], a1[4], a2[4];
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    int32_t r = v[e];
+    a0[e] = limb_lo(r);
+    r = (r - a0[e]) >> 8;
+    a1[e] = limb_lo(r);
+    r = (r - a1[e]) >> 8;
+    a2[e] = limb_lo(r);
+  }
+  l0 = pack4(a0[0], a0[1], a0[2], a0[3]);
+  l1 = pack4(a1[0], a1[1], a1[2], a1[3]);
+  l2 = pack4(a2[0], a2[1], a2[2], a2[3]);
+}
+
 // ---- wavefront reductions (wave64) ----
 __device__ __forceinline__ int64_t wave_max64(int64_t v) {
 #pragma unroll

@@ -160,27 +160,6 @@ __device__ __forceinline__ void ws_add(const LinArgs& p, int m, int n, int64_t v
   atomicAdd((unsigned long long*)&p.ws[(int64_t)m * p.N + n], (unsigned long long)v);
 }
 
-__device__ __forceinline__ uint32_t pack4(int32_t a, int32_t b, int32_t c, int32_t d) {
-  return (uint32_t)(a & 255) | ((uint32_t)(b & 255) << 8) | ((uint32_t)(c & 255) << 16) | ((uint32_t)(d & 255) << 24);
-}
-
-// Three int8 limb words (4 values each) of 4 int32 values (intops.split_limbs, src/bitexact/intops.py:62-70).
-__device__ __forceinline__ void split3(v4i v, uint32_t& l0, uint32_t& l1, uint32_t& l2) {
-  int32_t a0[4], a1[4], a2[4];
-#pragma unroll
-  for (int e = 0; e < 4; ++e) {
-    int32_t r = v[e];
-    a0[e] = limb_lo(r);
-    r = (r - a0[e]) >> 8;
-    a1[e] = limb_lo(r);
-    r = (r - a1[e]) >> 8;
-    a2[e] = limb_lo(r);
-  }
-  l0 = pack4(a0[0], a0[1], a0[2], a0[3]);
-  l1 = pack4(a1[0], a1[1], a1[2], a1[3]);
-  l2 = pack4(a2[0], a2[1], a2[2], a2[3]);
-}
-
 // Ring-stage barrier: wait until at most n of this wave's vector memory operations (the asynchronous LDS
 // loads of later stages) are outstanding and all its LDS reads are done (gfx9 s_waitcnt encoding: vmcnt <= n,
 // lgkmcnt = 0), then a bare s_barrier. __syncthreads() would add a release fence, i.e. vmcnt(0), and drain

@@ -110,7 +110,8 @@ int bx_int8_attn_paged(const int64_t* q, const int64_t* qpos, int64_t sqpos_r, c
 /* Fused form of exact/model.py's attention (src/bitexact/exact/model.py:113-119: bmm(qg, K^T), segs.softmax,
  * bmm(p, V)): qg int32 [Z, gT, HD] (strides sq_z, sq_row), shg int64 [Z, gT] (ssh_z = gT), qpos int64 [Z, gT]
  * (strides), K / V int32 [Z, S, HD] (strides; the integer Cache layout), outputs num int64 [Z, gT, HD],
- * den int64 [Z, gT]. The score matrix is never materialized. */
+ * den int64 [Z, gT]. The score matrix is never materialized. qg, K and V rows must be 16-byte aligned (base and
+ * strides multiples of 4 elements); K / V values are taken as their three signed base-256 limbs. */
 int bx_exact_attn_prefill(const int32_t* qg, int64_t sq_z, int64_t sq_row, const int64_t* shg, int64_t ssh_z,
                           const int64_t* qpos, int64_t sqpos_z, int64_t sqpos_row, const int32_t* K, int64_t sk_z,
                           int64_t sk_s, const int32_t* V, int64_t sv_z, int64_t sv_s, int32_t S, const int64_t* lut,
