@@ -667,37 +667,61 @@ struct PreSmem {
   int8_t Pl[4][3][16][64 + 16];
 };
 
+// A tile's K / V rows in registers (thread -> K: (key, 16-dim chunk) units; V: (4 keys, 4 dims) units), loaded
+// while the previous tile is computed, then split into limb planes in LDS.
 template <int HD>
-__device__ __forceinline__ void pre_stage(const AttnArgs& p, PreSmem<HD>& sm, int z, int key0, int kend, bool want_v) {
-  // K: thread -> (key, 16-dim chunk); V: thread -> (4 keys, 4 dims), packed 4 keys per dword
-  for (int u = threadIdx.x; u < 64 * (HD / 16); u += 256) {
+struct PreRegs {
+  v4i k[HD / 64][4];
+  v4i v[HD / 64][4];
+};
+
+template <int HD>
+__device__ __forceinline__ void pre_load(const AttnArgs& p, PreRegs<HD>& r, int z, int key0, int kend, bool want_v) {
+#pragma unroll
+  for (int t = 0; t < HD / 64; ++t) {
+    const int u = threadIdx.x + t * 256;
     const int kk = u / (HD / 16), c = u % (HD / 16);
     const int s = min(key0 + kk, kend - 1);
     const int32_t* kr = p.K + (int64_t)z * p.sk_z + (int64_t)s * p.sk_s + c * 16;
+#pragma unroll
+    for (int e4 = 0; e4 < 4; ++e4) r.k[t][e4] = *(const v4i*)(kr + e4 * 4);
+    if (want_v) {
+      const int kq = u % 16, dq = u / 16;
+#pragma unroll
+      for (int m = 0; m < 4; ++m) {
+        const int sv = min(key0 + 4 * kq + m, kend - 1);
+        r.v[t][m] = *(const v4i*)(p.V + (int64_t)z * p.sv_z + (int64_t)sv * p.sv_s + dq * 4);
+      }
+    }
+  }
+}
+
+template <int HD>
+__device__ __forceinline__ void pre_store(PreSmem<HD>& sm, const PreRegs<HD>& r, bool want_v) {
+#pragma unroll
+  for (int t = 0; t < HD / 64; ++t) {
+    const int u = threadIdx.x + t * 256;
+    const int kk = u / (HD / 16), c = u % (HD / 16);
     uint32_t w0[4], w1[4], w2[4];
 #pragma unroll
-    for (int e4 = 0; e4 < 4; ++e4) split3(*(const v4i*)(kr + e4 * 4), w0[e4], w1[e4], w2[e4]);
+    for (int e4 = 0; e4 < 4; ++e4) split3(r.k[t][e4], w0[e4], w1[e4], w2[e4]);
     *(v4i*)&sm.Ks[0][kk][c * 16] = v4i{(int)w0[0], (int)w0[1], (int)w0[2], (int)w0[3]};
     *(v4i*)&sm.Ks[1][kk][c * 16] = v4i{(int)w1[0], (int)w1[1], (int)w1[2], (int)w1[3]};
     *(v4i*)&sm.Ks[2][kk][c * 16] = v4i{(int)w2[0], (int)w2[1], (int)w2[2], (int)w2[3]};
-  }
-  if (!want_v) return;
-  for (int u = threadIdx.x; u < 16 * (HD / 4); u += 256) {
-    const int kq = u % 16, dq = u / 16;
-    uint32_t l[4][3];                                   // key quad member t: limb words of dims 4 dq .. + 3
+    if (want_v) {
+      const int kq = u % 16, dq = u / 16;
+      uint32_t l[4][3];
 #pragma unroll
-    for (int t = 0; t < 4; ++t) {
-      const int s = min(key0 + 4 * kq + t, kend - 1);
-      split3(*(const v4i*)(p.V + (int64_t)z * p.sv_z + (int64_t)s * p.sv_s + dq * 4), l[t][0], l[t][1], l[t][2]);
+      for (int m = 0; m < 4; ++m) split3(r.v[t][m], l[m][0], l[m][1], l[m][2]);
+#pragma unroll
+      for (int j = 0; j < 3; ++j)
+#pragma unroll
+        for (int d = 0; d < 4; ++d) {
+          const uint32_t word = ((l[0][j] >> (8 * d)) & 255) | (((l[1][j] >> (8 * d)) & 255) << 8) |
+                                (((l[2][j] >> (8 * d)) & 255) << 16) | (((l[3][j] >> (8 * d)) & 255) << 24);
+          *(uint32_t*)&sm.Vt[j][dq * 4 + d][kq * 4] = word;
+        }
     }
-#pragma unroll
-    for (int j = 0; j < 3; ++j)
-#pragma unroll
-      for (int d = 0; d < 4; ++d) {
-        const uint32_t word = ((l[0][j] >> (8 * d)) & 255) | (((l[1][j] >> (8 * d)) & 255) << 8) |
-                              (((l[2][j] >> (8 * d)) & 255) << 16) | (((l[3][j] >> (8 * d)) & 255) << 24);
-        *(uint32_t*)&sm.Vt[j][dq * 4 + d][kq * 4] = word;
-      }
   }
 }
 
@@ -725,7 +749,7 @@ __device__ __forceinline__ void pre_scores(const PreSmem<HD>& sm, const v4i (&qa
 }
 
 template <int HD>
-__global__ __launch_bounds__(256) void attn_pre_kernel(AttnArgs p) {
+__global__ __launch_bounds__(256, HD == 64 ? 2 : 1) void attn_pre_kernel(AttnArgs p) {
   extern __shared__ __align__(16) char smem_raw[];
   PreSmem<HD>& sm = *(PreSmem<HD>*)smem_raw;
   constexpr int KK = HD / 64, DB = HD / 16;
@@ -770,10 +794,13 @@ __global__ __launch_bounds__(256) void attn_pre_kernel(AttnArgs p) {
   const int ntile = (kb_end + 63) / 64;
 
   // ---- sweep 1: row maxima ----
+  PreRegs<HD> kv;
+  if (ntile > 0) pre_load<HD>(p, kv, z, 0, kb_end, false);
   for (int t = 0; t < ntile; ++t) {
     __syncthreads();
-    pre_stage<HD>(p, sm, z, t * 64, kb_end, false);
+    pre_store<HD>(sm, kv, false);
     __syncthreads();
+    if (t + 1 < ntile) pre_load<HD>(p, kv, z, (t + 1) * 64, kb_end, false);
 #pragma unroll
     for (int kb = 0; kb < 4; ++kb) {
       int64_t raw[4];
@@ -796,10 +823,12 @@ __global__ __launch_bounds__(256) void attn_pre_kernel(AttnArgs p) {
   for (int d = 0; d < DB; ++d)
 #pragma unroll
     for (int ww = 0; ww < 5; ++ww) pacc[d][ww] = v4i{0, 0, 0, 0};
+  if (ntile > 0) pre_load<HD>(p, kv, z, 0, kb_end, true);
   for (int t = 0; t < ntile; ++t) {
     __syncthreads();
-    pre_stage<HD>(p, sm, z, t * 64, kb_end, true);
+    pre_store<HD>(sm, kv, true);
     __syncthreads();
+    if (t + 1 < ntile) pre_load<HD>(p, kv, z, (t + 1) * 64, kb_end, true);
 #pragma unroll
     for (int kb = 0; kb < 4; ++kb) {
       int64_t raw[4];
