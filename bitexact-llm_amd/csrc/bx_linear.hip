@@ -8,7 +8,7 @@
 //    two groups in flight), one v_mfma_i32_16x16x64_i8 per (16-row block, weight plane). The first group is
 //    requested before the activations are staged. The k-slices meet in LDS with ds_add (int32 sums are exact:
 //    |sum| <= K 2^14 < 2^31), then the int32 limb products are joined in int64 (sum C_j[i M+m] 2^(8(i+j))).
-//  * tile_kernel (prefill and the 128-row int8 case). A 3-stage LDS ring is filled by asynchronous
+//  * tile_kernel (prefill and the 128-row int8 case). An LDS ring (2 or 3 stages) is filled by asynchronous
 //    global_load_lds_dwordx4 (1 KiB per wave instruction, XOR-swizzled 16-byte chunks so the MFMA operand
 //    reads are bank-conflict free); 32x64 wave tiles of v_mfma_i32_32x32x32_i8 run the NA x NB limb products
 //    into NA + NB - 1 int32 accumulators by limb weight i + j (|acc| <= 3 K 2^14 < 2^31 for K < 43690), joined
@@ -124,6 +124,35 @@ __device__ __forceinline__ int64_t residual_col(const LinArgs& p, const ColCtx& 
     for (int j = kRes; j < cc.cnt; ++j) B = add_wrap(B, mul_wrap((int64_t)qr[kcol(p, cc.ecp[j])], cc.evp[j]));
   }
   return B;
+}
+
+// The residuals of NR rows of the lane's column, gathered together: one wave-uniform branch per residual entry
+// with NR independent loads under it, so a column costs about wmax load latencies instead of NR wmax (per-row
+// calls put each row's loads behind its own branch). Integer sums wrap modulo 2^64, so the order of the terms
+// does not matter.
+template <int NR>
+__device__ __forceinline__ void residual_rows(const LinArgs& p, const ColCtx& cc, const int (&mrow)[NR],
+                                              int64_t (&B)[NR]) {
+#pragma unroll
+  for (int e = 0; e < NR; ++e) B[e] = 0;
+  if (cc.wmax <= 0) return;   // wave-uniform
+#pragma unroll
+  for (int j = 0; j < kRes; ++j) {
+    if (j < cc.wmax) {        // wave-uniform; padded entries have ev = 0
+      const int col = kcol(p, cc.ec[j]);
+      int32_t qv[NR];
+#pragma unroll
+      for (int e = 0; e < NR; ++e) qv[e] = p.q[(int64_t)mrow[e] * p.ldq + col];
+#pragma unroll
+      for (int e = 0; e < NR; ++e) B[e] = add_wrap(B[e], mul_wrap((int64_t)qv[e], cc.ev[j]));
+    }
+  }
+  for (int j = kRes; j < cc.cnt; ++j) {
+    const int col = kcol(p, cc.ecp[j]);
+    const int64_t ev = cc.evp[j];
+#pragma unroll
+    for (int e = 0; e < NR; ++e) B[e] = add_wrap(B[e], mul_wrap((int64_t)p.q[(int64_t)mrow[e] * p.ldq + col], ev));
+  }
 }
 
 __device__ __forceinline__ void finalize_col(const LinArgs& p, const ColCtx& cc, int m, int n, int64_t shm, int64_t v,
@@ -644,27 +673,32 @@ __global__ __launch_bounds__(WM * WN * 64) void tile_kernel(LinArgs p) {
     for (int t = 0; t < TN; ++t) {
       const int n = n0 + (wn * TN + t) * 32 + (lane & 31);
 #pragma unroll
-      for (int e0 = 0; e0 < 16; e0 += 4) {
-        int64_t v[4], B[4];
+      for (int e0 = 0; e0 < 16; e0 += 8) {   // 8 rows at a time: 16 would spill registers
+        int64_t B[8];
+        if (MODE == EXACT && nsplit == 1) {
+          int mrow[8];
 #pragma unroll
-        for (int u = 0; u < 4; ++u) {
-          const int e = e0 + u, r = (wm * TM + a) * 32 + (e >> 2) * 8 + (lane >> 5) * 4 + (e & 3);
-          v[u] = 0;
-#pragma unroll
-          for (int s2 = 0; s2 < NS; ++s2) v[u] += (int64_t)acc[s2][a][t][e] << (8 * s2);
-          B[u] = (MODE == EXACT && nsplit == 1 && n < p.N && m0 + r < p.M) ? residual_col(p, cc[t], m0 + r) : 0;
+          for (int u = 0; u < 8; ++u) {
+            const int e = e0 + u;
+            mrow[u] = min(m0 + (wm * TM + a) * 32 + (e >> 2) * 8 + (lane >> 5) * 4 + (e & 3), p.M - 1);
+          }
+          residual_rows<8>(p, cc[t], mrow, B);
         }
 #pragma unroll
-        for (int u = 0; u < 4; ++u) {
-          const int e = e0 + u, r = (wm * TM + a) * 32 + (e >> 2) * 8 + (lane >> 5) * 4 + (e & 3), m = m0 + r;
-          if (m < p.M && n < p.N) {
-            if (nsplit > 1)
-              ws_add(p, m, n, v[u]);
-            else if (MODE == EXACT)
-              finalize_col(p, cc[t], m, n, s_sh[r], v[u], B[u], bad);
-            else
-              finalize<MODE>(p, m, n, v[u], bad);
-          }
+        for (int u = 0; u < 8; ++u) {
+        const int e = e0 + u;
+        const int r = (wm * TM + a) * 32 + (e >> 2) * 8 + (lane >> 5) * 4 + (e & 3), m = m0 + r;
+        int64_t v = 0;
+#pragma unroll
+        for (int s2 = 0; s2 < NS; ++s2) v += (int64_t)acc[s2][a][t][e] << (8 * s2);
+        if (m < p.M && n < p.N) {
+          if (nsplit > 1)
+            ws_add(p, m, n, v);
+          else if (MODE == EXACT)
+            finalize_col(p, cc[t], m, n, s_sh[r], v, B[u], bad);
+          else
+            finalize<MODE>(p, m, n, v, bad);
+        }
         }
       }
     }
@@ -838,7 +872,11 @@ static const TileShape kTiles[4] = {{2, 2, 2, 2, 64, 3},    // 128 x 128, 64x64 
                                     {2, 2, 1, 2, 64, 3},    // 64 x 128 (few tiles)
                                     {2, 1, 1, 1, 64, 8},    // 64 x 32, deep ring (<= 64 output rows, decode)
                                     {2, 2, 1, 1, 64, 8}};   // 64 x 64, deep ring (int8 decode, 65..128 limb rows)
-static const TileShape kTileExact = {4, 2, 1, 2, 64, 3};   // 5 accumulator sets: 32x64 wave tiles
+// 5 accumulator sets: 32x64 wave tiles. Two stages: the next stage's loads are issued right after the barrier
+// that frees its buffer. A third stage was measured slower (config-3 down 1730-1810 vs 1900-1960 TOPS, gate / up
+// 1700-1830 vs 1890-1930). A CU streams at most ~35 GB/s even from L2 (measured), so a second stage in flight adds
+// no bandwidth, only more queued requests ahead of the waves' LDS reads.
+static const TileShape kTileExact = {4, 2, 1, 2, 64, 2};
 
 struct Plan {
   int wide;                       // wide kernel configuration (0: none)
@@ -1067,7 +1105,7 @@ static int launch_tile(LinArgs& p, const Plan& s, hipStream_t st) {
   bind_ws(p, s);
   if (s.tile == T_BIG) {
     if constexpr (NA * NB == 9)
-      return launch_tile_cfg<NA, NB, MODE, 4, 2, 1, 2, 64, 3>(p, s, st);   // kTileExact
+      return launch_tile_cfg<NA, NB, MODE, 4, 2, 1, 2, 64, 2>(p, s, st);   // kTileExact
     else
       return launch_tile_cfg<NA, NB, MODE, 2, 2, 2, 2, 64, 3>(p, s, st);
   }
