@@ -113,19 +113,6 @@ __device__ __forceinline__ ColCtx col_ctx(const LinArgs& p, int n) {
   return c;
 }
 
-// The sparse residual B of row m in column cc (segs.lin_y's ELL gather, src/bitexact/exact/segs.py:31).
-__device__ __forceinline__ int64_t residual_col(const LinArgs& p, const ColCtx& cc, int m) {
-  int64_t B = 0;
-  if (cc.wmax > 0) {   // wave-uniform
-    const int32_t* qr = p.q + (int64_t)m * p.ldq;
-#pragma unroll
-    for (int j = 0; j < kRes; ++j)   // padded entries have ev = 0; entries past every lane's count are skipped
-      if (j < cc.wmax) B = add_wrap(B, mul_wrap((int64_t)qr[kcol(p, cc.ec[j])], cc.ev[j]));
-    for (int j = kRes; j < cc.cnt; ++j) B = add_wrap(B, mul_wrap((int64_t)qr[kcol(p, cc.ecp[j])], cc.evp[j]));
-  }
-  return B;
-}
-
 // The residuals of NR rows of the lane's column, gathered together: one wave-uniform branch per residual entry
 // with NR independent loads under it, so a column costs about wmax load latencies instead of NR wmax (per-row
 // calls put each row's loads behind its own branch). Integer sums wrap modulo 2^64, so the order of the terms
@@ -709,14 +696,25 @@ __global__ __launch_bounds__(WM * WN * 64) void tile_kernel(LinArgs p) {
       for (int t = 0; t < TN; ++t) {
         const int n = n0 + (wn * TN + t) * 32 + (lane & 31);
 #pragma unroll
-        for (int e = 0; e < 16; ++e) {
-          const int r = (wm * TM + a) * 32 + (e >> 2) * 8 + (lane >> 5) * 4 + (e & 3), m = m0 + r;
-          if (m < p.M && n < p.N) {
-            const int64_t v = ws_take(p, m, n);
-            if (MODE == EXACT)
-              finalize_col(p, cc[t], m, n, s_sh[r], v, residual_col(p, cc[t], m), bad);
-            else
-              finalize<MODE>(p, m, n, v, bad);
+        for (int e0 = 0; e0 < 16; e0 += 8) {
+          int64_t v[8], B[8];
+          int mrow[8];
+#pragma unroll
+          for (int u = 0; u < 8; ++u) {
+            const int e = e0 + u, m = m0 + (wm * TM + a) * 32 + (e >> 2) * 8 + (lane >> 5) * 4 + (e & 3);
+            mrow[u] = min(m, p.M - 1);
+            v[u] = (m < p.M && n < p.N) ? ws_take(p, m, n) : 0;
+          }
+          if (MODE == EXACT) residual_rows<8>(p, cc[t], mrow, B);
+#pragma unroll
+          for (int u = 0; u < 8; ++u) {
+            const int e = e0 + u, r = (wm * TM + a) * 32 + (e >> 2) * 8 + (lane >> 5) * 4 + (e & 3), m = m0 + r;
+            if (m < p.M && n < p.N) {
+              if (MODE == EXACT)
+                finalize_col(p, cc[t], m, n, s_sh[r], v[u], B[u], bad);
+              else
+                finalize<MODE>(p, m, n, v[u], bad);
+            }
           }
         }
       }
@@ -864,14 +862,15 @@ __global__ __launch_bounds__(64 * WR * CG) void wide_kernel(LinArgs p) {
 // host planning and dispatch
 // =====================================================================================================
 // tile configurations: (WM, WN, TM, TN, S)
-enum TileCfg { T_BIG = 0, T_MID = 1, T_NARROW = 2, T_DEC = 3 };
+enum TileCfg { T_BIG = 0, T_MID = 1, T_NARROW = 2, T_DEC = 3, T_SMALL = 4 };
 struct TileShape {
   int wm, wn, tm, tn, bk, stages;
 };
-static const TileShape kTiles[4] = {{2, 2, 2, 2, 64, 3},    // 128 x 128, 64x64 wave tiles (prefill)
+static const TileShape kTiles[5] = {{2, 2, 2, 2, 64, 3},    // 128 x 128, 64x64 wave tiles (prefill)
                                     {2, 2, 1, 2, 64, 3},    // 64 x 128 (few tiles)
                                     {2, 1, 1, 1, 64, 8},    // 64 x 32, deep ring (<= 64 output rows, decode)
-                                    {2, 2, 1, 1, 64, 8}};   // 64 x 64, deep ring (int8 decode, 65..128 limb rows)
+                                    {2, 2, 1, 1, 64, 8},    // 64 x 64, deep ring (int8 decode, 65..128 limb rows)
+                                    {2, 2, 1, 1, 64, 3}};   // 64 x 64 (exact, when 64 x 128 tiles fill half the chip)
 // 5 accumulator sets: 32x64 wave tiles. Two stages: the next stage's loads are issued right after the barrier
 // that frees its buffer. A third stage was measured slower (config-3 down 1730-1810 vs 1900-1960 TOPS, gate / up
 // 1700-1830 vs 1890-1930). A CU streams at most ~35 GB/s even from L2 (measured), so a second stage in flight adds
@@ -1006,6 +1005,9 @@ static Plan make_plan(int rows_a, int M_out, int N, int K, int nb, int na, bool 
       s.tile = T_NARROW;
     else
       s.tile = big >= cus ? T_BIG : T_MID;
+    // exact prefill with few tiles (k / v projections, N = 512): 64 x 64 tiles keep every CU busy (a CU streams
+    // at most ~35 GB/s, so idle CUs cost more than the smaller tiles' lower reuse)
+    if (exact && s.tile == T_MID && 2 * (int64_t)((M_out + 63) / 64) * ((N + 127) / 128) <= cus) s.tile = T_SMALL;
     const TileShape ts = (s.tile == T_BIG && na * nb == 9) ? kTileExact : kTiles[s.tile];
     const int BM = 32 * ts.tm * ts.wm, BN = 32 * ts.tn * ts.wn;
     s.tiles_x = (N + BN - 1) / BN;
@@ -1110,6 +1112,8 @@ static int launch_tile(LinArgs& p, const Plan& s, hipStream_t st) {
       return launch_tile_cfg<NA, NB, MODE, 2, 2, 2, 2, 64, 3>(p, s, st);
   }
   if (s.tile == T_MID) return launch_tile_cfg<NA, NB, MODE, 2, 2, 1, 2, 64, 3>(p, s, st);
+  if constexpr (NA * NB == 9)
+    if (s.tile == T_SMALL) return launch_tile_cfg<NA, NB, MODE, 2, 2, 1, 1, 64, 3>(p, s, st);
   if constexpr (NB == 1) {
     if (s.tile == T_DEC) return launch_tile_cfg<NA, NB, MODE, 2, 2, 1, 1, 64, 8>(p, s, st);
   }

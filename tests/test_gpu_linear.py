@@ -50,7 +50,7 @@ def test_decompose_matches_oracle(dev):
         assert np.array_equal(got[k].cpu().numpy(), ref[k]), k
 
 
-@pytest.mark.parametrize("M,N,K", [(1, 256, 2048), (7, 3072, 2048), (37, 512, 8192), (300, 1024, 2048),
+@pytest.mark.parametrize("M,N,K", [(1, 256, 2048), (7, 3072, 2048), (37, 512, 8192), (300, 1024, 2048), (2048, 512, 2048),
                                    (21, 200, 320), (22, 130, 64)])
 def test_wmm_exact_extremes(dev, M, N, K):
     from bitexact.exact.wmm import wmm_hip
