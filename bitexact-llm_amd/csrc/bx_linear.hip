@@ -859,6 +859,81 @@ __global__ __launch_bounds__(64 * WR * CG) void wide_kernel(LinArgs p) {
 }
 
 // =====================================================================================================
+// staged kernel (int8 decode with <= 8 stacked activation rows)
+// =====================================================================================================
+// A block owns BNC output columns and the whole K range; its waves are CGW column groups x KSW k-slices. Wave
+// (cg, ks) copies its CR weight rows' KW-byte slices into a private LDS region with asynchronous
+// global_load_lds_dwordx4, one contiguous 1 KiB piece (1024 / KW rows) per instruction, all requested at once,
+// and its activation fragments straight into registers; then it runs v_mfma_i32_16x16x64_i8 from LDS. The
+// k-slices meet in LDS and the limb rows are joined in int64 per output. Contiguous 1 KiB pieces matter: a CU's
+// load pipeline moves contiguous kilobytes markedly faster than the 64-byte row segments of a direct MFMA-operand
+// load (measured: 5.7 vs 7.3-7.9 us for config 2's down GEMM at M = 1, whose 16.8 MB stream in 4.0 us at best).
+// C8: blocks of 8 columns (CR = 8; lanes 8-15 of the MFMA B operand repeat rows 0-7), so that N = 2048 still
+// gives 256 blocks without splitting K.
+template <int CW, int CGW, int KSW, int KW, int C8, int MODE>
+__global__ __launch_bounds__(64 * CGW * KSW) void staged_kernel(LinArgs p) {
+  constexpr int NW = CGW * KSW, NT = 64 * NW, CWE = C8 ? 1 : CW;
+  constexpr int CR = C8 ? 8 : 16 * CW, BNC = CR * CGW, RPI = 1024 / KW, NI = CR / RPI, STEPS = KW / 64;
+  constexpr int PITCH = 1024 + 16;   // LDS bytes per 1 KiB piece (the pad spreads rows over the banks)
+  static_assert(KW == 512 || KW == 1024, "k slice");
+  extern __shared__ __align__(16) char smem[];
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int cg = wave % CGW, ks = wave / CGW;
+  const int n0 = blockIdx.x * BNC + cg * CR, k0 = ks * KW;
+  char* wl = smem + wave * NI * PITCH;
+  {
+    const int lr = lane / (64 / RPI), lb = (lane % (64 / RPI)) * 16;
+#pragma unroll
+    for (int i = 0; i < NI; ++i) {
+      const int row = min(n0 + i * RPI + lr, p.N - 1);   // rows past N repeat the last row (never stored)
+      async16(p.w + (int64_t)row * p.ld_row + k0 + lb, wl + i * PITCH);
+    }
+  }
+  const auto ar = buf_rsrc(p.a);
+  const int r16 = lane & 15, kc = (lane >> 4) * 16;
+  v4i av[STEPS];
+  {
+    const int off = min(r16, p.rows_a - 1) * p.K + k0 + kc;   // rows past rows_a repeat the last row
+#pragma unroll
+    for (int s = 0; s < STEPS; ++s) av[s] = buf_load16(ar, off + s * 64);
+  }
+  __builtin_amdgcn_s_waitcnt(0);   // the wave's own copies and loads (its LDS region is private)
+  v4i acc[CWE];
+#pragma unroll
+  for (int c = 0; c < CWE; ++c) acc[c] = v4i{0, 0, 0, 0};
+#pragma unroll
+  for (int s = 0; s < STEPS; ++s)
+#pragma unroll
+    for (int c = 0; c < CWE; ++c) {
+      const int row = C8 ? (r16 & 7) : c * 16 + r16;
+      const v4i b = *(const v4i*)(wl + (row / RPI) * PITCH + (row % RPI) * KW + s * 64 + kc);
+      acc[c] = __builtin_amdgcn_mfma_i32_16x16x64_i8(av[s], b, acc[c], 0, 0, 0);
+    }
+  __syncthreads();
+  v4i* red = (v4i*)smem;   // [ks][cg][c][lane]
+#pragma unroll
+  for (int c = 0; c < CWE; ++c) red[((ks * CGW + cg) * CWE + c) * 64 + lane] = acc[c];
+  __syncthreads();
+  // output (m, n): limb row i M + m (< 16) of column cl sits at lane (row / 4) * 16 + cl % 16, element row % 4
+  const uint32_t* ri = (const uint32_t*)smem;
+  const int col = threadIdx.x % BNC, cgo = col / CR, cl = col % CR, cc = cl >> 4, j = cl & 15;
+  const int n = blockIdx.x * BNC + col;
+  const int nla = MODE == JOIN ? p.nl : 1;
+  bool bad = false;
+  for (int m = threadIdx.x / BNC; m < p.M; m += NT / BNC) {
+    int64_t v = 0;
+    for (int i = 0; i < nla; ++i) {
+      const int r = i * p.M + m, e = ((r >> 2) * 16 + j) * 4 + (r & 3);
+      uint32_t sum = 0;   // int32 sums wrap exactly; the total fits (|sum| <= K 2^14 < 2^31)
+#pragma unroll
+      for (int k2 = 0; k2 < KSW; ++k2) sum += ri[((k2 * CGW + cgo) * CWE + cc) * 256 + e];
+      v += (int64_t)(int32_t)sum << (8 * i);
+    }
+    if (n < p.N) finalize<MODE>(p, m, n, v, bad);
+  }
+}
+
+// =====================================================================================================
 // host planning and dispatch
 // =====================================================================================================
 // tile configurations: (WM, WN, TM, TN, S)
@@ -869,7 +944,8 @@ struct TileShape {
 static const TileShape kTiles[5] = {{2, 2, 2, 2, 64, 3},    // 128 x 128, 64x64 wave tiles (prefill)
                                     {2, 2, 1, 2, 64, 3},    // 64 x 128 (few tiles)
                                     {2, 1, 1, 1, 64, 8},    // 64 x 32, deep ring (<= 64 output rows, decode)
-                                    {2, 2, 1, 1, 64, 8},    // 64 x 64, deep ring (int8 decode, 65..128 limb rows)
+                                    {2, 2, 1, 1, 64, 4},    // 64 x 64 (int8 decode, 65..128 limb rows; 4 stages
+                                                            // measured faster than 8: 17.3 vs 18.2 us)
                                     {2, 2, 1, 1, 64, 3}};   // 64 x 64 (exact, when 64 x 128 tiles fill half the chip)
 // 5 accumulator sets: 32x64 wave tiles. Two stages: the next stage's loads are issued right after the barrier
 // that frees its buffer. A third stage was measured slower (config-3 down 1730-1810 vs 1900-1960 TOPS, gate / up
@@ -879,6 +955,7 @@ static const TileShape kTileExact = {4, 2, 1, 2, 64, 2};
 
 struct Plan {
   int wide;                       // wide kernel configuration (0: none)
+  int staged;                     // staged kernel configuration (0: none)
   bool gemv;
   int rb, cg, ks_waves, u, spw;   // gemv
   int parts, mp;                  // gemv row parts, output rows per part
@@ -960,11 +1037,31 @@ static int wide_cfg(int rows_a, int N, int K, bool exact) {
   return W_E96;
 }
 
+// staged configuration (int8, <= 8 stacked rows: one 16-row MFMA block, activations are a small share of a
+// CU's bytes): S_C8 = 8-column blocks of K / 1024 waves when that makes 1..2 blocks per CU (down: N = 2048,
+// K = 8192); S_C64 = 64-column blocks of 2 x 4 waves over K = 2048 when there is a block per CU (gate / up)
+enum StagedCfg { S_NONE = 0, S_C8 = 1, S_C64 = 2 };
+
+static int staged_cfg(int rows_a, int N, int K, bool exact, int cus) {
+  if (exact || rows_a > 8) return S_NONE;
+  const int b8 = (N + 7) / 8;
+  if (K % 1024 == 0 && (K / 1024 == 2 || K / 1024 == 4 || K / 1024 == 8 || K / 1024 == 16) && b8 >= cus &&
+      b8 <= 2 * cus)
+    return S_C8;
+  if (K == 2048 && (N + 63) / 64 >= cus) return S_C64;
+  return S_NONE;
+}
+
 static Plan make_plan(int rows_a, int M_out, int N, int K, int nb, int na, bool exact) {
   Plan s = {};
   const int cus = device_cus();
   const int nst = (K + 63) / 64;
   s.wide = wide_cfg(rows_a, N, K, exact);
+  s.staged = staged_cfg(rows_a, N, K, exact, cus);
+  if (s.staged != S_NONE) {
+    s.split = 1;
+    return s;
+  }
   // int8 decode with 65..128 stacked rows over a wide N (>= one 64-column tile per CU): 64 x 64 tiles with an
   // 8-stage ring read each weight once (17.2 vs 22.3 us for the gemv's two row parts at M = 64, N = 16384); at
   // N = 8192 the tiles would fill half the chip and the gemv stays faster
@@ -1115,7 +1212,7 @@ static int launch_tile(LinArgs& p, const Plan& s, hipStream_t st) {
   if constexpr (NA * NB == 9)
     if (s.tile == T_SMALL) return launch_tile_cfg<NA, NB, MODE, 2, 2, 1, 1, 64, 3>(p, s, st);
   if constexpr (NB == 1) {
-    if (s.tile == T_DEC) return launch_tile_cfg<NA, NB, MODE, 2, 2, 1, 1, 64, 8>(p, s, st);
+    if (s.tile == T_DEC) return launch_tile_cfg<NA, NB, MODE, 2, 2, 1, 1, 64, 4>(p, s, st);
   }
   return launch_tile_cfg<NA, NB, MODE, 2, 1, 1, 1, 64, 8>(p, s, st);
 }
@@ -1135,6 +1232,29 @@ static int launch_wide(LinArgs& p, const Plan& s, hipStream_t st) {
   // weight offsets of a block are 32-bit buffer offsets
   BX_REQUIRE((int64_t)p.ld_plane * 2 + (int64_t)64 * p.ld_row + p.K < (1LL << 31), "weight span exceeds 2^31 bytes");
   return launch_wide_cfg<3, 3, 2, 4, 128, MODE>(p, s, st);        // 96 limb rows: q of up to 32 tokens
+}
+
+template <int CW, int CGW, int KSW, int KW, int C8, int MODE>
+static int launch_staged_cfg(LinArgs& p, hipStream_t st) {
+  constexpr int CR = C8 ? 8 : 16 * CW, BNC = CR * CGW, NW = CGW * KSW;
+  const size_t lds = std::max((size_t)NW * (CR * KW / 1024) * 1040, (size_t)NW * (C8 ? 1 : CW) * 1024);
+  BX_REQUIRE(p.rows_a <= 16 && p.K == KSW * KW, "staged plan shape");
+  allow_lds(staged_kernel<CW, CGW, KSW, KW, C8, MODE>, lds);
+  staged_kernel<CW, CGW, KSW, KW, C8, MODE><<<(p.N + BNC - 1) / BNC, 64 * NW, lds, st>>>(p);
+  return check_launch("staged_kernel");
+}
+
+template <int MODE>
+static int launch_staged(LinArgs& p, const Plan& s, hipStream_t st) {
+  // activation offsets are 32-bit buffer offsets
+  BX_REQUIRE((int64_t)p.rows_a * p.K < kBufRange - 16, "activations span more than 2 GiB");
+  if (s.staged == S_C64) return launch_staged_cfg<2, 2, 4, 512, 0, MODE>(p, st);
+  switch (p.K / 1024) {
+    case 2: return launch_staged_cfg<1, 1, 2, 1024, 1, MODE>(p, st);
+    case 4: return launch_staged_cfg<1, 1, 4, 1024, 1, MODE>(p, st);
+    case 8: return launch_staged_cfg<1, 1, 8, 1024, 1, MODE>(p, st);
+    default: return launch_staged_cfg<1, 1, 16, 1024, 1, MODE>(p, st);
+  }
 }
 
 static bool aligned16(const void* x) { return ((uintptr_t)x & 15) == 0; }
@@ -1223,6 +1343,7 @@ static int int8_common(LinArgs& p, int mode, int64_t ws_bytes, hipStream_t st) {
   const int na = mode == RAW32 ? 1 : p.nl;
   const Plan s = make_plan(p.rows_a, p.M, p.N, p.K, 1, na, false);
   if (int rc = need_ws(p, s, ws_bytes, nullptr, 0)) return rc;
+  if (s.staged) return mode == JOIN ? launch_staged<JOIN>(p, s, st) : launch_staged<RAW32>(p, s, st);
   if (s.gemv) return mode == JOIN ? launch_gemv<1, JOIN>(p, s, st) : launch_gemv<1, RAW32>(p, s, st);
   if (mode == RAW32) return launch_tile<1, 1, RAW32>(p, s, st);
   if (p.nl == 1) return launch_tile<1, 1, JOIN>(p, s, st);

@@ -189,7 +189,7 @@ def test_int_mm_join(dev, M, nl):
     assert np.array_equal(y.cpu().numpy(), ref)
 
 
-@pytest.mark.parametrize("M", [1, 8, 33, 64])
+@pytest.mark.parametrize("M", [1, 4, 8, 33, 64])
 @pytest.mark.parametrize("N,K", [(8192, 2048), (2048, 8192), (16384, 2048)])
 def test_config2_int8_decode(dev, M, N, K):
     """Config 2 shapes at full size: int8 uniform weights, N(0,1) activations in 2 limbs."""
@@ -230,3 +230,24 @@ def test_standalone_epilogue_and_lin_y(dev):
         T3 = torch.stack([T[0] - X, X])                  # two split partials summing to T
         y3 = wmm.lin_y(T3, (qd, ec, ev), d, gg, shd)
         assert np.array_equal(y3.cpu().numpy(), ref)
+
+
+@pytest.mark.parametrize("N,K", [(2048, 2048), (2044, 4096), (2048, 8192), (2050, 16384), (16384, 2048)])
+def test_int8_staged_rows(dev, N, K):
+    """int8 decode with <= 8 stacked rows (the staged kernel: 8-column blocks over K / 1024 waves, or 64-column
+    blocks at K = 2048), join and raw int32 modes, against the float64 oracle."""
+    from bitexact.int8.gemm_skinny import int_mm, int_mm_join
+    g = np.random.default_rng(N + K)
+    w = g.integers(-127, 128, (N, K)).astype(np.int8)
+    w[0, :] = -127
+    for M in (1, 2, 3, 4):
+        z = g.integers(-(1 << 44), 1 << 44, (M, K))
+        q, _, _ = R.quant_rows(z, 2)
+        a = R.stack_limbs(q, 2)
+        y = int_mm_join(torch.from_numpy(a).to(dev), torch.from_numpy(w).to(dev), M, 2)
+        assert np.array_equal(y.cpu().numpy(), R.imm(q, w)), (M, "join")
+    for Rr in (1, 5, 8):
+        a = g.integers(-128, 128, (Rr, K)).astype(np.int8)
+        a[0, :] = -128
+        c = int_mm(torch.from_numpy(a).to(dev), torch.from_numpy(w).to(dev))
+        assert np.array_equal(c.cpu().numpy().astype(np.int64), R.imm(a, w)), (Rr, "raw")
