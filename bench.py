@@ -39,7 +39,7 @@ HBM_PEAK_GBS = 8000.0
 # HBM bytes per decode launch (average over the step's 6 GEMMs) from rocprofv3 --pmc FETCH_SIZE and WRITE_SIZE
 # runs of `bench.py --eager --no-prefill --no-attn --no-cpu --no-engine`, each scaled by what the same counter reads
 # for a plain 1 GiB device copy (profiles/decode_gemv_config2_hbm_traffic.txt).
-DECODE_TRAFFIC_PER_LAUNCH = 30065861
+DECODE_TRAFFIC_PER_LAUNCH = 30036526
 INT8_PEAK_TOPS = 5000.0
 # The reference's int8 MLP issues gate and up as one GEMM over wgu = cat(gate, up) [2 x 8192, 2048]
 # (src/bitexact/int8/consts.py:68, src/bitexact/int8/model.py:106), then down; the step follows that call pattern.
@@ -436,7 +436,8 @@ def main():
                                   "wgu (K=2048, N=2x8192), down (K=8192, N=2048), 2 activation limbs, int64 joined "
                                   "output",
                       "gemms_per_step": launches, "bytes_per_step": step_bytes, "weight_rotation": ">=1 GiB/shape"},
-           "roofline": {"bound": "hbm", "kernel": "gemv_kernel (each of the step's decode GEMMs is one launch)",
+           "roofline": {"bound": "hbm",
+                        "kernel": "decode GEMM launches (staged_kernel M=1, gemv_kernel, tile_kernel T_DEC M=64 gate|up)",
                         "achieved": r(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                         "frac": r(None if achieved is None else achieved / HBM_PEAK_GBS, 4),
                         "traffic": DECODE_TRAFFIC_PER_LAUNCH, "algorithmic_bytes_per_launch": step_bytes // launches,

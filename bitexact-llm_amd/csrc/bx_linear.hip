@@ -13,7 +13,9 @@
 //    reads are bank-conflict free); 32x64 wave tiles of v_mfma_i32_32x32x32_i8 run the NA x NB limb products
 //    into NA + NB - 1 int32 accumulators by limb weight i + j (|acc| <= 3 K 2^14 < 2^31 for K < 43690), joined
 //    in int64 in registers. Exact mode reads int8 limb planes of q written by split_q_kernel.
-// Both split K over blocks when the tile grid is small: partials meet in an int64 workspace with atomics and
+//  * staged_kernel (int8 decode, <= 8 stacked rows): weight k-slices copied into LDS as contiguous 1 KiB pieces,
+//    MFMA from LDS, no split-K. wide_kernel (exact decode, 65..96 limb rows) is described at its definition.
+// The gemv and tile kernels split K over blocks when the tile grid is small: partials meet in an int64 workspace with atomics and
 // the last block of a tile (device-scope counter) applies the epilogue and re-zeroes workspace and counter,
 // so one launch does everything. Integer sums are exact in any order, so tiles, splits and schedules never
 // change a bit.
