@@ -24,6 +24,37 @@ namespace bx {
 
 constexpr int kFK = 17, kFZ = 26, kFP = 22, kFT2 = 26, kExp2Bits = 14, kExp2One = 60;
 
+// A weight is exactly 0 once n >= FP + 2: the interpolated table value v lies in [0, 2^60] (the table falls
+// from 2^60), and rshc(v, 60 - FP + n) with a shift of at least 62 rounds it to 0 whatever entry was read. Such
+// scores (most of them: softmax weights are mostly negligible) read entry 0, so their loads share one cache
+// line instead of scattering over the 128 KiB table.
+constexpr int64_t kZeroN = kFP + 2;
+
+// attn_weight in two halves, so that a caller can issue the table loads of many scores before using any:
+// WeightAt holds the table position of one score (always inside the table: 0 <= idx < 2^14, whatever z is,
+// so loads for hidden keys are safe and their weight is discarded).
+struct WeightAt {
+  int64_t n, rr;
+  int idx;
+};
+
+__device__ __forceinline__ WeightAt weight_at(int64_t z, int64_t zshift, int64_t l2e) {
+  int64_t zf = rshc(z, zshift);
+  zf = imin(zf, 48LL << kFZ);
+  const int64_t t = rshc(mul_wrap(zf, l2e), kFZ + 28 - kFT2);
+  const int64_t f = t & ((1LL << kFT2) - 1);
+  WeightAt w;
+  w.n = t >> kFT2;
+  w.idx = w.n < kZeroN ? (int)(f >> (kFT2 - kExp2Bits)) : 0;
+  w.rr = f & ((1LL << (kFT2 - kExp2Bits)) - 1);
+  return w;
+}
+
+__device__ __forceinline__ int64_t weight_of(const WeightAt& w, int64_t a, int64_t b) {
+  const int64_t v = add_wrap(a, rshc(mul_wrap(b - a, w.rr), kFT2 - kExp2Bits));
+  return rshc(v, kExp2One - kFP + w.n);
+}
+
 // softmax_w's weight of one visible key (src/bitexact/exact/ops.py:133-143 over exp2neg_lut, 108-116).
 __device__ __forceinline__ int64_t attn_weight(int64_t z, int64_t zshift, const int64_t* lut, int64_t l2e) {
   int64_t zf = rshc(z, zshift);
@@ -31,7 +62,7 @@ __device__ __forceinline__ int64_t attn_weight(int64_t z, int64_t zshift, const 
   const int64_t t = rshc(mul_wrap(zf, l2e), kFZ + 28 - kFT2);
   const int64_t n = t >> kFT2;
   const int64_t f = t & ((1LL << kFT2) - 1);
-  const int64_t idx = f >> (kFT2 - kExp2Bits);
+  const int64_t idx = n < kZeroN ? f >> (kFT2 - kExp2Bits) : 0;
   const int64_t rr = f & ((1LL << (kFT2 - kExp2Bits)) - 1);
   const int64_t a = lut[idx];
   const int64_t v = add_wrap(a, rshc(mul_wrap(lut[idx + 1] - a, rr), kFT2 - kExp2Bits));
@@ -829,15 +860,35 @@ __global__ __launch_bounds__(256, HD == 64 ? 2 : 1) void attn_pre_kernel(AttnArg
     pre_store<HD>(sm, kv, true);
     __syncthreads();
     if (t + 1 < ntile) pre_load<HD>(p, kv, z, (t + 1) * 64, kb_end, true);
+    // per 16-key block, its 8 table loads are issued before any weight is formed (a load under a per-score
+    // branch would wait alone); NKB blocks at a time
+    constexpr int NKB = 1;
 #pragma unroll
-    for (int kb = 0; kb < 4; ++kb) {
-      int64_t raw[4];
-      pre_scores<HD>(sm, qa, kb, raw);
+    for (int kb2 = 0; kb2 < 4; kb2 += NKB) {
+      WeightAt wa[NKB][4];
+      int64_t ta[NKB][4], tb[NKB][4];
+#pragma unroll
+      for (int h = 0; h < NKB; ++h) {
+        int64_t raw[4];
+        pre_scores<HD>(sm, qa, kb2 + h, raw);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) wa[h][e] = weight_at(mx[e] - raw[e], shift[e], p.l2e);
+      }
+#pragma unroll
+      for (int h = 0; h < NKB; ++h)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          ta[h][e] = p.lut[wa[h][e].idx];
+          tb[h][e] = p.lut[wa[h][e].idx + 1];
+        }
+#pragma unroll
+      for (int h = 0; h < NKB; ++h) {
+      const int kb = kb2 + h;
       const int s = t * 64 + kb * 16 + (lane & 15);
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
-        int64_t pw = 0;
-        if (s < kb_end && s <= qpos[e]) pw = attn_weight(mx[e] - raw[e], shift[e], p.lut, p.l2e);
+        const int64_t w8 = weight_of(wa[h][e], ta[h][e], tb[h][e]);
+        const int64_t pw = (s < kb_end && s <= qpos[e]) ? w8 : 0;
         den[e] += pw;
         int32_t x = (int32_t)pw;                         // 0 <= p <= 2^22: three limbs
         const int32_t a0 = limb_lo(x);
@@ -848,6 +899,7 @@ __global__ __launch_bounds__(256, HD == 64 ? 2 : 1) void attn_pre_kernel(AttnArg
         sm.Pl[w][0][row][col] = (int8_t)a0;
         sm.Pl[w][1][row][col] = (int8_t)a1;
         sm.Pl[w][2][row][col] = (int8_t)limb_lo(x);
+      }
       }
     }
     __builtin_amdgcn_s_waitcnt(0xc07f);                  // this wave's LDS writes are done
