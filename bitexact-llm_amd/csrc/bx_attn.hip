@@ -75,9 +75,14 @@ __device__ __forceinline__ int64_t attn_weight(int64_t z, int64_t zshift, const 
 // rsh(e^z 2^FE, FE - FP) of z at step 2^-FA over [EXP_MIN, 0], 0 below it.
 constexpr int64_t kI8ZClamp = -(1LL << 38);
 constexpr int64_t kI8ZLo = -32LL * 4096;         // EXP_MIN << FA: table index 0
-__device__ __forceinline__ int64_t int8_weight(int64_t d, int zsh, int64_t zmul, const int32_t* ptab) {
+// The table index of int8_weight (negative: weight 0).
+__device__ __forceinline__ int64_t int8_index(int64_t d, int zsh, int64_t zmul) {
   const int64_t z = zmul == 0 ? rsh64(d, zsh) : rsh64(mul_wrap(imax(d, kI8ZClamp), zmul), zsh);
-  const int64_t idx = imax(z, kI8ZLo - 1) - kI8ZLo;
+  return imax(z, kI8ZLo - 1) - kI8ZLo;
+}
+
+__device__ __forceinline__ int64_t int8_weight(int64_t d, int zsh, int64_t zmul, const int32_t* ptab) {
+  const int64_t idx = int8_index(d, zsh, zmul);
   return idx >= 0 ? (int64_t)ptab[idx] : 0;
 }
 
@@ -425,10 +430,12 @@ struct KvRegs {
   v4i v[3][HD / 64];
 };
 
+// The cache block of key s (the block table entry: one load, issued an iteration ahead of the rows it locates).
+__device__ __forceinline__ int dec_page(const AttnArgs& p, int64_t brow, int s) { return p.bt[brow * p.sbt + s / p.bs]; }
+
 template <int HD, bool WANT_K, bool WANT_V>
-__device__ __forceinline__ void dec_load(const AttnArgs& p, int64_t brow, int h, int s, KvRegs<HD>& r) {
+__device__ __forceinline__ void dec_rows(const AttnArgs& p, int blk, int h, int s, KvRegs<HD>& r) {
   const int c = (threadIdx.x & 63) >> 4;
-  const int blk = p.bt[brow * p.sbt + s / p.bs];
   const int8_t* row = p.cache + (int64_t)blk * p.sc_nb + (int64_t)h * p.sc_h + (int64_t)(s % p.bs) * p.sc_bs + c * 16;
 #pragma unroll
   for (int j = 0; j < 3; ++j)
@@ -548,10 +555,15 @@ __global__ __launch_bounds__(kDecWaves * 64) void attn_dec_kernel(AttnArgs p) {
   if (PHASE == 0 || NS == 1) {
     int64_t best = kNeg;
     KvRegs<HD> cur, nxt;
-    if (w < nb16) dec_load<HD, true, false>(p, brow, h, min(lo + w * 16 + kl, hi - 1), cur);
+    // pipeline per wave: rows of block b + 8 and the page of block b + 16 are requested while block b is used
+    int pg = 0;
+    if (w < nb16) dec_rows<HD, true, false>(p, dec_page(p, brow, min(lo + w * 16 + kl, hi - 1)), h,
+                                            min(lo + w * 16 + kl, hi - 1), cur);
+    if (w + kDecWaves < nb16) pg = dec_page(p, brow, min(lo + (w + kDecWaves) * 16 + kl, hi - 1));
     for (int b = w; b < nb16; b += kDecWaves) {
       const int s = lo + b * 16 + kl;
-      if (b + kDecWaves < nb16) dec_load<HD, true, false>(p, brow, h, min(s + 16 * kDecWaves, hi - 1), nxt);
+      if (b + kDecWaves < nb16) dec_rows<HD, true, false>(p, pg, h, min(s + 16 * kDecWaves, hi - 1), nxt);
+      if (b + 2 * kDecWaves < nb16) pg = dec_page(p, brow, min(s + 32 * kDecWaves, hi - 1));
       const int64_t raw = dec_score<HD>(qa, cur);
       if (RAW && s < hi && s - lo < p.S) raw_cache[qo * p.S + (s - lo)] = raw;
       if (s < hi && s <= my_qpos) best = imax(best, raw);
@@ -582,14 +594,29 @@ __global__ __launch_bounds__(kDecWaves * 64) void attn_dec_kernel(AttnArgs p) {
 #pragma unroll
     for (int kk = 0; kk < KK; ++kk) num[i][kk] = 0;
   KvRegs<HD> cur, nxt;
-  if (w < nb16) dec_load<HD, !RAW, true>(p, brow, h, min(lo + w * 16 + kl, hi - 1), cur);
+  int pg = 0;
+  if (w < nb16) dec_rows<HD, !RAW, true>(p, dec_page(p, brow, min(lo + w * 16 + kl, hi - 1)), h,
+                                        min(lo + w * 16 + kl, hi - 1), cur);
+  if (w + kDecWaves < nb16) pg = dec_page(p, brow, min(lo + (w + kDecWaves) * 16 + kl, hi - 1));
   for (int b = w; b < nb16; b += kDecWaves) {
     const int s = lo + b * 16 + kl;
-    if (b + kDecWaves < nb16) dec_load<HD, !RAW, true>(p, brow, h, min(s + 16 * kDecWaves, hi - 1), nxt);
     const int64_t raw = RAW ? (s < hi && s - lo < p.S ? raw_cache[qo * p.S + (s - lo)] : 0) : dec_score<HD>(qa, cur);
-    int64_t pw = 0;
-    if (qo < nvalid && s < hi && s <= my_qpos)
-      pw = p.wrule == 0 ? attn_weight(mx - raw, shift, p.lut, p.l2e) : int8_weight(raw - mx, p.zsh, p.zmul, p.ptab);
+    // the weight's table loads go out before the next block's requests (loads complete in order: waiting for
+    // them then does not wait for the prefetch) and unconditionally (a hidden key's weight is discarded)
+    WeightAt wat;
+    int64_t ta = 0, tb = 0, i8 = 0;
+    if (p.wrule == 0) {
+      wat = weight_at(mx - raw, shift, p.l2e);
+      ta = p.lut[wat.idx];
+      tb = p.lut[wat.idx + 1];
+    } else {
+      i8 = int8_index(raw - mx, p.zsh, p.zmul);
+      ta = p.ptab[imin(imax(i8, 0), -kI8ZLo)];   // a visible key has d <= 0, so idx <= -kI8ZLo (z = 0)
+    }
+    if (b + kDecWaves < nb16) dec_rows<HD, !RAW, true>(p, pg, h, min(s + 16 * kDecWaves, hi - 1), nxt);
+    if (b + 2 * kDecWaves < nb16) pg = dec_page(p, brow, min(s + 32 * kDecWaves, hi - 1));
+    int64_t pw = p.wrule == 0 ? weight_of(wat, ta, tb) : (i8 >= 0 ? ta : 0);
+    if (!(qo < nvalid && s < hi && s <= my_qpos)) pw = 0;
     den += pw;
     sm.Ps[w][qo][kl] = (int32_t)pw;
     const int c = lane >> 4;

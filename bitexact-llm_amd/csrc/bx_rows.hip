@@ -12,6 +12,7 @@ constexpr int64_t kNegBig = -(1LL << 20);      // ops.NEG_BIG
 constexpr int kQB = 22;                        // |q| <= 2^22
 
 constexpr int kRowThreads = 1024;
+constexpr int kRowU = 4;   // elements per thread whose loads are issued together
 
 __device__ __forceinline__ int64_t block_max64(int64_t v, int64_t* sbuf) {
   v = wave_max64(v);
@@ -99,14 +100,27 @@ __global__ __launch_bounds__(kRowThreads) void norm_quant_kernel(NormArgs p) {
   const int32_t* er_row = nullptr;
   if (SRC == SRC_EMB) er_row = p.emb + p.ids[blockIdx.x] * (int64_t)D;
   int64_t amax = 0;
-  for (int i = threadIdx.x; i < D; i += kRowThreads) {
-    int64_t v;
-    if (SRC == SRC_EMB) v = er_row[i];
-    else if (SRC == SRC_ADD) v = add_wrap(xr[i], p.y[(int64_t)blockIdx.x * p.ldy + i]);
-    else v = xr[i];
-    if (SRC != SRC_X) xr[i] = v;
-    Xs[i] = v;
-    amax = imax(amax, v < 0 ? -v : v);
+  // kRowU elements per thread at a time, every load issued before the first store (the write-back to x could
+  // alias later loads, which would otherwise wait for it one element at a time)
+  const int64_t* yr = SRC == SRC_ADD ? p.y + (int64_t)blockIdx.x * p.ldy : nullptr;
+  for (int i0 = threadIdx.x; i0 < D; i0 += kRowU * kRowThreads) {
+    int64_t v[kRowU];
+#pragma unroll
+    for (int k = 0; k < kRowU; ++k) {
+      const int i = min(i0 + k * kRowThreads, D - 1);
+      if (SRC == SRC_EMB) v[k] = er_row[i];
+      else if (SRC == SRC_ADD) v[k] = add_wrap(xr[i], yr[i]);
+      else v[k] = xr[i];
+    }
+#pragma unroll
+    for (int k = 0; k < kRowU; ++k) {
+      const int i = i0 + k * kRowThreads;
+      if (i < D) {
+        if (SRC != SRC_X) xr[i] = v[k];
+        Xs[i] = v[k];
+        amax = imax(amax, v[k] < 0 ? -v[k] : v[k]);
+      }
+    }
   }
   amax = block_max64(amax, sbuf);
   if (threadIdx.x == 0 && amax >= (1LL << 40)) p.err[0] = 1;
@@ -124,10 +138,23 @@ __global__ __launch_bounds__(kRowThreads) void norm_quant_kernel(NormArgs p) {
   const int64_t V = s >= 0 ? shl(T, s) : sar(T, -s);
   const int64_t r = isqrt64(V), er = shx - p.FR - m;
   int64_t emax = kNegBig;
-  for (int i = threadIdx.x; i < D; i += kRowThreads) {
-    const int64_t P = div_round64(mul_wrap(Xs[i], p.gm[i]), p.ge[i] - p.FR - er + p.FN, r);
-    Ps[i] = P;
-    if (P != 0) emax = imax(emax, bitlen(P < 0 ? -P : P) - p.FN);
+  for (int i0 = threadIdx.x; i0 < D; i0 += kRowU * kRowThreads) {
+    int64_t gmv[kRowU], gev[kRowU];
+#pragma unroll
+    for (int k = 0; k < kRowU; ++k) {
+      const int i = min(i0 + k * kRowThreads, D - 1);
+      gmv[k] = p.gm[i];
+      gev[k] = p.ge[i];
+    }
+#pragma unroll
+    for (int k = 0; k < kRowU; ++k) {
+      const int i = i0 + k * kRowThreads;
+      if (i < D) {
+        const int64_t P = div_round64(mul_wrap(Xs[i], gmv[k]), gev[k] - p.FR - er + p.FN, r);
+        Ps[i] = P;
+        if (P != 0) emax = imax(emax, bitlen(P < 0 ? -P : P) - p.FN);
+      }
+    }
   }
   emax = block_max64(emax, sbuf);
   const int64_t shr = imax(emax - kQB, kNegBig);
@@ -141,11 +168,11 @@ __global__ __launch_bounds__(kRowThreads) void norm_quant_kernel(NormArgs p) {
 // with bitlen(|s|) + bitlen(|u|) > 62). ----
 constexpr int64_t kL2E30 = 1549082005LL;   // round(log2(e) 2^30) (ops.L2E30)
 
-__device__ __forceinline__ int64_t exp2neg30(int64_t t, const int64_t* lut) {   // ops.exp2neg_lut(t, lut, 30)
+// ops.exp2neg_lut(t, lut, 30) given the two table entries a = lut[idx], b = lut[idx + 1] at idx = (t mod 2^26) >> 12
+__device__ __forceinline__ int64_t exp2neg30_from(int64_t t, int64_t a, int64_t b) {
   const int64_t n = t >> 26, f = t & ((1LL << 26) - 1);
-  const int64_t idx = f >> 12, rr = f & 4095;
-  const int64_t a = lut[idx];
-  const int64_t v = add_wrap(a, rshc(mul_wrap(lut[idx + 1] - a, rr), 12));
+  const int64_t rr = f & 4095;
+  const int64_t v = add_wrap(a, rshc(mul_wrap(b - a, rr), 12));
   return rshc(v, 30 + n);
 }
 
@@ -158,12 +185,33 @@ __global__ __launch_bounds__(kRowThreads) void silu_quant_kernel(const int64_t* 
   const int eps = -2 * FR;
   int64_t emax = kNegBig;
   int bad = 0;
-  for (int i = threadIdx.x; i < ff; i += kRowThreads) {
-    const int64_t g = row[i], u = row[ff + i];
+  // kSiluU elements per thread at a time: their row loads, then their table loads, are issued together (one
+  // element after another, each waited for its own two dependent loads)
+  constexpr int kSiluU = 4;
+  for (int i0 = threadIdx.x; i0 < ff; i0 += kSiluU * kRowThreads) {
+  int64_t gv[kSiluU], uv[kSiluU], la[kSiluU], lb[kSiluU];
+#pragma unroll
+  for (int k = 0; k < kSiluU; ++k) {
+    const int i = min(i0 + k * kRowThreads, ff - 1);
+    gv[k] = row[i];
+    uv[k] = row[ff + i];
+  }
+#pragma unroll
+  for (int k = 0; k < kSiluU; ++k) {
+    const int64_t g = gv[k];
     const int64_t ga = g < 0 ? (int64_t)(0 - (uint64_t)g) : g;
-    const int64_t a = imin(ga, 64LL << FR);
-    const int64_t t = rshc(a * kL2E30, FR + 4);              // FR + 30 - FT2
-    const int64_t E = exp2neg30(t, lut);
+    const int64_t t = rshc(imin(ga, 64LL << FR) * kL2E30, FR + 4);   // FR + 30 - FT2
+    const int idx = (int)((t & ((1LL << 26) - 1)) >> 12);
+    la[k] = lut[idx];
+    lb[k] = lut[idx + 1];
+  }
+#pragma unroll
+  for (int k = 0; k < kSiluU; ++k) {
+    const int i = i0 + k * kRowThreads;
+    if (i >= ff) continue;
+    const int64_t g = gv[k], u = uv[k];
+    const int64_t ga = g < 0 ? (int64_t)(0 - (uint64_t)g) : g;
+    const int64_t E = exp2neg30_from(rshc(imin(ga, 64LL << FR) * kL2E30, FR + 4), la[k], lb[k]);
     const int64_t den = (1LL << 30) + E;
     const int64_t sig = g >= 0 ? fdiv_fast((1LL << 61) + den, 2 * den) : fdiv_fast(2 * (E << 30) + den, 2 * den);
     const int64_t gc = imin(imax(g, -(1LL << 32)), 1LL << 32);
@@ -174,6 +222,7 @@ __global__ __launch_bounds__(kRowThreads) void silu_quant_kernel(const int64_t* 
     const int64_t P = mul_wrap(sv, u);
     Ps[i] = P;
     if (P != 0) emax = imax(emax, bitlen(P < 0 ? (int64_t)(0 - (uint64_t)P) : P) + eps);
+  }
   }
   if (bad) err[0] = 1;
   emax = block_max64(emax, sbuf);
