@@ -251,3 +251,30 @@ def test_int8_staged_rows(dev, N, K):
         a[0, :] = -128
         c = int_mm(torch.from_numpy(a).to(dev), torch.from_numpy(w).to(dev))
         assert np.array_equal(c.cpu().numpy().astype(np.int64), R.imm(a, w)), (Rr, "raw")
+
+
+@pytest.mark.parametrize("M", [8, 100, 200])
+def test_exact_linear_dense_residual_rows(dev, M):
+    """Rows whose residual lists are long: one element of 2^20 sets the row grid at 2^-3, so every ordinary
+    N(0, 0.02) element of the row lands in the residual (hundreds of ELL entries; the epilogue keeps the first
+    4 of a column in registers and reads the rest from memory). M = 8: gemv path; 100, 200: tile path."""
+    from bitexact.vllm_plugin.exact_gemm import exact_linear
+    N, K = 160, 512
+    w = _bf16(N, K, 21)
+    for n in (1, 7, 64, 159):
+        w[n, (n * 7) % K] = 2.0 ** 20
+    dec = _dec(w)
+    limbs = torch.from_numpy(dec["limbs"]).to(dev)
+    d, gg = torch.from_numpy(dec["d"]).to(dev), torch.from_numpy(dec["g"]).to(dev)
+    cnt, ec, ev, Rr = _ell(dec, N, dev)
+    assert Rr > 64
+    g = np.random.default_rng(M + 5)
+    q = g.integers(-(1 << 22), (1 << 22) + 1, (M, K))
+    sh = g.integers(-30, -20, M)
+    ref, rflag, _ = R.epilogue(R.wmm_f64(q, dec["W"]), R.residual(q, dec["rr"], dec["rc"], dec["rv"], N),
+                               dec["d"], dec["g"], sh, R.FR, True)
+    flag = torch.zeros(1, dtype=torch.int32, device=dev)
+    y = exact_linear(torch.from_numpy(q).to(torch.int32).to(dev), torch.from_numpy(sh).to(dev), limbs, d, gg,
+                     cnt, ec, ev, Rr, flag, True)
+    assert np.array_equal(y.cpu().numpy(), ref), M
+    assert bool(flag.item()) == rflag, M
