@@ -92,11 +92,12 @@ def test_exact_linear_matches_oracle(dev, M):
         assert bool(flag.item()) == rflag, (M, lim)
 
 
-@pytest.mark.parametrize("M,N", [(22, 16384), (32, 16400), (42, 16384)])
-def test_exact_linear_wide_rows(dev, M, N):
-    """65..128 stacked limb rows over a wide N (the every-row strip path; N = 16400 leaves a partial column tile)."""
+@pytest.mark.parametrize("M,N,K", [(22, 16384, 512), (32, 16400, 512), (42, 16384, 512), (32, 2048, 512),
+                                   (27, 3000, 512), (32, 2048, 8192), (32, 3072, 2048)])
+def test_exact_linear_wide_rows(dev, M, N, K):
+    """65..96 limb rows: the wide kernel at N >= 8192 (every weight once; N = 16400 leaves a partial column tile),
+    the gemv's row parts below (N = 3000 leaves a partial column tile)."""
     from bitexact.vllm_plugin.exact_gemm import exact_linear
-    K = 512
     w = _bf16(N, K, 5)
     dec = _dec(w)
     limbs = torch.from_numpy(dec["limbs"]).to(dev)
