@@ -525,7 +525,7 @@ __global__ __launch_bounds__(256) void split_q_kernel(const int32_t* q, int64_t 
 // chunk slots, so the 16 lanes of each MFMA operand read phase hit 16 distinct bank groups.
 template <int BK>
 __device__ __forceinline__ int swz(int row) {
-  return BK == 64 ? (row >> 2) & 3 : (row >> 3) & 1;
+  return BK == 128 ? row & 7 : BK == 64 ? (row >> 2) & 3 : (row >> 3) & 1;
 }
 
 __device__ __forceinline__ void async16(const void* g, void* lds_base) {
@@ -535,7 +535,7 @@ __device__ __forceinline__ void async16(const void* g, void* lds_base) {
 
 template <int NA, int NB, int MODE, int WM, int WN, int TM, int TN, int BK, int S>
 __global__ __launch_bounds__(WM * WN * 64) void tile_kernel(LinArgs p) {
-  static_assert(BK == 32 || BK == 64, "k tile");
+  static_assert(BK == 32 || BK == 64 || BK == 128, "k tile");
   constexpr int NW = WM * WN;
   constexpr int BM = 32 * TM * WM, BN = 32 * TN * WN;
   constexpr int NS = NA + NB - 1;
@@ -946,8 +946,9 @@ struct TileShape {
 static const TileShape kTiles[5] = {{2, 2, 2, 2, 64, 3},    // 128 x 128, 64x64 wave tiles (prefill)
                                     {2, 2, 1, 2, 64, 3},    // 64 x 128 (few tiles)
                                     {2, 1, 1, 1, 64, 8},    // 64 x 32, deep ring (<= 64 output rows, decode)
-                                    {2, 2, 1, 1, 64, 4},    // 64 x 64 (int8 decode, 65..128 limb rows; 4 stages
-                                                            // measured faster than 8: 17.3 vs 18.2 us)
+                                    {2, 2, 1, 1, 128, 4},   // 64 x 64 (int8 decode, 65..128 limb rows): 128-byte
+                                                            // k tiles, so a load instruction covers 8 rows x a
+                                                            // whole 128-byte line (15.6 vs 17.4 us at BK = 64)
                                     {2, 2, 1, 1, 64, 3}};   // 64 x 64 (exact, when 64 x 128 tiles fill half the chip)
 // 5 accumulator sets: 32x64 wave tiles. Two stages: the next stage's loads are issued right after the barrier
 // that frees its buffer. A third stage was measured slower (config-3 down 1730-1810 vs 1900-1960 TOPS, gate / up
@@ -1112,15 +1113,16 @@ static Plan make_plan(int rows_a, int M_out, int N, int K, int nb, int na, bool 
     s.tiles_x = (N + BN - 1) / BN;
     s.tiles_y = (M_out + BM - 1) / BM;
     const int tiles = s.tiles_x * s.tiles_y;
+    const int nkt = (K + ts.bk - 1) / ts.bk;             // k tiles of this configuration
     int split = 1;
     if (2 * tiles < cus) {
       split = (cus + tiles - 1) / tiles;
-      const int max_split = nst / 4 > 1 ? nst / 4 : 1;   // keep >= 4 k tiles per split
+      const int max_split = nkt / 4 > 1 ? nkt / 4 : 1;   // keep >= 4 k tiles per split
       split = split > max_split ? max_split : split;
     }
-    const int kper = (nst + split - 1) / split;
-    s.kbytes = kper * 64;
-    s.split = (nst + kper - 1) / kper;
+    const int kper = (nkt + split - 1) / split;
+    s.kbytes = kper * ts.bk;                             // a split's K range: whole k tiles
+    s.split = (nkt + kper - 1) / kper;
     s.lds = (size_t)ts.stages * (na * BM + nb * BN) * ts.bk;
     if (exact) s.tmp_bytes = 3LL * M_out * K;
   }
@@ -1214,7 +1216,7 @@ static int launch_tile(LinArgs& p, const Plan& s, hipStream_t st) {
   if constexpr (NA * NB == 9)
     if (s.tile == T_SMALL) return launch_tile_cfg<NA, NB, MODE, 2, 2, 1, 1, 64, 3>(p, s, st);
   if constexpr (NB == 1) {
-    if (s.tile == T_DEC) return launch_tile_cfg<NA, NB, MODE, 2, 2, 1, 1, 64, 4>(p, s, st);
+    if (s.tile == T_DEC) return launch_tile_cfg<NA, NB, MODE, 2, 2, 1, 1, 128, 4>(p, s, st);
   }
   return launch_tile_cfg<NA, NB, MODE, 2, 1, 1, 1, 64, 8>(p, s, st);
 }

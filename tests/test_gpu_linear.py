@@ -279,3 +279,19 @@ def test_exact_linear_dense_residual_rows(dev, M):
                      cnt, ec, ev, Rr, flag, True)
     assert np.array_equal(y.cpu().numpy(), ref), M
     assert bool(flag.item()) == rflag, M
+
+
+@pytest.mark.parametrize("M", [33, 64])
+@pytest.mark.parametrize("K", [1008, 2112])
+def test_int8_tdec_k_tails(dev, M, K):
+    """int8 decode with 65..128 stacked rows at N = 16384 (64 x 64 tiles with 128-byte k tiles): K not a multiple
+    of the k tile (the last tile is partial and masked)."""
+    from bitexact.int8.gemm_skinny import int_mm_join
+    N = 16384
+    g = np.random.default_rng(M * 7 + K)
+    z = g.integers(-(1 << 44), 1 << 44, (M, K))
+    q, _, _ = R.quant_rows(z, 2)
+    a = R.stack_limbs(q, 2)
+    w = g.integers(-127, 128, (N, K)).astype(np.int8)
+    y = int_mm_join(torch.from_numpy(a).to(dev), torch.from_numpy(w).to(dev), M, 2)
+    assert np.array_equal(y.cpu().numpy(), R.imm(q, w))
