@@ -949,7 +949,7 @@ static const TileShape kTiles[5] = {{2, 2, 2, 2, 64, 3},    // 128 x 128, 64x64 
                                     {2, 2, 1, 1, 128, 4},   // 64 x 64 (int8 decode, 65..128 limb rows): 128-byte
                                                             // k tiles, so a load instruction covers 8 rows x a
                                                             // whole 128-byte line (15.6 vs 17.4 us at BK = 64)
-                                    {2, 2, 1, 1, 64, 3}};   // 64 x 64 (exact, when 64 x 128 tiles fill half the chip)
+                                    {2, 2, 1, 1, 128, 2}};  // 64 x 64 (exact, when 64 x 128 tiles fill half the chip)
 // 5 accumulator sets: 32x64 wave tiles. Two stages: the next stage's loads are issued right after the barrier
 // that frees its buffer. A third stage was measured slower (config-3 down 1730-1810 vs 1900-1960 TOPS, gate / up
 // 1700-1830 vs 1890-1930). A CU streams at most ~35 GB/s even from L2 (measured), so a second stage in flight adds
@@ -1214,7 +1214,7 @@ static int launch_tile(LinArgs& p, const Plan& s, hipStream_t st) {
   }
   if (s.tile == T_MID) return launch_tile_cfg<NA, NB, MODE, 2, 2, 1, 2, 64, 3>(p, s, st);
   if constexpr (NA * NB == 9)
-    if (s.tile == T_SMALL) return launch_tile_cfg<NA, NB, MODE, 2, 2, 1, 1, 64, 3>(p, s, st);
+    if (s.tile == T_SMALL) return launch_tile_cfg<NA, NB, MODE, 2, 2, 1, 1, 128, 2>(p, s, st);
   if constexpr (NB == 1) {
     if (s.tile == T_DEC) return launch_tile_cfg<NA, NB, MODE, 2, 2, 1, 1, 128, 4>(p, s, st);
   }
