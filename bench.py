@@ -39,7 +39,7 @@ HBM_PEAK_GBS = 8000.0
 # HBM bytes per decode launch (average over the step's 6 GEMMs) from rocprofv3 --pmc FETCH_SIZE and WRITE_SIZE
 # runs of `bench.py --eager --no-prefill --no-attn --no-cpu --no-engine`, each scaled by what the same counter reads
 # for a plain 1 GiB device copy (profiles/decode_gemv_config2_hbm_traffic.txt).
-DECODE_TRAFFIC_PER_LAUNCH = 30036526
+DECODE_TRAFFIC_PER_LAUNCH = 30040422
 INT8_PEAK_TOPS = 5000.0
 # The reference's int8 MLP issues gate and up as one GEMM over wgu = cat(gate, up) [2 x 8192, 2048]
 # (src/bitexact/int8/consts.py:68, src/bitexact/int8/model.py:106), then down; the step follows that call pattern.
