@@ -254,15 +254,15 @@ def test_int8_staged_rows(dev, N, K):
         assert np.array_equal(c.cpu().numpy().astype(np.int64), R.imm(a, w)), (Rr, "raw")
 
 
-@pytest.mark.parametrize("M", [8, 100, 200])
-def test_exact_linear_dense_residual_rows(dev, M):
+@pytest.mark.parametrize("M,N,K", [(8, 160, 512), (100, 160, 512), (200, 160, 512), (300, 1024, 2048)])
+def test_exact_linear_dense_residual_rows(dev, M, N, K):
     """Rows whose residual lists are long: one element of 2^20 sets the row grid at 2^-3, so every ordinary
     N(0, 0.02) element of the row lands in the residual (hundreds of ELL entries; the epilogue keeps the first
-    4 of a column in registers and reads the rest from memory). M = 8: gemv path; 100, 200: tile path."""
+    4 of a column in registers and reads the rest from memory). M = 8: gemv path; 100, 200: 64 x 64 tiles;
+    300 x 1024 x 2048: 64 x 64 tiles with K split in 4 (the last block of a tile applies the epilogue)."""
     from bitexact.vllm_plugin.exact_gemm import exact_linear
-    N, K = 160, 512
     w = _bf16(N, K, 21)
-    for n in (1, 7, 64, 159):
+    for n in (1, 7, 64, N - 1):
         w[n, (n * 7) % K] = 2.0 ** 20
     dec = _dec(w)
     limbs = torch.from_numpy(dec["limbs"]).to(dev)
