@@ -241,13 +241,13 @@ def test_int8_staged_rows(dev, N, K):
     g = np.random.default_rng(N + K)
     w = g.integers(-127, 128, (N, K)).astype(np.int8)
     w[0, :] = -127
-    for M in (1, 2, 3, 4):
+    for M in (1, 2, 3, 4, 5, 8):   # 5, 8: 10 and 16 stacked rows (the gemv)
         z = g.integers(-(1 << 44), 1 << 44, (M, K))
         q, _, _ = R.quant_rows(z, 2)
         a = R.stack_limbs(q, 2)
         y = int_mm_join(torch.from_numpy(a).to(dev), torch.from_numpy(w).to(dev), M, 2)
         assert np.array_equal(y.cpu().numpy(), R.imm(q, w)), (M, "join")
-    for Rr in (1, 5, 8):
+    for Rr in (1, 5, 8, 13, 16):
         a = g.integers(-128, 128, (Rr, K)).astype(np.int8)
         a[0, :] = -128
         c = int_mm(torch.from_numpy(a).to(dev), torch.from_numpy(w).to(dev))
