@@ -52,6 +52,8 @@ SIGNATURES = {
                                          I32, I32, P, P]),
     "bx_rope_qgroup": (ctypes.c_int, [P, I64, P, I64, I64, P, P, I32, I32, I32, I32, I32, I32, I32, I32, I32, I32,
                                       I32, P, P, P, P, P, P]),
+    "bx_rope_qgroup_store": (ctypes.c_int, [P, I64, P, I64, I64, P, P, I32, I32, I32, I32, I32, I32, I32, I32, I32,
+                                            I32, I32, P, P, P, P, P, I64, I64, I64, P, I32, P, P]),
     "bx_int8_quant_rows": (ctypes.c_int, [P, I64, I32, I32, I32, I32, P, P, P, P, P, P]),
     "bx_int8_post": (ctypes.c_int, [P, I64, P, I32, P, P, I32, P, I64, I32, I32, P, P]),
 }

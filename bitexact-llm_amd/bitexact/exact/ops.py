@@ -91,10 +91,13 @@ def attn_out(num, den, T, hkv):
     return q, sh
 
 
-def qkv_y(y, pos, cos, sin, B, T, dm, err=None, flag=None):
+def qkv_y(y, pos, cos, sin, B, T, dm, err=None, flag=None, store=None):
     """Segs.qkv_y (src/bitexact/exact/segs.py:170-173): y int64 [B T, (H + 2 HKV) HD] at FR, pos int64 [B, T],
     cos / sin int64 [n_pos, HD / 2] at FT, dm = (H, HKV, HD) -> qg int32 [B HKV, g T, HD], shg int64
-    [B HKV, g T, 1], k / v int64 [B, T, HKV, HD], err (bool tensor, or'ed into `err`)."""
+    [B HKV, g T, 1], k / v int64 [B, T, HKV, HD], err (bool tensor, or'ed into `err`).
+    store = (cache, slot): exact_fuse.qkv's fused store (src/bitexact/vllm_plugin/exact_fuse.py:372-386): K / V go
+    straight into the limb-plane cache (int8 [nb, HKV, bs, 8 HD]) at slot [B T] (< 0: skipped), and k / v are
+    returned as None."""
     _hip.require_cuda(y, pos, cos, sin)
     H, HKV, HD = dm
     assert y.dtype == torch.int64 and y.stride(-1) == 1 and y.shape[0] == B * T
@@ -106,9 +109,20 @@ def qkv_y(y, pos, cos, sin, B, T, dm, err=None, flag=None):
     assert cos.shape == sin.shape and cos.shape[1] == HD // 2
     qg = torch.empty(B * HKV, g * T, HD, dtype=torch.int32, device=dev)
     shg = torch.empty(B * HKV, g * T, 1, dtype=torch.long, device=dev)
+    fl = _flag(dev, flag)
+    if store is not None:
+        c, slot = store
+        _hip.require_cuda(c, slot)
+        assert c.dtype == torch.int8 and c.dim() == 4 and c.shape[1] == HKV and c.shape[3] >= 6 * HD and c.stride(3) == 1
+        slot = slot.reshape(-1).contiguous().long()
+        assert slot.shape[0] == B * T
+        _hip.call("bx_rope_qgroup_store", _hip.ptr(y), y.stride(0), _hip.ptr(pos), pos.stride(0), pos.stride(1),
+                  _hip.ptr(cos), _hip.ptr(sin), cos.shape[0], B, T, H, HKV, HD, FR, FT, FK, FV, FZ, _hip.ptr(qg),
+                  _hip.ptr(shg), None, None, _hip.ptr(c), c.stride(0), c.stride(1), c.stride(2), _hip.ptr(slot),
+                  c.shape[2], _hip.ptr(fl), _hip.stream_of(y))
+        return qg, shg, None, None, _or(err, fl, flag)
     k = torch.empty(B, T, HKV, HD, dtype=torch.long, device=dev)
     v = torch.empty(B, T, HKV, HD, dtype=torch.long, device=dev)
-    fl = _flag(dev, flag)
     _hip.call("bx_rope_qgroup", _hip.ptr(y), y.stride(0), _hip.ptr(pos), pos.stride(0), pos.stride(1),
               _hip.ptr(cos), _hip.ptr(sin), cos.shape[0], B, T, H, HKV, HD, FR, FT, FK, FV, FZ, _hip.ptr(qg),
               _hip.ptr(shg), _hip.ptr(k), _hip.ptr(v), _hip.ptr(fl), _hip.stream_of(y))

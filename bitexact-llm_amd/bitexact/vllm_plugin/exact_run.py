@@ -69,8 +69,8 @@ class ExactEngine:
         x, q, sh, _ = ops.embed_norm(self.emb, ids, *self.ga[0], flag=fl)
         for i in range(self.L):
             y = self.fused[i, "wqkv"](q, sh, fl, False)
-            qg, shg, k, v, _ = ops.qkv_y(y, pos.view(N, 1), self.cos, self.sin, N, 1, (self.H, HKV, HD), flag=fl)
-            tri_paged.store(kvs[i], slot, k[:, 0], v[:, 0])
+            qg, shg, _, _, _ = ops.qkv_y(y, pos.view(N, 1), self.cos, self.sin, N, 1, (self.H, HKV, HD), flag=fl,
+                                         store=(kvs[i], slot))   # K / V into the cache (exact_fuse.qkv)
             num, den = tri_exact_attn.attend(qg.view(N, HKV, G, HD), shg.view(N, HKV, G), qpos, kvs[i], bt, rmap,
                                              self.exp2, self.l2e)
             qo, sho = ops.attn_out(num.view(N * HKV, G, HD), den.view(N * HKV, G, 1), 1, HKV)

@@ -38,10 +38,31 @@ struct RopeArgs {
   int FR, FT, FK, FV, FZ;
   int32_t* qg;             // [B HKV, g T, HD]
   int64_t* shg;            // [B HKV, g T]
-  int64_t* k;              // [B, T, HKV, HD]
+  int64_t* k;              // [B, T, HKV, HD] (null: not written)
   int64_t* v;
   int32_t* err;
+  int8_t* cache;           // paged limb-plane cache [nb][HKV][bs][8 HD] (null: no store)
+  int64_t sc_nb, sc_h, sc_bs;
+  const int64_t* slot;     // [B T] cache slot of each token (< 0: not stored)
+  int bs;
 };
+
+// The three int8 limbs of a K (plane 0) or V (plane 3) value into the paged cache at the token's slot, as the
+// reference's fused qkv kernel stores them (src/bitexact/vllm_plugin/exact_fuse.py:223-236; tri_paged.store's
+// layout, src/bitexact/vllm_plugin/tri_paged.py:311-335): limb i at byte (plane + i) HD + d of the slot's row.
+__device__ __forceinline__ void store_limbs(const RopeArgs& p, int token, int h, int plane, int d, int64_t x) {
+  if (!p.cache) return;
+  const int64_t sl = p.slot[token];
+  if (sl < 0) return;                                  // dummy / padded tokens carry slot -1
+  int8_t* base = p.cache + (sl / p.bs) * p.sc_nb + h * p.sc_h + (sl % p.bs) * p.sc_bs + (int64_t)plane * p.HD + d;
+  int32_t r = (int32_t)x;                              // |x| <= 8355711: three signed base-256 limbs
+#pragma unroll
+  for (int i = 0; i < 3; ++i) {
+    const int32_t l = limb_lo(r);
+    base[i * p.HD] = (int8_t)l;
+    r = (r - l) >> 8;
+  }
+}
 
 // One block per token; wave w takes head rows w, w + 4, ...; lane l holds dims l + 64 e.
 template <int HD>
@@ -91,21 +112,21 @@ __global__ __launch_bounds__(256) void rope_qgroup_kernel(RopeArgs p) {
       if (lane == 0) p.shg[row] = shq;
     } else if (hr < p.H + p.HKV) {
       const int kh = hr - p.H;
-      int64_t* kr = p.k + ((int64_t)token * p.HKV + kh) * HD;
 #pragma unroll
       for (int e = 0; e < E; ++e) {
         const int64_t kv = rshc(out[e], p.FR + p.FT - p.FK);
         bad |= kv > kLim3 || kv < -kLim3;
-        kr[lane + 64 * e] = kv;
+        if (p.k) p.k[((int64_t)token * p.HKV + kh) * HD + lane + 64 * e] = kv;
+        store_limbs(p, token, kh, 0, lane + 64 * e, kv);
       }
     } else {
       const int vh = hr - p.H - p.HKV;
-      int64_t* vr = p.v + ((int64_t)token * p.HKV + vh) * HD;
 #pragma unroll
       for (int e = 0; e < E; ++e) {
         const int64_t vv = rshc(out[e], p.FR - p.FV);
         bad |= vv > kLim3 || vv < -kLim3;
-        vr[lane + 64 * e] = vv;
+        if (p.v) p.v[((int64_t)token * p.HKV + vh) * HD + lane + 64 * e] = vv;
+        store_limbs(p, token, vh, 3, lane + 64 * e, vv);
       }
     }
   }
@@ -201,17 +222,46 @@ __global__ __launch_bounds__(256) void exact_epilogue_kernel(const int64_t* T, i
 
 using namespace bx;
 
+static int rope_common(const int64_t* y, int64_t ldy, const int64_t* pos, int64_t spb, int64_t spt,
+                       const int64_t* cos, const int64_t* sin, int32_t npos, int32_t B, int32_t T, int32_t H,
+                       int32_t HKV, int32_t HD, int32_t FR, int32_t FT, int32_t FK, int32_t FV, int32_t FZ,
+                       int32_t* qg, int64_t* shg, int64_t* k, int64_t* v, int32_t* err, int8_t* cache, int64_t sc_nb,
+                       int64_t sc_h, int64_t sc_bs, const int64_t* slot, int32_t bs, hipStream_t stream);
+
 extern "C" int bx_rope_qgroup(const int64_t* y, int64_t ldy, const int64_t* pos, int64_t spb, int64_t spt,
                               const int64_t* cos, const int64_t* sin, int32_t npos, int32_t B, int32_t T, int32_t H,
                               int32_t HKV, int32_t HD, int32_t FR, int32_t FT, int32_t FK, int32_t FV, int32_t FZ,
                               int32_t* qg, int64_t* shg, int64_t* k, int64_t* v, int32_t* err, bx_stream_t stream) {
+  BX_REQUIRE(k && v, "null pointer");
+  return rope_common(y, ldy, pos, spb, spt, cos, sin, npos, B, T, H, HKV, HD, FR, FT, FK, FV, FZ, qg, shg, k, v, err,
+                     nullptr, 0, 0, 0, nullptr, 1, (hipStream_t)stream);
+}
+
+extern "C" int bx_rope_qgroup_store(const int64_t* y, int64_t ldy, const int64_t* pos, int64_t spb, int64_t spt,
+                                    const int64_t* cos, const int64_t* sin, int32_t npos, int32_t B, int32_t T,
+                                    int32_t H, int32_t HKV, int32_t HD, int32_t FR, int32_t FT, int32_t FK, int32_t FV,
+                                    int32_t FZ, int32_t* qg, int64_t* shg, int64_t* k, int64_t* v, int8_t* cache,
+                                    int64_t sc_nb, int64_t sc_h, int64_t sc_bs, const int64_t* slot, int32_t bs,
+                                    int32_t* err, bx_stream_t stream) {
+  BX_REQUIRE(cache && slot && bs > 0, "null cache / slot");
+  BX_REQUIRE(sc_bs >= 8LL * HD && sc_h >= (int64_t)bs * sc_bs && sc_nb >= (int64_t)HKV * sc_h, "cache strides");
+  return rope_common(y, ldy, pos, spb, spt, cos, sin, npos, B, T, H, HKV, HD, FR, FT, FK, FV, FZ, qg, shg, k, v, err,
+                     cache, sc_nb, sc_h, sc_bs, slot, bs, (hipStream_t)stream);
+}
+
+static int rope_common(const int64_t* y, int64_t ldy, const int64_t* pos, int64_t spb, int64_t spt,
+                       const int64_t* cos, const int64_t* sin, int32_t npos, int32_t B, int32_t T, int32_t H,
+                       int32_t HKV, int32_t HD, int32_t FR, int32_t FT, int32_t FK, int32_t FV, int32_t FZ,
+                       int32_t* qg, int64_t* shg, int64_t* k, int64_t* v, int32_t* err, int8_t* cache, int64_t sc_nb,
+                       int64_t sc_h, int64_t sc_bs, const int64_t* slot, int32_t bs, hipStream_t stream) {
   BX_REQUIRE(B >= 0 && T >= 0 && H > 0 && HKV > 0 && H % HKV == 0, "bad head counts");
   BX_REQUIRE(HD == 64 || HD == 128, "head_dim 64 or 128");
   BX_REQUIRE(ldy >= (int64_t)(H + 2 * HKV) * HD, "ldy too small");
   BX_REQUIRE(npos > 0, "empty rope tables");
   if (B == 0 || T == 0) return BX_OK;
-  BX_REQUIRE(y && pos && cos && sin && qg && shg && k && v && err, "null pointer");
-  RopeArgs p = {y, ldy, pos, spb, spt, cos, sin, npos, B, T, H, HKV, HD, FR, FT, FK, FV, FZ, qg, shg, k, v, err};
+  BX_REQUIRE(y && pos && cos && sin && qg && shg && err, "null pointer");
+  RopeArgs p = {y, ldy, pos, spb, spt, cos, sin, npos, B, T, H, HKV, HD, FR, FT, FK, FV, FZ, qg, shg, k, v, err,
+                cache, sc_nb, sc_h, sc_bs, slot, bs};
   const int blocks = B * T;
   if (HD == 64)
     rope_qgroup_kernel<64><<<blocks, 256, 0, (hipStream_t)stream>>>(p);

@@ -187,6 +187,18 @@ int bx_rope_qgroup(const int64_t* y, int64_t ldy, const int64_t* pos, int64_t sp
                    int32_t FR, int32_t FT, int32_t FK, int32_t FV, int32_t FZ, int32_t* qg, int64_t* shg, int64_t* k,
                    int64_t* v, int32_t* err, bx_stream_t stream);
 
+/* Replaces exact_fuse._qkv_kernel with STORE (src/bitexact/vllm_plugin/exact_fuse.py:179-236, called by
+ * exact_fuse.qkv, 372-386): bx_rope_qgroup, and the K / V values stored as three int8 limb planes into the paged
+ * cache (tri_paged.store's layout, src/bitexact/vllm_plugin/tri_paged.py:311-335) at slot[token] (cache int8
+ * [nb][HKV][bs][8 HD] with byte strides sc_nb, sc_h, sc_bs; tokens with slot < 0 are not stored). k / v may be
+ * null (then only the cache receives them). */
+int bx_rope_qgroup_store(const int64_t* y, int64_t ldy, const int64_t* pos, int64_t spb, int64_t spt,
+                         const int64_t* cos, const int64_t* sin, int32_t npos, int32_t B, int32_t T, int32_t H,
+                         int32_t HKV, int32_t HD, int32_t FR, int32_t FT, int32_t FK, int32_t FV, int32_t FZ,
+                         int32_t* qg, int64_t* shg, int64_t* k, int64_t* v, int8_t* cache, int64_t sc_nb,
+                         int64_t sc_h, int64_t sc_bs, const int64_t* slot, int32_t bs, int32_t* err,
+                         bx_stream_t stream);
+
 /* Replaces wmm.epilogue and segs.lin_y (src/bitexact/exact/wmm.py:132-150, src/bitexact/exact/segs.py:25-32): T int64
  * [nsplit, M, N] split partials (slice stride sts, row stride ldt) summed, residual B int64 [M, ldb] or (B null)
  * the ELL gather sum_j q[m, ell_col[n, j]] ell_val[n, j] (R entries per column), then y = round((T 2^d + B)

@@ -82,3 +82,29 @@ def test_int8_post(dev):
         y, flag = segs.post(acc.to(dev), m.to(dev), fmsh, mant.to(dev), e.to(dev))
         ry, rflag = R.int8_post(acc.numpy(), m.numpy(), fmsh, mant.numpy(), e.numpy())
         assert np.array_equal(y.cpu().numpy(), ry) and bool(flag) == rflag
+
+
+@pytest.mark.parametrize("HD,H,HKV,B,T,bs", [(64, 8, 2, 2, 5, 16), (128, 4, 2, 3, 7, 4), (64, 32, 8, 32, 1, 16)])
+def test_rope_qgroup_store(dev, HD, H, HKV, B, T, bs):
+    """The fused rope + cache store (exact_fuse.qkv with STORE) writes the same cache bytes as the separate
+    rope + tri_paged.store, skips slot < 0 and leaves every other cache byte as it was."""
+    from bitexact.exact import ops
+    from bitexact.vllm_plugin import tri_paged
+    g = torch.Generator().manual_seed(HD * T + B)
+    cos, sin = _tables(300, HD)
+    c, s = torch.from_numpy(cos).to(dev), torch.from_numpy(sin).to(dev)
+    y = torch.randint(-(1 << 30), 1 << 30, (B * T, (H + 2 * HKV) * HD), generator=g).to(dev)
+    pos = torch.randint(0, 300, (B, T), generator=g).to(dev)
+    nb = (B * T + bs - 1) // bs + 2
+    slot = torch.randperm(nb * bs, generator=g)[:B * T]
+    slot[1] = -1
+    slot = slot.to(dev)
+    c0 = torch.randint(-128, 128, (nb, HKV, bs, 8 * HD), generator=g, dtype=torch.int8).to(dev)
+    qg, shg, k, v, err = ops.qkv_y(y, pos, c, s, B, T, (H, HKV, HD))
+    ref = c0.clone()
+    tri_paged.store(ref, slot, k.view(B * T, HKV, HD), v.view(B * T, HKV, HD))
+    got = c0.clone()
+    qg2, shg2, k2, v2, err2 = ops.qkv_y(y, pos, c, s, B, T, (H, HKV, HD), store=(got, slot))
+    assert k2 is None and v2 is None
+    assert torch.equal(qg, qg2) and torch.equal(shg, shg2) and bool(err) == bool(err2)
+    assert torch.equal(got, ref)
