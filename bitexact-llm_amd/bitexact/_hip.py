@@ -23,6 +23,8 @@ SIGNATURES = {
     "bx_last_error": (ctypes.c_char_p, []),
     "bx_exact_linear": (ctypes.c_int, [P, I64, P, P, I64, I64, P, P, P, P, P, I32, P, I32, I32, I32, I32, I32, P,
                                        P, I64, P, I64, P]),
+    "bx_exact_linear_planes": (ctypes.c_int, [P, I64, P, P, I64, I64, P, P, P, P, P, I32, P, I32, I32, I32, I32,
+                                              I32, P, P, I64, P, P]),
     "bx_exact_linear_workspace": (I64, [I32, I32, I32]),
     "bx_exact_linear_scratch": (I64, [I32, I32, I32]),
     "bx_exact_wmm": (ctypes.c_int, [P, I64, P, I64, I64, P, I32, I32, I32, P, I64, P, I64, P]),
@@ -41,6 +43,7 @@ SIGNATURES = {
                                    I32, I32, P]),
     "bx_rmsnorm_quant": (ctypes.c_int, [P, I64, P, P, P, I64, P, I32, I32, I32, I32, P, P]),
     "bx_add_rmsnorm_quant": (ctypes.c_int, [P, I64, P, I64, P, P, P, I64, P, I32, I32, I32, I32, P, P]),
+    "bx_add_rmsnorm_quant_planes": (ctypes.c_int, [P, I64, P, I64, P, P, P, I64, P, P, I32, I32, I32, I32, P, P]),
     "bx_embed_rmsnorm_quant": (ctypes.c_int, [P, P, P, I64, P, P, P, I64, P, I32, I32, I32, I32, P, P]),
     "bx_silu_quant": (ctypes.c_int, [P, I64, I32, P, I32, P, I64, P, I32, P, P]),
     "bx_first_argmax": (ctypes.c_int, [P, I64, I32, I32, P, P]),

@@ -131,9 +131,10 @@ def qkv_y(y, pos, cos, sin, B, T, dm, err=None, flag=None, store=None):
 
 
 
-def add_norm_y(y, x, gm, ge, err=None, flag=None):
+def add_norm_y(y, x, gm, ge, err=None, flag=None, planes=False):
     """Segs.add_norm_y (src/bitexact/exact/segs.py:175-178): x int64 [M, D] += y (in place, as exact_fuse.add_norm's
-    store), then norm_quant of the sum. gm None: the add alone (returns q = sh = None)."""
+    store), then norm_quant of the sum. gm None: the add alone (returns q = sh = None). planes=True: q is returned
+    as (q, limb planes int8 [3, M, D]) for exact_linear's q_planes (the limb split done by the norm kernel)."""
     _hip.require_cuda(x, y)
     assert x.dtype == torch.int64 and y.dtype == torch.int64 and x.stride(-1) == 1 and y.stride(-1) == 1
     M, D = x.shape
@@ -146,6 +147,12 @@ def add_norm_y(y, x, gm, ge, err=None, flag=None):
     q = torch.empty(M, D, dtype=torch.int32, device=x.device)
     sh = torch.empty(M, dtype=torch.long, device=x.device)
     gm, ge = gm.contiguous().long(), ge.contiguous().long()
+    if planes:
+        pl = torch.empty(3, M, D, dtype=torch.int8, device=x.device)
+        _hip.call("bx_add_rmsnorm_quant_planes", _hip.ptr(x), x.stride(0), _hip.ptr(y), y.stride(0), _hip.ptr(gm),
+                  _hip.ptr(ge), _hip.ptr(q), D, _hip.ptr(sh), _hip.ptr(pl), M, D, FR, FN, _hip.ptr(fl),
+                  _hip.stream_of(x))
+        return x, (q, pl), sh, _or(err, fl, flag)
     _hip.call("bx_add_rmsnorm_quant", _hip.ptr(x), x.stride(0), _hip.ptr(y), y.stride(0), _hip.ptr(gm), _hip.ptr(ge),
               _hip.ptr(q), D, _hip.ptr(sh), M, D, FR, FN, _hip.ptr(fl), _hip.stream_of(x))
     return x, q, sh, _or(err, fl, flag)

@@ -11,8 +11,14 @@ from bitexact import _hip
 from bitexact.exact.consts import FR
 
 
-def exact_linear(q, sh, limbs, d, g, cnt, ec, ev, R, flag=None, checked=True, fr=FR):
-    """The fused exact linear on raw tensors; returns y (and sets flag)."""
+def needs_planes(M, N, K):
+    """Whether the exact linear at this shape reads q as int8 limb planes (then a caller that has them, from
+    ops.add_norm_y(planes=True), saves the split launch by passing them as q_planes)."""
+    return _hip.lib().bx_exact_linear_scratch(M, N, K) > 0
+
+
+def exact_linear(q, sh, limbs, d, g, cnt, ec, ev, R, flag=None, checked=True, fr=FR, q_planes=None):
+    """The fused exact linear on raw tensors; returns y (and sets flag). q_planes: q's int8 limb planes [3, M, K]."""
     _hip.require_cuda(q, limbs)
     assert q.dtype == torch.int32 and q.stride(1) == 1 and limbs.stride(2) == 1
     M, K = q.shape
@@ -22,6 +28,15 @@ def exact_linear(q, sh, limbs, d, g, cnt, ec, ev, R, flag=None, checked=True, fr
         assert flag is not None and flag.dtype == torch.int32
     y = torch.empty(M, N, dtype=torch.long, device=q.device)
     ws, wsb = _hip.workspace(q.device, _hip.lib().bx_exact_linear_workspace(M, N, K))
+    sh = sh.contiguous()
+    if q_planes is not None:
+        _hip.require_cuda(q_planes)
+        assert q_planes.dtype == torch.int8 and q_planes.shape == (3, M, K) and q_planes.is_contiguous()
+        _hip.call("bx_exact_linear_planes", _hip.ptr(q), q.stride(0), _hip.ptr(sh), _hip.ptr(limbs), limbs.stride(0),
+                  limbs.stride(1), _hip.ptr(d), _hip.ptr(g), _hip.ptr(cnt) if R else None,
+                  _hip.ptr(ec) if R else None, _hip.ptr(ev) if R else None, R, _hip.ptr(y), M, N, K, fr,
+                  int(checked), _hip.ptr(flag), _hip.ptr(ws), wsb, _hip.ptr(q_planes), _hip.stream_of(q))
+        return y
     tmp, tmpb = _hip.scratch(q.device, _hip.lib().bx_exact_linear_scratch(M, N, K))
     sh = sh.contiguous()
     _hip.call("bx_exact_linear", _hip.ptr(q), q.stride(0), _hip.ptr(sh), _hip.ptr(limbs), limbs.stride(0),
@@ -41,5 +56,9 @@ class FusedLin:
         self.has_res = self.R > 0
         self.cfg = cfg               # kept for signature parity; tiles never change the integers
 
-    def __call__(self, q, sh, flag, checked=True):
-        return exact_linear(q, sh, self.limbs, self.d, self.g, self.cnt, self.ec, self.ev, self.R, flag, checked)
+    def __call__(self, q, sh, flag, checked=True, q_planes=None):
+        return exact_linear(q, sh, self.limbs, self.d, self.g, self.cnt, self.ec, self.ev, self.R, flag, checked,
+                            q_planes=q_planes)
+
+    def needs_planes(self, M):
+        return needs_planes(M, self.N, self.limbs.shape[2])

@@ -74,8 +74,15 @@ class ExactEngine:
             num, den = tri_exact_attn.attend(qg.view(N, HKV, G, HD), shg.view(N, HKV, G), qpos, kvs[i], bt, rmap,
                                              self.exp2, self.l2e)
             qo, sho = ops.attn_out(num.view(N * HKV, G, HD), den.view(N * HKV, G, 1), 1, HKV)
-            x, q, sh, _ = ops.add_norm_y(self.fused[i, "wo"](qo, sho, fl, True), x, *self.gm[i], flag=fl)
-            q, sh, _ = ops.gu_silu_y(self.fused[i, "wgu"](q, sh, fl, False), self.exp2, flag=fl)
+            wgu = self.fused[i, "wgu"]
+            if wgu.needs_planes(N):   # the norm kernel also writes q's limb planes for the MFMA path
+                x, (q, pl), sh, _ = ops.add_norm_y(self.fused[i, "wo"](qo, sho, fl, True), x, *self.gm[i], flag=fl,
+                                                   planes=True)
+                y = wgu(q, sh, fl, False, q_planes=pl)
+            else:
+                x, q, sh, _ = ops.add_norm_y(self.fused[i, "wo"](qo, sho, fl, True), x, *self.gm[i], flag=fl)
+                y = wgu(q, sh, fl, False)
+            q, sh, _ = ops.gu_silu_y(y, self.exp2, flag=fl)
             nxt = self.ga[i + 1] if i + 1 < self.L else (None, None)
             x, q, sh, _ = ops.add_norm_y(self.fused[i, "wd"](q, sh, fl, True), x, *nxt, flag=fl)
         return x

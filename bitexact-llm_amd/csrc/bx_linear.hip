@@ -1277,7 +1277,8 @@ static int need_ws(const LinArgs& p, const Plan& s, int64_t ws_bytes, const void
 
 using namespace bx;
 
-static int exact_common(LinArgs& p, int mode, int64_t ws_bytes, void* tmp, int64_t tmp_bytes, hipStream_t st) {
+static int exact_common(LinArgs& p, int mode, int64_t ws_bytes, void* tmp, int64_t tmp_bytes, hipStream_t st,
+                        const int8_t* planes = nullptr) {
   BX_REQUIRE(p.M >= 0 && p.N >= 0 && p.K >= 0, "negative size");
   BX_REQUIRE(p.K % 16 == 0, "K %% 16 != 0 (K=%d)", p.K);
   BX_REQUIRE(p.K < 43690, "K >= 43690: int32 limb sums could overflow");
@@ -1287,15 +1288,20 @@ static int exact_common(LinArgs& p, int mode, int64_t ws_bytes, void* tmp, int64
   if (p.M == 0 || p.N == 0) return BX_OK;
   BX_REQUIRE(p.K > 0, "K == 0");
   p.rows_a = 3 * p.M;
-  const Plan s = make_plan(p.rows_a, p.M, p.N, p.K, 3, 3, true);
+  Plan s = make_plan(p.rows_a, p.M, p.N, p.K, 3, 3, true);
+  if (planes != nullptr) s.tmp_bytes = 0;   // the caller's limb planes replace the scratch
   if (int rc = need_ws(p, s, ws_bytes, tmp, tmp_bytes)) return rc;
   if (s.gemv) return mode == EXACT ? launch_gemv<3, EXACT>(p, s, st) : launch_gemv<3, WMM_T>(p, s, st);
-  int8_t* planes = (int8_t*)tmp;
-  const int64_t chunks = (int64_t)p.M * (p.K / 16);
-  const int blocks = (int)((chunks + 255) / 256 < 4096 ? (chunks + 255) / 256 : 4096);
-  split_q_kernel<<<blocks, 256, 0, st>>>(p.q, p.ldq, p.M, p.K, planes);
-  if (int rc = check_launch("split_q_kernel")) return rc;
-  p.a = planes;
+  if (planes != nullptr) {
+    p.a = planes;
+  } else {
+    int8_t* tp = (int8_t*)tmp;
+    const int64_t chunks = (int64_t)p.M * (p.K / 16);
+    const int blocks = (int)((chunks + 255) / 256 < 4096 ? (chunks + 255) / 256 : 4096);
+    split_q_kernel<<<blocks, 256, 0, st>>>(p.q, p.ldq, p.M, p.K, tp);
+    if (int rc = check_launch("split_q_kernel")) return rc;
+    p.a = tp;
+  }
   if (s.wide) return mode == EXACT ? launch_wide<EXACT>(p, s, st) : launch_wide<WMM_T>(p, s, st);
   return mode == EXACT ? launch_tile<3, 3, EXACT>(p, s, st) : launch_tile<3, 3, WMM_T>(p, s, st);
 }
@@ -1315,6 +1321,24 @@ extern "C" int bx_exact_linear(const int32_t* q, int64_t ldq, const int64_t* sh,
   BX_REQUIRE(!checked || flag, "checked needs a flag pointer");
   BX_REQUIRE(sh && d && g && y, "null pointer");
   return exact_common(p, EXACT, ws_bytes, tmp, tmp_bytes, (hipStream_t)stream);
+}
+
+extern "C" int bx_exact_linear_planes(const int32_t* q, int64_t ldq, const int64_t* sh, const int8_t* limbs,
+                                      int64_t ld_plane, int64_t ld_row, const int64_t* d, const int64_t* g,
+                                      const int32_t* ell_cnt, const int32_t* ell_col, const int64_t* ell_val,
+                                      int32_t R, int64_t* y, int32_t M, int32_t N, int32_t K, int32_t FR,
+                                      int32_t checked, int32_t* flag, void* ws, int64_t ws_bytes,
+                                      const int8_t* q_planes, bx_stream_t stream) {
+  BX_REQUIRE(q_planes && aligned16(q_planes), "q_planes: null or not 16-byte aligned");
+  LinArgs p = {};
+  p.q = q; p.ldq = ldq; p.w = limbs; p.ld_plane = ld_plane; p.ld_row = ld_row;
+  p.sh = sh; p.d = d; p.g = g; p.cnt = ell_cnt; p.ecol = ell_col; p.eval = ell_val; p.R = R;
+  p.out = y; p.flag = flag; p.checked = checked; p.FR = FR; p.M = M; p.N = N; p.K = K;
+  p.ws = (int64_t*)ws;
+  BX_REQUIRE(R >= 0 && (R == 0 || (ell_cnt && ell_col && ell_val)), "ELL residual arrays missing");
+  BX_REQUIRE(!checked || flag, "checked needs a flag pointer");
+  BX_REQUIRE(sh && d && g && y, "null pointer");
+  return exact_common(p, EXACT, ws_bytes, nullptr, 0, (hipStream_t)stream, q_planes);
 }
 
 extern "C" int bx_exact_wmm(const int32_t* q, int64_t ldq, const int8_t* limbs, int64_t ld_plane, int64_t ld_row,

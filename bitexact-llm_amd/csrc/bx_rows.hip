@@ -87,6 +87,8 @@ struct NormArgs {
   int64_t* sh;
   int D, lg, FR, FN;
   int32_t* err;
+  int8_t* planes;   // optional: q's signed int8 limb planes [3][M][D] (limb i of q[m][k] at i M D + m D + k)
+  int64_t plane;    // M D
 };
 
 template <int SRC>
@@ -158,7 +160,20 @@ __global__ __launch_bounds__(kRowThreads) void norm_quant_kernel(NormArgs p) {
   }
   emax = block_max64(emax, sbuf);
   const int64_t shr = imax(emax - kQB, kNegBig);
-  for (int i = threadIdx.x; i < D; i += kRowThreads) p.q[(int64_t)blockIdx.x * p.ldq + i] = (int32_t)rshc(Ps[i], shr + p.FN);
+  for (int i = threadIdx.x; i < D; i += kRowThreads) {
+    const int32_t qv = (int32_t)rshc(Ps[i], shr + p.FN);
+    p.q[(int64_t)blockIdx.x * p.ldq + i] = qv;
+    if (p.planes != nullptr) {   // the limb split of the exact GEMM's activation planes (split_q_kernel's)
+      int8_t* dst = p.planes + (int64_t)blockIdx.x * D + i;
+      int32_t r = qv;
+#pragma unroll
+      for (int l = 0; l < 3; ++l) {
+        const int32_t lo = limb_lo(r);
+        dst[l * p.plane] = (int8_t)lo;
+        r = (r - lo) >> 8;
+      }
+    }
+  }
   if (threadIdx.x == 0) p.sh[blockIdx.x] = shr;
 }
 
@@ -363,7 +378,7 @@ extern "C" int bx_rmsnorm_quant(const int64_t* x, int64_t ldx, const int64_t* gm
                                 int64_t ldq, int64_t* sh, int32_t M, int32_t D, int32_t FR, int32_t FN, int32_t* err,
                                 bx_stream_t stream) {
   BX_REQUIRE(gm && ge && q && sh, "null pointer");
-  NormArgs p = {const_cast<int64_t*>(x), ldx, nullptr, 0, nullptr, nullptr, gm, ge, q, ldq, sh, D, 0, FR, FN, err};
+  NormArgs p = {const_cast<int64_t*>(x), ldx, nullptr, 0, nullptr, nullptr, gm, ge, q, ldq, sh, D, 0, FR, FN, err, nullptr, 0};
   return launch_norm(p, SRC_X, M, stream);
 }
 
@@ -371,7 +386,18 @@ extern "C" int bx_add_rmsnorm_quant(int64_t* x, int64_t ldx, const int64_t* y, i
                                     const int64_t* ge, int32_t* q, int64_t ldq, int64_t* sh, int32_t M, int32_t D,
                                     int32_t FR, int32_t FN, int32_t* err, bx_stream_t stream) {
   BX_REQUIRE(y && ldy >= D, "y: null or ldy too small");
-  NormArgs p = {x, ldx, y, ldy, nullptr, nullptr, gm, ge, q, ldq, sh, D, 0, FR, FN, err};
+  NormArgs p = {x, ldx, y, ldy, nullptr, nullptr, gm, ge, q, ldq, sh, D, 0, FR, FN, err, nullptr, 0};
+  return launch_norm(p, SRC_ADD, M, stream);
+}
+
+extern "C" int bx_add_rmsnorm_quant_planes(int64_t* x, int64_t ldx, const int64_t* y, int64_t ldy, const int64_t* gm,
+                                           const int64_t* ge, int32_t* q, int64_t ldq, int64_t* sh, int8_t* planes,
+                                           int32_t M, int32_t D, int32_t FR, int32_t FN, int32_t* err,
+                                           bx_stream_t stream) {
+  BX_REQUIRE(y && ldy >= D, "y: null or ldy too small");
+  BX_REQUIRE(gm && ge && q && sh && planes, "null pointer");
+  BX_REQUIRE(D % 16 == 0, "D %% 16 != 0 (the limb planes are the exact GEMM's K-major operand)");
+  NormArgs p = {x, ldx, y, ldy, nullptr, nullptr, gm, ge, q, ldq, sh, D, 0, FR, FN, err, planes, (int64_t)M * D};
   return launch_norm(p, SRC_ADD, M, stream);
 }
 
@@ -379,7 +405,7 @@ extern "C" int bx_embed_rmsnorm_quant(const int32_t* emb, const int64_t* ids, in
                                       const int64_t* gm, const int64_t* ge, int32_t* q, int64_t ldq, int64_t* sh,
                                       int32_t M, int32_t D, int32_t FR, int32_t FN, int32_t* err, bx_stream_t stream) {
   BX_REQUIRE(emb && ids, "null pointer");
-  NormArgs p = {x, ldx, nullptr, 0, emb, ids, gm, ge, q, ldq, sh, D, 0, FR, FN, err};
+  NormArgs p = {x, ldx, nullptr, 0, emb, ids, gm, ge, q, ldq, sh, D, 0, FR, FN, err, nullptr, 0};
   return launch_norm(p, SRC_EMB, M, stream);
 }
 

@@ -47,6 +47,16 @@ int bx_exact_linear(const int32_t* q, int64_t ldq, const int64_t* sh, const int8
                     const int32_t* ell_col, const int64_t* ell_val, int32_t R, int64_t* y, int32_t M, int32_t N,
                     int32_t K, int32_t FR, int32_t checked, int32_t* flag, void* ws, int64_t ws_bytes, void* tmp,
                     int64_t tmp_bytes, bx_stream_t stream);
+/* bx_exact_linear with q's int8 limb planes supplied by the caller (q_planes int8 [3][M][K], limb i of q[m][k] at
+ * i M K + m K + k, as bx_add_rmsnorm_quant_planes writes them), so no limb-split launch and no scratch. q is still
+ * read (residual terms and the row-vector decode path). Same rule and arguments otherwise. Replaces the same
+ * reference calls as bx_exact_linear; the reference splits q into limb planes inside its GEMM kernels
+ * (src/bitexact/exact/wmm.py:79-121), so this entry has no separate reference counterpart. */
+int bx_exact_linear_planes(const int32_t* q, int64_t ldq, const int64_t* sh, const int8_t* limbs, int64_t ld_plane,
+                           int64_t ld_row, const int64_t* d, const int64_t* g, const int32_t* ell_cnt,
+                           const int32_t* ell_col, const int64_t* ell_val, int32_t R, int64_t* y, int32_t M,
+                           int32_t N, int32_t K, int32_t FR, int32_t checked, int32_t* flag, void* ws,
+                           int64_t ws_bytes, const int8_t* q_planes, bx_stream_t stream);
 int64_t bx_exact_linear_workspace(int32_t M, int32_t N, int32_t K);
 int64_t bx_exact_linear_scratch(int32_t M, int32_t N, int32_t K);
 
@@ -143,6 +153,13 @@ int bx_rmsnorm_quant(const int64_t* x, int64_t ldx, const int64_t* gm, const int
 int bx_add_rmsnorm_quant(int64_t* x, int64_t ldx, const int64_t* y, int64_t ldy, const int64_t* gm, const int64_t* ge,
                          int32_t* q, int64_t ldq, int64_t* sh, int32_t M, int32_t D, int32_t FR, int32_t FN, int32_t* err,
                          bx_stream_t stream);
+
+/* bx_add_rmsnorm_quant (gm required) that also writes the new q's signed int8 limb planes (planes int8
+ * [3][M][D], limb i of q[m][k] at i M D + m D + k) for bx_exact_linear_planes. D % 16 == 0. Replaces the same
+ * reference stage (exact_fuse.add_norm, src/bitexact/vllm_plugin/exact_fuse.py:361-364). */
+int bx_add_rmsnorm_quant_planes(int64_t* x, int64_t ldx, const int64_t* y, int64_t ldy, const int64_t* gm,
+                                const int64_t* ge, int32_t* q, int64_t ldq, int64_t* sh, int8_t* planes, int32_t M,
+                                int32_t D, int32_t FR, int32_t FN, int32_t* err, bx_stream_t stream);
 
 /* Replaces the model's `emb[ids].long()` + pre_norm (src/bitexact/exact/model.py:130-132; exact_fuse.embed_norm,
  * src/bitexact/vllm_plugin/exact_fuse.py:356-358): x[m] = emb[ids[m]] (emb int32 [V, D] at FR, widened to int64),

@@ -295,3 +295,35 @@ def test_int8_tdec_k_tails(dev, M, K):
     w = g.integers(-127, 128, (N, K)).astype(np.int8)
     y = int_mm_join(torch.from_numpy(a).to(dev), torch.from_numpy(w).to(dev), M, 2)
     assert np.array_equal(y.cpu().numpy(), R.imm(q, w))
+
+
+@pytest.mark.parametrize("M,N", [(32, 16384), (200, 2048), (8, 2048)])
+def test_exact_linear_norm_planes(dev, M, N):
+    """The add + norm kernel's limb planes fed to the exact linear (no split launch) give the same x, q, sh, y and
+    flag as the separate stages, and y matches the oracle: the wide kernel (M = 32, 96 limb rows), the tile kernel
+    (M = 200) and the row-vector path that ignores the planes (M = 8)."""
+    from bitexact.exact import ops
+    from bitexact.vllm_plugin.exact_gemm import exact_linear, needs_planes
+    K = 512
+    g = torch.Generator().manual_seed(M + N)
+    x = torch.randint(-(1 << 33), 1 << 33, (M, K), generator=g)
+    y = torch.randint(-(1 << 32), 1 << 32, (M, K), generator=g)
+    gm, ge = torch.randint(-255, 256, (K,), generator=g), torch.randint(-14, -6, (K,), generator=g)
+    x1, q1, sh1, e1 = ops.add_norm_y(y.to(dev), x.to(dev), gm.to(dev), ge.to(dev))
+    x2, (q2, pl), sh2, e2 = ops.add_norm_y(y.to(dev), x.to(dev), gm.to(dev), ge.to(dev), planes=True)
+    assert torch.equal(x1, x2) and torch.equal(q1, q2) and torch.equal(sh1, sh2) and bool(e1) == bool(e2)
+    assert pl.shape == (3, M, K)
+    assert needs_planes(M, N, K) == (M != 8)
+    dec = _dec(_bf16(N, K, 3))
+    limbs = torch.from_numpy(dec["limbs"]).to(dev)
+    d, gg = torch.from_numpy(dec["d"]).to(dev), torch.from_numpy(dec["g"]).to(dev)
+    cnt, ec, ev, Rr = _ell(dec, N, dev)
+    f1 = torch.zeros(1, dtype=torch.int32, device=dev)
+    f2 = torch.zeros(1, dtype=torch.int32, device=dev)
+    ya = exact_linear(q1, sh1, limbs, d, gg, cnt, ec, ev, Rr, f1, True)
+    yb = exact_linear(q2, sh2, limbs, d, gg, cnt, ec, ev, Rr, f2, True, q_planes=pl)
+    assert torch.equal(ya, yb) and f1.item() == f2.item()
+    qn, shn = q1.cpu().numpy().astype(np.int64), sh1.cpu().numpy()
+    ref, rflag, _ = R.epilogue(R.wmm_f64(qn, dec["W"]), R.residual(qn, dec["rr"], dec["rc"], dec["rv"], N),
+                               dec["d"], dec["g"], shn, R.FR, True)
+    assert np.array_equal(yb.cpu().numpy(), ref) and bool(f2.item()) == rflag
