@@ -128,7 +128,9 @@ int bx_exact_attn_prefill(const int32_t* qg, int64_t sq_z, int64_t sq_row, const
                           int64_t l2e, int64_t* num, int64_t* den, int32_t Z, int32_t gT, int32_t HD, bx_stream_t stream);
 
 /* Replaces tri_paged.store (src/bitexact/vllm_plugin/tri_paged.py:311-335): K / V (int32 or int64 [N, HKV, HD] with
- * token / head strides) written as 3 int8 limb planes each at cache slots slot int64 [N]; slot < 0 is skipped. */
+ * token / head strides) written as 3 int8 limb planes each at cache slots slot int64 [N]; slot < 0 is skipped.
+ * Slots are not range-checked on the device: slot < nb bs is the caller's contract, as for the reference's
+ * slot mapping. */
 int bx_kv_store(int8_t* cache, int64_t sc_nb, int64_t sc_h, int64_t sc_bs, int32_t bs, const int64_t* slot,
                 const void* k, int64_t skn, int64_t skh, const void* v, int64_t svn, int64_t svh, int32_t elem_bytes,
                 int32_t N, int32_t HKV, int32_t HD, bx_stream_t stream);
@@ -208,7 +210,7 @@ int bx_rope_qgroup(const int64_t* y, int64_t ldy, const int64_t* pos, int64_t sp
  * exact_fuse.qkv, 372-386): bx_rope_qgroup, and the K / V values stored as three int8 limb planes into the paged
  * cache (tri_paged.store's layout, src/bitexact/vllm_plugin/tri_paged.py:311-335) at slot[token] (cache int8
  * [nb][HKV][bs][8 HD] with byte strides sc_nb, sc_h, sc_bs; tokens with slot < 0 are not stored). k / v may be
- * null (then only the cache receives them). */
+ * null (then only the cache receives them). Slots are not range-checked (slot < nb bs is the caller's contract). */
 int bx_rope_qgroup_store(const int64_t* y, int64_t ldy, const int64_t* pos, int64_t spb, int64_t spt,
                          const int64_t* cos, const int64_t* sin, int32_t npos, int32_t B, int32_t T, int32_t H,
                          int32_t HKV, int32_t HD, int32_t FR, int32_t FT, int32_t FK, int32_t FV, int32_t FZ,
