@@ -77,6 +77,19 @@ __device__ __forceinline__ int64_t fdiv_fast(int64_t a, int64_t b) {
   return q;
 }
 
+// floor(a / b) for b > 0 given binv = 1 / (double) b: fdiv_fast with the float64 estimate formed by a
+// multiplication. Its relative error is a few 2^-53, so for |a / b| <= 2^52 the estimate is within a few units and
+// the same integer corrections bring it to the floor quotient (fdiv_fast's overflow bounds hold unchanged).
+__device__ __forceinline__ int64_t fdiv_rcp(int64_t a, int64_t b, double binv) {
+  const double qd = (double)a * binv;
+  if (!(qd < 4503599627370496.0 && qd > -4503599627370496.0)) return fdiv(a, b);
+  int64_t q = (int64_t)qd;
+  int64_t r = a - q * b;
+  while (r < 0) { --q; r += b; }
+  while (r >= b) { ++q; r -= b; }
+  return q;
+}
+
 // Signed base-256 digit and remainder (intops.split_limbs, src/bitexact/intops.py:62-70).
 __device__ __forceinline__ int32_t limb_lo(int32_t r) { return ((r + 128) & 255) - 128; }
 __device__ __forceinline__ int64_t limb_lo64(int64_t r) { return ((r + 128) & 255) - 128; }

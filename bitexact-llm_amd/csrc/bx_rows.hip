@@ -44,19 +44,24 @@ __device__ __forceinline__ int64_t isqrt64(int64_t x) {
   return (int64_t)s;
 }
 
-// ops.div_round (src/bitexact/exact/ops.py:37-57): round(a 2^p / r) by 28-bit long division, r > 0
-__device__ __forceinline__ int64_t div_round64(int64_t a, int64_t p, int64_t r) {
-  int64_t Q = fdiv_fast(a, r);
+// ops.div_round (src/bitexact/exact/ops.py:37-57): round(a 2^p / r) by 28-bit long division, r > 0, rinv =
+// 1 / (double) r (every quotient digit is estimated by a multiplication and corrected to the exact floor; a
+// caller dividing many values by one r forms rinv once). Digit steps with nothing left to shift (c = 0) add
+// floor(R / r) = 0 and are skipped.
+__device__ __forceinline__ int64_t div_round64(int64_t a, int64_t p, int64_t r, double rinv) {
+  int64_t Q = fdiv_rcp(a, r, rinv);
   int64_t R = a - Q * r;
   int64_t left = imax(p, 0);
 #pragma unroll
   for (int it = 0; it < 3; ++it) {
     const int64_t c = imin(left, 28);
-    const int64_t X = shl(R, c);
-    const int64_t q1 = fdiv_fast(X, r);
-    Q = add_wrap(shl(Q, c), q1);
-    R = X - q1 * r;
-    left -= c;
+    if (c > 0) {
+      const int64_t X = shl(R, c);
+      const int64_t q1 = fdiv_rcp(X, r, rinv);
+      Q = add_wrap(shl(Q, c), q1);
+      R = X - q1 * r;
+      left -= c;
+    }
   }
   const int64_t up = Q + (2 * R >= r ? 1 : 0);
   const int64_t k = imin(imax(-p, 1), 62);
@@ -139,6 +144,7 @@ __global__ __launch_bounds__(kRowThreads) void norm_quant_kernel(NormArgs p) {
   const int64_t s = 2 * m - p.lg;
   const int64_t V = s >= 0 ? shl(T, s) : sar(T, -s);
   const int64_t r = isqrt64(V), er = shx - p.FR - m;
+  const double rinv = 1.0 / (double)r;
   int64_t emax = kNegBig;
   for (int i0 = threadIdx.x; i0 < D; i0 += kRowU * kRowThreads) {
     int64_t gmv[kRowU], gev[kRowU];
@@ -152,7 +158,7 @@ __global__ __launch_bounds__(kRowThreads) void norm_quant_kernel(NormArgs p) {
     for (int k = 0; k < kRowU; ++k) {
       const int i = i0 + k * kRowThreads;
       if (i < D) {
-        const int64_t P = div_round64(mul_wrap(Xs[i], gmv[k]), gev[k] - p.FR - er + p.FN, r);
+        const int64_t P = div_round64(mul_wrap(Xs[i], gmv[k]), gev[k] - p.FR - er + p.FN, r, rinv);
         Ps[i] = P;
         if (P != 0) emax = imax(emax, bitlen(P < 0 ? -P : P) - p.FN);
       }
@@ -336,7 +342,7 @@ __global__ __launch_bounds__(kRowThreads) void attn_out_kernel(const int64_t* nu
     const int hh = c / HD, d = c % HD;
     const int64_t group = (int64_t)(o / T) * HKV + hh / g, query = (int64_t)(hh % g) * T + o % T;
     const int64_t dn = den[group * sd_group + query];   // >= 1 whenever the query sees a key (itself)
-    const int64_t v = dn > 0 ? div_round64(num[group * sn_group + query * sn_query + d], FR - FV, dn) : 0;
+    const int64_t v = dn > 0 ? div_round64(num[group * sn_group + query * sn_query + d], FR - FV, dn, 1.0 / (double)dn) : 0;
     Os[c] = v;
     if (v != 0) emax = imax(emax, bitlen(v < 0 ? -v : v) - FR);
   }
