@@ -64,7 +64,8 @@ __device__ __forceinline__ void store_limbs(const RopeArgs& p, int token, int h,
   }
 }
 
-// One block per token; wave w takes head rows w, w + 4, ...; lane l holds dims l + 64 e.
+// Grid (token, head-row group of 4): wave w of block (token, j) takes head row 4 j + w (one row per wave, so the
+// rows' loads are in flight together instead of one row after another); lane l holds dims l + 64 e.
 template <int HD>
 __global__ __launch_bounds__(256) void rope_qgroup_kernel(RopeArgs p) {
   constexpr int E = HD / 64, HALF = HD / 2;
@@ -78,7 +79,7 @@ __global__ __launch_bounds__(256) void rope_qgroup_kernel(RopeArgs p) {
   const int64_t* sr = p.sin + pos * HALF;
   const int g = p.H / p.HKV, rows = p.H + 2 * p.HKV;
   const int64_t eps = -(int64_t)(p.FR + p.FT);
-  for (int hr = wave; hr < rows; hr += 4) {
+  for (int hr = blockIdx.y * 4 + wave; hr < rows && hr < (int)blockIdx.y * 4 + 4; hr += 4) {
     const int64_t* x = yr + (int64_t)hr * HD;
     int64_t out[E];
     int64_t emax = kSegNegBig;
@@ -262,7 +263,7 @@ static int rope_common(const int64_t* y, int64_t ldy, const int64_t* pos, int64_
   BX_REQUIRE(y && pos && cos && sin && qg && shg && err, "null pointer");
   RopeArgs p = {y, ldy, pos, spb, spt, cos, sin, npos, B, T, H, HKV, HD, FR, FT, FK, FV, FZ, qg, shg, k, v, err,
                 cache, sc_nb, sc_h, sc_bs, slot, bs};
-  const int blocks = B * T;
+  const dim3 blocks(B * T, (H + 2 * HKV + 3) / 4);
   if (HD == 64)
     rope_qgroup_kernel<64><<<blocks, 256, 0, (hipStream_t)stream>>>(p);
   else
