@@ -416,7 +416,7 @@ struct DecSmem {
     int32_t Vs[kDecWaves][16][HD + 1];   // sweep 2: each wave's joined V rows
     int64_t red[kDecWaves][4][HD];        // after it: each wave's p V sums
   };
-  int32_t Ps[kDecWaves][4][16];
+  alignas(16) int32_t Ps[kDecWaves][16][4];   // sweep 2: [wave][key][query], one 16-byte read per key
   int64_t qpos[4];
   int64_t shift[4];
   int64_t mx[4];
@@ -618,7 +618,7 @@ __global__ __launch_bounds__(kDecWaves * 64) void attn_dec_kernel(AttnArgs p) {
     int64_t pw = p.wrule == 0 ? weight_of(wat, ta, tb) : (i8 >= 0 ? ta : 0);
     if (!(qo < nvalid && s < hi && s <= my_qpos)) pw = 0;
     den += pw;
-    sm.Ps[w][qo][kl] = (int32_t)pw;
+    sm.Ps[w][kl][qo] = (int32_t)pw;
     const int c = lane >> 4;
 #pragma unroll
     for (int kk = 0; kk < KK; ++kk) {
@@ -639,9 +639,10 @@ __global__ __launch_bounds__(kDecWaves * 64) void attn_dec_kernel(AttnArgs p) {
       int64_t vd[KK];
 #pragma unroll
       for (int kk = 0; kk < KK; ++kk) vd[kk] = sm.Vs[w][k][lane + 64 * kk];
+      const v4i pk = *(const v4i*)&sm.Ps[w][k][0];
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
-        const int64_t pv = sm.Ps[w][i][k];
+        const int64_t pv = pk[i];
 #pragma unroll
         for (int kk = 0; kk < KK; ++kk) num[i][kk] += pv * vd[kk];
       }
