@@ -5,6 +5,8 @@
 // (segs.softmax), and the attention output rule (segs.attn_out = div_round + regroup + quant).
 #include "bx_common.h"
 
+#include <algorithm>
+
 namespace bx {
 
 constexpr int64_t kEps60 = 11529215046068LL;   // round(1e-5 2^60) (src/bitexact/exact/ops.py:21)
@@ -197,6 +199,27 @@ __device__ __forceinline__ int64_t exp2neg30_from(int64_t t, int64_t a, int64_t 
   return rshc(v, 30 + n);
 }
 
+// silu(g) u at 2 FR for one element (ops.silu_mul, src/bitexact/exact/ops.py:119-130), given the two table entries
+// la = lut[idx], lb = lut[idx + 1] at silu_index(g); bad |= silu_mul's `not ok`.
+__device__ __forceinline__ int silu_index(int64_t g, int FR) {
+  const int64_t ga = g < 0 ? (int64_t)(0 - (uint64_t)g) : g;
+  const int64_t t = rshc(imin(ga, 64LL << FR) * kL2E30, FR + 4);   // FR + 30 - FT2
+  return (int)((t & ((1LL << 26) - 1)) >> 12);
+}
+
+__device__ __forceinline__ int64_t silu_elem(int64_t g, int64_t u, int64_t la, int64_t lb, int FR, int& bad) {
+  const int64_t ga = g < 0 ? (int64_t)(0 - (uint64_t)g) : g;
+  const int64_t E = exp2neg30_from(rshc(imin(ga, 64LL << FR) * kL2E30, FR + 4), la, lb);
+  const int64_t den = (1LL << 30) + E;
+  const int64_t sig = g >= 0 ? fdiv_fast((1LL << 61) + den, 2 * den) : fdiv_fast(2 * (E << 30) + den, 2 * den);
+  const int64_t gc = imin(imax(g, -(1LL << 32)), 1LL << 32);
+  const int64_t sv = rshc(mul_wrap(gc, sig), 30);
+  const int64_t ua = u < 0 ? (int64_t)(0 - (uint64_t)u) : u;
+  const int64_t sa = sv < 0 ? -sv : sv;
+  bad |= (bitlen(sa) + bitlen(ua) > 62) | (ga > (1LL << 32));
+  return mul_wrap(sv, u);
+}
+
 __global__ __launch_bounds__(kRowThreads) void silu_quant_kernel(const int64_t* gu, int64_t ldgu, int ff, const int64_t* lut,
                                                          int FR, int32_t* q, int64_t ldq, int64_t* sh, int32_t* err) {
   extern __shared__ __align__(16) char smem[];
@@ -219,10 +242,7 @@ __global__ __launch_bounds__(kRowThreads) void silu_quant_kernel(const int64_t* 
   }
 #pragma unroll
   for (int k = 0; k < kSiluU; ++k) {
-    const int64_t g = gv[k];
-    const int64_t ga = g < 0 ? (int64_t)(0 - (uint64_t)g) : g;
-    const int64_t t = rshc(imin(ga, 64LL << FR) * kL2E30, FR + 4);   // FR + 30 - FT2
-    const int idx = (int)((t & ((1LL << 26) - 1)) >> 12);
+    const int idx = silu_index(gv[k], FR);
     la[k] = lut[idx];
     lb[k] = lut[idx + 1];
   }
@@ -230,17 +250,7 @@ __global__ __launch_bounds__(kRowThreads) void silu_quant_kernel(const int64_t* 
   for (int k = 0; k < kSiluU; ++k) {
     const int i = i0 + k * kRowThreads;
     if (i >= ff) continue;
-    const int64_t g = gv[k], u = uv[k];
-    const int64_t ga = g < 0 ? (int64_t)(0 - (uint64_t)g) : g;
-    const int64_t E = exp2neg30_from(rshc(imin(ga, 64LL << FR) * kL2E30, FR + 4), la[k], lb[k]);
-    const int64_t den = (1LL << 30) + E;
-    const int64_t sig = g >= 0 ? fdiv_fast((1LL << 61) + den, 2 * den) : fdiv_fast(2 * (E << 30) + den, 2 * den);
-    const int64_t gc = imin(imax(g, -(1LL << 32)), 1LL << 32);
-    const int64_t sv = rshc(mul_wrap(gc, sig), 30);
-    const int64_t ua = u < 0 ? (int64_t)(0 - (uint64_t)u) : u;
-    const int64_t sa = sv < 0 ? -sv : sv;
-    bad |= (bitlen(sa) + bitlen(ua) > 62) | (ga > (1LL << 32));
-    const int64_t P = mul_wrap(sv, u);
+    const int64_t P = silu_elem(gv[k], uv[k], la[k], lb[k], FR, bad);
     Ps[i] = P;
     if (P != 0) emax = imax(emax, bitlen(P < 0 ? (int64_t)(0 - (uint64_t)P) : P) + eps);
   }
@@ -352,6 +362,65 @@ __global__ __launch_bounds__(kRowThreads) void attn_out_kernel(const int64_t* nu
   if (threadIdx.x == 0) sh[o] = shr;
 }
 
+// The same stage split over column chunks for few rows (one block per row would leave most CUs idle while each
+// streams its 16 ff bytes of gate | up): silu_part_kernel, grid (M, C), writes P (int64 [M, ff]) and each chunk's
+// exponent maximum (slot [M, C]) to scratch; silu_fin_kernel, grid (M, C), takes the row's maximum over its C
+// slots and writes q for its chunk (and sh from chunk 0). The kernel boundary orders the two; the integers are
+// silu_quant_kernel's.
+constexpr int kSiluPartThreads = 256;
+__global__ __launch_bounds__(kSiluPartThreads) void silu_part_kernel(const int64_t* gu, int64_t ldgu, int ff,
+                                                                     int chunk, const int64_t* lut, int FR,
+                                                                     int64_t* P, int64_t* slots, int32_t* err) {
+  __shared__ int64_t sbuf[16];
+  const int m = blockIdx.x, c = blockIdx.y, C = gridDim.y;
+  const int64_t* row = gu + (int64_t)m * ldgu;
+  const int i_lo = c * chunk, i_hi = min(ff, i_lo + chunk);
+  const int eps = -2 * (int)FR;
+  int64_t emax = kNegBig;
+  int bad = 0;
+  constexpr int U = 4;
+  for (int i0 = i_lo + threadIdx.x; i0 < i_hi; i0 += U * kSiluPartThreads) {
+    int64_t gv[U], uv[U], la[U], lb[U];
+#pragma unroll
+    for (int k = 0; k < U; ++k) {
+      const int i = min(i0 + k * kSiluPartThreads, i_hi - 1);
+      gv[k] = row[i];
+      uv[k] = row[ff + i];
+    }
+#pragma unroll
+    for (int k = 0; k < U; ++k) {
+      const int idx = silu_index(gv[k], FR);
+      la[k] = lut[idx];
+      lb[k] = lut[idx + 1];
+    }
+#pragma unroll
+    for (int k = 0; k < U; ++k) {
+      const int i = i0 + k * kSiluPartThreads;
+      if (i >= i_hi) continue;
+      const int64_t v = silu_elem(gv[k], uv[k], la[k], lb[k], FR, bad);
+      P[(int64_t)m * ff + i] = v;
+      if (v != 0) emax = imax(emax, bitlen(v < 0 ? (int64_t)(0 - (uint64_t)v) : v) + eps);
+    }
+  }
+  if (bad) err[0] = 1;
+  emax = block_max64(emax, sbuf);
+  if (threadIdx.x == 0) slots[(int64_t)m * C + c] = emax;
+}
+
+__global__ __launch_bounds__(kSiluPartThreads) void silu_fin_kernel(const int64_t* P, const int64_t* slots, int ff,
+                                                                    int chunk, int FR, int32_t* q, int64_t ldq,
+                                                                    int64_t* sh) {
+  const int m = blockIdx.x, c = blockIdx.y, C = gridDim.y;
+  int64_t emax = kNegBig;
+  for (int j = 0; j < C; ++j) emax = imax(emax, slots[(int64_t)m * C + j]);
+  const int64_t shr = imax(emax - kQB, kNegBig);
+  const int eps = -2 * (int)FR;
+  const int i_lo = c * chunk, i_hi = min(ff, i_lo + chunk);
+  for (int i = i_lo + threadIdx.x; i < i_hi; i += kSiluPartThreads)
+    q[(int64_t)m * ldq + i] = (int32_t)rshc(P[(int64_t)m * ff + i], shr - eps);
+  if (c == 0 && threadIdx.x == 0) sh[m] = shr;
+}
+
 }  // namespace bx
 
 using namespace bx;
@@ -426,6 +495,33 @@ extern "C" int bx_silu_quant(const int64_t* gu, int64_t ldgu, int32_t ff, const 
   allow_lds_rows((const void*)silu_quant_kernel, lds);
   silu_quant_kernel<<<M, kRowThreads, lds, (hipStream_t)stream>>>(gu, ldgu, ff, lut, FR, q, ldq, sh, err);
   return check_launch("silu_quant_kernel");
+}
+
+// silu chunks: about 1024 elements each, at most 64 per row
+static int silu_chunks(int ff) { return std::min(64, std::max(1, (ff + 1023) / 1024)); }
+
+extern "C" int64_t bx_silu_quant_scratch(int32_t M, int32_t ff) {
+  if (M <= 0 || ff <= 0) return 0;
+  return (int64_t)M * ff * 8 + (int64_t)M * silu_chunks(ff) * 8;
+}
+
+extern "C" int bx_silu_quant_ws(const int64_t* gu, int64_t ldgu, int32_t ff, const int64_t* lut, int32_t FR, int32_t* q,
+                                int64_t ldq, int64_t* sh, int32_t M, int32_t* err, void* tmp, int64_t tmp_bytes,
+                                bx_stream_t stream) {
+  BX_REQUIRE(M >= 0 && ff > 0 && ldgu >= 2 * (int64_t)ff && ldq >= ff, "bad sizes");
+  BX_REQUIRE(FR >= 0 && FR <= 24, "FR outside [0, 24]");
+  BX_REQUIRE(gu && lut && q && sh && err, "null pointer");
+  if (M == 0) return BX_OK;
+  BX_REQUIRE(tmp && tmp_bytes >= bx_silu_quant_scratch(M, ff) && ((uintptr_t)tmp & 7) == 0,
+             "scratch too small (%lld < %lld)", (long long)tmp_bytes, (long long)bx_silu_quant_scratch(M, ff));
+  const int C = silu_chunks(ff), chunk = (ff + C - 1) / C;
+  int64_t* P = (int64_t*)tmp;
+  int64_t* slots = P + (int64_t)M * ff;
+  const dim3 grid(M, C);
+  silu_part_kernel<<<grid, kSiluPartThreads, 0, (hipStream_t)stream>>>(gu, ldgu, ff, chunk, lut, FR, P, slots, err);
+  if (int rc = check_launch("silu_part_kernel")) return rc;
+  silu_fin_kernel<<<grid, kSiluPartThreads, 0, (hipStream_t)stream>>>(P, slots, ff, chunk, FR, q, ldq, sh);
+  return check_launch("silu_fin_kernel");
 }
 
 extern "C" int bx_first_argmax(const int64_t* v, int64_t ldv, int32_t M, int32_t N, int64_t* out, bx_stream_t stream) {

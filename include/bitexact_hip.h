@@ -177,6 +177,15 @@ int bx_embed_rmsnorm_quant(const int32_t* emb, const int64_t* ids, int64_t* x, i
 int bx_silu_quant(const int64_t* gu, int64_t ldgu, int32_t ff, const int64_t* lut, int32_t FR, int32_t* q, int64_t ldq,
                   int64_t* sh, int32_t M, int32_t* err, bx_stream_t stream);
 
+/* bx_silu_quant split over column chunks of about 1024 elements, for few rows (one block per row leaves most CUs
+ * idle): two launches on `stream`, with P and the chunk maxima in the caller's scratch (tmp, 8-byte aligned, at
+ * least bx_silu_quant_scratch(M, ff) bytes; no contents kept). Same rule, outputs and flag as bx_silu_quant, the
+ * reference stage it replaces (src/bitexact/exact/segs.py:120-128, 180-182). */
+int bx_silu_quant_ws(const int64_t* gu, int64_t ldgu, int32_t ff, const int64_t* lut, int32_t FR, int32_t* q,
+                     int64_t ldq, int64_t* sh, int32_t M, int32_t* err, void* tmp, int64_t tmp_bytes,
+                     bx_stream_t stream);
+int64_t bx_silu_quant_scratch(int32_t M, int32_t ff);
+
 /* Replaces intops.first_argmax (src/bitexact/intops.py:55-59), the greedy token of tri_logits
  * (src/bitexact/vllm_plugin/tri_logits.py:1-20): out[m] = the first index of the maximum of row m of v int64 [M, N]. */
 int bx_first_argmax(const int64_t* v, int64_t ldv, int32_t M, int32_t N, int64_t* out, bx_stream_t stream);

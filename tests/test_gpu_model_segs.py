@@ -96,6 +96,27 @@ def test_gu_silu(dev, M, ff):
     assert bool(ops.gu_silu_y(bad.to(dev), torch.from_numpy(lut).to(dev))[2]) and R.gu_silu_y(bad.numpy(), lut)[2]
 
 
+@pytest.mark.parametrize("M,ff", [(1, 8192), (32, 8192), (7, 96), (5, 3000), (130, 2048)])
+def test_gu_silu_split(dev, M, ff):
+    """The column-chunked SiLU stage (few rows) against the oracle and the row-per-block kernel: q, sh and the flag,
+    with ragged chunks (ff = 3000), a zero row and an overflowing element."""
+    from bitexact.exact import ops
+    g = torch.Generator().manual_seed(3 * M + ff)
+    gu = torch.randint(-(1 << 31), 1 << 31, (M, 2 * ff), generator=g)
+    gu[0, :ff] >>= 12
+    gu[-1, :ff] = 0
+    lut = R.exp2_table()
+    q, sh, flag = R.gu_silu_y(gu.numpy(), lut)
+    L = torch.from_numpy(lut).to(dev)
+    qa, sha, ea = ops.gu_silu_y(gu.to(dev), L, split=True)
+    qb, shb, eb = ops.gu_silu_y(gu.to(dev), L, split=False)
+    assert np.array_equal(qa.cpu().numpy(), q) and np.array_equal(sha.cpu().numpy(), sh) and bool(ea) == flag
+    assert torch.equal(qa, qb) and torch.equal(sha, shb) and bool(ea) == bool(eb)
+    bad = gu.clone()
+    bad[M // 2, ff - 1] = (1 << 32) + 1
+    assert bool(ops.gu_silu_y(bad.to(dev), L, split=True)[2]) and R.gu_silu_y(bad.numpy(), lut)[2]
+
+
 @pytest.mark.parametrize("M,N", [(1, 128256), (5, 1000), (3, 7)])
 def test_first_argmax(dev, M, N):
     """First index of the row maximum, ties included; a row of int64 minima gives 0."""
