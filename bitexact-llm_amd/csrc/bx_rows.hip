@@ -421,6 +421,63 @@ __global__ __launch_bounds__(kSiluPartThreads) void silu_fin_kernel(const int64_
   if (c == 0 && threadIdx.x == 0) sh[m] = shr;
 }
 
+// first_argmax split over column chunks for few rows (one block per row streams the whole row on one CU):
+// argmax_part_kernel, grid (M, C), writes each chunk's (maximum, its first index) to scratch slots; argmax_fin_kernel
+// takes, per row, the first chunk holding the row maximum (chunks in column order, so ties keep the smallest index).
+constexpr int kArgThreads = 256;
+__global__ __launch_bounds__(kArgThreads) void argmax_part_kernel(const int64_t* v, int64_t ldv, int N, int chunk,
+                                                                  int64_t* slots) {
+  __shared__ int64_t smax[kArgThreads / 64], sidx[kArgThreads / 64];
+  const int m = blockIdx.x, c = blockIdx.y, C = gridDim.y;
+  const int64_t* row = v + (int64_t)m * ldv;
+  const int i_lo = c * chunk, i_hi = min(N, i_lo + chunk);
+  int64_t best = INT64_MIN, idx = N;
+  constexpr int U = 8;
+  int i0 = i_lo + threadIdx.x;
+  for (; i0 + (U - 1) * kArgThreads < i_hi; i0 += U * kArgThreads) {
+    int64_t x[U];
+#pragma unroll
+    for (int u = 0; u < U; ++u) x[u] = __builtin_nontemporal_load(row + i0 + u * kArgThreads);
+#pragma unroll
+    for (int u = 0; u < U; ++u)
+      if (x[u] > best || idx == N) { best = x[u]; idx = i0 + u * kArgThreads; }
+  }
+  for (int i = i0; i < i_hi; i += kArgThreads) {
+    const int64_t x = row[i];
+    if (x > best || idx == N) { best = x; idx = i; }
+  }
+  int64_t mx = best;
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) mx = imax(mx, __shfl_xor(mx, o, 64));
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  if (lane == 0) smax[wave] = mx;
+  __syncthreads();
+  int64_t rm = smax[0];
+  for (int w = 1; w < kArgThreads / 64; ++w) rm = imax(rm, smax[w]);
+  int64_t cand = (best == rm) ? idx : N;
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) cand = imin(cand, __shfl_xor(cand, o, 64));
+  if (lane == 0) sidx[wave] = cand;
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    int64_t ri = sidx[0];
+    for (int w = 1; w < kArgThreads / 64; ++w) ri = imin(ri, sidx[w]);
+    slots[((int64_t)m * C + c) * 2] = rm;
+    slots[((int64_t)m * C + c) * 2 + 1] = ri;
+  }
+}
+
+__global__ __launch_bounds__(64) void argmax_fin_kernel(const int64_t* slots, int M, int N, int C, int64_t* out) {
+  const int m = blockIdx.x * 64 + threadIdx.x;
+  if (m >= M) return;
+  int64_t best = INT64_MIN, idx = N;
+  for (int c = 0; c < C; ++c) {
+    const int64_t sv = slots[((int64_t)m * C + c) * 2], si = slots[((int64_t)m * C + c) * 2 + 1];
+    if (sv > best || idx == N) { best = sv; idx = si; }
+  }
+  out[m] = idx;
+}
+
 }  // namespace bx
 
 using namespace bx;
@@ -530,6 +587,28 @@ extern "C" int bx_first_argmax(const int64_t* v, int64_t ldv, int32_t M, int32_t
   if (M == 0) return BX_OK;
   first_argmax_kernel<<<M, 1024, 0, (hipStream_t)stream>>>(v, ldv, N, out);
   return check_launch("first_argmax_kernel");
+}
+
+static int argmax_chunks(int N) { return std::min(64, std::max(1, (N + 8191) / 8192)); }
+
+extern "C" int64_t bx_first_argmax_scratch(int32_t M, int32_t N) {
+  if (M <= 0 || N <= 0) return 0;
+  return (int64_t)M * argmax_chunks(N) * 16;
+}
+
+extern "C" int bx_first_argmax_ws(const int64_t* v, int64_t ldv, int32_t M, int32_t N, int64_t* out, void* tmp,
+                                  int64_t tmp_bytes, bx_stream_t stream) {
+  BX_REQUIRE(M >= 0 && N > 0 && ldv >= N, "bad sizes");
+  BX_REQUIRE(v && out, "null pointer");
+  if (M == 0) return BX_OK;
+  BX_REQUIRE(tmp && tmp_bytes >= bx_first_argmax_scratch(M, N) && ((uintptr_t)tmp & 7) == 0,
+             "scratch too small (%lld < %lld)", (long long)tmp_bytes, (long long)bx_first_argmax_scratch(M, N));
+  const int C = argmax_chunks(N), chunk = (N + C - 1) / C;
+  int64_t* slots = (int64_t*)tmp;
+  argmax_part_kernel<<<dim3(M, C), kArgThreads, 0, (hipStream_t)stream>>>(v, ldv, N, chunk, slots);
+  if (int rc = check_launch("argmax_part_kernel")) return rc;
+  argmax_fin_kernel<<<(M + 63) / 64, 64, 0, (hipStream_t)stream>>>(slots, M, N, C, out);
+  return check_launch("argmax_fin_kernel");
 }
 
 extern "C" int bx_softmax_w(const int64_t* raw, int64_t ldr, const int64_t* qpos, const int64_t* sh, int32_t rows,

@@ -190,6 +190,14 @@ int64_t bx_silu_quant_scratch(int32_t M, int32_t ff);
  * (src/bitexact/vllm_plugin/tri_logits.py:1-20): out[m] = the first index of the maximum of row m of v int64 [M, N]. */
 int bx_first_argmax(const int64_t* v, int64_t ldv, int32_t M, int32_t N, int64_t* out, bx_stream_t stream);
 
+/* bx_first_argmax split over column chunks of about 8192 for few rows: two launches on `stream`, with each chunk's
+ * (maximum, first index) in the caller's scratch (tmp, 8-byte aligned, at least bx_first_argmax_scratch(M, N)
+ * bytes; no contents kept). Same result as bx_first_argmax, the reference rule it replaces
+ * (src/bitexact/intops.py:55-59). */
+int bx_first_argmax_ws(const int64_t* v, int64_t ldv, int32_t M, int32_t N, int64_t* out, void* tmp, int64_t tmp_bytes,
+                       bx_stream_t stream);
+int64_t bx_first_argmax_scratch(int32_t M, int32_t N);
+
 /* Replaces segs.softmax (src/bitexact/exact/segs.py:102-105, ops.softmax_w): weights p int32 [rows, S] at fp bits of
  * the scores raw int64 [rows, S] (key s visible iff s <= qpos[row]; hidden keys weigh 0) and den int64 [rows]. */
 int bx_softmax_w(const int64_t* raw, int64_t ldr, const int64_t* qpos, const int64_t* sh, int32_t rows, int32_t S,

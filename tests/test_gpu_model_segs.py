@@ -117,8 +117,9 @@ def test_gu_silu_split(dev, M, ff):
     assert bool(ops.gu_silu_y(bad.to(dev), L, split=True)[2]) and R.gu_silu_y(bad.numpy(), lut)[2]
 
 
-@pytest.mark.parametrize("M,N", [(1, 128256), (5, 1000), (3, 7)])
-def test_first_argmax(dev, M, N):
+@pytest.mark.parametrize("split", [False, True])
+@pytest.mark.parametrize("M,N", [(1, 128256), (5, 1000), (3, 7), (32, 128256), (4, 40000)])
+def test_first_argmax(dev, M, N, split):
     """First index of the row maximum, ties included; a row of int64 minima gives 0."""
     from bitexact.intops import first_argmax
     g = torch.Generator().manual_seed(N)
@@ -128,6 +129,8 @@ def test_first_argmax(dev, M, N):
         v[1] = -(1 << 63)
     if M > 2:
         v[2] = 5
+    if M > 3 and N > 9000:                                        # ties across chunk edges (8016 / 8192 wide)
+        v[3, 9000] = v[3, 8000] = v[3, N - 1] = 1 << 51
     want = [R.first_argmax(r) for r in v.numpy()]
-    assert first_argmax(v.to(dev)).cpu().tolist() == want
+    assert first_argmax(v.to(dev), split=split).cpu().tolist() == want
     assert want[0] == N // 3 and (M < 2 or want[1] == 0) and (M < 3 or want[2] == 0)
