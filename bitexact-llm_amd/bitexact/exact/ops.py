@@ -177,10 +177,11 @@ def embed_norm(emb, ids, gm, ge, err=None, flag=None):
 SILU_SPLIT_ROWS = 128   # fewer rows than this: the stage is split over column chunks (bx_silu_quant_ws)
 
 
-def gu_silu_y(y, lut, err=None, flag=None, split=None):
+def gu_silu_y(y, lut, err=None, flag=None, split=None, planes=False):
     """Segs.gu_silu_y (src/bitexact/exact/segs.py:180-182): y int64 [M, 2 ff] (gate | up) at FR ->
     (q int32 [M, ff], sh int64 [M], err | not ok). split: None picks by row count; True / False force the
-    column-chunked or the row-per-block kernel (the same integers either way)."""
+    column-chunked or the row-per-block kernel (the same integers either way). planes=True (column-chunked path):
+    q is returned as (q, limb planes int8 [3, M, ff]) for exact_linear's q_planes."""
     _hip.require_cuda(y, lut)
     assert y.dtype == torch.int64 and y.stride(-1) == 1 and y.shape[1] % 2 == 0
     M, ff = y.shape[0], y.shape[1] // 2
@@ -189,12 +190,14 @@ def gu_silu_y(y, lut, err=None, flag=None, split=None):
     fl = _flag(y.device, flag)
     lut = lut.contiguous().long()
     if split is None:
-        split = M < SILU_SPLIT_ROWS
+        split = M < SILU_SPLIT_ROWS or planes
+    assert split or not planes, "limb planes come from the column-chunked path"
     if split and M > 0:
         tmp, tmpb = _hip.scratch(y.device, _hip.lib().bx_silu_quant_scratch(M, ff))
+        pl = torch.empty(3, M, ff, dtype=torch.int8, device=y.device) if planes else None
         _hip.call("bx_silu_quant_ws", _hip.ptr(y), y.stride(0), ff, _hip.ptr(lut), FR, _hip.ptr(q), ff, _hip.ptr(sh),
-                  M, _hip.ptr(fl), _hip.ptr(tmp), tmpb, _hip.stream_of(y))
-        return q, sh, _or(err, fl, flag)
+                  _hip.ptr(pl), M, _hip.ptr(fl), _hip.ptr(tmp), tmpb, _hip.stream_of(y))
+        return ((q, pl) if planes else q), sh, _or(err, fl, flag)
     _hip.call("bx_silu_quant", _hip.ptr(y), y.stride(0), ff, _hip.ptr(lut), FR, _hip.ptr(q), ff, _hip.ptr(sh), M,
               _hip.ptr(fl), _hip.stream_of(y))
     return q, sh, _or(err, fl, flag)

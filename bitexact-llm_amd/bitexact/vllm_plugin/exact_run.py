@@ -82,9 +82,15 @@ class ExactEngine:
             else:
                 x, q, sh, _ = ops.add_norm_y(self.fused[i, "wo"](qo, sho, fl, True), x, *self.gm[i], flag=fl)
                 y = wgu(q, sh, fl, False)
-            q, sh, _ = ops.gu_silu_y(y, self.exp2, flag=fl)
+            wd = self.fused[i, "wd"]
+            if wd.needs_planes(N):   # the SiLU stage also writes q's limb planes for the MFMA path
+                (q, pl), sh, _ = ops.gu_silu_y(y, self.exp2, flag=fl, planes=True)
+                yd = wd(q, sh, fl, True, q_planes=pl)
+            else:
+                q, sh, _ = ops.gu_silu_y(y, self.exp2, flag=fl)
+                yd = wd(q, sh, fl, True)
             nxt = self.ga[i + 1] if i + 1 < self.L else (None, None)
-            x, q, sh, _ = ops.add_norm_y(self.fused[i, "wd"](q, sh, fl, True), x, *nxt, flag=fl)
+            x, q, sh, _ = ops.add_norm_y(yd, x, *nxt, flag=fl)
         return x
 
     def logits(self, h):

@@ -1076,7 +1076,11 @@ static Plan make_plan(int rows_a, int M_out, int N, int K, int nb, int na, bool 
     s.tmp_bytes = exact ? 3LL * M_out * K : 0;   // exact: q limb planes
     return s;
   }
-  if (!dec_tile && rows_a <= 128 && gemv_shape(na, M_out, N, K, nb, exact, cus, s)) {
+  // exact GEMMs of 22..32 rows (66..96 limb rows) with a long K (the engine's down projection, K = 8192) go to the
+  // MFMA tiles with K split: 25.6 vs 29.5 us at M = 32, N = 2048 (plus a limb split, unless the caller brings q's
+  // limb planes); at K = 2048 the gemv stays (11.0 vs 16.7 us at N = 2048)
+  const bool long_k_tile = exact && M_out > 21 && M_out <= 32 && K >= 8192;
+  if (!long_k_tile && !dec_tile && rows_a <= 128 && gemv_shape(na, M_out, N, K, nb, exact, cus, s)) {
     s.gemv = true;
     const int RA = 16 * s.rb, BNC = 16 * s.cg;
     const int steps = (nst + s.split - 1) / s.split;

@@ -409,15 +409,27 @@ __global__ __launch_bounds__(kSiluPartThreads) void silu_part_kernel(const int64
 
 __global__ __launch_bounds__(kSiluPartThreads) void silu_fin_kernel(const int64_t* P, const int64_t* slots, int ff,
                                                                     int chunk, int FR, int32_t* q, int64_t ldq,
-                                                                    int64_t* sh) {
+                                                                    int64_t* sh, int8_t* planes) {
   const int m = blockIdx.x, c = blockIdx.y, C = gridDim.y;
   int64_t emax = kNegBig;
   for (int j = 0; j < C; ++j) emax = imax(emax, slots[(int64_t)m * C + j]);
   const int64_t shr = imax(emax - kQB, kNegBig);
   const int eps = -2 * (int)FR;
   const int i_lo = c * chunk, i_hi = min(ff, i_lo + chunk);
-  for (int i = i_lo + threadIdx.x; i < i_hi; i += kSiluPartThreads)
-    q[(int64_t)m * ldq + i] = (int32_t)rshc(P[(int64_t)m * ff + i], shr - eps);
+  const int64_t plane = (int64_t)gridDim.x * ff;
+  for (int i = i_lo + threadIdx.x; i < i_hi; i += kSiluPartThreads) {
+    const int32_t qv = (int32_t)rshc(P[(int64_t)m * ff + i], shr - eps);
+    q[(int64_t)m * ldq + i] = qv;
+    if (planes != nullptr) {   // q's signed int8 limb planes [3][M][ff] for the exact GEMM (split_q_kernel's split)
+      int32_t r = qv;
+#pragma unroll
+      for (int l = 0; l < 3; ++l) {
+        const int32_t lo = limb_lo(r);
+        planes[l * plane + (int64_t)m * ff + i] = (int8_t)lo;
+        r = (r - lo) >> 8;
+      }
+    }
+  }
   if (c == 0 && threadIdx.x == 0) sh[m] = shr;
 }
 
@@ -563,8 +575,8 @@ extern "C" int64_t bx_silu_quant_scratch(int32_t M, int32_t ff) {
 }
 
 extern "C" int bx_silu_quant_ws(const int64_t* gu, int64_t ldgu, int32_t ff, const int64_t* lut, int32_t FR, int32_t* q,
-                                int64_t ldq, int64_t* sh, int32_t M, int32_t* err, void* tmp, int64_t tmp_bytes,
-                                bx_stream_t stream) {
+                                int64_t ldq, int64_t* sh, int8_t* planes, int32_t M, int32_t* err, void* tmp,
+                                int64_t tmp_bytes, bx_stream_t stream) {
   BX_REQUIRE(M >= 0 && ff > 0 && ldgu >= 2 * (int64_t)ff && ldq >= ff, "bad sizes");
   BX_REQUIRE(FR >= 0 && FR <= 24, "FR outside [0, 24]");
   BX_REQUIRE(gu && lut && q && sh && err, "null pointer");
@@ -577,7 +589,8 @@ extern "C" int bx_silu_quant_ws(const int64_t* gu, int64_t ldgu, int32_t ff, con
   const dim3 grid(M, C);
   silu_part_kernel<<<grid, kSiluPartThreads, 0, (hipStream_t)stream>>>(gu, ldgu, ff, chunk, lut, FR, P, slots, err);
   if (int rc = check_launch("silu_part_kernel")) return rc;
-  silu_fin_kernel<<<grid, kSiluPartThreads, 0, (hipStream_t)stream>>>(P, slots, ff, chunk, FR, q, ldq, sh);
+  BX_REQUIRE(!planes || ff % 16 == 0, "limb planes need ff %% 16 == 0");
+  silu_fin_kernel<<<grid, kSiluPartThreads, 0, (hipStream_t)stream>>>(P, slots, ff, chunk, FR, q, ldq, sh, planes);
   return check_launch("silu_fin_kernel");
 }
 

@@ -327,3 +327,32 @@ def test_exact_linear_norm_planes(dev, M, N):
     ref, rflag, _ = R.epilogue(R.wmm_f64(qn, dec["W"]), R.residual(qn, dec["rr"], dec["rc"], dec["rv"], N),
                                dec["d"], dec["g"], shn, R.FR, True)
     assert np.array_equal(yb.cpu().numpy(), ref) and bool(f2.item()) == rflag
+
+
+@pytest.mark.parametrize("M", [22, 32])
+def test_exact_linear_silu_planes(dev, M):
+    """The SiLU stage's limb planes fed to the exact linear at K = 8192 (MFMA tiles with K split) give the same q,
+    sh, y and flag as the separate stages, and y matches the oracle."""
+    from bitexact.exact import ops
+    from bitexact.vllm_plugin.exact_gemm import exact_linear, needs_planes
+    N, K = 2048, 8192
+    g = torch.Generator().manual_seed(M)
+    gu = torch.randint(-(1 << 31), 1 << 31, (M, 2 * K), generator=g)
+    lut = torch.from_numpy(R.exp2_table()).to(dev)
+    q1, sh1, e1 = ops.gu_silu_y(gu.to(dev), lut)
+    (q2, pl), sh2, e2 = ops.gu_silu_y(gu.to(dev), lut, planes=True)
+    assert torch.equal(q1, q2) and torch.equal(sh1, sh2) and bool(e1) == bool(e2) and pl.shape == (3, M, K)
+    assert needs_planes(M, N, K)
+    dec = _dec(_bf16(N, K, 5))
+    limbs = torch.from_numpy(dec["limbs"]).to(dev)
+    d, gg = torch.from_numpy(dec["d"]).to(dev), torch.from_numpy(dec["g"]).to(dev)
+    cnt, ec, ev, Rr = _ell(dec, N, dev)
+    f1 = torch.zeros(1, dtype=torch.int32, device=dev)
+    f2 = torch.zeros(1, dtype=torch.int32, device=dev)
+    ya = exact_linear(q1, sh1, limbs, d, gg, cnt, ec, ev, Rr, f1, True)
+    yb = exact_linear(q2, sh2, limbs, d, gg, cnt, ec, ev, Rr, f2, True, q_planes=pl)
+    assert torch.equal(ya, yb) and f1.item() == f2.item()
+    qn, shn = q1.cpu().numpy().astype(np.int64), sh1.cpu().numpy()
+    ref, rflag, _ = R.epilogue(R.wmm_f64(qn, dec["W"]), R.residual(qn, dec["rr"], dec["rc"], dec["rv"], N),
+                               dec["d"], dec["g"], shn, R.FR, True)
+    assert np.array_equal(yb.cpu().numpy(), ref) and bool(f2.item()) == rflag
