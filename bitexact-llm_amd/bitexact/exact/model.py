@@ -11,6 +11,21 @@ from bitexact.exact.wmm import wmm_hip
 from bitexact.vllm_plugin.exact_gemm import exact_linear
 
 
+def validate_ell(cnt, ec, R, K):
+    """Load-time check of an ELL residual (cnt int32 [N], ec int32 [N, >= R]): counts in [0, R] and every listed
+    column in [0, K). The kernels never read outside q on bad data (they raise the flag instead), but a damaged
+    weight file must fail here, where it is loaded, with an AssertionError."""
+    if R == 0:
+        return
+    cnt = cnt.long()
+    assert int(cnt.min()) >= 0 and int(cnt.max()) <= R, "ELL residual: a row count outside [0, R]"
+    assert ec.shape[1] >= R, "ELL residual: fewer column slots than R"
+    used = torch.arange(ec.shape[1], device=ec.device)[None, :] < cnt[:, None]
+    cols = ec.long()[used]
+    assert cols.numel() == 0 or (int(cols.min()) >= 0 and int(cols.max()) < K), \
+        "ELL residual: a column index outside [0, K)"
+
+
 class Lin:
     def __init__(self, c, name, device, gemm="hip", ell=True, R=0, cpu_lazy=False):
         dev = torch.device(device)
@@ -33,6 +48,7 @@ class Lin:
                 ec = torch.nn.functional.pad(ec, (0, pad))
                 ev = torch.nn.functional.pad(ev, (0, pad))
             self.ec, self.ev = ec.contiguous(), ev.contiguous()
+            validate_ell(self.cnt, self.ec, self.R, self.limbs.shape[2])
             return
         rr = self.rr.cpu()
         cnt = torch.bincount(rr, minlength=self.N) if rr.numel() else torch.zeros(self.N, dtype=torch.long)
@@ -44,6 +60,7 @@ class Lin:
         if rr.numel():
             ec[rr, j] = self.rc.cpu().to(torch.int32)
             ev[rr, j] = self.rv.cpu()
+        validate_ell(cnt, ec, self.R, self.limbs.shape[2])
         self.cnt = cnt.to(torch.int32).to(dev)
         self.ec, self.ev = ec.to(dev), ev.to(dev)
 

@@ -17,6 +17,18 @@ def needs_planes(M, N, K):
     return _hip.lib().bx_exact_linear_scratch(M, N, K) > 0
 
 
+KERNELS = {1: "gemv", 2: "wide", 3: "tile"}
+TILES = {0: "128x128", 1: "64x128", 2: "64x32", 3: "64x64-int8", 4: "64x64", -1: None}
+
+
+def plan(M, N, K):
+    """Which kernel the exact linear runs at (M, N, K): (kernel, tile, k_splits, blocks_per_split)."""
+    import ctypes
+    out = (ctypes.c_int32 * 4)()
+    _hip.call("bx_exact_linear_plan", M, N, K, out)
+    return KERNELS[out[0]], TILES[out[1]], out[2], out[3]
+
+
 def exact_linear(q, sh, limbs, d, g, cnt, ec, ev, R, flag=None, checked=True, fr=FR, q_planes=None):
     """The fused exact linear on raw tensors; returns y (and sets flag). q_planes: q's int8 limb planes [3, M, K]."""
     _hip.require_cuda(q, limbs)

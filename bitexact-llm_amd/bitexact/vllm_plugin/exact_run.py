@@ -83,7 +83,9 @@ class ExactEngine:
                 x, q, sh, _ = ops.add_norm_y(self.fused[i, "wo"](qo, sho, fl, True), x, *self.gm[i], flag=fl)
                 y = wgu(q, sh, fl, False)
             wd = self.fused[i, "wd"]
-            if wd.needs_planes(N):   # the SiLU stage also writes q's limb planes for the MFMA path
+            # the column-chunked SiLU stage also writes q's limb planes for the MFMA path; measured only for the
+            # few-row decode case (the chunked stage's own range), so prefill-sized steps keep the row kernel
+            if N < ops.SILU_SPLIT_ROWS and wd.needs_planes(N):
                 (q, pl), sh, _ = ops.gu_silu_y(y, self.exp2, flag=fl, planes=True)
                 yd = wd(q, sh, fl, True, q_planes=pl)
             else:

@@ -54,13 +54,29 @@ struct LinArgs {
   int tiles, parts_lg, mp;   // gemv: column tiles, log2 of the row parts per tile, output rows per part
 };
 
-// Residual column index kept inside the row of q (valid ELL data is always in [0, K); a corrupt index reads a
-// wrong value instead of memory outside q).
-__device__ __forceinline__ int kcol(const LinArgs& p, int32_t c) { return (int)min((uint32_t)c, (uint32_t)(p.K - 1)); }
+// Residual column index. Valid ELL data is always in [0, K) with counts in [0, R]; a corrupt index or count
+// (a damaged weight file) marks the output as untrustworthy: `corrupt` is raised (it sets flag[0] = 1 whenever
+// the caller passed a flag, checked or not) and the entry reads column 0 instead of memory outside q.
+__device__ __forceinline__ int kcol(const LinArgs& p, int32_t c, bool& corrupt) {
+  const bool out = (uint32_t)c >= (uint32_t)p.K;
+  corrupt |= out;
+  return out ? 0 : c;
+}
+
+__device__ __forceinline__ int kcnt(const LinArgs& p, int32_t c, bool& corrupt) {
+  const bool out = (uint32_t)c > (uint32_t)p.R;
+  corrupt |= out;
+  return out ? 0 : c;
+}
+
+// The kernels' flag write: numeric bound violations when `checked`, corrupt residual indices always.
+__device__ __forceinline__ void write_flag(const LinArgs& p, bool bad, bool corrupt) {
+  if (p.flag != nullptr && ((p.checked && bad) || corrupt)) p.flag[0] = 1;
+}
 
 // ---- epilogue shared by both kernels: one output element from its exact int64 dense value ----
 template <int MODE>
-__device__ __forceinline__ void finalize(const LinArgs& p, int m, int n, int64_t v, bool& bad) {
+__device__ __forceinline__ void finalize(const LinArgs& p, int m, int n, int64_t v, bool& bad, bool& corrupt) {
   const int64_t o = (int64_t)m * p.N + n;
   if (MODE == RAW32) {
     ((int32_t*)p.out)[o] = (int32_t)v;
@@ -70,11 +86,11 @@ __device__ __forceinline__ void finalize(const LinArgs& p, int m, int n, int64_t
     // segs.lin_y (src/bitexact/exact/segs.py:25-32): B from the ELL residual, then wmm.epilogue.
     int64_t B = 0;
     if (p.R > 0) {
-      const int c = min(max(p.cnt[n], 0), p.R);
+      const int c = kcnt(p, p.cnt[n], corrupt);
       const int32_t* qr = p.q + (int64_t)m * p.ldq;
       const int32_t* ec = p.ecol + (int64_t)n * p.R;
       const int64_t* ev = p.eval + (int64_t)n * p.R;
-      for (int j = 0; j < c; ++j) B = add_wrap(B, mul_wrap((int64_t)qr[kcol(p, ec[j])], ev[j]));
+      for (int j = 0; j < c; ++j) B = add_wrap(B, mul_wrap((int64_t)qr[kcol(p, ec[j], corrupt)], ev[j]));
     }
     const int64_t dn = p.d[n];
     const int64_t pe = p.sh[m] + p.g[n] - dn + p.FR;
@@ -90,6 +106,7 @@ constexpr int kRes = 4;
 struct ColCtx {
   int64_t d, gdr;        // d[n] and g[n] - d[n] + FR
   int cnt;
+  bool corrupt;          // an index or count of the column's list is out of range
   int wmax;              // largest count over the wave's columns (wave-uniform loop bound)
   int32_t ec[kRes];
   int64_t ev[kRes];
@@ -102,14 +119,15 @@ __device__ __forceinline__ ColCtx col_ctx(const LinArgs& p, int n) {
   const int nn = min(n, p.N - 1);
   c.d = p.d[nn];
   c.gdr = p.g[nn] - c.d + p.FR;
-  c.cnt = p.R > 0 ? min(max(p.cnt[nn], 0), p.R) : 0;   // entries stay inside the row's R slots
+  c.corrupt = false;
+  c.cnt = p.R > 0 ? kcnt(p, p.cnt[nn], c.corrupt) : 0;   // entries stay inside the row's R slots
   c.wmax = (int)wave_max64(c.cnt);
   c.ecp = p.ecol + (int64_t)nn * p.R;
   c.evp = p.eval + (int64_t)nn * p.R;
 #pragma unroll
   for (int j = 0; j < kRes; ++j) {
     const bool has = j < c.cnt;
-    c.ec[j] = has ? c.ecp[j] : 0;
+    c.ec[j] = has ? kcol(p, c.ecp[j], c.corrupt) : 0;
     c.ev[j] = has ? c.evp[j] : 0;
   }
   return c;
@@ -121,14 +139,14 @@ __device__ __forceinline__ ColCtx col_ctx(const LinArgs& p, int n) {
 // does not matter.
 template <int NR>
 __device__ __forceinline__ void residual_rows(const LinArgs& p, const ColCtx& cc, const int (&mrow)[NR],
-                                              int64_t (&B)[NR]) {
+                                              int64_t (&B)[NR], bool& corrupt) {
 #pragma unroll
   for (int e = 0; e < NR; ++e) B[e] = 0;
   if (cc.wmax <= 0) return;   // wave-uniform
 #pragma unroll
   for (int j = 0; j < kRes; ++j) {
     if (j < cc.wmax) {        // wave-uniform; padded entries have ev = 0
-      const int col = kcol(p, cc.ec[j]);
+      const int col = cc.ec[j];   // checked in col_ctx
       int32_t qv[NR];
 #pragma unroll
       for (int e = 0; e < NR; ++e) qv[e] = p.q[(int64_t)mrow[e] * p.ldq + col];
@@ -137,7 +155,7 @@ __device__ __forceinline__ void residual_rows(const LinArgs& p, const ColCtx& cc
     }
   }
   for (int j = kRes; j < cc.cnt; ++j) {
-    const int col = kcol(p, cc.ecp[j]);
+    const int col = kcol(p, cc.ecp[j], corrupt);
     const int64_t ev = cc.evp[j];
 #pragma unroll
     for (int e = 0; e < NR; ++e) B[e] = add_wrap(B[e], mul_wrap((int64_t)p.q[(int64_t)mrow[e] * p.ldq + col], ev));
@@ -145,8 +163,9 @@ __device__ __forceinline__ void residual_rows(const LinArgs& p, const ColCtx& cc
 }
 
 __device__ __forceinline__ void finalize_col(const LinArgs& p, const ColCtx& cc, int m, int n, int64_t shm, int64_t v,
-                                             int64_t B, bool& bad) {
+                                             int64_t B, bool& bad, bool& corrupt) {
   bool b;
+  corrupt |= cc.corrupt;
   ((int64_t*)p.out)[(int64_t)m * p.N + n] = exact_round_fast(v, B, cc.d, shm + cc.gdr, b);
   bad |= b;
 }
@@ -460,7 +479,7 @@ __global__ __launch_bounds__(64 * CG * KS) void gemv_kernel(LinArgs p) {
       }
   __syncthreads();
 
-  bool bad = false;
+  bool bad = false, corrupt = false;
   const int nsplit = gridDim.y;
   for (int e = tid; e < Ml * BNC; e += NT) {
     const int m = e / BNC, c = e - m * BNC, n = n0 + c;
@@ -481,15 +500,15 @@ __global__ __launch_bounds__(64 * CG * KS) void gemv_kernel(LinArgs p) {
     if (nsplit > 1)
       ws_add(p, m0 + m, n, v);
     else
-      finalize<MODE>(p, m0 + m, n, v, bad);
+      finalize<MODE>(p, m0 + m, n, v, bad, corrupt);
   }
   if (nsplit > 1 && splitk_last(p, blockIdx.x, nsplit, &s_last)) {
     for (int e = tid; e < Ml * BNC; e += NT) {
       const int m = e / BNC, n = n0 + (e - m * BNC);
-      if (n < p.N) finalize<MODE>(p, m0 + m, n, ws_take(p, m0 + m, n), bad);
+      if (n < p.N) finalize<MODE>(p, m0 + m, n, ws_take(p, m0 + m, n), bad, corrupt);
     }
   }
-  if (MODE == EXACT && p.checked && bad) p.flag[0] = 1;
+  if (MODE == EXACT) write_flag(p, bad, corrupt);
 }
 
 // =====================================================================================================
@@ -650,7 +669,7 @@ __global__ __launch_bounds__(WM * WN * 64) void tile_kernel(LinArgs p) {
   if (MODE == EXACT)
     for (int r = tid; r < BM; r += NW * 64) s_sh[r] = p.sh[min(m0 + r, p.M - 1)];
   __syncthreads();
-  bool bad = false;
+  bool bad = false, corrupt = false;
   const int nsplit = gridDim.z;
   ColCtx cc[TN];
   if (MODE == EXACT)
@@ -671,7 +690,7 @@ __global__ __launch_bounds__(WM * WN * 64) void tile_kernel(LinArgs p) {
             const int e = e0 + u;
             mrow[u] = min(m0 + (wm * TM + a) * 32 + (e >> 2) * 8 + (lane >> 5) * 4 + (e & 3), p.M - 1);
           }
-          residual_rows<8>(p, cc[t], mrow, B);
+          residual_rows<8>(p, cc[t], mrow, B, corrupt);
         }
 #pragma unroll
         for (int u = 0; u < 8; ++u) {
@@ -684,9 +703,9 @@ __global__ __launch_bounds__(WM * WN * 64) void tile_kernel(LinArgs p) {
           if (nsplit > 1)
             ws_add(p, m, n, v);
           else if (MODE == EXACT)
-            finalize_col(p, cc[t], m, n, s_sh[r], v, B[u], bad);
+            finalize_col(p, cc[t], m, n, s_sh[r], v, B[u], bad, corrupt);
           else
-            finalize<MODE>(p, m, n, v, bad);
+            finalize<MODE>(p, m, n, v, bad, corrupt);
         }
         }
       }
@@ -707,21 +726,21 @@ __global__ __launch_bounds__(WM * WN * 64) void tile_kernel(LinArgs p) {
             mrow[u] = min(m, p.M - 1);
             v[u] = (m < p.M && n < p.N) ? ws_take(p, m, n) : 0;
           }
-          if (MODE == EXACT) residual_rows<8>(p, cc[t], mrow, B);
+          if (MODE == EXACT) residual_rows<8>(p, cc[t], mrow, B, corrupt);
 #pragma unroll
           for (int u = 0; u < 8; ++u) {
             const int e = e0 + u, r = (wm * TM + a) * 32 + (e >> 2) * 8 + (lane >> 5) * 4 + (e & 3), m = m0 + r;
             if (m < p.M && n < p.N) {
               if (MODE == EXACT)
-                finalize_col(p, cc[t], m, n, s_sh[r], v[u], B[u], bad);
+                finalize_col(p, cc[t], m, n, s_sh[r], v[u], B[u], bad, corrupt);
               else
-                finalize<MODE>(p, m, n, v[u], bad);
+                finalize<MODE>(p, m, n, v[u], bad, corrupt);
             }
           }
         }
       }
   }
-  if (MODE == EXACT && p.checked && bad) p.flag[0] = 1;
+  if (MODE == EXACT) write_flag(p, bad, corrupt);
 }
 
 // =====================================================================================================
@@ -840,7 +859,7 @@ __global__ __launch_bounds__(64 * WR * CG) void wide_kernel(LinArgs p) {
         Cs[(j * RA + row) * BNC + col] = acc[r][j][e];
       }
   __syncthreads();
-  bool bad = false;
+  bool bad = false, corrupt = false;
   for (int e = tid; e < M * BNC; e += NT) {
     const int m = e / BNC, c = e - m * BNC, n = n0 + c;
     if (n >= p.N) continue;
@@ -855,9 +874,9 @@ __global__ __launch_bounds__(64 * WR * CG) void wide_kernel(LinArgs p) {
 #pragma unroll
         for (int j = 0; j < NB; ++j) v += (int64_t)Cs[(j * RA + i * M + m) * BNC + c] << (8 * (i + j));
     }
-    finalize<MODE>(p, m, n, v, bad);
+    finalize<MODE>(p, m, n, v, bad, corrupt);
   }
-  if (MODE == EXACT && p.checked && bad) p.flag[0] = 1;
+  if (MODE == EXACT) write_flag(p, bad, corrupt);
 }
 
 // =====================================================================================================
@@ -921,7 +940,7 @@ __global__ __launch_bounds__(64 * CGW * KSW) void staged_kernel(LinArgs p) {
   const int col = threadIdx.x % BNC, cgo = col / CR, cl = col % CR, cc = cl >> 4, j = cl & 15;
   const int n = blockIdx.x * BNC + col;
   const int nla = MODE == JOIN ? p.nl : 1;
-  bool bad = false;
+  bool bad = false, corrupt = false;
   for (int m = threadIdx.x / BNC; m < p.M; m += NT / BNC) {
     int64_t v = 0;
     for (int i = 0; i < nla; ++i) {
@@ -931,7 +950,7 @@ __global__ __launch_bounds__(64 * CGW * KSW) void staged_kernel(LinArgs p) {
       for (int k2 = 0; k2 < KSW; ++k2) sum += ri[((k2 * CGW + cgo) * CWE + cc) * 256 + e];
       v += (int64_t)(int32_t)sum << (8 * i);
     }
-    if (n < p.N) finalize<MODE>(p, m, n, v, bad);
+    if (n < p.N) finalize<MODE>(p, m, n, v, bad, corrupt);
   }
 }
 
@@ -1078,8 +1097,9 @@ static Plan make_plan(int rows_a, int M_out, int N, int K, int nb, int na, bool 
   }
   // exact GEMMs of 22..32 rows (66..96 limb rows) with a long K (the engine's down projection, K = 8192) go to the
   // MFMA tiles with K split: 25.6 vs 29.5 us at M = 32, N = 2048 (plus a limb split, unless the caller brings q's
-  // limb planes); at K = 2048 the gemv stays (11.0 vs 16.7 us at N = 2048)
-  const bool long_k_tile = exact && M_out > 21 && M_out <= 32 && K >= 8192;
+  // limb planes); at K = 2048 the gemv stays (11.0 vs 16.7 us at N = 2048). Wider N (where the plan would pick the
+  // 64 x 32 deep-ring tile) was not measured and stays on the gemv.
+  const bool long_k_tile = exact && M_out > 21 && M_out <= 32 && K >= 8192 && N <= 3072;   // measured at N = 2048
   if (!long_k_tile && !dec_tile && rows_a <= 128 && gemv_shape(na, M_out, N, K, nb, exact, cus, s)) {
     s.gemv = true;
     const int RA = 16 * s.rb, BNC = 16 * s.cg;
@@ -1405,4 +1425,17 @@ extern "C" int bx_int8_gemm_join(const int8_t* a, const int8_t* w, int64_t* y, i
 extern "C" int64_t bx_int8_gemm_workspace(int32_t M, int32_t N, int32_t K, int32_t nl) {
   if (M <= 0 || N <= 0 || K <= 0 || nl < 1 || nl > 3) return 0;
   return make_plan(nl * M, M, N, K, 1, nl, false).ws_bytes;
+}
+
+// Which kernel bx_exact_linear launches for (M, N, K) (tests use it to prove they reach every configuration):
+// out[0] = 1 gemv, 2 wide, 3 tile; out[1] = tile configuration (0 T_BIG, 1 T_MID, 2 T_NARROW, 3 T_DEC,
+// 4 T_SMALL; -1 otherwise); out[2] = K splits; out[3] = blocks per split.
+extern "C" int bx_exact_linear_plan(int32_t M, int32_t N, int32_t K, int32_t* out) {
+  BX_REQUIRE(out && M > 0 && N > 0 && K > 0, "bad plan query");
+  const Plan s = make_plan(3 * M, M, N, K, 3, 3, true);
+  out[0] = s.gemv ? 1 : s.wide ? 2 : 3;
+  out[1] = (s.gemv || s.wide) ? -1 : s.tile;
+  out[2] = s.split;
+  out[3] = s.gemv ? s.tiles_x * s.parts : s.tiles_x * s.tiles_y;
+  return BX_OK;
 }

@@ -583,13 +583,13 @@ extern "C" int bx_silu_quant_ws(const int64_t* gu, int64_t ldgu, int32_t ff, con
   if (M == 0) return BX_OK;
   BX_REQUIRE(tmp && tmp_bytes >= bx_silu_quant_scratch(M, ff) && ((uintptr_t)tmp & 7) == 0,
              "scratch too small (%lld < %lld)", (long long)tmp_bytes, (long long)bx_silu_quant_scratch(M, ff));
+  BX_REQUIRE(!planes || ff % 16 == 0, "limb planes need ff %% 16 == 0");
   const int C = silu_chunks(ff), chunk = (ff + C - 1) / C;
   int64_t* P = (int64_t*)tmp;
   int64_t* slots = P + (int64_t)M * ff;
   const dim3 grid(M, C);
   silu_part_kernel<<<grid, kSiluPartThreads, 0, (hipStream_t)stream>>>(gu, ldgu, ff, chunk, lut, FR, P, slots, err);
   if (int rc = check_launch("silu_part_kernel")) return rc;
-  BX_REQUIRE(!planes || ff % 16 == 0, "limb planes need ff %% 16 == 0");
   silu_fin_kernel<<<grid, kSiluPartThreads, 0, (hipStream_t)stream>>>(P, slots, ff, chunk, FR, q, ldq, sh, planes);
   return check_launch("silu_fin_kernel");
 }

@@ -197,7 +197,7 @@ __global__ __launch_bounds__(256) void exact_epilogue_kernel(const int64_t* T, i
                                                              const int64_t* sh, int FR, int checked, int64_t* y,
                                                              int64_t ldy, int M, int N, int32_t* flag) {
   const int64_t total = (int64_t)M * N;
-  bool bad_any = false;
+  bool bad_any = false, corrupt = false;
   for (int64_t i = blockIdx.x * 256LL + threadIdx.x; i < total; i += (int64_t)gridDim.x * 256) {
     const int m = (int)(i / N), n = (int)(i - (int64_t)m * N);
     int64_t t = 0;
@@ -207,7 +207,11 @@ __global__ __launch_bounds__(256) void exact_epilogue_kernel(const int64_t* T, i
       b = B[(int64_t)m * ldb + n];
     } else {
       for (int j = 0; j < R; ++j) {
-        const int c = (int)min((uint32_t)ec[(int64_t)n * R + j], (uint32_t)(K - 1));   // valid ELL: [0, K)
+        // valid ELL columns are in [0, K); a corrupt one reads column 0 and raises the flag
+        const uint32_t c0 = (uint32_t)ec[(int64_t)n * R + j];
+        const bool out = c0 >= (uint32_t)K;
+        corrupt |= out;
+        const int c = out ? 0 : (int)c0;
         b = add_wrap(b, mul_wrap((int64_t)q[(int64_t)m * ldq + c], ev[(int64_t)n * R + j]));
       }
     }
@@ -216,7 +220,7 @@ __global__ __launch_bounds__(256) void exact_epilogue_kernel(const int64_t* T, i
     y[(int64_t)m * ldy + n] = exact_round(t, b, dn, sh[m] + g[n] - dn + FR, bad);
     bad_any |= bad;
   }
-  if (checked && wave_or(bad_any ? 1 : 0) && (threadIdx.x & 63) == 0) flag[0] = 1;
+  if (wave_or(((checked && bad_any) || corrupt) ? 1 : 0) && flag != nullptr && (threadIdx.x & 63) == 0) flag[0] = 1;
 }
 
 }  // namespace bx

@@ -41,6 +41,10 @@ int bx_version(void);
  * segs.lin_y(*Lin(q), sh, checked) (src/bitexact/exact/segs.py:25-32, src/bitexact/exact/model.py:61-70):
  * y int64 [M, N] = round((q W^T 2^d + B) 2^(sh + g - d + FR)) with B = sum_j q[m, col[n,j]] val[n,j];
  * when `checked`, sets flag[0] = 1 where wmm.epilogue(checked=True) would (src/bitexact/exact/wmm.py:132-150).
+ * A corrupt residual list (a column outside [0, K) or a count outside [0, R]) also sets flag[0] = 1, checked or
+ * not, whenever `flag` is given; a bad column reads q[m][0] and a bad count drops the row's list instead of
+ * reading outside q. The Python layer validates the ELL arrays once when weights are loaded
+ * (bitexact.exact.model.validate_ell).
  * Requires K % 16 == 0, ldq % 4 == 0, ld_row % 16 == 0, 16-byte aligned q and limbs. */
 int bx_exact_linear(const int32_t* q, int64_t ldq, const int64_t* sh, const int8_t* limbs, int64_t ld_plane,
                     int64_t ld_row, const int64_t* d, const int64_t* g, const int32_t* ell_cnt,
@@ -59,6 +63,11 @@ int bx_exact_linear_planes(const int32_t* q, int64_t ldq, const int64_t* sh, con
                            int64_t ws_bytes, const int8_t* q_planes, bx_stream_t stream);
 int64_t bx_exact_linear_workspace(int32_t M, int32_t N, int32_t K);
 int64_t bx_exact_linear_scratch(int32_t M, int32_t N, int32_t K);
+/* Introspection, no reference counterpart (the reference picks Triton configs per shape from static tables,
+ * src/bitexact/vllm_plugin/exact_gemm.py:205-226): which kernel bx_exact_linear runs for (M, N, K).
+ * out int32 [4] = {kernel: 1 gemv, 2 wide, 3 tile; tile config: 0 128x128, 1 64x128, 2 64x32, 3 64x64 int8 decode,
+ * 4 64x64 exact, -1 none; K splits; blocks per split}. Tests use it to show every configuration is reached. */
+int bx_exact_linear_plan(int32_t M, int32_t N, int32_t K, int32_t* out);
 
 /* Replaces wmm_triton / wmm_cublas / wmm_cpu (src/bitexact/exact/wmm.py:79-121): the exact dense product
  * T int64 [M, N] = q W^T (one slice of the reference's [split, M, N] partials). */

@@ -78,3 +78,20 @@ def test_constants_digest_and_file_roundtrip(tmp_path):
     assert set(d) == set(c) and d["n_layers"] == 2 and d["cfg"] == {"hidden_size": 64}
     assert all(torch.equal(d[k], c[k]) for k in c if torch.is_tensor(c[k]))
     assert consts.sha256(d) == consts.sha256(c)
+
+
+def test_validate_ell_rejects_corrupt_lists():
+    """The load-time ELL check: valid lists pass; a count outside [0, R] or a listed column outside [0, K) raises
+    AssertionError (unused padding slots are not checked)."""
+    import pytest
+    import torch
+    from bitexact.exact.model import validate_ell
+    cnt = torch.tensor([0, 2, 1], dtype=torch.int32)
+    ec = torch.tensor([[0, 0], [3, 63], [5, 999]], dtype=torch.int32)   # row 2's second slot is padding
+    validate_ell(cnt, ec, 2, 64)
+    for c2, e2 in ((torch.tensor([0, 3, 1], dtype=torch.int32), ec),
+                   (torch.tensor([-1, 2, 1], dtype=torch.int32), ec),
+                   (cnt, torch.tensor([[0, 0], [3, 64], [5, 0]], dtype=torch.int32)),
+                   (cnt, torch.tensor([[0, 0], [-2, 1], [5, 0]], dtype=torch.int32))):
+        with pytest.raises(AssertionError):
+            validate_ell(c2, e2, 2, 64)

@@ -356,3 +356,33 @@ def test_exact_linear_silu_planes(dev, M):
     ref, rflag, _ = R.epilogue(R.wmm_f64(qn, dec["W"]), R.residual(qn, dec["rr"], dec["rc"], dec["rv"], N),
                                dec["d"], dec["g"], shn, R.FR, True)
     assert np.array_equal(yb.cpu().numpy(), ref) and bool(f2.item()) == rflag
+
+
+@pytest.mark.parametrize("M", [4, 200])
+def test_corrupt_ell_index_sets_flag(dev, M):
+    """A residual column outside [0, K) or a count above R (a damaged weight) never reads outside q: the linear
+    raises the flag, checked or not, on the row-vector path (M = 4) and the tile path (M = 200). Valid lists leave
+    the flag clear."""
+    from bitexact.vllm_plugin.exact_gemm import exact_linear
+    N, K = 160, 512
+    dec = _dec(_bf16(N, K, 11))
+    limbs = torch.from_numpy(dec["limbs"]).to(dev)
+    d, gg = torch.from_numpy(dec["d"]).to(dev), torch.from_numpy(dec["g"]).to(dev)
+    cnt, ec, ev, Rr = _ell(dec, N, dev)
+    q = torch.ones(M, K, dtype=torch.int32, device=dev)
+    sh = torch.full((M,), -30, dtype=torch.long, device=dev)
+    for checked in (True, False):
+        flag = torch.zeros(1, dtype=torch.int32, device=dev)
+        exact_linear(q, sh, limbs, d, gg, cnt, ec, ev, Rr, flag, checked)
+        assert flag.item() == 0
+    n0 = int(torch.nonzero(cnt).flatten()[0])
+    for kind in ("col", "cnt"):
+        ec2, cnt2 = ec.clone(), cnt.clone()
+        if kind == "col":
+            ec2[n0, 0] = K + 5
+        else:
+            cnt2[n0] = Rr + 1
+        for checked in (True, False):
+            flag = torch.zeros(1, dtype=torch.int32, device=dev)
+            exact_linear(q, sh, limbs, d, gg, cnt2, ec2, ev, Rr, flag, checked)
+            assert flag.item() == 1, (kind, checked)
