@@ -28,6 +28,9 @@ SIGNATURES = {
     "bx_exact_linear_workspace": (I64, [I32, I32, I32]),
     "bx_exact_linear_scratch": (I64, [I32, I32, I32]),
     "bx_exact_linear_plan": (ctypes.c_int, [I32, I32, I32, P]),
+    "bx_exact_linear_noalloc": (ctypes.c_int, [P, I64, P, P, I64, I64, P, P, P, P, P, I32, P, I32, I32, I32, I32,
+                                               I32, P, P]),
+    "bx_exact_linear_noalloc_limit": (I64, []),
     "bx_exact_wmm": (ctypes.c_int, [P, I64, P, I64, I64, P, I32, I32, I32, P, I64, P, I64, P]),
     "bx_decompose_rows": (ctypes.c_int, [P, I32, I32, P, P, P, P, P, P]),
     "bx_decompose_residual": (ctypes.c_int, [P, I32, I32, P, P, P, P, I32, P]),

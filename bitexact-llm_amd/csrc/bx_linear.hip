@@ -22,6 +22,7 @@
 #include "bx_common.h"
 
 #include <algorithm>
+#include <mutex>
 
 namespace bx {
 
@@ -1438,4 +1439,70 @@ extern "C" int bx_exact_linear_plan(int32_t M, int32_t N, int32_t K, int32_t* ou
   out[2] = s.split;
   out[3] = s.gemv ? s.tiles_x * s.parts : s.tiles_x * s.tiles_y;
   return BX_OK;
+}
+
+// ---- the exact linear without caller buffers ----
+// `scratch` is a file-scope device array: each GPU the library runs on holds its own copy until the process ends.
+// Its first kNoAllocWs bytes are the split-K workspace (int64 partial sums and tile counters), the rest the q limb
+// planes. Host code never passes `scratch` itself to a kernel (in host code the name is only a stand-in): the
+// device address comes from hipGetSymbolAddress, once per device, with that device current.
+constexpr int64_t kNoAllocWs = 8LL << 20;
+constexpr int64_t kNoAllocTmp = 24LL << 20;
+static __device__ __align__(256) int8_t scratch[kNoAllocWs + kNoAllocTmp];
+
+namespace bx {
+
+static std::mutex g_scratch_mu;
+static void* g_scratch_ptr[64] = {};
+
+static int scratch_ptr(void** out) {
+  int dev = -1;
+  BX_REQUIRE(hipGetDevice(&dev) == hipSuccess && dev >= 0 && dev < 64, "no current HIP device");
+  std::lock_guard<std::mutex> lk(g_scratch_mu);
+  if (g_scratch_ptr[dev] == nullptr) {
+    void* p = nullptr;
+    const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || p == nullptr) {
+      set_error("hipGetSymbolAddress(scratch): %s", hipGetErrorString(e));
+      return BX_EHIP;
+    }
+    g_scratch_ptr[dev] = p;
+  }
+  *out = g_scratch_ptr[dev];
+  return BX_OK;
+}
+
+__global__ __launch_bounds__(256) void zero_kernel(int4* p, int64_t n16) {
+  for (int64_t i = blockIdx.x * 256LL + threadIdx.x; i < n16; i += (int64_t)gridDim.x * 256) p[i] = int4{0, 0, 0, 0};
+}
+
+}  // namespace bx
+
+extern "C" int64_t bx_exact_linear_noalloc_limit(void) { return kNoAllocWs + kNoAllocTmp; }
+
+extern "C" int bx_exact_linear_noalloc(const int32_t* q, int64_t ldq, const int64_t* sh, const int8_t* limbs,
+                                       int64_t ld_plane, int64_t ld_row, const int64_t* d, const int64_t* g,
+                                       const int32_t* ell_cnt, const int32_t* ell_col, const int64_t* ell_val,
+                                       int32_t R, int64_t* y, int32_t M, int32_t N, int32_t K, int32_t FR,
+                                       int32_t checked, int32_t* flag, bx_stream_t stream) {
+  BX_REQUIRE(M >= 0 && N >= 0 && K >= 0, "negative size");
+  if (M == 0 || N == 0) return BX_OK;
+  BX_REQUIRE(K > 0, "K == 0");
+  const Plan s = make_plan(3 * M, M, N, K, 3, 3, true);
+  BX_REQUIRE(s.ws_bytes <= kNoAllocWs, "no-alloc linear: split-K workspace of %lld bytes exceeds the static %lld",
+             (long long)s.ws_bytes, (long long)kNoAllocWs);
+  BX_REQUIRE(s.tmp_bytes <= kNoAllocTmp, "no-alloc linear: limb-plane scratch of %lld bytes exceeds the static %lld",
+             (long long)s.tmp_bytes, (long long)kNoAllocTmp);
+  void* base = nullptr;
+  if (int rc = scratch_ptr(&base)) return rc;
+  // the workspace contract wants zeros on entry; the array keeps whatever the last call left, so clear the part
+  // this call uses (a fill kernel, so the call stays capturable)
+  if (s.ws_bytes > 0) {
+    const int64_t n16 = (s.ws_bytes + 15) / 16;
+    const int blocks = (int)std::min<int64_t>((n16 + 255) / 256, 1024);
+    zero_kernel<<<blocks, 256, 0, (hipStream_t)stream>>>((int4*)base, n16);
+    if (int rc = check_launch("zero_kernel")) return rc;
+  }
+  return bx_exact_linear(q, ldq, sh, limbs, ld_plane, ld_row, d, g, ell_cnt, ell_col, ell_val, R, y, M, N, K, FR,
+                         checked, flag, base, kNoAllocWs, (int8_t*)base + kNoAllocWs, kNoAllocTmp, stream);
 }

@@ -63,6 +63,17 @@ int bx_exact_linear_planes(const int32_t* q, int64_t ldq, const int64_t* sh, con
                            int64_t ws_bytes, const int8_t* q_planes, bx_stream_t stream);
 int64_t bx_exact_linear_workspace(int32_t M, int32_t N, int32_t K);
 int64_t bx_exact_linear_scratch(int32_t M, int32_t N, int32_t K);
+/* No counterpart in the reference. For callers that cannot allocate device memory (code under HIP graph capture,
+ * tight serving loops, harnesses that forbid hipMalloc): bx_exact_linear with its split-K workspace and limb-plane
+ * scratch taken from a static device array of bx_exact_linear_noalloc_limit() bytes (32 MiB: 8 MiB workspace,
+ * 24 MiB scratch) that each GPU holds until the process ends. Shapes whose plan needs more fail with BX_EINVAL.
+ * Allocates nothing. Every call on one GPU shares that GPU's array: calls that overlap in time on one GPU (two
+ * streams, two threads) race and give wrong results. Same rule, arguments and flag as bx_exact_linear. */
+int bx_exact_linear_noalloc(const int32_t* q, int64_t ldq, const int64_t* sh, const int8_t* limbs, int64_t ld_plane,
+                            int64_t ld_row, const int64_t* d, const int64_t* g, const int32_t* ell_cnt,
+                            const int32_t* ell_col, const int64_t* ell_val, int32_t R, int64_t* y, int32_t M,
+                            int32_t N, int32_t K, int32_t FR, int32_t checked, int32_t* flag, bx_stream_t stream);
+int64_t bx_exact_linear_noalloc_limit(void);
 /* Introspection, no reference counterpart (the reference picks Triton configs per shape from static tables,
  * src/bitexact/vllm_plugin/exact_gemm.py:205-226): which kernel bx_exact_linear runs for (M, N, K).
  * out int32 [4] = {kernel: 1 gemv, 2 wide, 3 tile; tile config: 0 128x128, 1 64x128, 2 64x32, 3 64x64 int8 decode,
