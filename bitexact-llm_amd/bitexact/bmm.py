@@ -7,9 +7,12 @@ na / nb signed base-256 limbs -> exact int64 [Z, M, N] on the GPU.
 import torch
 
 from bitexact import _hip
+from bitexact._ops import empty, op
 
 
-def bmm(a, b, na=3, nb=3):
+@op("bmm(Tensor a, Tensor b, int na, int nb) -> Tensor",
+    lambda a, b, na, nb: empty((a.shape[0], a.shape[1], b.shape[2]), torch.long, a))
+def _bmm(a, b, na, nb):
     _hip.require_cuda(a, b)
     Z, M, K = a.shape
     N = b.shape[2]
@@ -21,3 +24,8 @@ def bmm(a, b, na=3, nb=3):
               b.element_size(), b.stride(0), b.stride(1), b.stride(2), _hip.ptr(c), c.stride(0), c.stride(1),
               c.stride(2), Z, M, N, K, na, nb, _hip.stream_of(a))
     return c
+
+
+def bmm(a, b, na=3, nb=3):
+    """Exact a @ b for [Z, M, K] x [Z, K, N] integer tensors -> int64 [Z, M, N]."""
+    return _bmm(a, b, int(na), int(nb))

@@ -10,6 +10,7 @@ num int64 [Z, gT, HD], den int64 [Z, gT, 1].
 import torch
 
 from bitexact import _hip
+from bitexact._ops import empty, op
 
 
 def _aligned_rows(t):
@@ -18,7 +19,14 @@ def _aligned_rows(t):
     return t if ok else t.contiguous()
 
 
-def prefill(qg, shg, K, V, qpos, lut, l2e):
+def _prefill_fake(qg, shg, K, V, qpos, lut, l2e):
+    Z, gT, HD = qg.shape
+    return empty((Z, gT, HD), torch.long, qg), empty((Z, gT, 1), torch.long, qg)
+
+
+@op("attn_prefill(Tensor qg, Tensor shg, Tensor K, Tensor V, Tensor qpos, Tensor lut, int l2e) -> (Tensor, Tensor)",
+    _prefill_fake)
+def _prefill(qg, shg, K, V, qpos, lut, l2e):
     _hip.require_cuda(qg, shg, K, V, qpos, lut)
     Z, gT, HD = qg.shape
     S = K.shape[1]
@@ -35,3 +43,7 @@ def prefill(qg, shg, K, V, qpos, lut, l2e):
               qpos.stride(0), qpos.stride(1), _hip.ptr(K), K.stride(0), K.stride(1), _hip.ptr(V), V.stride(0),
               V.stride(1), S, _hip.ptr(lut), int(l2e), _hip.ptr(num), _hip.ptr(den), Z, gT, HD, _hip.stream_of(qg))
     return num, den
+
+
+def prefill(qg, shg, K, V, qpos, lut, l2e):
+    return _prefill(qg, shg, K, V, qpos, lut, int(l2e))

@@ -16,6 +16,7 @@ gu_silu_y(y, lut, err)          Segs.gu_silu_y: silu(gate) up + quantization at 
 import torch
 
 from bitexact import _hip
+from bitexact._ops import empty, op
 from bitexact.exact.consts import FR
 
 FN = 40
@@ -43,21 +44,33 @@ def _or(err, flag, given):
     return e if err is None else (err | e)
 
 
-def norm_quant(x, gm, ge, err=None, flag=None):
+@op("norm_quant(Tensor x, Tensor gm, Tensor ge, Tensor(a!) flag) -> (Tensor, Tensor)",
+    lambda x, gm, ge, flag: (empty(x.shape, torch.int32, x), empty(x.shape[:1], torch.long, x)))
+def _norm_quant(x, gm, ge, flag):
     _hip.require_cuda(x, gm, ge)
-    assert x.dtype == torch.int64 and x.stride(-1) == 1
+    assert x.dtype == torch.int64 and x.stride(-1) == 1 and x.dim() == 2
     M, D = x.shape
     q = torch.empty(M, D, dtype=torch.int32, device=x.device)
     sh = torch.empty(M, dtype=torch.long, device=x.device)
-    fl = _flag(x.device, flag)
     gm, ge = gm.contiguous().long(), ge.contiguous().long()     # kept alive until the launch is queued
     _hip.call("bx_rmsnorm_quant", _hip.ptr(x), x.stride(0), _hip.ptr(gm), _hip.ptr(ge), _hip.ptr(q), D, _hip.ptr(sh),
-              M, D, FR, FN, _hip.ptr(fl), _hip.stream_of(x))
+              M, D, FR, FN, _hip.ptr(flag), _hip.stream_of(x))
+    return q, sh
+
+
+def norm_quant(x, gm, ge, err=None, flag=None):
+    fl = _flag(x.device, flag)
+    q, sh = _norm_quant(x, gm, ge, fl)
     return q, sh, _or(err, fl, flag)
 
 
-def softmax(raw, qpos, shg, lut, l2e, kbits=FK, fp=FP):
-    """raw int64 [..., S] scores, qpos / shg broadcastable [..., 1] -> (p int32 [..., S], den int64 [..., 1])."""
+def _softmax_fake(raw, qpos, shg, lut, l2e, kbits, fp):
+    return empty(raw.shape, torch.int32, raw), empty((*raw.shape[:-1], 1), torch.long, raw)
+
+
+@op("softmax(Tensor raw, Tensor qpos, Tensor shg, Tensor lut, int l2e, int kbits, int fp) -> (Tensor, Tensor)",
+    _softmax_fake)
+def _softmax(raw, qpos, shg, lut, l2e, kbits, fp):
     _hip.require_cuda(raw, qpos, shg, lut)
     S = raw.shape[-1]
     lead = raw.shape[:-1]
@@ -75,8 +88,19 @@ def softmax(raw, qpos, shg, lut, l2e, kbits=FK, fp=FP):
     return p.view(*lead, S), den.view(*lead, 1)
 
 
-def attn_out(num, den, T, hkv):
-    """num int64 [Z = B HKV, g T, HD], den [Z, g T, 1] -> (q int32 [B T, H HD], sh int64 [B T])."""
+def softmax(raw, qpos, shg, lut, l2e, kbits=FK, fp=FP):
+    """raw int64 [..., S] scores, qpos / shg broadcastable [..., 1] -> (p int32 [..., S], den int64 [..., 1])."""
+    return _softmax(raw, qpos, shg, lut, int(l2e), int(kbits), int(fp))
+
+
+def _attn_out_fake(num, den, T, hkv):
+    Z, gT, HD = num.shape
+    rows = (Z // hkv) * T
+    return empty((rows, hkv * (gT // T) * HD), torch.int32, num), empty((rows,), torch.long, num)
+
+
+@op("attn_out(Tensor num, Tensor den, int T, int hkv) -> (Tensor, Tensor)", _attn_out_fake)
+def _attn_out(num, den, T, hkv):
     _hip.require_cuda(num, den)
     Z, gT, HD = num.shape
     g = gT // T
@@ -91,6 +115,64 @@ def attn_out(num, den, T, hkv):
     return q, sh
 
 
+def attn_out(num, den, T, hkv):
+    """num int64 [Z = B HKV, g T, HD], den [Z, g T, 1] -> (q int32 [B T, H HD], sh int64 [B T])."""
+    return _attn_out(num, den, int(T), int(hkv))
+
+
+def _qkv_fake(y, pos, cos, sin, B, T, H, HKV, HD, flag):
+    g = H // HKV
+    return (empty((B * HKV, g * T, HD), torch.int32, y), empty((B * HKV, g * T, 1), torch.long, y),
+            empty((B, T, HKV, HD), torch.long, y), empty((B, T, HKV, HD), torch.long, y))
+
+
+def _qkv_check(y, pos, cos, sin, B, T, H, HKV, HD):
+    _hip.require_cuda(y, pos, cos, sin)
+    assert y.dtype == torch.int64 and y.stride(-1) == 1 and y.shape[0] == B * T
+    assert y.shape[1] >= (H + 2 * HKV) * HD and H % HKV == 0
+    assert pos.dtype == torch.int64 and pos.dim() == 2
+    assert cos.shape == sin.shape and cos.shape[1] == HD // 2
+
+
+@op("qkv_y(Tensor y, Tensor pos, Tensor cos, Tensor sin, int B, int T, int H, int HKV, int HD, Tensor(a!) flag) -> "
+    "(Tensor, Tensor, Tensor, Tensor)", _qkv_fake)
+def _qkv_y(y, pos, cos, sin, B, T, H, HKV, HD, flag):
+    _qkv_check(y, pos, cos, sin, B, T, H, HKV, HD)
+    g = H // HKV
+    dev = y.device
+    cos, sin = cos.contiguous().long(), sin.contiguous().long()
+    qg = torch.empty(B * HKV, g * T, HD, dtype=torch.int32, device=dev)
+    shg = torch.empty(B * HKV, g * T, 1, dtype=torch.long, device=dev)
+    k = torch.empty(B, T, HKV, HD, dtype=torch.long, device=dev)
+    v = torch.empty(B, T, HKV, HD, dtype=torch.long, device=dev)
+    _hip.call("bx_rope_qgroup", _hip.ptr(y), y.stride(0), _hip.ptr(pos), pos.stride(0), pos.stride(1),
+              _hip.ptr(cos), _hip.ptr(sin), cos.shape[0], B, T, H, HKV, HD, FR, FT, FK, FV, FZ, _hip.ptr(qg),
+              _hip.ptr(shg), _hip.ptr(k), _hip.ptr(v), _hip.ptr(flag), _hip.stream_of(y))
+    return qg, shg, k, v
+
+
+@op("qkv_y_store(Tensor y, Tensor pos, Tensor cos, Tensor sin, int B, int T, int H, int HKV, int HD, "
+    "Tensor(a!) flag, Tensor(b!) cache, Tensor slot) -> (Tensor, Tensor)",
+    lambda y, pos, cos, sin, B, T, H, HKV, HD, flag, cache, slot: _qkv_fake(y, pos, cos, sin, B, T, H, HKV, HD,
+                                                                              flag)[:2])
+def _qkv_y_store(y, pos, cos, sin, B, T, H, HKV, HD, flag, c, slot):
+    _qkv_check(y, pos, cos, sin, B, T, H, HKV, HD)
+    g = H // HKV
+    dev = y.device
+    cos, sin = cos.contiguous().long(), sin.contiguous().long()
+    qg = torch.empty(B * HKV, g * T, HD, dtype=torch.int32, device=dev)
+    shg = torch.empty(B * HKV, g * T, 1, dtype=torch.long, device=dev)
+    _hip.require_cuda(c, slot)
+    assert c.dtype == torch.int8 and c.dim() == 4 and c.shape[1] == HKV and c.shape[3] >= 6 * HD and c.stride(3) == 1
+    slot = slot.reshape(-1).contiguous().long()
+    assert slot.shape[0] == B * T
+    _hip.call("bx_rope_qgroup_store", _hip.ptr(y), y.stride(0), _hip.ptr(pos), pos.stride(0), pos.stride(1),
+              _hip.ptr(cos), _hip.ptr(sin), cos.shape[0], B, T, H, HKV, HD, FR, FT, FK, FV, FZ, _hip.ptr(qg),
+              _hip.ptr(shg), None, None, _hip.ptr(c), c.stride(0), c.stride(1), c.stride(2), _hip.ptr(slot),
+              c.shape[2], _hip.ptr(flag), _hip.stream_of(y))
+    return qg, shg
+
+
 def qkv_y(y, pos, cos, sin, B, T, dm, err=None, flag=None, store=None):
     """Segs.qkv_y (src/bitexact/exact/segs.py:170-173): y int64 [B T, (H + 2 HKV) HD] at FR, pos int64 [B, T],
     cos / sin int64 [n_pos, HD / 2] at FT, dm = (H, HKV, HD) -> qg int32 [B HKV, g T, HD], shg int64
@@ -98,68 +180,74 @@ def qkv_y(y, pos, cos, sin, B, T, dm, err=None, flag=None, store=None):
     store = (cache, slot): exact_fuse.qkv's fused store (src/bitexact/vllm_plugin/exact_fuse.py:372-386): K / V go
     straight into the limb-plane cache (int8 [nb, HKV, bs, 8 HD]) at slot [B T] (< 0: skipped), and k / v are
     returned as None."""
-    _hip.require_cuda(y, pos, cos, sin)
-    H, HKV, HD = dm
-    assert y.dtype == torch.int64 and y.stride(-1) == 1 and y.shape[0] == B * T
-    assert y.shape[1] >= (H + 2 * HKV) * HD and H % HKV == 0
-    g = H // HKV
-    dev = y.device
+    H, HKV, HD = (int(v) for v in dm)
+    fl = _flag(y.device, flag)
     pos = pos.long()
-    cos, sin = cos.contiguous().long(), sin.contiguous().long()
-    assert cos.shape == sin.shape and cos.shape[1] == HD // 2
-    qg = torch.empty(B * HKV, g * T, HD, dtype=torch.int32, device=dev)
-    shg = torch.empty(B * HKV, g * T, 1, dtype=torch.long, device=dev)
-    fl = _flag(dev, flag)
     if store is not None:
         c, slot = store
-        _hip.require_cuda(c, slot)
-        assert c.dtype == torch.int8 and c.dim() == 4 and c.shape[1] == HKV and c.shape[3] >= 6 * HD and c.stride(3) == 1
-        slot = slot.reshape(-1).contiguous().long()
-        assert slot.shape[0] == B * T
-        _hip.call("bx_rope_qgroup_store", _hip.ptr(y), y.stride(0), _hip.ptr(pos), pos.stride(0), pos.stride(1),
-                  _hip.ptr(cos), _hip.ptr(sin), cos.shape[0], B, T, H, HKV, HD, FR, FT, FK, FV, FZ, _hip.ptr(qg),
-                  _hip.ptr(shg), None, None, _hip.ptr(c), c.stride(0), c.stride(1), c.stride(2), _hip.ptr(slot),
-                  c.shape[2], _hip.ptr(fl), _hip.stream_of(y))
+        qg, shg = _qkv_y_store(y, pos, cos, sin, int(B), int(T), H, HKV, HD, fl, c, slot)
         return qg, shg, None, None, _or(err, fl, flag)
-    k = torch.empty(B, T, HKV, HD, dtype=torch.long, device=dev)
-    v = torch.empty(B, T, HKV, HD, dtype=torch.long, device=dev)
-    _hip.call("bx_rope_qgroup", _hip.ptr(y), y.stride(0), _hip.ptr(pos), pos.stride(0), pos.stride(1),
-              _hip.ptr(cos), _hip.ptr(sin), cos.shape[0], B, T, H, HKV, HD, FR, FT, FK, FV, FZ, _hip.ptr(qg),
-              _hip.ptr(shg), _hip.ptr(k), _hip.ptr(v), _hip.ptr(fl), _hip.stream_of(y))
+    qg, shg, k, v = _qkv_y(y, pos, cos, sin, int(B), int(T), H, HKV, HD, fl)
     return qg, shg, k, v, _or(err, fl, flag)
 
 
-
-
-def add_norm_y(y, x, gm, ge, err=None, flag=None, planes=False):
-    """Segs.add_norm_y (src/bitexact/exact/segs.py:175-178): x int64 [M, D] += y (in place, as exact_fuse.add_norm's
-    store), then norm_quant of the sum. gm None: the add alone (returns q = sh = None). planes=True: q is returned
-    as (q, limb planes int8 [3, M, D]) for exact_linear's q_planes (the limb split done by the norm kernel)."""
+@op("add_rows(Tensor y, Tensor(a!) x, Tensor(b!) flag) -> ()", lambda y, x, flag: None)
+def _add_rows(y, x, flag):
     _hip.require_cuda(x, y)
     assert x.dtype == torch.int64 and y.dtype == torch.int64 and x.stride(-1) == 1 and y.stride(-1) == 1
     M, D = x.shape
     y = y.view(M, D) if y.dim() != 2 else y
-    fl = _flag(x.device, flag)
-    if gm is None:
-        _hip.call("bx_add_rmsnorm_quant", _hip.ptr(x), x.stride(0), _hip.ptr(y), y.stride(0), None, None, None, D, None,
-                  M, D, FR, FN, _hip.ptr(fl), _hip.stream_of(x))
-        return x, None, None, _or(err, fl, flag)
+    _hip.call("bx_add_rmsnorm_quant", _hip.ptr(x), x.stride(0), _hip.ptr(y), y.stride(0), None, None, None, D, None,
+              M, D, FR, FN, _hip.ptr(flag), _hip.stream_of(x))
+
+
+def _add_norm_fake(y, x, gm, ge, flag, planes):
+    M, D = x.shape
+    return (empty((M, D), torch.int32, x), empty((3, M, D) if planes else (0,), torch.int8, x),
+            empty((M,), torch.long, x))
+
+
+@op("add_norm(Tensor y, Tensor(a!) x, Tensor gm, Tensor ge, Tensor(b!) flag, bool planes) -> (Tensor, Tensor, Tensor)",
+    _add_norm_fake)
+def _add_norm(y, x, gm, ge, flag, planes):
+    _hip.require_cuda(x, y)
+    assert x.dtype == torch.int64 and y.dtype == torch.int64 and x.stride(-1) == 1 and y.stride(-1) == 1
+    M, D = x.shape
+    y = y.view(M, D) if y.dim() != 2 else y
     q = torch.empty(M, D, dtype=torch.int32, device=x.device)
     sh = torch.empty(M, dtype=torch.long, device=x.device)
     gm, ge = gm.contiguous().long(), ge.contiguous().long()
     if planes:
         pl = torch.empty(3, M, D, dtype=torch.int8, device=x.device)
         _hip.call("bx_add_rmsnorm_quant_planes", _hip.ptr(x), x.stride(0), _hip.ptr(y), y.stride(0), _hip.ptr(gm),
-                  _hip.ptr(ge), _hip.ptr(q), D, _hip.ptr(sh), _hip.ptr(pl), M, D, FR, FN, _hip.ptr(fl),
+                  _hip.ptr(ge), _hip.ptr(q), D, _hip.ptr(sh), _hip.ptr(pl), M, D, FR, FN, _hip.ptr(flag),
                   _hip.stream_of(x))
-        return x, (q, pl), sh, _or(err, fl, flag)
+        return q, pl, sh
     _hip.call("bx_add_rmsnorm_quant", _hip.ptr(x), x.stride(0), _hip.ptr(y), y.stride(0), _hip.ptr(gm), _hip.ptr(ge),
-              _hip.ptr(q), D, _hip.ptr(sh), M, D, FR, FN, _hip.ptr(fl), _hip.stream_of(x))
-    return x, q, sh, _or(err, fl, flag)
+              _hip.ptr(q), D, _hip.ptr(sh), M, D, FR, FN, _hip.ptr(flag), _hip.stream_of(x))
+    return q, torch.empty(0, dtype=torch.int8, device=x.device), sh
 
 
-def embed_norm(emb, ids, gm, ge, err=None, flag=None):
-    """x = emb[ids].long() (emb int32 [V, D]) and its pre_norm (src/bitexact/exact/model.py:130-132) -> (x, q, sh, err)."""
+def add_norm_y(y, x, gm, ge, err=None, flag=None, planes=False):
+    """Segs.add_norm_y (src/bitexact/exact/segs.py:175-178): x int64 [M, D] += y (in place, as exact_fuse.add_norm's
+    store), then norm_quant of the sum. gm None: the add alone (returns q = sh = None). planes=True: q is returned
+    as (q, limb planes int8 [3, M, D]) for exact_linear's q_planes (the limb split done by the norm kernel)."""
+    fl = _flag(x.device, flag)
+    if gm is None:
+        _add_rows(y, x, fl)
+        return x, None, None, _or(err, fl, flag)
+    q, pl, sh = _add_norm(y, x, gm, ge, fl, bool(planes))
+    return x, ((q, pl) if planes else q), sh, _or(err, fl, flag)
+
+
+def _embed_fake(emb, ids, gm, ge, flag):
+    M, D = ids.numel(), emb.shape[1]
+    return empty((M, D), torch.long, emb), empty((M, D), torch.int32, emb), empty((M,), torch.long, emb)
+
+
+@op("embed_norm(Tensor emb, Tensor ids, Tensor gm, Tensor ge, Tensor(a!) flag) -> (Tensor, Tensor, Tensor)",
+    _embed_fake)
+def _embed_norm(emb, ids, gm, ge, flag):
     _hip.require_cuda(emb, ids, gm, ge)
     assert emb.dtype == torch.int32 and emb.is_contiguous()
     ids = ids.reshape(-1).contiguous().long()
@@ -167,14 +255,46 @@ def embed_norm(emb, ids, gm, ge, err=None, flag=None):
     x = torch.empty(M, D, dtype=torch.long, device=emb.device)
     q = torch.empty(M, D, dtype=torch.int32, device=emb.device)
     sh = torch.empty(M, dtype=torch.long, device=emb.device)
-    fl = _flag(emb.device, flag)
     gm, ge = gm.contiguous().long(), ge.contiguous().long()
     _hip.call("bx_embed_rmsnorm_quant", _hip.ptr(emb), _hip.ptr(ids), _hip.ptr(x), D, _hip.ptr(gm), _hip.ptr(ge),
-              _hip.ptr(q), D, _hip.ptr(sh), M, D, FR, FN, _hip.ptr(fl), _hip.stream_of(emb))
+              _hip.ptr(q), D, _hip.ptr(sh), M, D, FR, FN, _hip.ptr(flag), _hip.stream_of(emb))
+    return x, q, sh
+
+
+def embed_norm(emb, ids, gm, ge, err=None, flag=None):
+    """x = emb[ids].long() (emb int32 [V, D]) and its pre_norm (src/bitexact/exact/model.py:130-132) -> (x, q, sh, err)."""
+    fl = _flag(emb.device, flag)
+    x, q, sh = _embed_norm(emb, ids, gm, ge, fl)
     return x, q, sh, _or(err, fl, flag)
 
 
 SILU_SPLIT_ROWS = 128   # fewer rows than this: the stage is split over column chunks (bx_silu_quant_ws)
+
+
+def _silu_fake(y, lut, flag, split, planes):
+    M, ff = y.shape[0], y.shape[1] // 2
+    return (empty((M, ff), torch.int32, y), empty((3, M, ff) if planes else (0,), torch.int8, y),
+            empty((M,), torch.long, y))
+
+
+@op("gu_silu(Tensor y, Tensor lut, Tensor(a!) flag, bool split, bool planes) -> (Tensor, Tensor, Tensor)", _silu_fake)
+def _gu_silu(y, lut, flag, split, planes):
+    _hip.require_cuda(y, lut)
+    assert y.dtype == torch.int64 and y.stride(-1) == 1 and y.shape[1] % 2 == 0
+    M, ff = y.shape[0], y.shape[1] // 2
+    q = torch.empty(M, ff, dtype=torch.int32, device=y.device)
+    sh = torch.empty(M, dtype=torch.long, device=y.device)
+    lut = lut.contiguous().long()
+    assert split or not planes, "limb planes come from the column-chunked path"
+    pl = torch.empty((3, M, ff) if planes else (0,), dtype=torch.int8, device=y.device)
+    if split and M > 0:
+        tmp, tmpb = _hip.scratch(y.device, _hip.lib().bx_silu_quant_scratch(M, ff))
+        _hip.call("bx_silu_quant_ws", _hip.ptr(y), y.stride(0), ff, _hip.ptr(lut), FR, _hip.ptr(q), ff, _hip.ptr(sh),
+                  _hip.ptr(pl) if planes else None, M, _hip.ptr(flag), _hip.ptr(tmp), tmpb, _hip.stream_of(y))
+        return q, pl, sh
+    _hip.call("bx_silu_quant", _hip.ptr(y), y.stride(0), ff, _hip.ptr(lut), FR, _hip.ptr(q), ff, _hip.ptr(sh), M,
+              _hip.ptr(flag), _hip.stream_of(y))
+    return q, pl, sh
 
 
 def gu_silu_y(y, lut, err=None, flag=None, split=None, planes=False):
@@ -182,22 +302,8 @@ def gu_silu_y(y, lut, err=None, flag=None, split=None, planes=False):
     (q int32 [M, ff], sh int64 [M], err | not ok). split: None picks by row count; True / False force the
     column-chunked or the row-per-block kernel (the same integers either way). planes=True (column-chunked path):
     q is returned as (q, limb planes int8 [3, M, ff]) for exact_linear's q_planes."""
-    _hip.require_cuda(y, lut)
-    assert y.dtype == torch.int64 and y.stride(-1) == 1 and y.shape[1] % 2 == 0
-    M, ff = y.shape[0], y.shape[1] // 2
-    q = torch.empty(M, ff, dtype=torch.int32, device=y.device)
-    sh = torch.empty(M, dtype=torch.long, device=y.device)
     fl = _flag(y.device, flag)
-    lut = lut.contiguous().long()
     if split is None:
-        split = M < SILU_SPLIT_ROWS or planes
-    assert split or not planes, "limb planes come from the column-chunked path"
-    if split and M > 0:
-        tmp, tmpb = _hip.scratch(y.device, _hip.lib().bx_silu_quant_scratch(M, ff))
-        pl = torch.empty(3, M, ff, dtype=torch.int8, device=y.device) if planes else None
-        _hip.call("bx_silu_quant_ws", _hip.ptr(y), y.stride(0), ff, _hip.ptr(lut), FR, _hip.ptr(q), ff, _hip.ptr(sh),
-                  _hip.ptr(pl), M, _hip.ptr(fl), _hip.ptr(tmp), tmpb, _hip.stream_of(y))
-        return ((q, pl) if planes else q), sh, _or(err, fl, flag)
-    _hip.call("bx_silu_quant", _hip.ptr(y), y.stride(0), ff, _hip.ptr(lut), FR, _hip.ptr(q), ff, _hip.ptr(sh), M,
-              _hip.ptr(fl), _hip.stream_of(y))
-    return q, sh, _or(err, fl, flag)
+        split = y.shape[0] < SILU_SPLIT_ROWS or planes
+    q, pl, sh = _gu_silu(y, lut, fl, bool(split), bool(planes))
+    return ((q, pl) if planes else q), sh, _or(err, fl, flag)

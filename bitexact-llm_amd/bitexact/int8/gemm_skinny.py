@@ -8,6 +8,7 @@ K * 127 * 128 < 2^31). int_mm_join(a, w, M, nl) also joins the nl limb row block
 import torch
 
 from bitexact import _hip
+from bitexact._ops import empty, op
 
 
 def _check(a, w):
@@ -16,6 +17,7 @@ def _check(a, w):
     assert a.is_contiguous() and w.is_contiguous() and a.shape[1] == w.shape[1]
 
 
+@op("int_mm(Tensor a, Tensor w) -> Tensor", lambda a, w: empty((a.shape[0], w.shape[0]), torch.int32, a))
 def int_mm(a, w):
     _check(a, w)
     R, K = a.shape
@@ -26,6 +28,8 @@ def int_mm(a, w):
     return c
 
 
+@op("int_mm_join(Tensor a, Tensor w, int M, int nl) -> Tensor",
+    lambda a, w, M, nl: empty((M, w.shape[0]), torch.long, a))
 def int_mm_join(a, w, M, nl):
     """a: nl row blocks of M limb rows (rows beyond nl M, e.g. stack_limbs' padding, are ignored)."""
     _check(a, w)

@@ -8,6 +8,7 @@ flags. Decode-sized M streams the weight planes once (split-K, one launch); pref
 import torch
 
 from bitexact import _hip
+from bitexact._ops import empty, op
 from bitexact.exact.consts import FR
 
 
@@ -29,8 +30,13 @@ def plan(M, N, K):
     return KERNELS[out[0]], TILES[out[1]], out[2], out[3]
 
 
-def exact_linear(q, sh, limbs, d, g, cnt, ec, ev, R, flag=None, checked=True, fr=FR, q_planes=None):
-    """The fused exact linear on raw tensors; returns y (and sets flag). q_planes: q's int8 limb planes [3, M, K]."""
+def _exact_linear_fake(q, sh, limbs, d, g, cnt, ec, ev, R, flag, checked, fr, q_planes):
+    return empty((q.shape[0], limbs.shape[1]), torch.long, q)
+
+
+@op("exact_linear(Tensor q, Tensor sh, Tensor limbs, Tensor d, Tensor g, Tensor? cnt, Tensor? ec, Tensor? ev, "
+    "int R, Tensor(a!)? flag, bool checked, int fr, Tensor? q_planes) -> Tensor", _exact_linear_fake)
+def _exact_linear(q, sh, limbs, d, g, cnt, ec, ev, R, flag, checked, fr, q_planes):
     _hip.require_cuda(q, limbs)
     assert q.dtype == torch.int32 and q.stride(1) == 1 and limbs.stride(2) == 1
     M, K = q.shape
@@ -50,12 +56,16 @@ def exact_linear(q, sh, limbs, d, g, cnt, ec, ev, R, flag=None, checked=True, fr
                   int(checked), _hip.ptr(flag), _hip.ptr(ws), wsb, _hip.ptr(q_planes), _hip.stream_of(q))
         return y
     tmp, tmpb = _hip.scratch(q.device, _hip.lib().bx_exact_linear_scratch(M, N, K))
-    sh = sh.contiguous()
     _hip.call("bx_exact_linear", _hip.ptr(q), q.stride(0), _hip.ptr(sh), _hip.ptr(limbs), limbs.stride(0),
               limbs.stride(1), _hip.ptr(d), _hip.ptr(g), _hip.ptr(cnt) if R else None,
               _hip.ptr(ec) if R else None, _hip.ptr(ev) if R else None, R, _hip.ptr(y), M, N, K, fr, int(checked),
               _hip.ptr(flag), _hip.ptr(ws), wsb, _hip.ptr(tmp), tmpb, _hip.stream_of(q))
     return y
+
+
+def exact_linear(q, sh, limbs, d, g, cnt, ec, ev, R, flag=None, checked=True, fr=FR, q_planes=None):
+    """The fused exact linear on raw tensors; returns y (and sets flag). q_planes: q's int8 limb planes [3, M, K]."""
+    return _exact_linear(q, sh, limbs, d, g, cnt, ec, ev, int(R), flag, bool(checked), int(fr), q_planes)
 
 
 class FusedLin:

@@ -12,7 +12,7 @@ import torch
 
 from bitexact.exact import ops
 from bitexact.exact.consts import FR, dims
-from bitexact.exact.model import Lin
+from bitexact.exact.model import GEMMS, Lin
 from bitexact.intops import first_argmax
 from bitexact.vllm_plugin import tri_exact_attn, tri_paged
 from bitexact.vllm_plugin.exact_gemm import FusedLin
@@ -23,10 +23,14 @@ NAMES = ("wqkv", "wo", "wgu", "wd")
 class ExactEngine:
     """c: constants dict with the reference's keys (exact.consts.build, or random_constants here)."""
 
-    def __init__(self, c, dev):
+    def __init__(self, c, dev, compiled=False, gemm="triton"):
+        """compiled / gemm: the reference's arguments (exact_run.py:24). Every stage here is already one HIP launch
+        and every gemm value is served by the HIP linear (the same integers), so neither changes the kernels."""
         dev = torch.device(dev)
         if dev.type != "cuda":
             raise AssertionError("bitexact (MI355X) ExactEngine runs on the GPU only")
+        assert gemm in GEMMS, f"gemm must be one of {GEMMS}"
+        self.compiled, self.gemm = compiled, gemm
         self.dev = dev
         self.L = c["n_layers"]
         self.H, self.HKV, self.HD, self.D, self.FF = dims(c.get("cfg", {}))
@@ -44,6 +48,8 @@ class ExactEngine:
         self.gm = [gam(f"{i}.gm") for i in range(self.L)]
         self.gf = gam("gf")
         self.cos, self.sin, self.exp2 = t("cos").long(), t("sin").long(), t("exp2").long()
+        self.ln = c["ln"].to(dev) if "ln" in c else None
+        self.sha = c.get("sha256")
         # one sticky int32 flag for every bound check of every stage (the reference's fl and err together)
         self.fl = torch.zeros(1, dtype=torch.int32, device=dev)
 
@@ -59,8 +65,9 @@ class ExactEngine:
 
     def forward(self, kvs, ids, pos, slot, bt, rmap):
         """ids, pos, slot [N]: the step's tokens (slot < 0: padding, redirected to the null block 0); bt [*, nblk]
-        int32 block table and rmap [N] the table row of each token. Returns the residual stream [N, D] int64 at FR
-        (src/bitexact/vllm_plugin/exact_run.py:106-128 with the fused stages of its 130-155)."""
+        int32 block table and rmap [N] the table row of each token. kvs None: no cache (the reference's memory
+        profiling run): nothing is stored and the attention output is 0. Returns the residual stream [N, D] int64
+        at FR (src/bitexact/vllm_plugin/exact_run.py:55-128 with the fused stages of its 130-155)."""
         N, G, HKV, HD = ids.shape[0], self.G, self.HKV, self.HD
         pos = pos.long().contiguous()
         slot = torch.where(slot < 0, torch.zeros_like(slot), slot).long()
@@ -69,10 +76,15 @@ class ExactEngine:
         x, q, sh, _ = ops.embed_norm(self.emb, ids, *self.ga[0], flag=fl)
         for i in range(self.L):
             y = self.fused[i, "wqkv"](q, sh, fl, False)
-            qg, shg, _, _, _ = ops.qkv_y(y, pos.view(N, 1), self.cos, self.sin, N, 1, (self.H, HKV, HD), flag=fl,
-                                         store=(kvs[i], slot))   # K / V into the cache (exact_fuse.qkv)
-            num, den = tri_exact_attn.attend(qg.view(N, HKV, G, HD), shg.view(N, HKV, G), qpos, kvs[i], bt, rmap,
-                                             self.exp2, self.l2e)
+            if kvs is None:
+                ops.qkv_y(y, pos.view(N, 1), self.cos, self.sin, N, 1, (self.H, HKV, HD), flag=fl)
+                num = torch.zeros(N, HKV, G, HD, dtype=torch.long, device=y.device)
+                den = torch.ones(N, HKV, G, 1, dtype=torch.long, device=y.device)
+            else:
+                qg, shg, _, _, _ = ops.qkv_y(y, pos.view(N, 1), self.cos, self.sin, N, 1, (self.H, HKV, HD),
+                                             flag=fl, store=(kvs[i], slot))   # K / V into the cache (exact_fuse.qkv)
+                num, den = tri_exact_attn.attend(qg.view(N, HKV, G, HD), shg.view(N, HKV, G), qpos, kvs[i], bt,
+                                                 rmap, self.exp2, self.l2e)
             qo, sho = ops.attn_out(num.view(N * HKV, G, HD), den.view(N * HKV, G, 1), 1, HKV)
             wgu = self.fused[i, "wgu"]
             if wgu.needs_planes(N):   # the norm kernel also writes q's limb planes for the MFMA path

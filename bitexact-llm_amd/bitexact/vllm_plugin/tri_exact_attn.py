@@ -9,6 +9,7 @@ integers).
 import torch
 
 from bitexact import _hip
+from bitexact._ops import empty, op
 
 BQ = 4
 BLOCK_TARGET = 256          # blocks (of 8 waves) to aim for: 1 per MI355X compute unit
@@ -24,7 +25,14 @@ def default_nsplit(R, HKV, nblk, bs):
     return max(1, min(64, BLOCK_TARGET // tiles, keys // 128))
 
 
-def attend(q, sh, qpos, cache, bt, rmap, lut, l2e, nsplit=None, bn=64, warps=4):
+def _attend_fake(q, sh, qpos, cache, bt, rmap, lut, l2e, nsplit):
+    R, HKV, M, HD = q.shape
+    return empty((R, HKV, M, HD), torch.long, q), empty((R, HKV, M, 1), torch.long, q)
+
+
+@op("attend_exact(Tensor q, Tensor sh, Tensor qpos, Tensor cache, Tensor bt, Tensor rmap, Tensor lut, int l2e, "
+    "int nsplit) -> (Tensor, Tensor)", _attend_fake)
+def _attend(q, sh, qpos, cache, bt, rmap, lut, l2e, nsplit):
     _hip.require_cuda(q, sh, qpos, cache, bt, rmap, lut)
     R, HKV, M, HD = q.shape
     assert M <= BQ and cache.shape[1] == HKV and cache.shape[3] >= 6 * HD and cache.stride(3) == 1
@@ -32,8 +40,6 @@ def attend(q, sh, qpos, cache, bt, rmap, lut, l2e, nsplit=None, bn=64, warps=4):
     assert q.dtype == torch.int32 and cache.dtype == torch.int8 and bt.dtype == torch.int32
     q, sh, qpos = q.contiguous(), sh.contiguous().long(), qpos.contiguous().long()
     rmap, lut = rmap.contiguous().long(), lut.contiguous().long()
-    if nsplit is None:
-        nsplit = default_nsplit(R, HKV, bt.shape[1], cache.shape[2])
     num = torch.empty(R, HKV, M, HD, dtype=torch.long, device=q.device)
     den = torch.empty(R, HKV, M, 1, dtype=torch.long, device=q.device)
     ws, wsb = _hip.workspace(q.device, _hip.lib().bx_attn_paged_workspace(R, HKV, M, HD) if nsplit > 1 else 0)
@@ -42,3 +48,9 @@ def attend(q, sh, qpos, cache, bt, rmap, lut, l2e, nsplit=None, bn=64, warps=4):
               bt.shape[1], _hip.ptr(rmap), _hip.ptr(lut), int(l2e), _hip.ptr(num), _hip.ptr(den), R, HKV, M, HD,
               int(nsplit), _hip.ptr(ws), wsb, _hip.stream_of(q))
     return num, den
+
+
+def attend(q, sh, qpos, cache, bt, rmap, lut, l2e, nsplit=None, bn=64, warps=4):
+    if nsplit is None:
+        nsplit = default_nsplit(q.shape[0], q.shape[1], bt.shape[1], cache.shape[2])
+    return _attend(q, sh, qpos, cache, bt, rmap, lut, int(l2e), int(nsplit))

@@ -9,8 +9,10 @@ paged attention over that cache (one HIP kernel, two launches when the keys are 
 import torch
 
 from bitexact import _hip
+from bitexact._ops import empty, op
 
 
+@op("kv_store(Tensor(a!) c, Tensor slot, Tensor k, Tensor v) -> ()", lambda c, slot, k, v: None)
 def store(c, slot, k, v):
     """K / V (int32 or int64 [N, HKV, HD], |.| within 3 limbs) of the tokens at cache slots slot [N] into the
     limb-plane cache c (int8 [nb, HKV, bs, 8 HD]); slot < 0 is skipped."""
@@ -51,16 +53,28 @@ def attend(q, qpos, cache, bt, ptab, nsplit=None, bm=None, bn=None, warps=4):
     """int8-mode paged attention (src/bitexact/vllm_plugin/tri_paged.py:363-401): q int64 [R, HKV, M, HD], qpos int64
     [R, M], cache int8 [nb, HKV, bs, 8 HD], bt int32 [R, *], ptab = weight_table(exp table) -> (num int64
     [R, HKV, M, HD], den int64 [R, HKV, M, 1]). bm / bn / warps are accepted for signature parity."""
+    if nsplit is None:
+        R, HKV, M, _ = q.shape
+        tiles = max(1, R * HKV * ((M + 3) // 4))
+        keys = max(1, bt.shape[1] * cache.shape[2])
+        nsplit = 1 if tiles >= 128 else max(1, min(64, SM_TARGET // tiles, keys // 128))
+    return _attend_int8(q, qpos, cache, bt, ptab, int(nsplit))
+
+
+def _attend_int8_fake(q, qpos, cache, bt, ptab, nsplit):
+    R, HKV, M, HD = q.shape
+    return empty((R, HKV, M, HD), torch.long, q), empty((R, HKV, M, 1), torch.long, q)
+
+
+@op("attend_int8(Tensor q, Tensor qpos, Tensor cache, Tensor bt, Tensor ptab, int nsplit) -> (Tensor, Tensor)",
+    _attend_int8_fake)
+def _attend_int8(q, qpos, cache, bt, ptab, nsplit):
     _hip.require_cuda(q, qpos, cache, bt, ptab)
     R, HKV, M, HD = q.shape
     assert cache.shape[1] == HKV and cache.shape[3] >= 6 * HD and cache.stride(3) == 1
     assert bt.shape[1] * cache.shape[2] < 43690
     assert cache.dtype == torch.int8 and bt.dtype == torch.int32 and ptab.dtype == torch.int32
     q, qpos, ptab = q.contiguous().long(), qpos.contiguous().long(), ptab.contiguous()
-    if nsplit is None:
-        tiles = max(1, R * HKV * ((M + 3) // 4))
-        keys = max(1, bt.shape[1] * cache.shape[2])
-        nsplit = 1 if tiles >= 128 else max(1, min(64, SM_TARGET // tiles, keys // 128))
     num = torch.empty(R, HKV, M, HD, dtype=torch.long, device=q.device)
     den = torch.empty(R, HKV, M, 1, dtype=torch.long, device=q.device)
     ws, wsb = _hip.workspace(q.device, _hip.lib().bx_attn_paged_workspace(R, HKV, M, HD) if nsplit > 1 else 0)

@@ -1441,6 +1441,21 @@ extern "C" int bx_exact_linear_plan(int32_t M, int32_t N, int32_t K, int32_t* ou
   return BX_OK;
 }
 
+// The int8 GEMM's plan for M output rows of nl stacked limbs (nl = 0: the raw int32 GEMM of M stacked rows):
+// out[0] = 1 gemv, 3 tile, 4 staged; out[1] = tile configuration (-1 otherwise); out[2] = K splits; out[3] =
+// blocks per split; out[4] = gemv column groups (16 columns each); out[5] = gemv row parts.
+extern "C" int bx_int8_gemm_plan(int32_t M, int32_t N, int32_t K, int32_t nl, int32_t* out) {
+  BX_REQUIRE(out && M > 0 && N > 0 && K > 0 && nl >= 0 && nl <= 3, "bad plan query");
+  const Plan s = nl == 0 ? make_plan(M, M, N, K, 1, 1, false) : make_plan(nl * M, M, N, K, 1, nl, false);
+  out[0] = s.staged ? 4 : s.gemv ? 1 : 3;
+  out[1] = (s.gemv || s.staged) ? -1 : s.tile;
+  out[2] = s.split;
+  out[3] = s.gemv ? s.tiles_x * s.parts : s.tiles_x * s.tiles_y;
+  out[4] = s.gemv ? s.cg : 0;
+  out[5] = s.gemv ? s.parts : 0;
+  return BX_OK;
+}
+
 // ---- the exact linear without caller buffers ----
 // `scratch` is a file-scope device array: each GPU the library runs on holds its own copy until the process ends.
 // Its first kNoAllocWs bytes are the split-K workspace (int64 partial sums and tile counters), the rest the q limb

@@ -95,3 +95,74 @@ def test_validate_ell_rejects_corrupt_lists():
                    (cnt, torch.tensor([[0, 0], [-2, 1], [5, 0]], dtype=torch.int32))):
         with pytest.raises(AssertionError):
             validate_ell(c2, e2, 2, 64)
+
+
+def test_torch_ops_registered_with_meta_shapes():
+    """Every kernel entry is a torch.ops.bitexact_hip operator whose fake / meta kernel gives the output shapes
+    and dtypes (what torch.compile traces with); no device is touched."""
+    import torch
+    import bitexact.bmm  # noqa: F401
+    import bitexact.exact.attention  # noqa: F401
+    import bitexact.exact.ops  # noqa: F401
+    import bitexact.exact.wmm  # noqa: F401
+    import bitexact.int8.gemm_skinny  # noqa: F401
+    import bitexact.int8.segs  # noqa: F401
+    import bitexact.intops  # noqa: F401
+    import bitexact.vllm_plugin.exact_gemm  # noqa: F401
+    import bitexact.vllm_plugin.tri_exact_attn  # noqa: F401
+    import bitexact.vllm_plugin.tri_paged  # noqa: F401
+    ops = torch.ops.bitexact_hip
+    m = lambda *s, dt=torch.int64: torch.empty(*s, dtype=dt, device="meta")
+    i32, i8 = torch.int32, torch.int8
+    fl = m(1, dt=i32)
+    y = ops.exact_linear(m(8, 64, dt=i32), m(8), m(3, 32, 64, dt=i8), m(32), m(32), None, None, None, 0, fl, True,
+                         24, None)
+    assert y.shape == (8, 32) and y.dtype == torch.int64
+    assert ops.wmm(m(8, 64, dt=i32), m(3, 32, 64, dt=i8)).shape == (1, 8, 32)
+    yy, f = ops.epilogue(m(2, 8, 32), None, m(8, 64, dt=i32), m(32, 2, dt=i32), m(32, 2), m(32), m(32), m(8), 24, True)
+    assert yy.shape == (8, 32) and f.shape == (1,)
+    assert ops.int_mm(m(16, 64, dt=i8), m(32, 64, dt=i8)).dtype == i32
+    assert ops.int_mm_join(m(16, 64, dt=i8), m(32, 64, dt=i8), 8, 2).shape == (8, 32)
+    assert ops.bmm(m(4, 3, 64, dt=i32), m(4, 64, 5, dt=i32), 3, 3).shape == (4, 3, 5)
+    q, sh = ops.norm_quant(m(5, 256), m(256), m(256), fl)
+    assert q.dtype == i32 and sh.shape == (5,)
+    p, den = ops.softmax(m(2, 3, 40), m(2, 3, 1), m(2, 3, 1), m(16385), 387270501, 17, 22)
+    assert p.shape == (2, 3, 40) and p.dtype == i32 and den.shape == (2, 3, 1)
+    qo, so = ops.attn_out(m(4, 12, 64), m(4, 12, 1), 3, 2)
+    assert qo.shape == (6, 512) and so.shape == (6,)
+    qg, shg, k, v = ops.qkv_y(m(6, 3072), m(2, 3), m(4096, 32), m(4096, 32), 2, 3, 32, 8, 64, fl)
+    assert qg.shape == (16, 12, 64) and k.shape == (2, 3, 8, 64)
+    qg2, _ = ops.qkv_y_store(m(6, 3072), m(2, 3), m(4096, 32), m(4096, 32), 2, 3, 32, 8, 64, fl,
+                             m(9, 8, 16, 512, dt=i8), m(6))
+    assert qg2.shape == qg.shape
+    q, pl, sh = ops.add_norm(m(5, 64), m(5, 64), m(64), m(64), fl, True)
+    assert pl.shape == (3, 5, 64)
+    x, q, sh = ops.embed_norm(m(300, 64, dt=i32), m(7), m(64), m(64), fl)
+    assert x.shape == (7, 64) and q.dtype == i32
+    q, pl, sh = ops.gu_silu(m(5, 128), m(16385), fl, True, False)
+    assert q.shape == (5, 64) and pl.numel() == 0
+    assert ops.first_argmax(m(3, 100), False).shape == (3,)
+    num, den = ops.attend_exact(m(2, 8, 4, 64, dt=i32), m(2, 8, 4), m(2, 4), m(9, 8, 16, 512, dt=i8),
+                                m(2, 4, dt=i32), m(2), m(16385), 387270501, 1)
+    assert num.shape == (2, 8, 4, 64) and den.shape == (2, 8, 4, 1)
+    num, den = ops.attend_int8(m(2, 8, 4, 64), m(2, 4), m(9, 8, 16, 512, dt=i8), m(2, 4, dt=i32), m(4097, dt=i32), 1)
+    assert num.shape == (2, 8, 4, 64)
+    num, den = ops.attn_prefill(m(4, 12, 64, dt=i32), m(4, 12, 1), m(4, 3, 64, dt=i32), m(4, 3, 64, dt=i32),
+                                m(4, 12, 1), m(16385), 387270501)
+    assert num.shape == (4, 12, 64)
+    a, as_, sh, mant, e = ops.int8_quant_rows(m(5, 64), 2, True)
+    assert a.shape == (10, 64) and mant.shape == (5,)
+    yp, f = ops.int8_post(m(5, 32), m(32), 3, m(5), m(5))
+    assert yp.shape == (5, 32)
+
+
+def test_no_cpu_path():
+    """The product has no CPU fallback: device-less layers and the float64 product raise."""
+    import pytest
+    import torch
+    from bitexact.exact.wmm import wmm_cpu
+    from bitexact.llama import Cache
+    with pytest.raises(AssertionError):
+        wmm_cpu(torch.zeros(1, 16, dtype=torch.int32), None)
+    with pytest.raises(AssertionError):
+        Cache(1, 1, 4, "cpu")
