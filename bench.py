@@ -360,12 +360,16 @@ def copy_calibrate(dev):
     print(json.dumps({"copy_bytes_each_way": 1 << 30, "copies": 20}), flush=True)
 
 
-def cpu_baseline(budget_s=20.0):
+def _blas_threads():
+    from threadpoolctl import threadpool_info
+    return max([i.get("num_threads", 1) for i in threadpool_info()] or [1])
+
+
+def cpu_baseline(budget_s=10.0):
     """oracle/bxref.py's float64 restatement of the int8 GEMM (the reference's CPU path imm,
     src/bitexact/int8/ops.py:87-90) on the config-2 shapes at M = 8, on the host cores; GB/s of the same
     algorithmic bytes as the GPU figure."""
     import numpy as np
-    from threadpoolctl import threadpool_info
     sys.path.insert(0, HERE)
     from oracle import bxref as R
     rng = np.random.default_rng(0)
@@ -380,10 +384,44 @@ def cpu_baseline(budget_s=20.0):
             t_tot += time.perf_counter() - t0
             b_tot += N * K + 2 * M * K + 8 * M * N
         runs += 1
-    threads = max([i.get("num_threads", 1) for i in threadpool_info()] or [1])
-    return {"value": round(b_tot / t_tot / 1e9, 3), "unit": "GB/s", "cores": threads, "kind": "port",
+    return {"value": round(b_tot / t_tot / 1e9, 3), "unit": "GB/s", "cores": _blas_threads(),
+            "host_cores": os.cpu_count(), "kind": "port",
             "sample": f"oracle float64 imm (numpy BLAS) on config-2 gate/up/down at M={M}, {runs} passes, "
                       f"{t_tot:.1f} s of GEMM time"}
+
+
+def cpu_baseline_exact(budget_s=8.0):
+    """The exact linear on the host cores as the reference's CPU path computes it: oracle/bxref.py's float64
+    wmm_f64 + residual + epilogue (src/bitexact/exact/wmm.py:117-150) on config 1 (M = 8, K = N = 2048) and on
+    config 3's q/o shape (M = 2048, K = N = 2048); effective limb-op TOPS (9 x 2 M N K per call), as the GPU's."""
+    import numpy as np
+    import torch
+    sys.path.insert(0, HERE)
+    from oracle import bxref as R
+    out = {}
+    for tag, M in (("config1_M8", 8), ("config3_q_o_M2048", 2048)):
+        N = K = 2048
+        g = torch.Generator().manual_seed(M)
+        w = (torch.randn(N, K, generator=g) * 0.02).to(torch.bfloat16)
+        dec = R.decompose(w.view(torch.int16).numpy())
+        rng = np.random.default_rng(M)
+        q = rng.integers(-(1 << 22), (1 << 22) + 1, (M, K))
+        sh = rng.integers(-30, -20, M)
+        t_tot, runs = 0.0, 0
+        while t_tot < budget_s / 2 and runs < 1000:
+            t0 = time.perf_counter()
+            T = R.wmm_f64(q, dec["W"])
+            B = R.residual(q, dec["rr"], dec["rc"], dec["rv"], N)
+            R.epilogue(T, B, dec["d"], dec["g"], sh, R.FR, True)
+            t_tot += time.perf_counter() - t0
+            runs += 1
+        ops = 9 * 2 * M * N * K
+        out[tag] = {"us_per_call": round(t_tot / runs * 1e6, 1), "TOPS": round(ops * runs / t_tot / 1e12, 4),
+                    "calls": runs}
+    out.update({"unit": "limb-op TOPS", "cores": _blas_threads(), "host_cores": os.cpu_count(), "kind": "port",
+                "sample": "oracle float64 wmm_f64 + residual + epilogue (the reference's wmm_cpu chain), "
+                          "bf16 N(0,0.02) weights, |q| <= 2^22"})
+    return out
 
 
 def main():
@@ -459,6 +497,7 @@ def main():
     if not args.no_cpu:
         log("cpu baseline ...")
         out["cpu_baseline"] = cpu_baseline()
+        out["cpu_baseline_exact"] = cpu_baseline_exact()
     print(json.dumps(out), flush=True)
 
 

@@ -167,6 +167,28 @@ def test_decompose_invariants():
     # minimality of g: one grid step finer would overflow 3 limbs (rows with any weight)
     nzrow = (W != 0).any(1)
     assert (np.abs(W[nzrow]).max(1) > R.LIM3 // 2).all()
+    # minimality of the residual grid gf = g - d: in every row with residual entries some rv is odd (a coarser
+    # grid would lose that bit; a finer one would change d, rv and the model digest while keeping the value)
+    for r in np.unique(dec["rr"]):
+        assert (dec["rv"][dec["rr"] == r] & 1).any(), r
+    assert (d[np.setdiff1d(np.arange(len(d)), dec["rr"])] == 0).all()   # rows without residual: d = 0
+
+
+def test_emb_fixed_closed_form():
+    """The embedding rounding (src/bitexact/exact/consts.py:131-135) against the exact rational rule
+    floor(w 2^FR + 1/2) for every bf16 value of a sample that covers ties, tiny values and both signs."""
+    from fractions import Fraction
+    g = np.random.default_rng(11)
+    bits = rand_bf16_bits(6, 64, 5)
+    extra = np.array([0x0000, 0x8000, 0x3F80, 0xBF80, 0x3300, 0xB300, 0x3380, 0xB380, 0x3340, 0xB340, 0x2F80,
+                      0x0001, 0x8001, 0x42FE, 0xC2FE], dtype=np.uint16).view(np.int16)
+    bits = np.concatenate([bits.reshape(-1), extra, g.integers(0x2E00, 0x3E00, 64).astype(np.int16)])[None, :]
+    m = R.engine_constants(bits, {}, {}, np.zeros((1, 32), np.int64), np.zeros((1, 32), np.int64), 0)
+    sm, ex = R.bf16_parts(bits)
+    for i in range(bits.shape[1]):
+        w = Fraction(int(sm[0, i])) * (Fraction(2) ** int(ex[0, i]))
+        ref = (w * (1 << R.FR) + Fraction(1, 2)).__floor__()
+        assert int(m["emb"][0, i]) == ref, (hex(int(bits[0, i]) & 0xFFFF), int(m["emb"][0, i]), ref)
 
 
 def test_linear_closed_form():
