@@ -22,6 +22,7 @@
 #include "bx_common.h"
 
 #include <algorithm>
+#include <cstdlib>
 #include <mutex>
 
 namespace bx {
@@ -553,6 +554,94 @@ __device__ __forceinline__ void async16(const void* g, void* lds_base) {
                                    (void __attribute__((address_space(3)))*)lds_base, 16, 0, 0);
 }
 
+// ---- epilogue of the tile kernels, straight from the accumulators: lane (l % 32) owns column (wn TN + t) 32 +
+// l % 32 of each 32-column block t, so the column contexts (d, g, residual list) stay in registers; the row
+// exponents are read from LDS. Stores of 32 lanes cover 256 contiguous bytes of a row. With K split over blocks
+// (gridDim.z > 1) the partials go to the workspace and the last block of the tile applies the epilogue. ----
+template <int NS, int MODE, int WM, int WN, int TM, int TN>
+__device__ __forceinline__ void tile_epilogue(const LinArgs& p, v16i (&acc)[NS][TM][TN], int m0, int n0, int wm,
+                                              int wn) {
+  constexpr int NW = WM * WN, BM = 32 * TM * WM;
+  const int tid = threadIdx.x, lane = tid & 63;
+  __shared__ int s_last;
+  __shared__ int64_t s_sh[MODE == EXACT ? BM : 1];
+  if (MODE == EXACT)
+    for (int r = tid; r < BM; r += NW * 64) s_sh[r] = p.sh[min(m0 + r, p.M - 1)];
+  __syncthreads();
+  bool bad = false, corrupt = false;
+  const int nsplit = gridDim.z;
+  ColCtx cc[TN];
+  if (MODE == EXACT)
+#pragma unroll
+    for (int t = 0; t < TN; ++t) cc[t] = col_ctx(p, n0 + (wn * TN + t) * 32 + (lane & 31));
+#pragma unroll
+  for (int a = 0; a < TM; ++a)
+#pragma unroll
+    for (int t = 0; t < TN; ++t) {
+      const int n = n0 + (wn * TN + t) * 32 + (lane & 31);
+#pragma unroll
+      for (int e0 = 0; e0 < 16; e0 += 8) {   // 8 rows at a time: 16 would spill registers
+        int64_t B[8];
+        if (MODE == EXACT && nsplit == 1) {
+          int mrow[8];
+#pragma unroll
+          for (int u = 0; u < 8; ++u) {
+            const int e = e0 + u;
+            mrow[u] = min(m0 + (wm * TM + a) * 32 + (e >> 2) * 8 + (lane >> 5) * 4 + (e & 3), p.M - 1);
+          }
+          residual_rows<8>(p, cc[t], mrow, B, corrupt);
+        }
+#pragma unroll
+        for (int u = 0; u < 8; ++u) {
+        const int e = e0 + u;
+        const int r = (wm * TM + a) * 32 + (e >> 2) * 8 + (lane >> 5) * 4 + (e & 3), m = m0 + r;
+        int64_t v = 0;
+#pragma unroll
+        for (int s2 = 0; s2 < NS; ++s2) v += (int64_t)acc[s2][a][t][e] << (8 * s2);
+        if (m < p.M && n < p.N) {
+          if (nsplit > 1)
+            ws_add(p, m, n, v);
+          else if (MODE == EXACT)
+            finalize_col(p, cc[t], m, n, s_sh[r], v, B[u], bad, corrupt);
+          else
+            finalize<MODE>(p, m, n, v, bad, corrupt);
+        }
+        }
+      }
+    }
+  if (nsplit > 1 && splitk_last(p, blockIdx.y * gridDim.x + blockIdx.x, nsplit, &s_last)) {
+#pragma unroll
+    for (int a = 0; a < TM; ++a)
+#pragma unroll
+      for (int t = 0; t < TN; ++t) {
+        const int n = n0 + (wn * TN + t) * 32 + (lane & 31);
+#pragma unroll
+        for (int e0 = 0; e0 < 16; e0 += 8) {
+          int64_t v[8], B[8];
+          int mrow[8];
+#pragma unroll
+          for (int u = 0; u < 8; ++u) {
+            const int e = e0 + u, m = m0 + (wm * TM + a) * 32 + (e >> 2) * 8 + (lane >> 5) * 4 + (e & 3);
+            mrow[u] = min(m, p.M - 1);
+            v[u] = (m < p.M && n < p.N) ? ws_take(p, m, n) : 0;
+          }
+          if (MODE == EXACT) residual_rows<8>(p, cc[t], mrow, B, corrupt);
+#pragma unroll
+          for (int u = 0; u < 8; ++u) {
+            const int e = e0 + u, r = (wm * TM + a) * 32 + (e >> 2) * 8 + (lane >> 5) * 4 + (e & 3), m = m0 + r;
+            if (m < p.M && n < p.N) {
+              if (MODE == EXACT)
+                finalize_col(p, cc[t], m, n, s_sh[r], v[u], B[u], bad, corrupt);
+              else
+                finalize<MODE>(p, m, n, v[u], bad, corrupt);
+            }
+          }
+        }
+      }
+  }
+  if (MODE == EXACT) write_flag(p, bad, corrupt);
+}
+
 template <int NA, int NB, int MODE, int WM, int WN, int TM, int TN, int BK, int S>
 __global__ __launch_bounds__(WM * WN * 64) void tile_kernel(LinArgs p) {
   static_assert(BK == 32 || BK == 64 || BK == 128, "k tile");
@@ -565,7 +654,6 @@ __global__ __launch_bounds__(WM * WN * 64) void tile_kernel(LinArgs p) {
   constexpr int LWL = LT / NW, LWX = LT % NW;                 // per wave: LWL + 1 for the first LWX waves
   static_assert((LWL + (LWX > 0)) * (S - 2) < 64, "vmcnt range");
   extern __shared__ __align__(16) char smem[];
-  __shared__ int s_last;
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int wm = wave % WM, wn = wave / WM;
@@ -663,85 +751,273 @@ __global__ __launch_bounds__(WM * WN * 64) void tile_kernel(LinArgs p) {
     }
   }
 
-  // ---- epilogue straight from the accumulators: lane (l % 32) owns column (wn TN + t) 32 + l % 32 of each
-  // 32-column block t, so the column contexts (d, g, residual list) stay in registers; the row exponents are
-  // read from LDS. Stores of 32 lanes cover 256 contiguous bytes of a row. ----
-  __shared__ int64_t s_sh[MODE == EXACT ? BM : 1];
-  if (MODE == EXACT)
-    for (int r = tid; r < BM; r += NW * 64) s_sh[r] = p.sh[min(m0 + r, p.M - 1)];
-  __syncthreads();
-  bool bad = false, corrupt = false;
-  const int nsplit = gridDim.z;
-  ColCtx cc[TN];
-  if (MODE == EXACT)
+  tile_epilogue<NS, MODE, WM, WN, TM, TN>(p, acc, m0, n0, wm, wn);
+}
+
+// =====================================================================================================
+// xtile kernel: the exact prefill GEMM (3 x 3 limb planes, K % 64 == 0) on 128 x 128 block tiles, software
+// pipelined.
+//  * Main loop: 8 waves (4 x 2) of 32 x 64 wave tiles, five int32 accumulator sets by limb weight i + j. The
+//    3-stage LDS ring (64-deep k tiles, 48 KiB each) is filled by buffer_load_dwordx4 ... lds (the k advance is
+//    the scalar offset, so a lane keeps one 32-bit offset per load instruction) with the tile kernel's XOR
+//    swizzle. A wave works in half-steps of 32 k: while the 18 MFMAs of one half-step run, the 9 LDS operand
+//    reads of the next are in flight (two operand sets in registers). The ring barrier sits between the two
+//    half-steps of a k tile; the stage it frees is refilled 3 k tiles ahead.
+//  * Epilogue context in LDS: before the loop, the block's row exponents, each column's d and g - d + FR, and a
+//    compact list of the columns' residual entries (k, v; at most kXtEmax per block) are staged in LDS. When the
+//    ring stops refilling (3 k tiles before the end), the freed stage receives, by LDS DMA gathers, q[m][k] of
+//    every listed entry for the block's 128 rows, so the epilogue's residual terms are LDS reads instead of
+//    dependent global round trips. Blocks with more entries read the residual from global memory.
+// =====================================================================================================
+constexpr int kXtBM = 128, kXtBN = 128, kXtBK = 64, kXtS = 3, kXtEmax = 96;
+constexpr int kXtStage = 6 * kXtBM * kXtBK;                               // 48 KiB
+constexpr int kXtCtx = 3 * kXtBM * 8 + kXtEmax * 12 + 132 * 4;            // epilogue context after the ring
+constexpr size_t kXtLds = (size_t)kXtS * kXtStage + kXtCtx;
+
+struct XtOps {
+  v4i a[3], b[3][2];
+};
+
+__device__ __forceinline__ void buf_lds16(__amdgpu_buffer_rsrc_t r, void* lds, int voff, int soff) {
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (__attribute__((address_space(3))) void*)lds, 16, voff, soff, 0, 0);
+}
+
+__device__ __forceinline__ void buf_lds4(__amdgpu_buffer_rsrc_t r, void* lds, int voff) {
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (__attribute__((address_space(3))) void*)lds, 4, voff, 0, 0, 0);
+}
+
+template <int MODE>
+__global__ __launch_bounds__(512) void xtile_kernel(LinArgs p) {
+  constexpr int WM = 4, TN = 2, BM = kXtBM, BN = kXtBN, BK = kXtBK, S = kXtS, STAGE = kXtStage;
+  constexpr int SA = 3 * BM * BK, LPW = 6;                  // 1 KiB load instructions per wave per stage
+  constexpr bool EX = MODE == EXACT;
+  extern __shared__ __align__(16) char smem[];
+  int64_t* s_sh = (int64_t*)(smem + S * STAGE);             // [BM] row exponents
+  int64_t* s_d = s_sh + BM;                                 // [BN] d
+  int64_t* s_gdr = s_d + BN;                                // [BN] g - d + FR
+  int64_t* s_ev = s_gdr + BN;                               // [kXtEmax] residual values of the compact list
+  int32_t* s_ek = (int32_t*)(s_ev + kXtEmax);               // [kXtEmax] residual columns (k) of the list
+  int32_t* s_cs = s_ek + kXtEmax;                           // [BN + 1] list start of each column
+
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);   // wave-uniform (scalar) from here on
+  const int wm = wave % WM, wn = wave / WM;
+  const int m0 = blockIdx.y * BM, n0 = blockIdx.x * BN;
+  const int nk = p.K / BK;                                  // K % 64 == 0 and no K split (planner)
+
+  // ---- epilogue context (waves 0 - 3, before their ring loads) ----
+  int E = 0;
+  bool ctx_corrupt = false;             // a residual index or count of the block's columns is out of range
+  if (EX && wave < 4) {
+    const int c = tid & 127;
+    if (tid < 128) {
+      const int n = min(n0 + c, p.N - 1);
+      const int64_t dn = p.d[n];
+      const int cnt = p.R > 0 ? kcnt(p, p.cnt[n], ctx_corrupt) : 0;
+      s_d[c] = dn;
+      s_gdr[c] = p.g[n] - dn + p.FR;
+      s_cs[c] = n0 + c < p.N ? cnt : 0;
+    } else {
+      s_sh[c] = p.sh[min(m0 + c, p.M - 1)];
+    }
+  }
+  if (EX) ring_barrier<63>();                               // LDS only: the counts are visible
+  if (EX && wave == 0) {                                    // exclusive prefix of the 128 counts, 2 per lane
+    const int c0 = s_cs[2 * lane], c1 = s_cs[2 * lane + 1];
+    int x = c0 + c1;
 #pragma unroll
-    for (int t = 0; t < TN; ++t) cc[t] = col_ctx(p, n0 + (wn * TN + t) * 32 + (lane & 31));
+    for (int o = 1; o < 64; o <<= 1) {
+      const int y = __shfl_up(x, o, 64);
+      if (lane >= o) x += y;
+    }
+    const int excl = x - c0 - c1;
+    s_cs[2 * lane] = excl;
+    s_cs[2 * lane + 1] = excl + c0;
+    if (lane == 63) s_cs[BN] = x;
+  }
+  if (EX) ring_barrier<63>();
+  if (EX) E = s_cs[BN];
+  if (EX && tid < 128 && E <= kXtEmax) {                    // the compact list: (k, v) of every entry
+    const int c = tid, n = min(n0 + c, p.N - 1);
+    const int e0 = s_cs[c], e1 = s_cs[c + 1];
+    for (int e = e0; e < e1; ++e) {
+      s_ek[e] = kcol(p, p.ecol[(int64_t)n * p.R + (e - e0)], ctx_corrupt);
+      s_ev[e] = p.eval[(int64_t)n * p.R + (e - e0)];
+    }
+  }
+
+  // ---- ring loads: waves 0 - 3 load the A planes, 4 - 7 the B planes; instruction i of a wave covers 16 rows x
+  // 64 bytes (lane: row lane / 4, 16-byte chunk lane % 4, swizzled) ----
+  const int lrow = lane >> 2, lch = ((lane & 3) ^ swz<BK>(lrow)) << 4;
+  const bool isA = wave < 4;
+  const __amdgpu_buffer_rsrc_t rsrc = isA ? __builtin_amdgcn_make_buffer_rsrc(const_cast<int8_t*>(p.a), (short)0,
+                                                                               kBufRange, 0x00020000)
+                                          : __builtin_amdgcn_make_buffer_rsrc(const_cast<int8_t*>(p.w), (short)0,
+                                                                               kBufRange, 0x00020000);
+  int voff[LPW];
 #pragma unroll
-  for (int a = 0; a < TM; ++a)
+  for (int i = 0; i < LPW; ++i) {
+    const int inst = (wave & 3) * LPW + i, pl = inst >> 3, row = (inst & 7) * 16 + lrow;
+    voff[i] = isA ? pl * p.M * p.K + min(m0 + row, p.M - 1) * p.K + lch
+                  : pl * (int)p.ld_plane + min(n0 + row, p.N - 1) * (int)p.ld_row + lch;
+  }
+  auto issue = [&](int kt, int stage) {
+    char* sbase = smem + stage * STAGE + wave * LPW * 1024;
 #pragma unroll
-    for (int t = 0; t < TN; ++t) {
-      const int n = n0 + (wn * TN + t) * 32 + (lane & 31);
+    for (int i = 0; i < LPW; ++i) buf_lds16(rsrc, sbase + i * 1024, voff[i], kt * BK);
+  };
+
+  const int arow = wm * 32 + (lane & 31);
+  const int brow0 = (wn * TN) * 32 + (lane & 31), brow1 = brow0 + 32;
+  auto load_ops = [&](XtOps& o, int stage, int h) {
+    const char* base = smem + stage * STAGE;
+    const int c = 2 * h + (lane >> 5);
 #pragma unroll
-      for (int e0 = 0; e0 < 16; e0 += 8) {   // 8 rows at a time: 16 would spill registers
-        int64_t B[8];
-        if (MODE == EXACT && nsplit == 1) {
-          int mrow[8];
+    for (int i = 0; i < 3; ++i) o.a[i] = *(const v4i*)(base + i * BM * BK + arow * BK + ((c ^ swz<BK>(arow)) << 4));
 #pragma unroll
-          for (int u = 0; u < 8; ++u) {
-            const int e = e0 + u;
-            mrow[u] = min(m0 + (wm * TM + a) * 32 + (e >> 2) * 8 + (lane >> 5) * 4 + (e & 3), p.M - 1);
-          }
-          residual_rows<8>(p, cc[t], mrow, B, corrupt);
-        }
+    for (int j = 0; j < 3; ++j) {
+      o.b[j][0] = *(const v4i*)(base + SA + j * BN * BK + brow0 * BK + ((c ^ swz<BK>(brow0)) << 4));
+      o.b[j][1] = *(const v4i*)(base + SA + j * BN * BK + brow1 * BK + ((c ^ swz<BK>(brow1)) << 4));
+    }
+  };
+
+  // q gathers for the compact residual list into the freed stage: entry e, rows 0..127 at gbase + 512 e
+  const __amdgpu_buffer_rsrc_t qrsrc =
+      __builtin_amdgcn_make_buffer_rsrc(const_cast<int32_t*>(p.q), (short)0, kBufRange, 0x00020000);
+  auto gather = [&](char* gbase) {
+    for (int x = wave; x < 2 * E; x += 8) {
+      const int e = x >> 1, r = (x & 1) * 64 + lane;
+      buf_lds4(qrsrc, gbase + e * 512 + (x & 1) * 256, (min(m0 + r, p.M - 1) * (int)p.ldq + s_ek[e]) * 4);
+    }
+  };
+  const bool gat = EX && E > 0 && E <= kXtEmax;
+  char* gbase = nullptr;
+
+  v16i acc[5][1][TN];
 #pragma unroll
-        for (int u = 0; u < 8; ++u) {
+  for (int s2 = 0; s2 < 5; ++s2)
+#pragma unroll
+    for (int t = 0; t < TN; ++t)
+#pragma unroll
+      for (int e = 0; e < 16; ++e) acc[s2][0][t][e] = 0;
+
+  // the nine limb products, ordered so that products into one accumulator are at least two MFMAs apart
+  auto mfmas = [&](const XtOps& o) {
+#pragma unroll
+    for (int u = 0; u < 9; ++u) {
+      constexpr int I[9] = {0, 0, 1, 0, 1, 2, 1, 2, 2}, J[9] = {0, 1, 0, 2, 1, 0, 2, 1, 2};
+      const int i = I[u], j = J[u];
+#pragma unroll
+      for (int t = 0; t < TN; ++t)
+        acc[i + j][0][t] = __builtin_amdgcn_mfma_i32_32x32x32_i8(o.a[i], o.b[j][t], acc[i + j][0][t], 0, 0, 0);
+    }
+  };
+
+#pragma unroll
+  for (int t = 0; t < S; ++t)
+    if (t < nk) issue(t, t);
+  // first k tile landed (later stages may still be in flight) and visible to every wave
+  if (S - 1 < nk)
+    ring_barrier<LPW * (S - 1)>();
+  else
+    ring_barrier<0>();
+
+  XtOps cur, nxt;
+  if (nk > 0) load_ops(cur, 0, 0);
+  // every iteration but the last: no branch around the operand reads, so the compiler's LDS waits stay exact
+  for (int it = 0; it + 1 < nk; ++it) {
+    const int st = it % S;
+    load_ops(nxt, st, 1);
+    mfmas(cur);
+    __builtin_amdgcn_sched_barrier(0);
+    // k tile it + 1 landed (the tiles after it may be in flight), and no wave reads stage st any more
+    if (it + S - 1 >= nk)
+      ring_barrier<0>();
+    else
+      ring_barrier<LPW * (S - 2)>();
+    if (it + S < nk) {
+      issue(it + S, st);
+    } else if (it + S == nk && gat) {   // the ring stops refilling: stage st takes the residual gathers
+      gbase = smem + st * STAGE;
+      gather(gbase);
+    }
+    load_ops(cur, (it + 1) % S, 0);
+    __builtin_amdgcn_sched_barrier(0);
+    mfmas(nxt);
+  }
+  if (nk > 0) {
+    load_ops(nxt, (nk - 1) % S, 1);
+    mfmas(cur);
+    mfmas(nxt);
+  }
+  if (gat && gbase == nullptr) {        // short K: the ring was never retired, gather into stage 0 now
+    ring_barrier<0>();
+    gbase = smem;
+    gather(gbase);
+  }
+  ring_barrier<0>();                    // gathers landed; context visible
+
+  // ---- epilogue: lane (l % 32) owns column (wn TN + t) 32 + l % 32 of each 32-column block t and rows
+  // wm 32 + (e / 4) 8 + (l / 32) 4 + e % 4 of the 32 x 32 MFMA block ----
+  bool bad = false, corrupt = ctx_corrupt;
+  const int32_t* gq = (const int32_t*)gbase;
+#pragma unroll
+  for (int t = 0; t < TN; ++t) {
+    const int nl = (wn * TN + t) * 32 + (lane & 31), n = n0 + nl;
+    int64_t dn = 0, gdr = 0;
+    int cs0 = 0, cs1 = 0;
+    if (EX) {
+      dn = s_d[nl];
+      gdr = s_gdr[nl];
+      if (E > 0 && E <= kXtEmax) {
+        cs0 = s_cs[nl];
+        cs1 = s_cs[nl + 1];
+      }
+    }
+#pragma unroll
+    for (int e0 = 0; e0 < 16; e0 += 4) {
+      int64_t B[4] = {0, 0, 0, 0};
+      int rl[4];
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
         const int e = e0 + u;
-        const int r = (wm * TM + a) * 32 + (e >> 2) * 8 + (lane >> 5) * 4 + (e & 3), m = m0 + r;
+        rl[u] = wm * 32 + (e >> 2) * 8 + (lane >> 5) * 4 + (e & 3);
+      }
+      if (EX && E > kXtEmax && n < p.N) {   // long residual lists: read from global memory
+        const int c = kcnt(p, p.cnt[n], corrupt);
+        for (int j = 0; j < c; ++j) {
+          const int col = kcol(p, p.ecol[(int64_t)n * p.R + j], corrupt);
+          const int64_t v = p.eval[(int64_t)n * p.R + j];
+#pragma unroll
+          for (int u = 0; u < 4; ++u)
+            B[u] = add_wrap(B[u], mul_wrap((int64_t)p.q[(int64_t)min(m0 + rl[u], p.M - 1) * p.ldq + col], v));
+        }
+      } else if (EX) {
+        for (int x = cs0; x < cs1; ++x) {
+          const int64_t v = s_ev[x];
+#pragma unroll
+          for (int u = 0; u < 4; ++u) B[u] = add_wrap(B[u], mul_wrap((int64_t)gq[x * 128 + rl[u]], v));
+        }
+      }
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        const int e = e0 + u, m = m0 + rl[u];
         int64_t v = 0;
 #pragma unroll
-        for (int s2 = 0; s2 < NS; ++s2) v += (int64_t)acc[s2][a][t][e] << (8 * s2);
+        for (int s2 = 0; s2 < 5; ++s2) v += (int64_t)acc[s2][0][t][e] << (8 * s2);
         if (m < p.M && n < p.N) {
-          if (nsplit > 1)
-            ws_add(p, m, n, v);
-          else if (MODE == EXACT)
-            finalize_col(p, cc[t], m, n, s_sh[r], v, B[u], bad, corrupt);
-          else
-            finalize<MODE>(p, m, n, v, bad, corrupt);
-        }
+          if (EX) {
+            bool b;
+            ((int64_t*)p.out)[(int64_t)m * p.N + n] = exact_round_fast(v, B[u], dn, s_sh[rl[u]] + gdr, b);
+            bad |= b;
+          } else {
+            ((int64_t*)p.out)[(int64_t)m * p.N + n] = v;
+          }
         }
       }
     }
-  if (nsplit > 1 && splitk_last(p, blockIdx.y * gridDim.x + blockIdx.x, nsplit, &s_last)) {
-#pragma unroll
-    for (int a = 0; a < TM; ++a)
-#pragma unroll
-      for (int t = 0; t < TN; ++t) {
-        const int n = n0 + (wn * TN + t) * 32 + (lane & 31);
-#pragma unroll
-        for (int e0 = 0; e0 < 16; e0 += 8) {
-          int64_t v[8], B[8];
-          int mrow[8];
-#pragma unroll
-          for (int u = 0; u < 8; ++u) {
-            const int e = e0 + u, m = m0 + (wm * TM + a) * 32 + (e >> 2) * 8 + (lane >> 5) * 4 + (e & 3);
-            mrow[u] = min(m, p.M - 1);
-            v[u] = (m < p.M && n < p.N) ? ws_take(p, m, n) : 0;
-          }
-          if (MODE == EXACT) residual_rows<8>(p, cc[t], mrow, B, corrupt);
-#pragma unroll
-          for (int u = 0; u < 8; ++u) {
-            const int e = e0 + u, r = (wm * TM + a) * 32 + (e >> 2) * 8 + (lane >> 5) * 4 + (e & 3), m = m0 + r;
-            if (m < p.M && n < p.N) {
-              if (MODE == EXACT)
-                finalize_col(p, cc[t], m, n, s_sh[r], v[u], B[u], bad, corrupt);
-              else
-                finalize<MODE>(p, m, n, v[u], bad, corrupt);
-            }
-          }
-        }
-      }
   }
-  if (MODE == EXACT) write_flag(p, bad, corrupt);
+  if (EX) write_flag(p, bad, corrupt);
 }
 
 // =====================================================================================================
@@ -1227,13 +1503,30 @@ static int launch_tile_cfg(LinArgs& p, const Plan& s, hipStream_t st) {
   return check_launch("tile_kernel");
 }
 
+// The xtile kernel's conditions: whole 64-deep k tiles, no K split, 32-bit buffer offsets for q, its limb planes
+// and the weight planes.
+static bool xtile_fits(const LinArgs& p, const Plan& s) {
+  return s.split == 1 && p.K % kXtBK == 0 && 3LL * p.M * p.K < kBufRange - 16 &&
+         2 * p.ld_plane + (int64_t)p.N * p.ld_row < kBufRange - 16 && (int64_t)p.M * p.ldq * 4 < kBufRange - 16;
+}
+
 template <int NA, int NB, int MODE>
 static int launch_tile(LinArgs& p, const Plan& s, hipStream_t st) {
   p.ks = s.kbytes;
   bind_ws(p, s);
   if (s.tile == T_BIG) {
-    if constexpr (NA * NB == 9)
+    if constexpr (NA * NB == 9 && (MODE == EXACT || MODE == WMM_T)) {
+      const char* xe = getenv("BX_XTILE");
+      const int xt = xe ? atoi(xe) : 1;
+      if (xt && xtile_fits(p, s)) {
+        allow_lds(xtile_kernel<MODE>, kXtLds);
+        xtile_kernel<MODE><<<dim3(s.tiles_x, s.tiles_y, 1), 512, kXtLds, st>>>(p);
+        return check_launch("xtile_kernel");
+      }
       return launch_tile_cfg<NA, NB, MODE, 4, 2, 1, 2, 64, 2>(p, s, st);   // kTileExact
+    } else if constexpr (NA * NB == 9) {
+      return launch_tile_cfg<NA, NB, MODE, 4, 2, 1, 2, 64, 2>(p, s, st);   // kTileExact
+    }
     else
       return launch_tile_cfg<NA, NB, MODE, 2, 2, 2, 2, 64, 3>(p, s, st);
   }
