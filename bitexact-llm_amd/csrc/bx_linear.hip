@@ -24,6 +24,7 @@
 #include <algorithm>
 #include <cstdlib>
 #include <mutex>
+#include <type_traits>
 
 namespace bx {
 
@@ -54,6 +55,7 @@ struct LinArgs {
   int spw;               // gemv: k steps per wave
   int nla;               // gemv: stacked activation groups (exact 3, JOIN nl, RAW32 1); rows_a = nla M
   int tiles, parts_lg, mp;   // gemv: column tiles, log2 of the row parts per tile, output rows per part
+  int xcd_remap;             // xtile: XCD-grouped tile order (tile count a multiple of 8, row tiles of 4)
 };
 
 // Residual column index. Valid ELL data is always in [0, K) with counts in [0, R]; a corrupt index or count
@@ -786,8 +788,10 @@ __device__ __forceinline__ void buf_lds4(__amdgpu_buffer_rsrc_t r, void* lds, in
   __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (__attribute__((address_space(3))) void*)lds, 4, voff, 0, 0, 0);
 }
 
+__device__ unsigned long long xt_stamps[65536 * 4];   // [b][4] stamps, then [65536 * 2 + b] barrier wait
 template <int MODE>
 __global__ __launch_bounds__(512) void xtile_kernel(LinArgs p) {
+  unsigned long long T0 = __builtin_amdgcn_s_memrealtime(), T1 = 0, T2 = 0, TW = 0, TV = 0;
   constexpr int WM = 4, TN = 2, BM = kXtBM, BN = kXtBN, BK = kXtBK, S = kXtS, STAGE = kXtStage;
   constexpr int SA = 3 * BM * BK, LPW = 6;                  // 1 KiB load instructions per wave per stage
   constexpr bool EX = MODE == EXACT;
@@ -802,7 +806,17 @@ __global__ __launch_bounds__(512) void xtile_kernel(LinArgs p) {
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);   // wave-uniform (scalar) from here on
   const int wm = wave % WM, wn = wave / WM;
-  const int m0 = blockIdx.y * BM, n0 = blockIdx.x * BN;
+  // XCD-aware tile order: blocks are dispatched round-robin over the 8 XCDs (block b on XCD b % 8); the tiles an
+  // XCD runs together form 4-row x 8-column patches, so they share A and B rows in that XCD's L2
+  int tx = blockIdx.x, ty = blockIdx.y;
+  if (p.xcd_remap) {
+    const int T = gridDim.x * gridDim.y, b = blockIdx.y * gridDim.x + blockIdx.x;
+    const int v = (b & 7) * (T >> 3) + (b >> 3);
+    const int grp = v / (4 * gridDim.x), in = v - grp * 4 * gridDim.x;
+    ty = grp * 4 + (in & 3);
+    tx = in >> 2;
+  }
+  const int m0 = ty * BM, n0 = tx * BN;
   const int nk = p.K / BK;                                  // K % 64 == 0 and no K split (planner)
 
   // ---- epilogue context (waves 0 - 3, before their ring loads) ----
@@ -922,28 +936,64 @@ __global__ __launch_bounds__(512) void xtile_kernel(LinArgs p) {
   else
     ring_barrier<0>();
 
+  T1 = __builtin_amdgcn_s_memrealtime();
   XtOps cur, nxt;
   if (nk > 0) load_ops(cur, 0, 0);
-  // every iteration but the last: no branch around the operand reads, so the compiler's LDS waits stay exact
-  for (int it = 0; it + 1 < nk; ++it) {
+  // One k tile: the second half-step's operands are read during the first half-step's MFMAs, the ring barrier,
+  // then (REFILL) the freed stage's refill and the next tile's first operands during the second half-step's MFMAs.
+  // Iterations with and without the refill are separate loops, so no branch splits a scheduling region.
+  auto step = [&](int it, auto refill) {
+    constexpr bool REFILL = decltype(refill)::value;
     const int st = it % S;
     load_ops(nxt, st, 1);
     mfmas(cur);
+    // interleave: 9 x (2 MFMAs, 1 LDS read)
+#pragma unroll
+    for (int g2 = 0; g2 < 9; ++g2) {
+      __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);
+      __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+    }
     __builtin_amdgcn_sched_barrier(0);
     // k tile it + 1 landed (the tiles after it may be in flight), and no wave reads stage st any more
-    if (it + S - 1 >= nk)
-      ring_barrier<0>();
-    else
+    if (REFILL)
       ring_barrier<LPW * (S - 2)>();
-    if (it + S < nk) {
-      issue(it + S, st);
-    } else if (it + S == nk && gat) {   // the ring stops refilling: stage st takes the residual gathers
-      gbase = smem + st * STAGE;
+    else
+      ring_barrier<0>();
+    __builtin_amdgcn_sched_barrier(0);
+    if (REFILL) issue(it + S, st);
+    load_ops(cur, (it + 1) % S, 0);
+    mfmas(nxt);
+    if (REFILL) {
+      // 6 x (2 MFMAs, 1 buffer load, 1 LDS read), then 3 x (2 MFMAs, 1 LDS read)
+#pragma unroll
+      for (int g2 = 0; g2 < 6; ++g2) {
+        __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);
+        __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);
+        __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+      }
+#pragma unroll
+      for (int g2 = 0; g2 < 3; ++g2) {
+        __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);
+        __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+      }
+    } else {
+#pragma unroll
+      for (int g2 = 0; g2 < 9; ++g2) {
+        __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);
+        __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+      }
+    }
+    __builtin_amdgcn_sched_barrier(0);
+  };
+  int it = 0;
+  for (; it + S < nk; ++it) step(it, std::true_type{});
+  for (; it + 1 < nk; ++it) {
+    step(it, std::false_type{});
+    if (gat && gbase == nullptr) {      // the ring stopped refilling: stage it % S, free since this step's barrier,
+                                        // takes the residual gathers
+      gbase = smem + (it % S) * STAGE;
       gather(gbase);
     }
-    load_ops(cur, (it + 1) % S, 0);
-    __builtin_amdgcn_sched_barrier(0);
-    mfmas(nxt);
   }
   if (nk > 0) {
     load_ops(nxt, (nk - 1) % S, 1);
@@ -956,6 +1006,7 @@ __global__ __launch_bounds__(512) void xtile_kernel(LinArgs p) {
     gather(gbase);
   }
   ring_barrier<0>();                    // gathers landed; context visible
+  T2 = __builtin_amdgcn_s_memrealtime();
 
   // ---- epilogue: lane (l % 32) owns column (wn TN + t) 32 + l % 32 of each 32-column block t and rows
   // wm 32 + (e / 4) 8 + (l / 32) 4 + e % 4 of the 32 x 32 MFMA block ----
@@ -1018,6 +1069,15 @@ __global__ __launch_bounds__(512) void xtile_kernel(LinArgs p) {
     }
   }
   if (EX) write_flag(p, bad, corrupt);
+  if (tid == 0) {
+    const int b = blockIdx.y * gridDim.x + blockIdx.x;
+    if (b < 65536) {
+      xt_stamps[b * 4] = T0; xt_stamps[b * 4 + 1] = T1; xt_stamps[b * 4 + 2] = T2;
+      xt_stamps[b * 4 + 3] = __builtin_amdgcn_s_memrealtime();
+      xt_stamps[65536 * 2 + b] = TW;
+      xt_stamps[65536 * 3 + b] = TV;
+    }
+  }
 }
 
 // =====================================================================================================
@@ -1519,6 +1579,8 @@ static int launch_tile(LinArgs& p, const Plan& s, hipStream_t st) {
       const char* xe = getenv("BX_XTILE");
       const int xt = xe ? atoi(xe) : 1;
       if (xt && xtile_fits(p, s)) {
+        const char* xr = getenv("BX_XCD");
+        p.xcd_remap = (xr ? atoi(xr) : 1) && (s.tiles_x * s.tiles_y) % 8 == 0 && s.tiles_y % 4 == 0;
         allow_lds(xtile_kernel<MODE>, kXtLds);
         xtile_kernel<MODE><<<dim3(s.tiles_x, s.tiles_y, 1), 512, kXtLds, st>>>(p);
         return check_launch("xtile_kernel");
@@ -1813,4 +1875,8 @@ extern "C" int bx_exact_linear_noalloc(const int32_t* q, int64_t ldq, const int6
   }
   return bx_exact_linear(q, ldq, sh, limbs, ld_plane, ld_row, d, g, ell_cnt, ell_col, ell_val, R, y, M, N, K, FR,
                          checked, flag, base, kNoAllocWs, (int8_t*)base + kNoAllocWs, kNoAllocTmp, stream);
+}
+
+extern "C" int bx_xt_stamps(unsigned long long* host, int n) {
+  return hipMemcpyFromSymbol(host, HIP_SYMBOL(xt_stamps), (size_t)n * 32) == hipSuccess ? 0 : -2;
 }
