@@ -773,11 +773,12 @@ __global__ __launch_bounds__(WM * WN * 64) void tile_kernel(LinArgs p) {
 // =====================================================================================================
 constexpr int kXtBM = 128, kXtBN = 128, kXtBK = 64, kXtS = 3, kXtEmax = 96;
 constexpr int kXtStage = 6 * kXtBM * kXtBK;                               // 48 KiB
-constexpr int kXtCtx = 3 * kXtBM * 8 + kXtEmax * 12 + 132 * 4;            // epilogue context after the ring
+constexpr int kXtCtx = 3 * kXtBM * 8 + kXtEmax * 12 + 132 * 4 + 32;       // epilogue context after the ring
 constexpr size_t kXtLds = (size_t)kXtS * kXtStage + kXtCtx;
 
+template <int TM, int TN>
 struct XtOps {
-  v4i a[3], b[3][2];
+  v4i a[3][TM], b[3][TN];
 };
 
 __device__ __forceinline__ void buf_lds16(__amdgpu_buffer_rsrc_t r, void* lds, int voff, int soff) {
@@ -789,11 +790,15 @@ __device__ __forceinline__ void buf_lds4(__amdgpu_buffer_rsrc_t r, void* lds, in
 }
 
 __device__ unsigned long long xt_stamps[65536 * 4];   // [b][4] stamps, then [65536 * 2 + b] barrier wait
-template <int MODE>
-__global__ __launch_bounds__(512) void xtile_kernel(LinArgs p) {
+// WM x WN waves of (32 TM) x (32 TN) wave tiles; launched as 4 x 2 waves of 32 x 64 (2 waves per SIMD: the five
+// accumulator sets take 160 registers). 2 x 2 waves of 64 x 64 at one wave per SIMD would halve the operand reads
+// per MFMA, but the compiler then moves the 320 accumulators between AGPRs and VGPRs inside the loop.
+template <int MODE, int WM, int WN, int TM, int TN>
+__global__ __launch_bounds__(WM * WN * 64) void xtile_kernel(LinArgs p) {
   unsigned long long T0 = __builtin_amdgcn_s_memrealtime(), T1 = 0, T2 = 0, TW = 0, TV = 0;
-  constexpr int WM = 4, TN = 2, BM = kXtBM, BN = kXtBN, BK = kXtBK, S = kXtS, STAGE = kXtStage;
-  constexpr int SA = 3 * BM * BK, LPW = 6;                  // 1 KiB load instructions per wave per stage
+  constexpr int NW = WM * WN, BM = kXtBM, BN = kXtBN, BK = kXtBK, S = kXtS, STAGE = kXtStage;
+  static_assert(32 * WM * TM == BM && 32 * WN * TN == BN, "wave layout");
+  constexpr int SA = 3 * BM * BK, LPW = 48 / NW;            // 1 KiB load instructions per wave per stage
   constexpr bool EX = MODE == EXACT;
   extern __shared__ __align__(16) char smem[];
   int64_t* s_sh = (int64_t*)(smem + S * STAGE);             // [BM] row exponents
@@ -802,6 +807,7 @@ __global__ __launch_bounds__(512) void xtile_kernel(LinArgs p) {
   int64_t* s_ev = s_gdr + BN;                               // [kXtEmax] residual values of the compact list
   int32_t* s_ek = (int32_t*)(s_ev + kXtEmax);               // [kXtEmax] residual columns (k) of the list
   int32_t* s_cs = s_ek + kXtEmax;                           // [BN + 1] list start of each column
+  int64_t* s_mm = (int64_t*)(s_cs + 132);                   // [4] min / max of the row exponents, per half
 
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);   // wave-uniform (scalar) from here on
@@ -819,10 +825,10 @@ __global__ __launch_bounds__(512) void xtile_kernel(LinArgs p) {
   const int m0 = ty * BM, n0 = tx * BN;
   const int nk = p.K / BK;                                  // K % 64 == 0 and no K split (planner)
 
-  // ---- epilogue context (waves 0 - 3, before their ring loads) ----
+  // ---- epilogue context (threads 0 - 255, before their ring loads) ----
   int E = 0;
   bool ctx_corrupt = false;             // a residual index or count of the block's columns is out of range
-  if (EX && wave < 4) {
+  if (EX && tid < 256) {
     const int c = tid & 127;
     if (tid < 128) {
       const int n = min(n0 + c, p.N - 1);
@@ -832,7 +838,18 @@ __global__ __launch_bounds__(512) void xtile_kernel(LinArgs p) {
       s_gdr[c] = p.g[n] - dn + p.FR;
       s_cs[c] = n0 + c < p.N ? cnt : 0;
     } else {
-      s_sh[c] = p.sh[min(m0 + c, p.M - 1)];
+      const int64_t v = p.sh[min(m0 + c, p.M - 1)];
+      s_sh[c] = v;
+      int64_t lo = v, hi = v;
+#pragma unroll
+      for (int o = 32; o > 0; o >>= 1) {
+        lo = imin(lo, __shfl_xor(lo, o, 64));
+        hi = imax(hi, __shfl_xor(hi, o, 64));
+      }
+      if (lane == 0) {
+        s_mm[2 * (c >> 6)] = lo;
+        s_mm[2 * (c >> 6) + 1] = hi;
+      }
     }
   }
   if (EX) ring_barrier<63>();                               // LDS only: the counts are visible
@@ -860,10 +877,10 @@ __global__ __launch_bounds__(512) void xtile_kernel(LinArgs p) {
     }
   }
 
-  // ---- ring loads: waves 0 - 3 load the A planes, 4 - 7 the B planes; instruction i of a wave covers 16 rows x
-  // 64 bytes (lane: row lane / 4, 16-byte chunk lane % 4, swizzled) ----
+  // ---- ring loads: the first half of the waves load the A planes, the second half the B planes; instruction i of
+  // a wave covers 16 rows x 64 bytes (lane: row lane / 4, 16-byte chunk lane % 4, swizzled) ----
   const int lrow = lane >> 2, lch = ((lane & 3) ^ swz<BK>(lrow)) << 4;
-  const bool isA = wave < 4;
+  const bool isA = wave < NW / 2;
   const __amdgpu_buffer_rsrc_t rsrc = isA ? __builtin_amdgcn_make_buffer_rsrc(const_cast<int8_t*>(p.a), (short)0,
                                                                                kBufRange, 0x00020000)
                                           : __builtin_amdgcn_make_buffer_rsrc(const_cast<int8_t*>(p.w), (short)0,
@@ -871,7 +888,7 @@ __global__ __launch_bounds__(512) void xtile_kernel(LinArgs p) {
   int voff[LPW];
 #pragma unroll
   for (int i = 0; i < LPW; ++i) {
-    const int inst = (wave & 3) * LPW + i, pl = inst >> 3, row = (inst & 7) * 16 + lrow;
+    const int inst = (wave % (NW / 2)) * LPW + i, pl = inst >> 3, row = (inst & 7) * 16 + lrow;
     voff[i] = isA ? pl * p.M * p.K + min(m0 + row, p.M - 1) * p.K + lch
                   : pl * (int)p.ld_plane + min(n0 + row, p.N - 1) * (int)p.ld_row + lch;
   }
@@ -881,25 +898,30 @@ __global__ __launch_bounds__(512) void xtile_kernel(LinArgs p) {
     for (int i = 0; i < LPW; ++i) buf_lds16(rsrc, sbase + i * 1024, voff[i], kt * BK);
   };
 
-  const int arow = wm * 32 + (lane & 31);
-  const int brow0 = (wn * TN) * 32 + (lane & 31), brow1 = brow0 + 32;
-  auto load_ops = [&](XtOps& o, int stage, int h) {
+  auto load_ops = [&](XtOps<TM, TN>& o, int stage, int h) {
     const char* base = smem + stage * STAGE;
     const int c = 2 * h + (lane >> 5);
 #pragma unroll
-    for (int i = 0; i < 3; ++i) o.a[i] = *(const v4i*)(base + i * BM * BK + arow * BK + ((c ^ swz<BK>(arow)) << 4));
+    for (int i = 0; i < 3; ++i)
 #pragma unroll
-    for (int j = 0; j < 3; ++j) {
-      o.b[j][0] = *(const v4i*)(base + SA + j * BN * BK + brow0 * BK + ((c ^ swz<BK>(brow0)) << 4));
-      o.b[j][1] = *(const v4i*)(base + SA + j * BN * BK + brow1 * BK + ((c ^ swz<BK>(brow1)) << 4));
-    }
+      for (int a2 = 0; a2 < TM; ++a2) {
+        const int arow = (wm * TM + a2) * 32 + (lane & 31);
+        o.a[i][a2] = *(const v4i*)(base + i * BM * BK + arow * BK + ((c ^ swz<BK>(arow)) << 4));
+      }
+#pragma unroll
+    for (int j = 0; j < 3; ++j)
+#pragma unroll
+      for (int t = 0; t < TN; ++t) {
+        const int brow = (wn * TN + t) * 32 + (lane & 31);
+        o.b[j][t] = *(const v4i*)(base + SA + j * BN * BK + brow * BK + ((c ^ swz<BK>(brow)) << 4));
+      }
   };
 
   // q gathers for the compact residual list into the freed stage: entry e, rows 0..127 at gbase + 512 e
   const __amdgpu_buffer_rsrc_t qrsrc =
       __builtin_amdgcn_make_buffer_rsrc(const_cast<int32_t*>(p.q), (short)0, kBufRange, 0x00020000);
   auto gather = [&](char* gbase) {
-    for (int x = wave; x < 2 * E; x += 8) {
+    for (int x = wave; x < 2 * E; x += NW) {
       const int e = x >> 1, r = (x & 1) * 64 + lane;
       buf_lds4(qrsrc, gbase + e * 512 + (x & 1) * 256, (min(m0 + r, p.M - 1) * (int)p.ldq + s_ek[e]) * 4);
     }
@@ -907,23 +929,27 @@ __global__ __launch_bounds__(512) void xtile_kernel(LinArgs p) {
   const bool gat = EX && E > 0 && E <= kXtEmax;
   char* gbase = nullptr;
 
-  v16i acc[5][1][TN];
+  v16i acc[5][TM][TN];
 #pragma unroll
   for (int s2 = 0; s2 < 5; ++s2)
 #pragma unroll
-    for (int t = 0; t < TN; ++t)
+    for (int a2 = 0; a2 < TM; ++a2)
 #pragma unroll
-      for (int e = 0; e < 16; ++e) acc[s2][0][t][e] = 0;
+      for (int t = 0; t < TN; ++t)
+#pragma unroll
+        for (int e = 0; e < 16; ++e) acc[s2][a2][t][e] = 0;
 
   // the nine limb products, ordered so that products into one accumulator are at least two MFMAs apart
-  auto mfmas = [&](const XtOps& o) {
+  auto mfmas = [&](const XtOps<TM, TN>& o) {
 #pragma unroll
     for (int u = 0; u < 9; ++u) {
       constexpr int I[9] = {0, 0, 1, 0, 1, 2, 1, 2, 2}, J[9] = {0, 1, 0, 2, 1, 0, 2, 1, 2};
       const int i = I[u], j = J[u];
 #pragma unroll
-      for (int t = 0; t < TN; ++t)
-        acc[i + j][0][t] = __builtin_amdgcn_mfma_i32_32x32x32_i8(o.a[i], o.b[j][t], acc[i + j][0][t], 0, 0, 0);
+      for (int a2 = 0; a2 < TM; ++a2)
+#pragma unroll
+        for (int t = 0; t < TN; ++t)
+          acc[i + j][a2][t] = __builtin_amdgcn_mfma_i32_32x32x32_i8(o.a[i][a2], o.b[j][t], acc[i + j][a2][t], 0, 0, 0);
     }
   };
 
@@ -937,20 +963,22 @@ __global__ __launch_bounds__(512) void xtile_kernel(LinArgs p) {
     ring_barrier<0>();
 
   T1 = __builtin_amdgcn_s_memrealtime();
-  XtOps cur, nxt;
+  XtOps<TM, TN> cur, nxt;
   if (nk > 0) load_ops(cur, 0, 0);
   // One k tile: the second half-step's operands are read during the first half-step's MFMAs, the ring barrier,
   // then (REFILL) the freed stage's refill and the next tile's first operands during the second half-step's MFMAs.
   // Iterations with and without the refill are separate loops, so no branch splits a scheduling region.
+  constexpr int NR = 3 * (TM + TN), MR = 9 * TM * TN / NR;   // LDS reads and MFMAs per read in a half-step
+  static_assert(NR * MR == 9 * TM * TN && LPW <= NR, "interleave");
   auto step = [&](int it, auto refill) {
     constexpr bool REFILL = decltype(refill)::value;
     const int st = it % S;
     load_ops(nxt, st, 1);
     mfmas(cur);
-    // interleave: 9 x (2 MFMAs, 1 LDS read)
+    // interleave: NR x (MR MFMAs, 1 LDS read)
 #pragma unroll
-    for (int g2 = 0; g2 < 9; ++g2) {
-      __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);
+    for (int g2 = 0; g2 < NR; ++g2) {
+      __builtin_amdgcn_sched_group_barrier(0x008, MR, 0);
       __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
     }
     __builtin_amdgcn_sched_barrier(0);
@@ -964,22 +992,22 @@ __global__ __launch_bounds__(512) void xtile_kernel(LinArgs p) {
     load_ops(cur, (it + 1) % S, 0);
     mfmas(nxt);
     if (REFILL) {
-      // 6 x (2 MFMAs, 1 buffer load, 1 LDS read), then 3 x (2 MFMAs, 1 LDS read)
+      // LPW x (MR MFMAs, 1 buffer load, 1 LDS read), then the remaining LDS reads with MR MFMAs each
 #pragma unroll
-      for (int g2 = 0; g2 < 6; ++g2) {
-        __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);
+      for (int g2 = 0; g2 < LPW; ++g2) {
+        __builtin_amdgcn_sched_group_barrier(0x008, MR, 0);
         __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);
         __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
       }
 #pragma unroll
-      for (int g2 = 0; g2 < 3; ++g2) {
-        __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);
+      for (int g2 = LPW; g2 < NR; ++g2) {
+        __builtin_amdgcn_sched_group_barrier(0x008, MR, 0);
         __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
       }
     } else {
 #pragma unroll
-      for (int g2 = 0; g2 < 9; ++g2) {
-        __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);
+      for (int g2 = 0; g2 < NR; ++g2) {
+        __builtin_amdgcn_sched_group_barrier(0x008, MR, 0);
         __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
       }
     }
@@ -1012,11 +1040,21 @@ __global__ __launch_bounds__(512) void xtile_kernel(LinArgs p) {
   // wm 32 + (e / 4) 8 + (l / 32) 4 + e % 4 of the 32 x 32 MFMA block ----
   bool bad = false, corrupt = ctx_corrupt;
   const int32_t* gq = (const int32_t*)gbase;
+  // Rounding: exact_round_fast's quick form applies where k = -(sh + g - d + FR) satisfies d <= k, 1 <= k <= 62 and
+  // |T| < 2^59, |B| < 2^60. The k conditions hold for every row of a column when they hold for the block's smallest
+  // and largest row exponent; |T| < 2^59 holds for K <= 8192 (3-limb q and W: |q W| < 2^46). So a lane checks its
+  // column once and each element only checks |B|; an element outside takes the full rule.
+  int64_t shlo = 0, shhi = 0;
+  if (EX) {
+    shlo = imin(s_mm[0], s_mm[2]);
+    shhi = imax(s_mm[1], s_mm[3]);
+  }
 #pragma unroll
   for (int t = 0; t < TN; ++t) {
     const int nl = (wn * TN + t) * 32 + (lane & 31), n = n0 + nl;
     int64_t dn = 0, gdr = 0;
     int cs0 = 0, cs1 = 0;
+    bool colok = false;
     if (EX) {
       dn = s_d[nl];
       gdr = s_gdr[nl];
@@ -1024,7 +1062,10 @@ __global__ __launch_bounds__(512) void xtile_kernel(LinArgs p) {
         cs0 = s_cs[nl];
         cs1 = s_cs[nl + 1];
       }
+      colok = p.K <= 8192 && shhi + gdr + dn <= 0 && shhi + gdr <= -1 && shlo + gdr >= -62;
     }
+#pragma unroll
+    for (int a2 = 0; a2 < TM; ++a2)
 #pragma unroll
     for (int e0 = 0; e0 < 16; e0 += 4) {
       int64_t B[4] = {0, 0, 0, 0};
@@ -1032,7 +1073,7 @@ __global__ __launch_bounds__(512) void xtile_kernel(LinArgs p) {
 #pragma unroll
       for (int u = 0; u < 4; ++u) {
         const int e = e0 + u;
-        rl[u] = wm * 32 + (e >> 2) * 8 + (lane >> 5) * 4 + (e & 3);
+        rl[u] = (wm * TM + a2) * 32 + (e >> 2) * 8 + (lane >> 5) * 4 + (e & 3);
       }
       if (EX && E > kXtEmax && n < p.N) {   // long residual lists: read from global memory
         const int c = kcnt(p, p.cnt[n], corrupt);
@@ -1055,16 +1096,21 @@ __global__ __launch_bounds__(512) void xtile_kernel(LinArgs p) {
         const int e = e0 + u, m = m0 + rl[u];
         int64_t v = 0;
 #pragma unroll
-        for (int s2 = 0; s2 < 5; ++s2) v += (int64_t)acc[s2][0][t][e] << (8 * s2);
-        if (m < p.M && n < p.N) {
-          if (EX) {
-            bool b;
-            ((int64_t*)p.out)[(int64_t)m * p.N + n] = exact_round_fast(v, B[u], dn, s_sh[rl[u]] + gdr, b);
-            bad |= b;
-          } else {
-            ((int64_t*)p.out)[(int64_t)m * p.N + n] = v;
+        for (int s2 = 0; s2 < 5; ++s2) v += (int64_t)acc[s2][a2][t][e] << (8 * s2);
+        int64_t y = v;
+        if (EX) {
+          const int64_t k = -(s_sh[rl[u]] + gdr);
+          const bool fast = colok && (uint64_t)(B[u] + (1LL << 60)) < (uint64_t)(1LL << 61);
+          y = (v + ((B[u] + (1LL << (k - 1))) >> dn)) >> (k - dn);
+          if (__builtin_amdgcn_ballot_w64(!fast)) {   // rare: some lane needs the full rule
+            if (!fast) {
+              bool b;
+              y = exact_round(v, B[u], dn, -k, b);
+              bad |= b && m < p.M && n < p.N;
+            }
           }
         }
+        if (m < p.M && n < p.N) ((int64_t*)p.out)[(int64_t)m * p.N + n] = y;
       }
     }
   }
@@ -1581,8 +1627,8 @@ static int launch_tile(LinArgs& p, const Plan& s, hipStream_t st) {
       if (xt && xtile_fits(p, s)) {
         const char* xr = getenv("BX_XCD");
         p.xcd_remap = (xr ? atoi(xr) : 1) && (s.tiles_x * s.tiles_y) % 8 == 0 && s.tiles_y % 4 == 0;
-        allow_lds(xtile_kernel<MODE>, kXtLds);
-        xtile_kernel<MODE><<<dim3(s.tiles_x, s.tiles_y, 1), 512, kXtLds, st>>>(p);
+        allow_lds(xtile_kernel<MODE, 4, 2, 1, 2>, kXtLds);
+        xtile_kernel<MODE, 4, 2, 1, 2><<<dim3(s.tiles_x, s.tiles_y, 1), 512, kXtLds, st>>>(p);
         return check_launch("xtile_kernel");
       }
       return launch_tile_cfg<NA, NB, MODE, 4, 2, 1, 2, 64, 2>(p, s, st);   // kTileExact
