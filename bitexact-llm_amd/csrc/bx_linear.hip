@@ -789,13 +789,11 @@ __device__ __forceinline__ void buf_lds4(__amdgpu_buffer_rsrc_t r, void* lds, in
   __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (__attribute__((address_space(3))) void*)lds, 4, voff, 0, 0, 0);
 }
 
-__device__ unsigned long long xt_stamps[65536 * 4];   // [b][4] stamps, then [65536 * 2 + b] barrier wait
 // WM x WN waves of (32 TM) x (32 TN) wave tiles; launched as 4 x 2 waves of 32 x 64 (2 waves per SIMD: the five
 // accumulator sets take 160 registers). 2 x 2 waves of 64 x 64 at one wave per SIMD would halve the operand reads
 // per MFMA, but the compiler then moves the 320 accumulators between AGPRs and VGPRs inside the loop.
 template <int MODE, int WM, int WN, int TM, int TN>
 __global__ __launch_bounds__(WM * WN * 64) void xtile_kernel(LinArgs p) {
-  unsigned long long T0 = __builtin_amdgcn_s_memrealtime(), T1 = 0, T2 = 0, TW = 0, TV = 0;
   constexpr int NW = WM * WN, BM = kXtBM, BN = kXtBN, BK = kXtBK, S = kXtS, STAGE = kXtStage;
   static_assert(32 * WM * TM == BM && 32 * WN * TN == BN, "wave layout");
   constexpr int SA = 3 * BM * BK, LPW = 48 / NW;            // 1 KiB load instructions per wave per stage
@@ -962,7 +960,6 @@ __global__ __launch_bounds__(WM * WN * 64) void xtile_kernel(LinArgs p) {
   else
     ring_barrier<0>();
 
-  T1 = __builtin_amdgcn_s_memrealtime();
   XtOps<TM, TN> cur, nxt;
   if (nk > 0) load_ops(cur, 0, 0);
   // One k tile: the second half-step's operands are read during the first half-step's MFMAs, the ring barrier,
@@ -1034,7 +1031,6 @@ __global__ __launch_bounds__(WM * WN * 64) void xtile_kernel(LinArgs p) {
     gather(gbase);
   }
   ring_barrier<0>();                    // gathers landed; context visible
-  T2 = __builtin_amdgcn_s_memrealtime();
 
   // ---- epilogue: lane (l % 32) owns column (wn TN + t) 32 + l % 32 of each 32-column block t and rows
   // wm 32 + (e / 4) 8 + (l / 32) 4 + e % 4 of the 32 x 32 MFMA block ----
@@ -1115,15 +1111,6 @@ __global__ __launch_bounds__(WM * WN * 64) void xtile_kernel(LinArgs p) {
     }
   }
   if (EX) write_flag(p, bad, corrupt);
-  if (tid == 0) {
-    const int b = blockIdx.y * gridDim.x + blockIdx.x;
-    if (b < 65536) {
-      xt_stamps[b * 4] = T0; xt_stamps[b * 4 + 1] = T1; xt_stamps[b * 4 + 2] = T2;
-      xt_stamps[b * 4 + 3] = __builtin_amdgcn_s_memrealtime();
-      xt_stamps[65536 * 2 + b] = TW;
-      xt_stamps[65536 * 3 + b] = TV;
-    }
-  }
 }
 
 // =====================================================================================================
@@ -1622,11 +1609,11 @@ static int launch_tile(LinArgs& p, const Plan& s, hipStream_t st) {
   bind_ws(p, s);
   if (s.tile == T_BIG) {
     if constexpr (NA * NB == 9 && (MODE == EXACT || MODE == WMM_T)) {
-      const char* xe = getenv("BX_XTILE");
-      const int xt = xe ? atoi(xe) : 1;
+      // BX_XTILE=0 / BX_XCD=0 switch the pipelined tile / its XCD-grouped order off (the same integers either way)
+      static const int xt = getenv("BX_XTILE") ? atoi(getenv("BX_XTILE")) : 1;
+      static const int xcd = getenv("BX_XCD") ? atoi(getenv("BX_XCD")) : 1;
       if (xt && xtile_fits(p, s)) {
-        const char* xr = getenv("BX_XCD");
-        p.xcd_remap = (xr ? atoi(xr) : 1) && (s.tiles_x * s.tiles_y) % 8 == 0 && s.tiles_y % 4 == 0;
+        p.xcd_remap = xcd && (s.tiles_x * s.tiles_y) % 8 == 0 && s.tiles_y % 4 == 0;
         allow_lds(xtile_kernel<MODE, 4, 2, 1, 2>, kXtLds);
         xtile_kernel<MODE, 4, 2, 1, 2><<<dim3(s.tiles_x, s.tiles_y, 1), 512, kXtLds, st>>>(p);
         return check_launch("xtile_kernel");
@@ -1923,6 +1910,3 @@ extern "C" int bx_exact_linear_noalloc(const int32_t* q, int64_t ldq, const int6
                          checked, flag, base, kNoAllocWs, (int8_t*)base + kNoAllocWs, kNoAllocTmp, stream);
 }
 
-extern "C" int bx_xt_stamps(unsigned long long* host, int n) {
-  return hipMemcpyFromSymbol(host, HIP_SYMBOL(xt_stamps), (size_t)n * 32) == hipSuccess ? 0 : -2;
-}

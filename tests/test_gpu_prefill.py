@@ -130,3 +130,15 @@ def test_lm_head_column_sample(dev):
             assert bool(flag.item())
     del dec, w
     torch.cuda.empty_cache()
+
+
+def test_prefill_k_tail_fallback(dev):
+    """K % 64 != 0 at a 128 x 128-tile shape: the pipelined tile needs whole 64-deep k tiles, so the plain 128 x 128
+    tile (2-stage ring, masked last k tile) serves it; same integers."""
+    _check(_weights(2048, 2000, 8, (5,)), 2048, dev, "128x128", 19, dense_rows=(5,), ranges=RANGES[:2])
+
+
+def test_prefill_xtile_order_off(dev):
+    """The pipelined tile with a tile grid that is not a multiple of 8 (15 x 18 tiles), where the XCD-grouped order is
+    off, at K = 8192."""
+    _check(_weights(2304, 8192, 9), 1920, dev, "128x128", 23, ranges=RANGES[:1])
