@@ -1114,6 +1114,151 @@ __global__ __launch_bounds__(WM * WN * 64) void xtile_kernel(LinArgs p) {
 }
 
 // =====================================================================================================
+// stream kernel: decode GEMMs (at most 128 stacked activation rows) as a weight stream through an LDS ring.
+// A block owns 64 output columns and a K range (the grid splits K when the column tiles alone do not fill the
+// chip). Its weight rows (NB planes x 64 x 128-byte k chunks) and all its activation rows (padded to RP, a
+// multiple of 32) go through an S-stage ring filled by buffer_load_dwordx4 ... lds (1 KiB = 8 rows x 128 bytes per
+// instruction; 16-byte chunks XOR-swizzled by (row / 2) % 8 so the 16 rows an MFMA operand read touches fall in 16
+// distinct bank groups), S - 1 stages ahead of the MFMAs. Each of the 4 waves owns 16 columns:
+// v_mfma_i32_16x16x64_i8 over the valid 16-row activation blocks and the NB weight planes. The int32 limb
+// products meet in LDS (or, for the join of whole 16-row limb blocks, in registers) and are joined per output in
+// int64. One block walks the whole K range (the plan takes the kernel only where N / 64 tiles cover the chip).
+// =====================================================================================================
+constexpr int kStBK = 128, kStC = 64;
+
+template <int RBM, int NB, int S, int MODE, int NWV = 4>
+__global__ __launch_bounds__(64 * NWV) void stream_kernel(LinArgs p) {
+  constexpr int RP = RBM < 2 ? 32 : 16 * RBM, BK = kStBK, C = 16 * NWV, NT = 64 * NWV;   // loaded rows: x 32
+  constexpr int SA = RP * BK, STAGE = SA + NB * C * BK;
+  constexpr int LA = RP / 8, LT = LA + NB * C / 8, LPW = LT / NWV;   // 1 KiB load instructions per stage / wave
+  static_assert(LT % NWV == 0, "load instructions per stage must split over the waves");
+  extern __shared__ __align__(16) char smem[];
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int n0 = blockIdx.x * C, kb = 0;
+  const int nks = p.K / BK;
+  const int rows = p.rows_a;                                  // <= 16 RBM (rows past it repeat the last row)
+
+  const auto ra = __builtin_amdgcn_make_buffer_rsrc(const_cast<int8_t*>(p.a), (short)0, kBufRange, 0x00020000);
+  const auto rw = __builtin_amdgcn_make_buffer_rsrc(const_cast<int8_t*>(p.w), (short)0, kBufRange, 0x00020000);
+  int voff[LPW];
+#pragma unroll
+  for (int i = 0; i < LPW; ++i) {
+    const int inst = wave * LPW + i;
+    const int r8 = inst < LA ? inst : (inst - LA) % (C / 8);      // 8-row group within the A or W plane tile
+    const int row = r8 * 8 + (lane >> 3);
+    const int lch = ((lane & 7) ^ ((row >> 1) & 7)) << 4;
+    if (inst < LA) {
+      voff[i] = min(row, rows - 1) * p.K + kb + lch;
+    } else {
+      const int pl = (inst - LA) / (C / 8);
+      voff[i] = pl * (int)p.ld_plane + min(n0 + row, p.N - 1) * (int)p.ld_row + kb + lch;
+    }
+  }
+  auto issue = [&](int it, int stage) {
+    char* sbase = smem + stage * STAGE;
+#pragma unroll
+    for (int i = 0; i < LPW; ++i) {
+      const int inst = wave * LPW + i;
+      buf_lds16(inst < LA ? ra : rw, sbase + inst * 1024, voff[i], it * BK);
+    }
+  };
+
+  v4i acc[RBM][NB];
+#pragma unroll
+  for (int r = 0; r < RBM; ++r)
+#pragma unroll
+    for (int j = 0; j < NB; ++j) acc[r][j] = v4i{0, 0, 0, 0};
+
+#pragma unroll
+  for (int t = 0; t < S - 1; ++t)
+    if (t < nks) issue(t, t);
+  const int r16 = lane & 15, wrow = wave * 16 + r16;
+  for (int it = 0; it < nks; ++it) {
+    // stage it landed (later ones may be in flight) and every wave is done with stage it - 1
+    if (it + S - 2 < nks)
+      ring_barrier<LPW * (S - 2)>();
+    else
+      ring_barrier<0>();
+    if (it + S - 1 < nks) issue(it + S - 1, (it + S - 1) % S);
+    const char* base = smem + (it % S) * STAGE;
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      const int c = 4 * h + (lane >> 4);
+      v4i b[NB];
+#pragma unroll
+      for (int j = 0; j < NB; ++j)
+        b[j] = *(const v4i*)(base + SA + (j * C + wrow) * BK + ((c ^ ((wrow >> 1) & 7)) << 4));
+      v4i a[RBM];
+#pragma unroll
+      for (int r = 0; r < RBM; ++r) {
+        const int arow = r * 16 + r16;
+        a[r] = *(const v4i*)(base + arow * BK + ((c ^ ((arow >> 1) & 7)) << 4));
+      }
+#pragma unroll
+      for (int r = 0; r < RBM; ++r)
+#pragma unroll
+        for (int j = 0; j < NB; ++j) acc[r][j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a[r], b[j], acc[r][j], 0, 0, 0);
+    }
+  }
+
+  ring_barrier<0>();
+  bool bad = false, corrupt = false;
+  const int Mo = MODE == RAW32 ? rows : p.M;                   // output rows
+  // ---- JOIN with whole 16-row limb blocks (M % 16 == 0): limb row i M + m sits in block m / 16 + i M / 16 of the
+  // same lane and element, so the join is done in registers ----
+  if constexpr (MODE == JOIN && NB == 1) {
+    if (p.M % 16 == 0 && p.nl * p.M <= RP) {   // block-uniform
+      const int n = n0 + wave * 16 + (lane & 15), bm = p.M >> 4;
+#pragma unroll
+      for (int r = 0; r < RBM; ++r) {
+        if (r < bm) {
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            int64_t v = 0;
+#pragma unroll
+            for (int i = 0; i < 3; ++i) {
+              const int ri = r + i * bm;
+              if (i < p.nl && ri < RBM) v += (int64_t)acc[ri < RBM ? ri : 0][0][e] << (8 * i);
+            }
+            const int m = r * 16 + (lane >> 4) * 4 + e;
+            if (n < p.N) ((int64_t*)p.out)[(int64_t)m * p.N + n] = v;
+          }
+        }
+      }
+      return;
+    }
+  }
+  // ---- products to LDS: Cs[j][row][col] (row: stacked activation row, col: block column; pitch C + 1 so the
+  // four row groups of a store land in different banks) ----
+  constexpr int CP = C + 1;
+  int32_t* Cs = (int32_t*)smem;
+#pragma unroll
+  for (int r = 0; r < RBM; ++r)
+#pragma unroll
+    for (int j = 0; j < NB; ++j)
+#pragma unroll
+      for (int e = 0; e < 4; ++e)
+        Cs[(j * RP + r * 16 + (lane >> 4) * 4 + e) * CP + wave * 16 + (lane & 15)] = acc[r][j][e];
+  __syncthreads();
+  const int nla = MODE == JOIN ? p.nl : MODE == RAW32 ? 1 : 3;
+  for (int o = tid; o < Mo * C; o += NT) {
+    const int m = o / C, c = o - m * C, n = n0 + c;
+    if (n >= p.N) continue;
+    int64_t v = 0;
+    if (MODE == RAW32) {
+      v = Cs[m * CP + c];
+    } else {
+      for (int i = 0; i < nla; ++i)
+#pragma unroll
+        for (int j = 0; j < NB; ++j) v += (int64_t)Cs[(j * RP + i * p.M + m) * CP + c] << (8 * (i + j));
+    }
+    finalize<MODE>(p, m, n, v, bad, corrupt);
+  }
+  if (MODE == EXACT) write_flag(p, bad, corrupt);
+}
+
+// =====================================================================================================
 // wide kernel (exact-mode decode with 65..96 limb rows, wide N)
 // =====================================================================================================
 // A block owns BNC = 16 CG output columns and every limb row of q (RA = 16 RBW WR >= 3 M), so each weight byte
@@ -1346,6 +1491,7 @@ static const TileShape kTiles[5] = {{2, 2, 2, 2, 64, 3},    // 128 x 128, 64x64 
 static const TileShape kTileExact = {4, 2, 1, 2, 64, 2};
 
 struct Plan {
+  int stream;                     // stream kernel: activation row blocks RBM (0: none)
   int wide;                       // wide kernel configuration (0: none)
   int staged;                     // staged kernel configuration (0: none)
   bool gemv;
@@ -1444,10 +1590,30 @@ static int staged_cfg(int rows_a, int N, int K, bool exact, int cus) {
   return S_NONE;
 }
 
+// Stream plan (int8 decode, <= 128 stacked rows, K % 128 == 0, at least one 64-column tile per CU, no K split).
+// Measured per launch (graph replay, 1x MI355X) against the gemv / staged kernels: M = 64, N = 16384: 14.3 vs
+// 15.7 us; M = 8: 8.6 vs 8.9 us; M = 1: 8.2 vs 8.4 us. With N = 2048 or 8192 the K split it would need (partials
+// through agent-scope slots or a second launch) lost to the gemv / staged kernels (7.2 - 21 vs 6.0 - 16 us), so
+// those shapes keep them.
+static bool stream_plan(int rows_a, int M_out, int N, int K, bool exact, int cus, Plan& s) {
+  static const int on = getenv("BX_STREAM") ? atoi(getenv("BX_STREAM")) : 1;
+  if (!on || exact || rows_a > 128 || rows_a < 1 || K % kStBK != 0) return false;
+  if ((N + kStC - 1) / kStC < cus) return false;
+  s.stream = rows_a <= 16 ? 1 : rows_a <= 32 ? 2 : rows_a <= 64 ? 4 : 8;
+  s.tiles_x = (N + kStC - 1) / kStC;
+  s.tiles_y = 1;
+  s.kbytes = K;
+  s.split = 1;
+  s.ws_bytes = 0;
+  s.tmp_bytes = 0;
+  return true;
+}
+
 static Plan make_plan(int rows_a, int M_out, int N, int K, int nb, int na, bool exact) {
   Plan s = {};
   const int cus = device_cus();
   const int nst = (K + 63) / 64;
+  if (stream_plan(rows_a, M_out, N, K, exact, cus, s)) return s;
   s.wide = wide_cfg(rows_a, N, K, exact);
   s.staged = staged_cfg(rows_a, N, K, exact, cus);
   if (s.staged != S_NONE) {
@@ -1674,10 +1840,30 @@ static int launch_staged(LinArgs& p, const Plan& s, hipStream_t st) {
   }
 }
 
+template <int RBM, int NB, int S, int MODE, int NWV = 4>
+static int launch_stream_cfg(LinArgs& p, const Plan& s, hipStream_t st) {
+  const size_t lds = (size_t)S * kStBK * ((RBM < 2 ? 32 : 16 * RBM) + NB * 16 * NWV);
+  allow_lds(stream_kernel<RBM, NB, S, MODE, NWV>, lds);
+  stream_kernel<RBM, NB, S, MODE, NWV><<<dim3(s.tiles_x, s.split), 64 * NWV, lds, st>>>(p);
+  return check_launch("stream_kernel");
+}
+
+template <int MODE>
+static int launch_stream(LinArgs& p, const Plan& s, hipStream_t st) {
+  BX_REQUIRE((int64_t)p.rows_a * p.K < kBufRange - 16 && (int64_t)p.N * p.ld_row < kBufRange - 16,
+             "stream path: activations and weights must span less than 2 GiB");
+  p.ks = s.kbytes;
+  // ring depth: 4 stages at 16 rows (8 measured ~0.5 us slower per launch at M = 1), 8 at 32 / 64, 6 at 128
+  if (s.stream == 1) return launch_stream_cfg<1, 1, 4, MODE>(p, s, st);
+  if (s.stream == 2) return launch_stream_cfg<2, 1, 8, MODE>(p, s, st);
+  if (s.stream == 4) return launch_stream_cfg<4, 1, 8, MODE>(p, s, st);
+  return launch_stream_cfg<8, 1, 6, MODE>(p, s, st);
+}
+
 static bool aligned16(const void* x) { return ((uintptr_t)x & 15) == 0; }
 
 static int need_ws(const LinArgs& p, const Plan& s, int64_t ws_bytes, const void* tmp, int64_t tmp_bytes) {
-  if (s.split > 1)
+  if (s.ws_bytes > 0)
     BX_REQUIRE(p.ws != nullptr && ws_bytes >= s.ws_bytes, "workspace too small (%lld < %lld)", (long long)ws_bytes,
                (long long)s.ws_bytes);
   if (s.tmp_bytes > 0)
@@ -1784,6 +1970,7 @@ static int int8_common(LinArgs& p, int mode, int64_t ws_bytes, hipStream_t st) {
   const int na = mode == RAW32 ? 1 : p.nl;
   const Plan s = make_plan(p.rows_a, p.M, p.N, p.K, 1, na, false);
   if (int rc = need_ws(p, s, ws_bytes, nullptr, 0)) return rc;
+  if (s.stream) return mode == JOIN ? launch_stream<JOIN>(p, s, st) : launch_stream<RAW32>(p, s, st);
   if (s.staged) return mode == JOIN ? launch_staged<JOIN>(p, s, st) : launch_staged<RAW32>(p, s, st);
   if (s.gemv) return mode == JOIN ? launch_gemv<1, JOIN>(p, s, st) : launch_gemv<1, RAW32>(p, s, st);
   if (mode == RAW32) return launch_tile<1, 1, RAW32>(p, s, st);
@@ -1835,8 +2022,8 @@ extern "C" int bx_exact_linear_plan(int32_t M, int32_t N, int32_t K, int32_t* ou
 extern "C" int bx_int8_gemm_plan(int32_t M, int32_t N, int32_t K, int32_t nl, int32_t* out) {
   BX_REQUIRE(out && M > 0 && N > 0 && K > 0 && nl >= 0 && nl <= 3, "bad plan query");
   const Plan s = nl == 0 ? make_plan(M, M, N, K, 1, 1, false) : make_plan(nl * M, M, N, K, 1, nl, false);
-  out[0] = s.staged ? 4 : s.gemv ? 1 : 3;
-  out[1] = (s.gemv || s.staged) ? -1 : s.tile;
+  out[0] = s.stream ? 5 : s.staged ? 4 : s.gemv ? 1 : 3;
+  out[1] = (s.gemv || s.staged || s.stream) ? -1 : s.tile;
   out[2] = s.split;
   out[3] = s.gemv ? s.tiles_x * s.parts : s.tiles_x * s.tiles_y;
   out[4] = s.gemv ? s.cg : 0;

@@ -1,6 +1,7 @@
 """HIP exact / int8 linear kernels against the CPU oracle, bit for bit (reference tests/test_exact_ops.py:137-152,
 tests/test_gemm_skinny.py, tests/test_vllm_exact_gemm.py: shapes, row counts, extremes, magnitude ranges)."""
 
+import ctypes
 import numpy as np
 import pytest
 import torch
@@ -386,3 +387,29 @@ def test_corrupt_ell_index_sets_flag(dev, M):
             flag = torch.zeros(1, dtype=torch.int32, device=dev)
             exact_linear(q, sh, limbs, d, gg, cnt2, ec2, ev, Rr, flag, checked)
             assert flag.item() == 1, (kind, checked)
+
+
+@pytest.mark.parametrize("N,K", [(16384, 2048), (16400, 1024), (32768, 512)])
+def test_int8_stream_wide(dev, N, K):
+    """int8 decode where the 64-column tiles cover the chip without a K split (the stream kernel): a partial last
+    column tile (N = 16400), join in registers (M % 16 == 0) and through LDS (other M), raw int32 rows up to 128,
+    extreme operands, against the float64 oracle."""
+    from bitexact.int8.gemm_skinny import int_mm, int_mm_join
+    from bitexact import _hip
+    g = np.random.default_rng(N + K)
+    w = g.integers(-128, 128, (N, K)).astype(np.int8)
+    w[N - 1, :] = -128
+    wd = torch.from_numpy(w).to(dev)
+    for M, nl in ((1, 2), (16, 2), (32, 3), (21, 3), (48, 2), (64, 2), (40, 1)):
+        out = (ctypes.c_int32 * 6)()
+        assert _hip.lib().bx_int8_gemm_plan(M, N, K, nl, out) == 0 and out[0] == 5, (M, nl, list(out))
+        z = g.integers(-(1 << 44), 1 << 44, (M, K))
+        q, _, _ = R.quant_rows(z, nl)
+        a = R.stack_limbs(q, nl)
+        y = int_mm_join(torch.from_numpy(a).to(dev), wd, M, nl)
+        assert np.array_equal(y.cpu().numpy(), R.imm(q, w)), (M, nl)
+    for Rr in (1, 7, 16, 33, 64, 100, 128):
+        a = g.integers(-128, 128, (Rr, K)).astype(np.int8)
+        a[0, :] = -128
+        c = int_mm(torch.from_numpy(a).to(dev), wd)
+        assert np.array_equal(c.cpu().numpy().astype(np.int64), R.imm(a, w)), (Rr, "raw")
