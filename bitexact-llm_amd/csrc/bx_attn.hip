@@ -136,6 +136,7 @@ struct AttnArgs {
   int64_t* num_ws;                // [groups, nq, HD]
   int64_t* den_ws;                // [groups, nq]
   int32_t* sem;                   // [groups]
+  uint64_t exch_ticks;            // attn_dec_exch_kernel: longest wait for the other splits' maxima (100 MHz ticks)
 };
 
 template <int QT, int HD>
@@ -408,7 +409,9 @@ __global__ __launch_bounds__(256) void attn_kernel(AttnArgs p) {
 // last block of a tile (counter) combines them, so no value is accumulated with atomics.
 constexpr int kDecWaves = 8;
 constexpr int kDecMaxSplit = 64;
-constexpr int64_t kDecWsSplitBudget = 4096;   // the workspace query sizes for min(64, 4096 / tiles) splits
+constexpr int64_t kDecWsSplitBudget = 4096;
+constexpr uint64_t kDecExchTicks = 20000;     // the exchange kernel's longest wait: 200 us at 100 MHz
+constexpr int kDecExchBlocks = 256;           // the exchange kernel: at most one block per compute unit   // the workspace query sizes for min(64, 4096 / tiles) splits
 
 template <int HD>
 struct DecSmem {
@@ -490,6 +493,155 @@ __device__ __forceinline__ DecWs dec_ws(const AttnArgs& p, int T, int NS, int HD
   return w;
 }
 
+// The MFMA A operand of a tile's queries: limb (m & 3) of query (m >> 2), m = lane & 15, dims kk 64 +
+// (lane >> 4) 16 + [0, 16); the fourth row of each query and queries past nvalid are 0. In two steps, so that a
+// caller can issue the query loads first and use them after its other requests: dec_q_load reads the lane's 16
+// values per 64 dims (16-byte loads when q is 16-byte aligned), dec_q_limbs packs the lane's limb.
+template <int HD>
+struct DecQ {
+  int32_t x[HD / 64][16];
+};
+
+template <int HD>
+__device__ __forceinline__ void dec_q_load(const AttnArgs& p, int group, int q0, int nvalid, int lane, DecQ<HD>& q) {
+  const int m = lane & 15, qi = m >> 2, li = m & 3, c = lane >> 4;
+  const bool live = qi < nvalid && li < 3;
+  const int64_t base = group * p.sq_tile + (int64_t)(q0 + qi) * p.sq_row + c * 16;
+  const bool vec = !p.q64 && ((reinterpret_cast<uintptr_t>(p.q + base)) & 15) == 0;
+#pragma unroll
+  for (int kk = 0; kk < HD / 64; ++kk) {
+    if (vec) {
+#pragma unroll
+      for (int e4 = 0; e4 < 4; ++e4) {
+        const v4i v = live ? *(const v4i*)(p.q + base + kk * 64 + e4 * 4) : v4i{0, 0, 0, 0};
+#pragma unroll
+        for (int e = 0; e < 4; ++e) q.x[kk][e4 * 4 + e] = v[e];
+      }
+    } else {
+#pragma unroll
+      for (int e = 0; e < 16; ++e) {
+        const int64_t qidx = base + kk * 64 + e;
+        q.x[kk][e] = live ? (p.q64 ? (int32_t)p.q64[qidx] : p.q[qidx]) : 0;
+      }
+    }
+  }
+}
+
+template <int HD>
+__device__ __forceinline__ void dec_q_limbs(const DecQ<HD>& q, int lane, v4i (&qa)[HD / 64]) {
+  const int li = lane & 3;
+#pragma unroll
+  for (int kk = 0; kk < HD / 64; ++kk) {
+    int32_t word[4];
+#pragma unroll
+    for (int e4 = 0; e4 < 4; ++e4) {
+      uint32_t wv = 0;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        int32_t x = q.x[kk][e4 * 4 + e];
+        const int32_t a0 = limb_lo(x);
+        x = (x - a0) >> 8;
+        const int32_t a1 = limb_lo(x);
+        x = (x - a1) >> 8;
+        const int32_t a2 = limb_lo(x);
+        const int32_t v = li == 0 ? a0 : li == 1 ? a1 : li == 2 ? a2 : 0;
+        wv |= (uint32_t)(v & 255) << (8 * e);
+      }
+      word[e4] = (int32_t)wv;
+    }
+    qa[kk] = v4i{word[0], word[1], word[2], word[3]};
+  }
+}
+
+template <int HD>
+__device__ __forceinline__ void dec_qa(const AttnArgs& p, int group, int q0, int nvalid, int lane, v4i (&qa)[HD / 64]) {
+  DecQ<HD> q;
+  dec_q_load<HD>(p, group, q0, nvalid, lane, q);
+  dec_q_limbs<HD>(q, lane, qa);
+}
+
+// The block's p V and weight sums (waves added in order) to the outputs (one split) or to the split's workspace
+// slots; the last block of a tile (counter) adds the slots in split order, writes the outputs and puts the
+// workspace back to zero (maxima slots included).
+template <int HD>
+__device__ __forceinline__ void dec_finish(const AttnArgs& p, DecSmem<HD>& sm, const DecWs& ws, int64_t den,
+                                           int64_t (&num)[4][HD / 64], int tile, int sp, int NS, int group, int q0,
+                                           int nvalid) {
+  constexpr int KK = HD / 64;
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6, kl = lane & 15, qo = lane >> 4;
+#pragma unroll
+  for (int o = 1; o < 16; o <<= 1) den += __shfl_xor(den, o, 64);
+  if (kl == 0) sm.den[w][qo] = den;
+  __syncthreads();                                 // red overlays the waves' V rows
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+#pragma unroll
+    for (int kk = 0; kk < KK; ++kk) sm.red[w][i][lane + 64 * kk] = num[i][kk];
+  __syncthreads();
+  // the block's sums, waves in order: thread u -> (query u / HD, dim u % HD)
+  for (int u = threadIdx.x; u < 4 * HD + 4; u += kDecWaves * 64) {
+    int64_t t = 0;
+    if (u < 4 * HD) {
+      for (int ww = 0; ww < kDecWaves; ++ww) t += sm.red[ww][u / HD][u % HD];
+    } else {
+      for (int ww = 0; ww < kDecWaves; ++ww) t += sm.den[ww][u - 4 * HD];
+    }
+    const int i = u < 4 * HD ? u / HD : u - 4 * HD;
+    if (i >= nvalid) continue;
+    if (NS == 1) {
+      if (u < 4 * HD) p.num[group * p.snum_tile + (int64_t)(q0 + i) * p.snum_row + u % HD] = t;
+      else p.den[group * p.sden_tile + q0 + i] = t;
+    } else {
+      const int64_t slot = (int64_t)tile * NS + sp;
+      if (u < 4 * HD) ws_store(&ws.num[(slot * 4 + i) * HD + u % HD], t);
+      else ws_store(&ws.den[slot * 4 + i], t);
+    }
+  }
+  if (NS == 1) return;
+  // every split arrives (its slot stores complete first); the last one adds the slots in split order
+  __builtin_amdgcn_s_waitcnt(0);
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    const bool last = atomicAdd(&ws.sem[tile], 1) == NS - 1;
+    if (last) atomicExch(&ws.sem[tile], 0);
+    sm.s_last = last;
+  }
+  __syncthreads();
+  if (!sm.s_last) return;
+  // every (split, entry) slot is read at once and added into LDS (exact in any order); the slots go back to
+  // zero, so the workspace is left as it was found
+  int64_t* fin = &sm.red[0][0][0];                 // 4 HD + 4 sums
+  for (int u = threadIdx.x; u < 4 * HD + 4; u += kDecWaves * 64) fin[u] = 0;
+  __syncthreads();
+  constexpr int NT = kDecWaves * 64, UB = 8;      // UB slot loads in flight per thread
+  const int nslot = NS * (4 * HD + 4);
+  for (int u0 = threadIdx.x; u0 < nslot; u0 += NT * UB) {
+    int64_t v[UB];
+    int64_t* src[UB];
+#pragma unroll
+    for (int b = 0; b < UB; ++b) {
+      const int u = u0 + b * NT;
+      const int k = u / (4 * HD + 4), e = u % (4 * HD + 4);
+      const int64_t slot = (int64_t)tile * NS + k;
+      src[b] = e < 4 * HD ? &ws.num[slot * 4 * HD + e] : &ws.den[slot * 4 + (e - 4 * HD)];
+      v[b] = u < nslot ? ws_load(src[b]) : 0;
+    }
+#pragma unroll
+    for (int b = 0; b < UB; ++b) {
+      const int u = u0 + b * NT;
+      if (u < nslot) {
+        atomicAdd((unsigned long long*)&fin[u % (4 * HD + 4)], (unsigned long long)v[b]);
+        ws_store(src[b], 0);
+      }
+    }
+  }
+  for (int u = threadIdx.x; u < NS * 4; u += kDecWaves * 64) ws_store(&ws.mx[(int64_t)tile * NS * 4 + u], 0);
+  __syncthreads();
+  for (int u = threadIdx.x; u < nvalid * HD; u += kDecWaves * 64)
+    p.num[group * p.snum_tile + (int64_t)(q0 + u / HD) * p.snum_row + u % HD] = fin[u];
+  if (threadIdx.x < nvalid) p.den[group * p.sden_tile + q0 + threadIdx.x] = fin[4 * HD + threadIdx.x];
+}
+
 // RAW (single launch only): sweep 1 keeps every score of the block's key range (p.S >= hi - lo of them per
 // query) in dynamic LDS and sweep 2 reads them back, so K is read once.
 template <int HD, int PHASE, bool RAW>
@@ -514,34 +666,8 @@ __global__ __launch_bounds__(kDecWaves * 64) void attn_dec_kernel(AttnArgs p) {
     sm.shift[i] = ok && p.sh ? (int64_t)(kFK + 3 - kFZ) - p.sh[group * p.sh_tile + q0 + i] : 0;
     sm.mx[i] = kNeg;
   }
-  // A operand: limb (m & 3) of query (m >> 2), m = lane & 15, dims kk 64 + (lane >> 4) 16 + [0, 16)
   v4i qa[KK];
-  {
-    const int m = lane & 15, qi = m >> 2, li = m & 3, c = lane >> 4;
-    const bool live = qi < nvalid && li < 3;
-#pragma unroll
-    for (int kk = 0; kk < KK; ++kk) {
-      int32_t word[4];
-#pragma unroll
-      for (int e4 = 0; e4 < 4; ++e4) {
-        uint32_t wv = 0;
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          const int64_t qidx = group * p.sq_tile + (int64_t)(q0 + qi) * p.sq_row + kk * 64 + c * 16 + e4 * 4 + e;
-          int32_t x = live ? (p.q64 ? (int32_t)p.q64[qidx] : p.q[qidx]) : 0;
-          const int32_t a0 = limb_lo(x);
-          x = (x - a0) >> 8;
-          const int32_t a1 = limb_lo(x);
-          x = (x - a1) >> 8;
-          const int32_t a2 = limb_lo(x);
-          const int32_t v = li == 0 ? a0 : li == 1 ? a1 : a2;
-          wv |= (uint32_t)(v & 255) << (8 * e);
-        }
-        word[e4] = (int32_t)wv;
-      }
-      qa[kk] = v4i{word[0], word[1], word[2], word[3]};
-    }
-  }
+  dec_qa<HD>(p, group, q0, nvalid, lane, qa);
   __syncthreads();
   int64_t kend = 0;
   for (int i = 0; i < 4; ++i) kend = imax(kend, sm.qpos[i] + 1);
@@ -651,62 +777,178 @@ __global__ __launch_bounds__(kDecWaves * 64) void attn_dec_kernel(AttnArgs p) {
     __builtin_amdgcn_wave_barrier();
     cur = nxt;
   }
+  dec_finish<HD>(p, sm, ws, den, num, tile, sp, NS, group, q0, nvalid);
+}
+
+// ---- paged decode attention, key splits in one launch ----
+// Grid (query tiles, key splits), every block normally resident at once (the host takes this kernel for at most
+// one block per compute unit). A block's key range is at most 16 NBW kDecWaves keys, so wave w holds the K and V
+// limb rows of its NBW 16-key blocks in registers: the block-table entries, then every K and V row, are requested
+// at once, before the queries are read. Scores stay in registers. The splits of a tile exchange their maxima
+// through the workspace: each publishes its own (as mx - kNeg + 1; 0 = not yet published) and waits for the
+// others' for at most p.exch_ticks of the 100 MHz real-time counter; a block that has not seen them all by then
+// computes the maxima over the tile's keys itself, so the wait always ends and the integers never depend on which
+// blocks ran together. Weights, p V and the split sums then follow attn_dec_kernel's sweep 2 and dec_finish,
+// so K and V are each read once.
+template <int HD, int NBW>
+__global__ __launch_bounds__(kDecWaves * 64) void attn_dec_exch_kernel(AttnArgs p) {
+  __shared__ DecSmem<HD> sm;
+  __shared__ int64_t s_best[kDecWaves][4];
+  constexpr int KK = HD / 64;
+  const int tiles = (p.nq + 3) / 4;
+  const int tile = blockIdx.x, T = gridDim.x, sp = blockIdx.y, NS = gridDim.y;
+  const int group = tile / tiles, q0 = (tile % tiles) * 4;
+  const int nvalid = min(4, p.nq - q0);
+  const int h = group % p.hkv;
+  const int64_t brow = p.rmap ? p.rmap[group / p.hkv] : group / p.hkv;
+  const int lane = threadIdx.x & 63, w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int kl = lane & 15, qo = lane >> 4;
+  const DecWs ws = dec_ws(p, T, NS, HD);
+
+  DecQ<HD> qv;                                     // the queries first: used after every other request
+  dec_q_load<HD>(p, group, q0, nvalid, lane, qv);
+  // the tile's query positions, read by every lane (the key range needs their maximum)
+  int64_t qp[4];
 #pragma unroll
-  for (int o = 1; o < 16; o <<= 1) den += __shfl_xor(den, o, 64);
-  if (kl == 0) sm.den[w][qo] = den;
-  __syncthreads();                                 // red overlays the waves' V rows
+  for (int i = 0; i < 4; ++i)
+    qp[i] = i < nvalid ? p.qpos[(group / p.qpos_div) * p.qpos_tile + (int64_t)(q0 + i) * p.qpos_row] : -1;
+  const int64_t kend = imax(imax(qp[0], qp[1]), imax(qp[2], qp[3])) + 1;
+  const int64_t my_qpos = qo == 0 ? qp[0] : qo == 1 ? qp[1] : qo == 2 ? qp[2] : qp[3];
+  int64_t lo64, hi64;
+  split_range(kend, NS, sp, lo64, hi64);
+  const int lo = (int)lo64, hi = (int)hi64;
+  const int nb16 = (hi - lo + 15) / 16;            // <= NBW kDecWaves (the host's bound on the split size)
+  int pg[NBW];
+#pragma unroll
+  for (int t = 0; t < NBW; ++t)
+    pg[t] = w + t * kDecWaves < nb16 ? dec_page(p, brow, min(lo + (w + t * kDecWaves) * 16 + kl, hi - 1)) : 0;
+  KvRegs<HD> kv[NBW];
+#pragma unroll
+  for (int t = 0; t < NBW; ++t)
+    if (w + t * kDecWaves < nb16)
+      dec_rows<HD, true, true>(p, pg[t], h, min(lo + (w + t * kDecWaves) * 16 + kl, hi - 1), kv[t]);
+  if (threadIdx.x < 4) sm.mx[threadIdx.x] = kNeg;
+  const int64_t shift = qo < nvalid && p.sh ? (int64_t)(kFK + 3 - kFZ) - p.sh[group * p.sh_tile + q0 + qo] : 0;
+  v4i qa[KK];
+  dec_q_limbs<HD>(qv, lane, qa);
+
+  // scores and this split's maxima
+  int64_t raw[NBW];
+  int64_t best = kNeg;
+#pragma unroll
+  for (int t = 0; t < NBW; ++t) {
+    raw[t] = 0;
+    if (w + t * kDecWaves < nb16) {                // wave-uniform
+      const int s = lo + (w + t * kDecWaves) * 16 + kl;
+      raw[t] = dec_score<HD>(qa, kv[t]);
+      if (s < hi && s <= my_qpos) best = imax(best, raw[t]);
+    }
+  }
+#pragma unroll
+  for (int o = 1; o < 16; o <<= 1) best = imax(best, __shfl_xor(best, o, 64));
+  if (kl == 0) s_best[w][qo] = best;
+  __syncthreads();
+  if (threadIdx.x < 4) {
+    int64_t m = kNeg;
+    for (int ww = 0; ww < kDecWaves; ++ww) m = imax(m, s_best[ww][threadIdx.x]);
+    ws_store(&ws.mx[((int64_t)tile * NS + sp) * 4 + threadIdx.x], m - kNeg + 1);
+  }
+  bool seen = true;
+  if (threadIdx.x < NS * 4) {
+    int64_t* a = &ws.mx[(int64_t)tile * NS * 4 + threadIdx.x];
+    const uint64_t t0 = __builtin_amdgcn_s_memrealtime();
+    int64_t v = ws_load(a);
+    while (v == 0 && __builtin_amdgcn_s_memrealtime() - t0 < p.exch_ticks) {
+      __builtin_amdgcn_s_sleep(1);
+      v = ws_load(a);
+    }
+    seen = v != 0;
+    if (seen) atomicMax((long long*)&sm.mx[threadIdx.x & 3], (long long)(v - 1 + kNeg));
+  }
+  if (!__syncthreads_and(seen)) {
+    // maxima over every key of the tile, from the cache (rows of 16 keys, the waves in turn)
+    const int nall = (int)((kend + 15) / 16);
+    int64_t b2 = kNeg;
+    for (int i = w; i < nall; i += kDecWaves) {
+      const int s = min(i * 16 + kl, (int)kend - 1);
+      KvRegs<HD> r;
+      dec_rows<HD, true, false>(p, dec_page(p, brow, s), h, s, r);
+      const int64_t sc = dec_score<HD>(qa, r);
+      if (i * 16 + kl < kend && s <= my_qpos) b2 = imax(b2, sc);
+    }
+#pragma unroll
+    for (int o = 1; o < 16; o <<= 1) b2 = imax(b2, __shfl_xor(b2, o, 64));
+    if (kl == 0) atomicMax((long long*)&sm.mx[qo], (long long)b2);
+    __syncthreads();
+  }
+
+  // weights (every table load first), den, p V
+  const int64_t mx = sm.mx[qo];
+  int64_t pw[NBW];
+  {
+    WeightAt wat[NBW];
+    int64_t ta[NBW], tb[NBW], i8[NBW];
+#pragma unroll
+    for (int t = 0; t < NBW; ++t) {
+      if (p.wrule == 0) {
+        wat[t] = weight_at(mx - raw[t], shift, p.l2e);
+        ta[t] = p.lut[wat[t].idx];
+        tb[t] = p.lut[wat[t].idx + 1];
+      } else {
+        i8[t] = int8_index(raw[t] - mx, p.zsh, p.zmul);
+        ta[t] = p.ptab[imin(imax(i8[t], 0), -kI8ZLo)];   // a visible key has d <= 0, so idx <= -kI8ZLo (z = 0)
+      }
+    }
+#pragma unroll
+    for (int t = 0; t < NBW; ++t) {
+      const int s = lo + (w + t * kDecWaves) * 16 + kl;
+      pw[t] = p.wrule == 0 ? weight_of(wat[t], ta[t], tb[t]) : (i8[t] >= 0 ? ta[t] : 0);
+      if (!(w + t * kDecWaves < nb16 && qo < nvalid && s < hi && s <= my_qpos)) pw[t] = 0;
+    }
+  }
+  int64_t den = 0;
+  int64_t num[4][KK];
 #pragma unroll
   for (int i = 0; i < 4; ++i)
 #pragma unroll
-    for (int kk = 0; kk < KK; ++kk) sm.red[w][i][lane + 64 * kk] = num[i][kk];
-  __syncthreads();
-  // the block's sums, waves in order: thread u -> (query u / HD, dim u % HD)
-  for (int u = threadIdx.x; u < 4 * HD + 4; u += kDecWaves * 64) {
-    int64_t t = 0;
-    if (u < 4 * HD) {
-      for (int ww = 0; ww < kDecWaves; ++ww) t += sm.red[ww][u / HD][u % HD];
-    } else {
-      for (int ww = 0; ww < kDecWaves; ++ww) t += sm.den[ww][u - 4 * HD];
+    for (int kk = 0; kk < KK; ++kk) num[i][kk] = 0;
+  const int c = lane >> 4;
+#pragma unroll
+  for (int t = 0; t < NBW; ++t) {
+    if (w + t * kDecWaves >= nb16) break;          // wave-uniform
+    den += pw[t];
+    sm.Ps[w][kl][qo] = (int32_t)pw[t];
+#pragma unroll
+    for (int kk = 0; kk < KK; ++kk) {
+#pragma unroll
+      for (int e4 = 0; e4 < 4; ++e4) {
+        const int32_t w0 = kv[t].v[0][kk][e4], w1 = kv[t].v[1][kk][e4], w2 = kv[t].v[2][kk][e4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const int32_t b0 = (w0 << (24 - 8 * e)) >> 24, b1 = (w1 << (24 - 8 * e)) >> 24, b2 = (w2 << (24 - 8 * e)) >> 24;
+          sm.Vs[w][kl][kk * 64 + c * 16 + e4 * 4 + e] = b0 + b1 * 256 + b2 * 65536;
+        }
+      }
     }
-    const int i = u < 4 * HD ? u / HD : u - 4 * HD;
-    if (i >= nvalid) continue;
-    if (NS == 1) {
-      if (u < 4 * HD) p.num[group * p.snum_tile + (int64_t)(q0 + i) * p.snum_row + u % HD] = t;
-      else p.den[group * p.sden_tile + q0 + i] = t;
-    } else {
-      const int64_t slot = (int64_t)tile * NS + sp;
-      if (u < 4 * HD) ws_store(&ws.num[(slot * 4 + i) * HD + u % HD], t);
-      else ws_store(&ws.den[slot * 4 + i], t);
+    __builtin_amdgcn_s_waitcnt(0xc07f);           // lgkmcnt(0): this wave's LDS writes are done
+    __builtin_amdgcn_wave_barrier();
+#pragma unroll
+    for (int k = 0; k < 16; ++k) {
+      int64_t vd[KK];
+#pragma unroll
+      for (int kk = 0; kk < KK; ++kk) vd[kk] = sm.Vs[w][k][lane + 64 * kk];
+      const v4i pk = *(const v4i*)&sm.Ps[w][k][0];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int64_t pv = pk[i];
+#pragma unroll
+        for (int kk = 0; kk < KK; ++kk) num[i][kk] += pv * vd[kk];
+      }
     }
+    __builtin_amdgcn_s_waitcnt(0xc07f);
+    __builtin_amdgcn_wave_barrier();
   }
-  if (NS == 1) return;
-  // every split arrives (its slot stores complete first); the last one adds the slots in split order
-  __builtin_amdgcn_s_waitcnt(0);
-  __syncthreads();
-  if (threadIdx.x == 0) {
-    const bool last = atomicAdd(&ws.sem[tile], 1) == NS - 1;
-    if (last) atomicExch(&ws.sem[tile], 0);
-    sm.s_last = last;
-  }
-  __syncthreads();
-  if (!sm.s_last) return;
-  // every (split, entry) slot is read at once and added into LDS (exact in any order); the slots go back to
-  // zero, so the workspace is left as it was found
-  int64_t* fin = &sm.red[0][0][0];                 // 4 HD + 4 sums
-  for (int u = threadIdx.x; u < 4 * HD + 4; u += kDecWaves * 64) fin[u] = 0;
-  __syncthreads();
-  for (int u = threadIdx.x; u < NS * (4 * HD + 4); u += kDecWaves * 64) {
-    const int k = u / (4 * HD + 4), e = u % (4 * HD + 4);
-    const int64_t slot = (int64_t)tile * NS + k;
-    int64_t* src = e < 4 * HD ? &ws.num[slot * 4 * HD + e] : &ws.den[slot * 4 + (e - 4 * HD)];
-    atomicAdd((unsigned long long*)&fin[e], (unsigned long long)ws_load(src));
-    ws_store(src, 0);
-  }
-  for (int u = threadIdx.x; u < NS * 4; u += kDecWaves * 64) ws_store(&ws.mx[(int64_t)tile * NS * 4 + u], 0);
-  __syncthreads();
-  for (int u = threadIdx.x; u < nvalid * HD; u += kDecWaves * 64)
-    p.num[group * p.snum_tile + (int64_t)(q0 + u / HD) * p.snum_row + u % HD] = fin[u];
-  if (threadIdx.x < nvalid) p.den[group * p.sden_tile + q0 + threadIdx.x] = fin[4 * HD + threadIdx.x];
+  dec_finish<HD>(p, sm, ws, den, num, tile, sp, NS, group, q0, nvalid);
 }
 
 // ---- fused prefill attention on MFMA (contiguous int32 K / V) ----
@@ -1019,6 +1261,15 @@ template <int HD>
 static int launch_dec(AttnArgs& p, int groups, int64_t max_keys, hipStream_t st) {
   const int tiles = (p.nq + 3) / 4;
   dim3 grid(groups * tiles, p.nsplit);
+  const int64_t chunk = ((max_keys + p.nsplit - 1) / p.nsplit + 63) / 64 * 64;   // keys per split, at most
+  if (p.nsplit > 1 && chunk <= 64 * kDecWaves && (int64_t)grid.x * grid.y <= kDecExchBlocks) {
+    // BX_ATTN_EXCH_TICKS (tests): a shorter wait, down to 0, where blocks compute the maxima they have not seen
+    const char* et = getenv("BX_ATTN_EXCH_TICKS");
+    p.exch_ticks = et ? (uint64_t)strtoull(et, nullptr, 10) : kDecExchTicks;
+    if (chunk <= 32 * kDecWaves) attn_dec_exch_kernel<HD, 2><<<grid, kDecWaves * 64, 0, st>>>(p);
+    else attn_dec_exch_kernel<HD, 4><<<grid, kDecWaves * 64, 0, st>>>(p);
+    return check_launch("attn_dec_exch_kernel");
+  }
   if (p.nsplit > 1) {
     attn_dec_kernel<HD, 0, false><<<grid, kDecWaves * 64, 0, st>>>(p);
     if (int rc = check_launch("attn_dec_kernel(max)")) return rc;

@@ -82,6 +82,36 @@ def test_paged_attention_rmap_and_empty_rows(dev):
         assert np.array_equal(num.cpu().numpy(), ref[0]) and np.array_equal(den.cpu().numpy(), ref[1]), ns
 
 
+@pytest.mark.parametrize("ticks,ns", [(None, 8), ("0", 8), (None, 4), ("0", 4)])
+def test_paged_attention_split_exchange(dev, monkeypatch, ticks, ns):
+    """Config 4's decode shape (4 rows x 8 KV heads, 2048 keys, group 4) over 8 or 4 key splits in one launch, where the
+    splits of a tile exchange their maxima through the workspace: equal to the unsplit launch and to the oracle on
+    a sample of tiles, three calls in a row. ticks "0": no wait for the other splits, each block computes the
+    maxima it has not seen from the keys (the path a block takes when its partners are not resident)."""
+    from bitexact.vllm_plugin import tri_exact_attn, tri_paged
+    if ticks is not None:
+        monkeypatch.setenv("BX_ATTN_EXCH_TICKS", ticks)
+    g = torch.Generator().manual_seed(11)
+    B, HKV, M, HD, S, bs = 4, 8, 4, 64, 2048, 16
+    nblk = S // bs
+    c = torch.randint(-R.LIM3, R.LIM3 + 1, (B * nblk, HKV, bs, 2 * HD), generator=g).to(torch.int32)
+    cl = tri_paged.to_limbs(c.to(dev))
+    bt = torch.randperm(B * nblk, generator=g).to(torch.int32).reshape(B, nblk)
+    qpos = torch.tensor([[S - 1] * M, [S - 1, 1000, 5, 0], [1500] * M, [2047, 2046, 64, 63]])
+    q = torch.randint(-(1 << 22), (1 << 22) + 1, (B, HKV, M, HD), generator=g).to(torch.int32)
+    sh = torch.randint(-40, -25, (B, HKV, M), generator=g)
+    args = (q.to(dev), sh.to(dev), qpos.to(dev), cl, bt.to(dev), torch.arange(B).to(dev), _lut(dev), R.L2E28)
+    assert tri_exact_attn.default_nsplit(B, HKV, nblk, bs) == 8
+    n1, d1 = tri_exact_attn.attend(*args, nsplit=1)
+    for _ in range(3):
+        n8, d8 = tri_exact_attn.attend(*args, nsplit=ns)
+        assert torch.equal(n8, n1) and torch.equal(d8, d1)
+    rows = [0, 1]
+    ref_num, ref_den = R.paged_attend(q[rows].numpy(), sh[rows].numpy(), qpos[rows].numpy(), c.numpy(),
+                                      bt[rows].numpy(), np.arange(2), R.exp2_table(), R.L2E28)
+    assert np.array_equal(n8[:2].cpu().numpy(), ref_num) and np.array_equal(d8[:2].cpu().numpy(), ref_den)
+
+
 @pytest.mark.parametrize("HD", [64, 128])
 def test_prefill_attention(dev, HD):
     from bitexact.exact.attention import prefill
