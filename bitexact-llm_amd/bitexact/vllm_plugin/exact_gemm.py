@@ -18,7 +18,7 @@ def needs_planes(M, N, K):
     return _hip.lib().bx_exact_linear_scratch(M, N, K) > 0
 
 
-KERNELS = {1: "gemv", 2: "wide", 3: "tile"}
+KERNELS = {1: "gemv", 2: "wide", 3: "tile", 5: "stream"}
 TILES = {0: "128x128", 1: "64x128", 2: "64x32", 3: "64x64-int8", 4: "64x64", -1: None}
 
 

@@ -1135,8 +1135,8 @@ __global__ __launch_bounds__(64 * NWV) void stream_kernel(LinArgs p) {
   extern __shared__ __align__(16) char smem[];
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int n0 = blockIdx.x * C, kb = 0;
-  const int nks = p.K / BK;
+  const int n0 = blockIdx.x * C, kb = blockIdx.y * p.ks;
+  const int nks = min(p.ks, p.K - kb) / BK;
   const int rows = p.rows_a;                                  // <= 16 RBM (rows past it repeat the last row)
 
   const auto ra = __builtin_amdgcn_make_buffer_rsrc(const_cast<int8_t*>(p.a), (short)0, kBufRange, 0x00020000);
@@ -1242,6 +1242,64 @@ __global__ __launch_bounds__(64 * NWV) void stream_kernel(LinArgs p) {
         Cs[(j * RP + r * 16 + (lane >> 4) * 4 + e) * CP + wave * 16 + (lane & 15)] = acc[r][j][e];
   __syncthreads();
   const int nla = MODE == JOIN ? p.nl : MODE == RAW32 ? 1 : 3;
+  if constexpr (MODE == EXACT || MODE == WMM_T) {
+    // a wave per row group, a lane per column: the column's epilogue context is read once and the residual
+    // gathers of 8 rows go out together
+    // (K split: the partial sums go to the zeroed int64 workspace and the tile's last block finishes them)
+    constexpr int RG = NT / C;
+    __shared__ int s_last;
+    const int c = tid % C, rg = tid / C, n = n0 + c;
+    const bool split = gridDim.y > 1;
+    ColCtx cc;
+    if constexpr (MODE == EXACT) cc = col_ctx(p, n);
+    auto finish8 = [&](int m0, const int (&mrow)[8], const int64_t (&v)[8]) {
+      int64_t B[8];
+      if constexpr (MODE == EXACT) residual_rows<8>(p, cc, mrow, B, corrupt);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const int m = m0 + e * RG;
+        if (m < Mo && n < p.N) {
+          if constexpr (MODE == EXACT) finalize_col(p, cc, m, n, p.sh[m], v[e], B[e], bad, corrupt);
+          else ((int64_t*)p.out)[(int64_t)m * p.N + n] = v[e];
+        }
+      }
+    };
+    for (int m0 = rg; m0 < Mo; m0 += 8 * RG) {     // wave-uniform
+      int mrow[8];
+      int64_t v[8];
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        mrow[e] = min(m0 + e * RG, Mo - 1);
+        v[e] = 0;
+#pragma unroll
+        for (int i = 0; i < 3; ++i)
+#pragma unroll
+          for (int j = 0; j < NB; ++j) v[e] += (int64_t)Cs[(j * RP + i * p.M + mrow[e]) * CP + c] << (8 * (i + j));
+      }
+      if (split) {
+#pragma unroll
+        for (int e = 0; e < 8; ++e)
+          if (m0 + e * RG < Mo && n < p.N) ws_add(p, m0 + e * RG, n, v[e]);
+      } else {
+        finish8(m0, mrow, v);
+      }
+    }
+    if (split && splitk_last(p, blockIdx.x, gridDim.y, &s_last)) {
+      for (int m0 = rg; m0 < Mo; m0 += 8 * RG) {
+        int mrow[8];
+        int64_t v[8];
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          const int m = m0 + e * RG;
+          mrow[e] = min(m, Mo - 1);
+          v[e] = (m < Mo && n < p.N) ? ws_take(p, m, n) : 0;
+        }
+        finish8(m0, mrow, v);
+      }
+    }
+    if (MODE == EXACT) write_flag(p, bad, corrupt);
+    return;
+  }
   for (int o = tid; o < Mo * C; o += NT) {
     const int m = o / C, c = o - m * C, n = n0 + c;
     if (n >= p.N) continue;
@@ -1590,22 +1648,31 @@ static int staged_cfg(int rows_a, int N, int K, bool exact, int cus) {
   return S_NONE;
 }
 
-// Stream plan (int8 decode, <= 128 stacked rows, K % 128 == 0, at least one 64-column tile per CU, no K split).
-// Measured per launch (graph replay, 1x MI355X) against the gemv / staged kernels: M = 64, N = 16384: 14.3 vs
-// 15.7 us; M = 8: 8.6 vs 8.9 us; M = 1: 8.2 vs 8.4 us. With N = 2048 or 8192 the K split it would need (partials
-// through agent-scope slots or a second launch) lost to the gemv / staged kernels (7.2 - 21 vs 6.0 - 16 us), so
-// those shapes keep them.
+// Stream plan: <= 128 stacked activation rows (int8 decode; exact decode from 49 limb rows, 17 <= M <= 42),
+// K % 128 == 0, 64-column tiles. Int8 takes it when the tiles alone cover the chip (no K split). Measured per launch
+// (graph replay, 1x MI355X) against the gemv / staged kernels: M = 64, N = 16384: 14.3 vs 15.7 us; M = 8: 8.6 vs
+// 8.9 us; M = 1: 8.2 vs 8.4 us. With N = 2048 or 8192 the K split it would need lost to them (7.2 - 21 vs 6.0 -
+// 16 us), so those shapes keep them. Exact mode at M = 32: N = 16384: 26.5 vs 39.1 us (wide kernel), N = 128256:
+// 203 vs 289 us; narrow N splits K over the zeroed workspace when every block keeps >= 1024 k (N = 2048, K = 8192:
+// 24.3 vs 30.4 us on the 64 x 64 tile); at K = 2048 (8 splits of 256 k: 16.4 vs 11.7 us) the gemv stays.
 static bool stream_plan(int rows_a, int M_out, int N, int K, bool exact, int cus, Plan& s) {
   static const int on = getenv("BX_STREAM") ? atoi(getenv("BX_STREAM")) : 1;
-  if (!on || exact || rows_a > 128 || rows_a < 1 || K % kStBK != 0) return false;
-  if ((N + kStC - 1) / kStC < cus) return false;
-  s.stream = rows_a <= 16 ? 1 : rows_a <= 32 ? 2 : rows_a <= 64 ? 4 : 8;
+  if (!on || rows_a > 128 || rows_a < (exact ? 49 : 1) || K % kStBK != 0) return false;
   s.tiles_x = (N + kStC - 1) / kStC;
   s.tiles_y = 1;
-  s.kbytes = K;
   s.split = 1;
-  s.ws_bytes = 0;
-  s.tmp_bytes = 0;
+  if (s.tiles_x < cus) {   // exact only: K split until the tiles cover the chip
+    if (!exact) return false;
+    const int nch = K / kStBK;
+    const int want = std::min(nch, (cus + s.tiles_x - 1) / s.tiles_x);
+    const int per = (nch + want - 1) / want;
+    if (per < 8) return false;   // under 1024 k per block the split's fixed costs lose to the gemv
+    s.split = (nch + per - 1) / per;
+  }
+  s.stream = rows_a <= 16 ? 1 : rows_a <= 32 ? 2 : rows_a <= 64 ? 4 : (exact && rows_a <= 96) ? 6 : 8;
+  s.kbytes = (K / kStBK + s.split - 1) / s.split * kStBK;
+  s.ws_bytes = s.split > 1 ? ws_size(M_out, N, s.tiles_x) : 0;
+  s.tmp_bytes = exact ? 3LL * M_out * K : 0;   // exact: q limb planes (unless the caller brings them)
   return true;
 }
 
@@ -1842,7 +1909,8 @@ static int launch_staged(LinArgs& p, const Plan& s, hipStream_t st) {
 
 template <int RBM, int NB, int S, int MODE, int NWV = 4>
 static int launch_stream_cfg(LinArgs& p, const Plan& s, hipStream_t st) {
-  const size_t lds = (size_t)S * kStBK * ((RBM < 2 ? 32 : 16 * RBM) + NB * 16 * NWV);
+  constexpr int RP = RBM < 2 ? 32 : 16 * RBM;
+  const size_t lds = std::max((size_t)S * kStBK * (RP + NB * 16 * NWV), (size_t)NB * RP * (16 * NWV + 1) * 4);
   allow_lds(stream_kernel<RBM, NB, S, MODE, NWV>, lds);
   stream_kernel<RBM, NB, S, MODE, NWV><<<dim3(s.tiles_x, s.split), 64 * NWV, lds, st>>>(p);
   return check_launch("stream_kernel");
@@ -1850,9 +1918,19 @@ static int launch_stream_cfg(LinArgs& p, const Plan& s, hipStream_t st) {
 
 template <int MODE>
 static int launch_stream(LinArgs& p, const Plan& s, hipStream_t st) {
-  BX_REQUIRE((int64_t)p.rows_a * p.K < kBufRange - 16 && (int64_t)p.N * p.ld_row < kBufRange - 16,
+  constexpr bool EX = MODE == EXACT || MODE == WMM_T;
+  BX_REQUIRE((int64_t)p.rows_a * p.K < kBufRange - 16 &&
+                 (EX ? 2 * p.ld_plane : 0) + (int64_t)p.N * p.ld_row < kBufRange - 16,
              "stream path: activations and weights must span less than 2 GiB");
   p.ks = s.kbytes;
+  bind_ws(p, s);
+  if constexpr (EX) {   // three weight planes: 4-stage rings (3 at 128 rows) within the 160 KiB of LDS
+    if (s.stream == 1) return launch_stream_cfg<1, 3, 4, MODE>(p, s, st);
+    if (s.stream == 2) return launch_stream_cfg<2, 3, 4, MODE>(p, s, st);
+    if (s.stream == 4) return launch_stream_cfg<4, 3, 4, MODE>(p, s, st);
+    if (s.stream == 6) return launch_stream_cfg<6, 3, 4, MODE>(p, s, st);
+    return launch_stream_cfg<8, 3, 3, MODE>(p, s, st);
+  }
   // ring depth: 4 stages at 16 rows (8 measured ~0.5 us slower per launch at M = 1), 8 at 32 / 64, 6 at 128
   if (s.stream == 1) return launch_stream_cfg<1, 1, 4, MODE>(p, s, st);
   if (s.stream == 2) return launch_stream_cfg<2, 1, 8, MODE>(p, s, st);
@@ -1901,6 +1979,7 @@ static int exact_common(LinArgs& p, int mode, int64_t ws_bytes, void* tmp, int64
     if (int rc = check_launch("split_q_kernel")) return rc;
     p.a = tp;
   }
+  if (s.stream) return mode == EXACT ? launch_stream<EXACT>(p, s, st) : launch_stream<WMM_T>(p, s, st);
   if (s.wide) return mode == EXACT ? launch_wide<EXACT>(p, s, st) : launch_wide<WMM_T>(p, s, st);
   return mode == EXACT ? launch_tile<3, 3, EXACT>(p, s, st) : launch_tile<3, 3, WMM_T>(p, s, st);
 }
@@ -2004,13 +2083,13 @@ extern "C" int64_t bx_int8_gemm_workspace(int32_t M, int32_t N, int32_t K, int32
 }
 
 // Which kernel bx_exact_linear launches for (M, N, K) (tests use it to prove they reach every configuration):
-// out[0] = 1 gemv, 2 wide, 3 tile; out[1] = tile configuration (0 T_BIG, 1 T_MID, 2 T_NARROW, 3 T_DEC,
+// out[0] = 1 gemv, 2 wide, 3 tile, 5 stream; out[1] = tile configuration (0 T_BIG, 1 T_MID, 2 T_NARROW, 3 T_DEC,
 // 4 T_SMALL; -1 otherwise); out[2] = K splits; out[3] = blocks per split.
 extern "C" int bx_exact_linear_plan(int32_t M, int32_t N, int32_t K, int32_t* out) {
   BX_REQUIRE(out && M > 0 && N > 0 && K > 0, "bad plan query");
   const Plan s = make_plan(3 * M, M, N, K, 3, 3, true);
-  out[0] = s.gemv ? 1 : s.wide ? 2 : 3;
-  out[1] = (s.gemv || s.wide) ? -1 : s.tile;
+  out[0] = s.stream ? 5 : s.gemv ? 1 : s.wide ? 2 : 3;
+  out[1] = (s.gemv || s.wide || s.stream) ? -1 : s.tile;
   out[2] = s.split;
   out[3] = s.gemv ? s.tiles_x * s.parts : s.tiles_x * s.tiles_y;
   return BX_OK;

@@ -76,7 +76,7 @@ int bx_exact_linear_noalloc(const int32_t* q, int64_t ldq, const int64_t* sh, co
 int64_t bx_exact_linear_noalloc_limit(void);
 /* Introspection, no reference counterpart (the reference picks Triton configs per shape from static tables,
  * src/bitexact/vllm_plugin/exact_gemm.py:205-226): which kernel bx_exact_linear runs for (M, N, K).
- * out int32 [4] = {kernel: 1 gemv, 2 wide, 3 tile; tile config: 0 128x128, 1 64x128, 2 64x32, 3 64x64 int8 decode,
+ * out int32 [4] = {kernel: 1 gemv, 2 wide, 3 tile, 5 stream; tile config: 0 128x128, 1 64x128, 2 64x32, 3 64x64 int8 decode,
  * 4 64x64 exact, -1 none; K splits; blocks per split}. Tests use it to show every configuration is reached. */
 int bx_exact_linear_plan(int32_t M, int32_t N, int32_t K, int32_t* out);
 

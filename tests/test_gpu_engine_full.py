@@ -53,8 +53,8 @@ def test_full_geometry_batch_invariance_and_lm_head(dev, engine):
             h32, lg32 = h, lg
     assert len(set(shas.values())) == 1, shas
     assert not bool(eng.err)
-    # the lm_head at M = 32 on the wide kernel against the oracle, columns at every 64-column tile edge + random
-    assert plan(B, eng.V, eng.D)[0] == "wide"
+    # the lm_head at M = 32 on the stream kernel against the oracle, columns at every 64-column tile edge + random
+    assert plan(B, eng.V, eng.D)[0] == "stream"
     q, sh, _ = ops.norm_quant(h32, *eng.gf)
     cols = np.unique(np.concatenate([np.arange(0, eng.V, 64), np.arange(63, eng.V, 64),
                                      np.random.default_rng(2).integers(0, eng.V, 256)]))

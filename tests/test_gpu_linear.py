@@ -52,7 +52,7 @@ def test_decompose_matches_oracle(dev):
 
 
 @pytest.mark.parametrize("M,N,K", [(1, 256, 2048), (7, 3072, 2048), (37, 512, 8192), (300, 1024, 2048), (2048, 512, 2048),
-                                   (21, 200, 320), (22, 130, 64)])
+                                   (21, 200, 320), (22, 130, 64), (32, 16384, 256), (32, 2048, 8192)])
 def test_wmm_exact_extremes(dev, M, N, K):
     from bitexact.exact.wmm import wmm_hip
     g = np.random.default_rng(M * 1000 + N)
@@ -93,12 +93,18 @@ def test_exact_linear_matches_oracle(dev, M):
         assert bool(flag.item()) == rflag, (M, lim)
 
 
-@pytest.mark.parametrize("M,N,K", [(22, 16384, 512), (32, 16400, 512), (42, 16384, 512), (32, 2048, 512),
-                                   (27, 3000, 512), (32, 2048, 8192), (32, 3072, 2048)])
-def test_exact_linear_wide_rows(dev, M, N, K):
-    """65..96 limb rows: the wide kernel at N >= 8192 (every weight once; N = 16400 leaves a partial column tile),
-    the gemv's row parts below (N = 3000 leaves a partial column tile)."""
-    from bitexact.vllm_plugin.exact_gemm import exact_linear
+@pytest.mark.parametrize("M,N,K,kern", [(22, 16384, 512, "stream"), (32, 16400, 512, "stream"),
+                                        (42, 16384, 512, "stream"), (17, 16384, 512, "stream"),
+                                        (33, 16384, 256, "stream"), (32, 8192, 512, "wide"), (32, 2048, 512, "gemv"),
+                                        (27, 3000, 512, "gemv"), (32, 2048, 8192, "stream"),
+                                        (40, 4096, 8192, "stream"), (32, 3072, 2048, "gemv")])
+def test_exact_linear_wide_rows(dev, M, N, K, kern):
+    """49..128 limb rows (17 <= M <= 42): the stream kernel where its 64-column tiles cover the chip (N = 16400
+    leaves a partial column tile; 51, 66, 96, 99, 126 limb rows) or K splits into >= 1024-k parts (N = 2048 / 4096,
+    K = 8192: the zeroed workspace and the tile's last block), the wide kernel at N = 8192 with K = 512, the gemv's
+    row parts otherwise (N = 3000 leaves a partial column tile)."""
+    from bitexact.vllm_plugin.exact_gemm import exact_linear, plan
+    assert plan(M, N, K)[0] == kern, plan(M, N, K)
     w = _bf16(N, K, 5)
     dec = _dec(w)
     limbs = torch.from_numpy(dec["limbs"]).to(dev)
@@ -255,12 +261,14 @@ def test_int8_staged_rows(dev, N, K):
         assert np.array_equal(c.cpu().numpy().astype(np.int64), R.imm(a, w)), (Rr, "raw")
 
 
-@pytest.mark.parametrize("M,N,K", [(8, 160, 512), (100, 160, 512), (200, 160, 512), (300, 1024, 2048)])
+@pytest.mark.parametrize("M,N,K", [(8, 160, 512), (100, 160, 512), (200, 160, 512), (300, 1024, 2048),
+                                   (32, 16384, 512), (32, 2048, 8192)])
 def test_exact_linear_dense_residual_rows(dev, M, N, K):
     """Rows whose residual lists are long: one element of 2^20 sets the row grid at 2^-3, so every ordinary
     N(0, 0.02) element of the row lands in the residual (hundreds of ELL entries; the epilogue keeps the first
     4 of a column in registers and reads the rest from memory). M = 8: gemv path; 100, 200: 64 x 64 tiles;
-    300 x 1024 x 2048: 64 x 64 tiles with K split in 4 (the last block of a tile applies the epilogue)."""
+    300 x 1024 x 2048: 64 x 64 tiles with K split in 4 (the last block of a tile applies the epilogue); M = 32: the
+    stream kernel, without and with K split."""
     from bitexact.vllm_plugin.exact_gemm import exact_linear
     w = _bf16(N, K, 21)
     for n in (1, 7, 64, N - 1):
