@@ -113,6 +113,7 @@ struct AttnArgs {
   int64_t sbt;
   const int64_t* rmap;
   int bs, hkv;
+  int nblk;                       // paged: block-table entries per row
   const int32_t* K;               // contiguous: [Z, S, HD] with strides
   const int32_t* V;
   int64_t sk_z, sk_s, sv_z, sv_s;
@@ -780,6 +781,200 @@ __global__ __launch_bounds__(kDecWaves * 64) void attn_dec_kernel(AttnArgs p) {
   dec_finish<HD>(p, sm, ws, den, num, tile, sp, NS, group, q0, nvalid);
 }
 
+// A key's weight in two halves: dec_w_issue sends the table loads of one score (always inside the table,
+// whatever the score: a hidden key's weight is discarded), dec_w_value forms the weight once they are in.
+struct DecW {
+  WeightAt wat;
+  int64_t ta, tb, i8;
+};
+
+__device__ __forceinline__ DecW dec_w_issue(const AttnArgs& p, int64_t raw, int64_t mx, int64_t shift) {
+  DecW d;
+  d.tb = 0;
+  d.i8 = 0;
+  if (p.wrule == 0) {
+    d.wat = weight_at(mx - raw, shift, p.l2e);
+    d.ta = p.lut[d.wat.idx];
+    d.tb = p.lut[d.wat.idx + 1];
+  } else {
+    d.i8 = int8_index(raw - mx, p.zsh, p.zmul);
+    d.ta = p.ptab[imin(imax(d.i8, 0), -kI8ZLo)];   // a visible key has d <= 0, so idx <= -kI8ZLo (z = 0)
+  }
+  return d;
+}
+
+__device__ __forceinline__ int64_t dec_w_value(const AttnArgs& p, const DecW& d) {
+  return p.wrule == 0 ? weight_of(d.wat, d.ta, d.tb) : (d.i8 >= 0 ? d.ta : 0);
+}
+
+// p V of one 16-key block of a wave: the weights (lane: key kl, query qo) and the joined V rows (from the three
+// limb planes the lane holds: key kl, dims of chunk lane >> 4) meet in the wave's LDS slice; lane l then adds
+// sum_k p[k][i] V[k][l + 64 kk] for the four queries i.
+template <int HD>
+__device__ __forceinline__ void dec_pv(DecSmem<HD>& sm, int w, int lane, int64_t pw, const v4i (&v)[3][HD / 64],
+                                       int64_t (&num)[4][HD / 64]) {
+  constexpr int KK = HD / 64;
+  const int kl = lane & 15, qo = lane >> 4, c = lane >> 4;
+  sm.Ps[w][kl][qo] = (int32_t)pw;
+#pragma unroll
+  for (int kk = 0; kk < KK; ++kk) {
+#pragma unroll
+    for (int e4 = 0; e4 < 4; ++e4) {
+      const int32_t w0 = v[0][kk][e4], w1 = v[1][kk][e4], w2 = v[2][kk][e4];
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const int32_t b0 = (w0 << (24 - 8 * e)) >> 24, b1 = (w1 << (24 - 8 * e)) >> 24, b2 = (w2 << (24 - 8 * e)) >> 24;
+        sm.Vs[w][kl][kk * 64 + c * 16 + e4 * 4 + e] = b0 + b1 * 256 + b2 * 65536;
+      }
+    }
+  }
+  __builtin_amdgcn_s_waitcnt(0xc07f);           // lgkmcnt(0): this wave's LDS writes are done
+  __builtin_amdgcn_wave_barrier();
+#pragma unroll
+  for (int k = 0; k < 16; ++k) {
+    int64_t vd[KK];
+#pragma unroll
+    for (int kk = 0; kk < KK; ++kk) vd[kk] = sm.Vs[w][k][lane + 64 * kk];
+    const v4i pk = *(const v4i*)&sm.Ps[w][k][0];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int64_t pv = pk[i];
+#pragma unroll
+      for (int kk = 0; kk < KK; ++kk) num[i][kk] += pv * vd[kk];
+    }
+  }
+  __builtin_amdgcn_s_waitcnt(0xc07f);
+  __builtin_amdgcn_wave_barrier();
+}
+
+// One key row's three limb planes (K: planes 0-2, V: planes 3-5 of the cache row) for the lane: key s of cache
+// block pg, dims of chunk lane >> 4.
+template <int HD>
+__device__ __forceinline__ void dec_planes(const AttnArgs& p, int pg, int h, int s, int first, v4i (&r)[3][HD / 64]) {
+  const int c = (threadIdx.x & 63) >> 4;
+  const int8_t* row = p.cache + (int64_t)pg * p.sc_nb + (int64_t)h * p.sc_h + (int64_t)(s % p.bs) * p.sc_bs + c * 16;
+#pragma unroll
+  for (int j = 0; j < 3; ++j)
+#pragma unroll
+    for (int kk = 0; kk < HD / 64; ++kk) r[j][kk] = *(const v4i*)(row + (first + j) * HD + kk * 64);
+}
+
+template <int HD>
+__device__ __forceinline__ int64_t dec_score_k(const v4i (&qa)[HD / 64], const v4i (&k)[3][HD / 64]) {
+  int64_t raw = 0;
+#pragma unroll
+  for (int j = 0; j < 3; ++j) {
+    v4i acc = {0, 0, 0, 0};
+#pragma unroll
+    for (int kk = 0; kk < HD / 64; ++kk) acc = __builtin_amdgcn_mfma_i32_16x16x64_i8(qa[kk], k[j][kk], acc, 0, 0, 0);
+    const int64_t t = (int64_t)acc[0] + ((int64_t)acc[1] << 8) + ((int64_t)acc[2] << 16);
+    raw += t << (8 * j);
+  }
+  return raw;
+}
+
+// ---- paged decode attention, one block per query tile, up to kDecRawKeys keys ----
+// The tile's block-table entries are copied to LDS first, so locating a key row costs an LDS read rather than a
+// memory round trip. Each wave keeps the limb rows of its next DR 16-key blocks in flight (a register ring, the
+// loop unrolled by DR). Sweep 1 streams K, keeps every score in LDS and the per-query maxima; sweep 2 streams V
+// and forms weights and p V from the kept scores, so K and V are each read once.
+constexpr int kDecDepth = 3;
+template <int HD>
+__global__ __launch_bounds__(kDecWaves * 64) void attn_dec_raw_kernel(AttnArgs p) {
+  __shared__ DecSmem<HD> sm;
+  extern __shared__ __align__(16) int64_t raw_cache[];     // [4][p.S] scores, then the block-table entries
+  constexpr int KK = HD / 64, DR = kDecDepth;
+  const int tiles = (p.nq + 3) / 4;
+  const int tile = blockIdx.x;
+  const int group = tile / tiles, q0 = (tile % tiles) * 4;
+  const int nvalid = min(4, p.nq - q0);
+  const int h = group % p.hkv;
+  const int64_t brow = p.rmap ? p.rmap[group / p.hkv] : group / p.hkv;
+  const int lane = threadIdx.x & 63, w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int kl = lane & 15, qo = lane >> 4;
+  int32_t* spg = (int32_t*)(raw_cache + 4 * (int64_t)p.S);
+
+  DecQ<HD> qv;
+  dec_q_load<HD>(p, group, q0, nvalid, lane, qv);
+  // the block-table row (every entry the launch may reach: p.S / bs + 1), independent of the positions
+  const int npg = p.S / p.bs + 1 < p.nblk ? p.S / p.bs + 1 : p.nblk;
+  for (int i = threadIdx.x; i < npg; i += kDecWaves * 64) spg[i] = p.bt[brow * p.sbt + i];
+  int64_t qp[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+    qp[i] = i < nvalid ? p.qpos[(group / p.qpos_div) * p.qpos_tile + (int64_t)(q0 + i) * p.qpos_row] : -1;
+  const int kend = (int)imin(imax(imax(qp[0], qp[1]), imax(qp[2], qp[3])) + 1, p.S);   // qpos < nblk bs <= p.S
+  const int64_t my_qpos = qo == 0 ? qp[0] : qo == 1 ? qp[1] : qo == 2 ? qp[2] : qp[3];
+  if (threadIdx.x < 4) sm.mx[threadIdx.x] = kNeg;
+  const int64_t shift = qo < nvalid && p.sh ? (int64_t)(kFK + 3 - kFZ) - p.sh[group * p.sh_tile + q0 + qo] : 0;
+  __syncthreads();
+  v4i qa[KK];
+  dec_q_limbs<HD>(qv, lane, qa);
+  const int nb16 = (kend + 15) / 16;
+  auto rows = [&](int i, int first, v4i (&r)[3][KK]) {
+    const int s = min(i * 16 + kl, kend - 1);
+    dec_planes<HD>(p, spg[s / p.bs], h, s, first, r);
+  };
+
+  // ---- sweep 1: K, scores into LDS, maxima ----
+  {
+    v4i kr[DR][3][KK];
+#pragma unroll
+    for (int d = 0; d < DR; ++d)
+      if (w + d * kDecWaves < nb16) rows(w + d * kDecWaves, 0, kr[d]);
+    int64_t best = kNeg;
+    for (int b0 = w; b0 < nb16; b0 += DR * kDecWaves) {
+#pragma unroll
+      for (int d = 0; d < DR; ++d) {
+        const int i = b0 + d * kDecWaves;
+        if (i < nb16) {                              // wave-uniform
+          const int64_t raw = dec_score_k<HD>(qa, kr[d]);
+          if (i + DR * kDecWaves < nb16) rows(i + DR * kDecWaves, 0, kr[d]);
+          const int s = i * 16 + kl;
+          if (s < kend) raw_cache[qo * p.S + s] = raw;
+          if (s < kend && s <= my_qpos) best = imax(best, raw);
+        }
+      }
+    }
+#pragma unroll
+    for (int o = 1; o < 16; o <<= 1) best = imax(best, __shfl_xor(best, o, 64));
+    if (kl == 0) atomicMax((long long*)&sm.mx[qo], (long long)best);
+  }
+  // the first V rows go out before the maxima are complete
+  v4i vr[DR][3][KK];
+#pragma unroll
+  for (int d = 0; d < DR; ++d)
+    if (w + d * kDecWaves < nb16) rows(w + d * kDecWaves, 3, vr[d]);
+  __builtin_amdgcn_s_waitcnt(0xc07f);             // LDS only (lgkmcnt(0)): the V loads stay in flight
+  asm volatile("s_barrier" ::: "memory");
+
+  // ---- sweep 2: V, weights from the kept scores, den, p V ----
+  const int64_t mx = sm.mx[qo];
+  int64_t den = 0;
+  int64_t num[4][KK];
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+#pragma unroll
+    for (int kk = 0; kk < KK; ++kk) num[i][kk] = 0;
+  for (int b0 = w; b0 < nb16; b0 += DR * kDecWaves) {
+#pragma unroll
+    for (int d = 0; d < DR; ++d) {
+      const int i = b0 + d * kDecWaves;
+      if (i < nb16) {                                // wave-uniform
+        const int s = i * 16 + kl;
+        const int64_t raw = s < kend ? raw_cache[qo * p.S + s] : 0;
+        const DecW wt = dec_w_issue(p, raw, mx, shift);
+        int64_t pw = dec_w_value(p, wt);
+        if (!(qo < nvalid && s < kend && s <= my_qpos)) pw = 0;
+        den += pw;
+        dec_pv<HD>(sm, w, lane, pw, vr[d], num);
+        if (i + DR * kDecWaves < nb16) rows(i + DR * kDecWaves, 3, vr[d]);
+      }
+    }
+  }
+  dec_finish<HD>(p, sm, DecWs{}, den, num, tile, 0, 1, group, q0, nvalid);
+}
+
 // ---- paged decode attention, key splits in one launch ----
 // Grid (query tiles, key splits), every block normally resident at once (the host takes this kernel for at most
 // one block per compute unit). A block's key range is at most 16 NBW kDecWaves keys, so wave w holds the K and V
@@ -1278,11 +1473,11 @@ static int launch_dec(AttnArgs& p, int groups, int64_t max_keys, hipStream_t st)
   }
   if (max_keys <= kDecRawKeys) {
     p.S = (int)((max_keys + 15) / 16 * 16);
-    const size_t lds = (size_t)4 * p.S * 8;
-    hipFuncSetAttribute((const void*)attn_dec_kernel<HD, 1, true>, hipFuncAttributeMaxDynamicSharedMemorySize,
-                        (int)(4 * kDecRawKeys * 8));
-    attn_dec_kernel<HD, 1, true><<<grid, kDecWaves * 64, lds, st>>>(p);
-    return check_launch("attn_dec_kernel(raw)");
+    const size_t lds = (size_t)4 * p.S * 8 + ((size_t)p.S / p.bs + 2) * 4;   // scores + block-table entries
+    hipFuncSetAttribute((const void*)attn_dec_raw_kernel<HD>, hipFuncAttributeMaxDynamicSharedMemorySize,
+                        (int)(4 * kDecRawKeys * 8 + (kDecRawKeys + 2) * 4));
+    attn_dec_raw_kernel<HD><<<grid, kDecWaves * 64, lds, st>>>(p);
+    return check_launch("attn_dec_raw_kernel");
   }
   attn_dec_kernel<HD, 1, false><<<grid, kDecWaves * 64, 0, st>>>(p);
   return check_launch("attn_dec_kernel");
@@ -1324,7 +1519,7 @@ extern "C" int bx_exact_attn_paged(const int32_t* q, const int64_t* sh, const in
   p.sh = sh; p.sh_tile = M;
   p.qpos = qpos; p.qpos_tile = sqpos_r; p.qpos_row = 1; p.qpos_div = HKV; p.nq = M;
   p.cache = cache; p.sc_nb = sc_nb; p.sc_h = sc_h; p.sc_bs = sc_bs; p.bt = bt; p.sbt = sbt; p.rmap = rmap;
-  p.bs = bs; p.hkv = HKV;
+  p.bs = bs; p.hkv = HKV; p.nblk = nblk;
   p.lut = lut; p.l2e = l2e;
   p.num = num; p.den = den; p.snum_tile = (int64_t)M * HD; p.snum_row = HD; p.sden_tile = M;
   p.nsplit = nsplit;
@@ -1359,7 +1554,7 @@ extern "C" int bx_int8_attn_paged(const int64_t* q, const int64_t* qpos, int64_t
   p.q64 = q; p.sq_tile = (int64_t)M * HD; p.sq_row = HD;
   p.qpos = qpos; p.qpos_tile = sqpos_r; p.qpos_row = 1; p.qpos_div = HKV; p.nq = M;
   p.cache = cache; p.sc_nb = sc_nb; p.sc_h = sc_h; p.sc_bs = sc_bs; p.bt = bt; p.sbt = sbt; p.rmap = nullptr;
-  p.bs = bs; p.hkv = HKV;
+  p.bs = bs; p.hkv = HKV; p.nblk = nblk;
   // int8.segs.score_rule (src/bitexact/int8/segs.py:29-37): FQ = 14, FA = 12; head_dim 128 scales by 2^-1/2
   p.wrule = 1; p.ptab = ptab;
   p.zsh = 2 * 14 + 3 - 12 + (HD == 128 ? 24 : 0);

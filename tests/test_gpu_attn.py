@@ -82,6 +82,34 @@ def test_paged_attention_rmap_and_empty_rows(dev):
         assert np.array_equal(num.cpu().numpy(), ref[0]) and np.array_equal(den.cpu().numpy(), ref[1]), ns
 
 
+@pytest.mark.parametrize("HD,bs,nblk,M", [(64, 16, 128, 4), (128, 4, 300, 3), (64, 1, 700, 1), (128, 16, 9, 2)])
+def test_paged_attention_one_block_per_tile(dev, HD, bs, nblk, M):
+    """The unsplit launch for rows of at most 2048 keys (block-table row copied to LDS, scores kept in LDS, K and V
+    streamed once through a register ring): cache blocks of 16, 4 and 1 keys, the full 2048-key reach, queries
+    past nvalid, a query with no visible key; against the oracle."""
+    from bitexact.vllm_plugin import tri_exact_attn, tri_paged
+    g = torch.Generator().manual_seed(HD + bs + nblk)
+    HKV, Rr = 2, 3
+    nb = Rr * nblk + 1
+    c = torch.randint(-R.LIM3, R.LIM3 + 1, (nb, HKV, bs, 2 * HD), generator=g).to(torch.int32)
+    cl = tri_paged.to_limbs(c.to(dev))
+    bt = (1 + torch.randperm(Rr * nblk, generator=g)).to(torch.int32).reshape(Rr, nblk)
+    S = nblk * bs
+    qpos = torch.randint(0, S, (Rr, M), generator=g)
+    qpos[0, 0] = S - 1
+    if M > 1:
+        qpos[1, 1] = -1
+    q = torch.randint(-(1 << 22), (1 << 22) + 1, (Rr, HKV, M, HD), generator=g).to(torch.int32)
+    sh = torch.randint(-40, -10, (Rr, HKV, M), generator=g)
+    rmap = torch.tensor([2, 0, 1])
+    l2e = R.L2E28_HD[HD]
+    ref = R.paged_attend(q.numpy(), sh.numpy(), qpos.numpy(), c.numpy(), bt.numpy(), rmap.numpy(), R.exp2_table(),
+                         l2e)
+    num, den = tri_exact_attn.attend(q.to(dev), sh.to(dev), qpos.to(dev), cl, bt.to(dev), rmap.to(dev), _lut(dev),
+                                     l2e, nsplit=1)
+    assert np.array_equal(num.cpu().numpy(), ref[0]) and np.array_equal(den.cpu().numpy(), ref[1])
+
+
 @pytest.mark.parametrize("ticks,ns", [(None, 8), ("0", 8), (None, 4), ("0", 4)])
 def test_paged_attention_split_exchange(dev, monkeypatch, ticks, ns):
     """Config 4's decode shape (4 rows x 8 KV heads, 2048 keys, group 4) over 8 or 4 key splits in one launch, where the
