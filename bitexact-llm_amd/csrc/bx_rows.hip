@@ -50,7 +50,22 @@ __device__ __forceinline__ int64_t isqrt64(int64_t x) {
 // 1 / (double) r (every quotient digit is estimated by a multiplication and corrected to the exact floor; a
 // caller dividing many values by one r forms rinv once). Digit steps with nothing left to shift (c = 0) add
 // floor(R / r) = 0 and are skipped.
+//
+// Short form: for 0 <= p <= 62, r < 2^34 and |a 2^p / r| < 2^51 the long division never wraps, so its value is
+// round-half-up of the exact quotient. The float64 estimate qd (three roundings of relative size 2^-53) is then
+// within 1 of floor(a 2^p / r); the remainder a 2^p - q r of that estimate is below 2 r < 2^63 in magnitude, so
+// it is exact in wrapping 64-bit arithmetic, and one correction step brings q to the floor.
 __device__ __forceinline__ int64_t div_round64(int64_t a, int64_t p, int64_t r, double rinv) {
+  if (p >= 0 && p <= 62 && r < (1LL << 34)) {
+    const double qd = (double)a * ldexp(1.0, (int)p) * rinv;
+    if (qd < 2251799813685248.0 && qd > -2251799813685248.0) {
+      int64_t q = (int64_t)floor(qd);
+      int64_t rem = (int64_t)(((uint64_t)a << p) - (uint64_t)q * (uint64_t)r);
+      if (rem < 0) { --q; rem += r; }
+      if (rem >= r) { ++q; rem -= r; }
+      return q + (2 * rem >= r ? 1 : 0);
+    }
+  }
   int64_t Q = fdiv_rcp(a, r, rinv);
   int64_t R = a - Q * r;
   int64_t left = imax(p, 0);

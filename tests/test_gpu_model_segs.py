@@ -42,6 +42,31 @@ def test_add_norm(dev, M, D):
     assert bool(ops.add_norm_y(big.to(dev), torch.zeros(M, D, dtype=torch.long, device=dev), None, None)[3])
 
 
+@pytest.mark.parametrize("M,D", [(1, 512), (7, 2048), (32, 2048), (129, 2048), (20, 4096)])
+def test_add_norm_rows_planes(dev, M, D):
+    """add + norm with limb planes, then norm_quant of the new x: q, sh, planes, the new x and the flag, two calls
+    in a row, the second with a row over the bound."""
+    from bitexact.exact import ops
+    g = torch.Generator().manual_seed(M + D)
+    gm, ge = _gamma(g, D)
+    for call in range(2):
+        x = torch.randint(-(1 << 33), 1 << 33, (M, D), generator=g)
+        y = torch.randint(-(1 << 32), 1 << 32, (M, D), generator=g)
+        x[0] >>= 20 + call
+        if call == 1:
+            x[-1, 5] = 1 << 41
+        xs, q, sh, flag = R.add_norm_y(y.numpy(), x.numpy(), gm.numpy(), ge.numpy())
+        xd = x.to(dev)
+        xo, (qd, pl), shd, err = ops.add_norm_y(y.to(dev), xd, gm.to(dev), ge.to(dev), planes=True)
+        assert np.array_equal(xo.cpu().numpy(), xs), call
+        assert np.array_equal(qd.cpu().numpy(), q) and np.array_equal(shd.cpu().numpy(), sh), call
+        assert np.array_equal(pl.cpu().numpy(), np.stack([lo.astype(np.int8) for lo in R.split_limbs(q, 3)[0]])), call
+        assert bool(err) == flag == (call == 1)
+        q2, sh2, _ = ops.norm_quant(xd, gm.to(dev), ge.to(dev))
+        rq, rsh, _ = R.norm_quant(xs, gm.numpy(), ge.numpy())
+        assert np.array_equal(q2.cpu().numpy(), rq) and np.array_equal(sh2.cpu().numpy(), rsh), call
+
+
 def test_add_norm_golden(dev):
     """norm_quant of the reference's golden rows, reached as 0 + x."""
     from bitexact.exact import ops
