@@ -42,7 +42,8 @@ SIGNATURES = {
                                            I32, I32, I32, P, I64, P]),
     "bx_attn_paged_workspace": (I64, [I32, I32, I32, I32]),
     "bx_exact_attn_prefill": (ctypes.c_int, [P, I64, I64, P, I64, P, I64, I64, P, I64, I64, P, I64, I64, I32, P, I64,
-                                             P, P, I32, I32, I32, P]),
+                                             P, P, I32, I32, I32, P, I64, P]),
+    "bx_attn_prefill_scratch": (I64, [I32, I32, I32]),
     "bx_kv_store": (ctypes.c_int, [P, I64, I64, I64, I32, P, P, I64, I64, P, I64, I64, I32, I32, I32, I32, P]),
     "bx_limb_bmm": (ctypes.c_int, [P, I32, I64, I64, I64, P, I32, I64, I64, I64, P, I64, I64, I64, I32, I32, I32, I32,
                                    I32, I32, P]),

@@ -19,14 +19,14 @@ def _aligned_rows(t):
     return t if ok else t.contiguous()
 
 
-def _prefill_fake(qg, shg, K, V, qpos, lut, l2e):
+def _prefill_fake(qg, shg, K, V, qpos, lut, l2e, planes):
     Z, gT, HD = qg.shape
     return empty((Z, gT, HD), torch.long, qg), empty((Z, gT, 1), torch.long, qg)
 
 
-@op("attn_prefill(Tensor qg, Tensor shg, Tensor K, Tensor V, Tensor qpos, Tensor lut, int l2e) -> (Tensor, Tensor)",
-    _prefill_fake)
-def _prefill(qg, shg, K, V, qpos, lut, l2e):
+@op("attn_prefill(Tensor qg, Tensor shg, Tensor K, Tensor V, Tensor qpos, Tensor lut, int l2e, bool planes) -> "
+    "(Tensor, Tensor)", _prefill_fake)
+def _prefill(qg, shg, K, V, qpos, lut, l2e, planes):
     _hip.require_cuda(qg, shg, K, V, qpos, lut)
     Z, gT, HD = qg.shape
     S = K.shape[1]
@@ -39,11 +39,16 @@ def _prefill(qg, shg, K, V, qpos, lut, l2e):
     lut = lut.contiguous().long()
     num = torch.empty(Z, gT, HD, dtype=torch.long, device=qg.device)
     den = torch.empty(Z, gT, 1, dtype=torch.long, device=qg.device)
+    need = _hip.lib().bx_attn_prefill_scratch(Z, S, HD) if planes else 0
+    tmp, tmpb = _hip.scratch(qg.device, need) if need > 0 else (None, 0)
     _hip.call("bx_exact_attn_prefill", _hip.ptr(qg), qg.stride(0), qg.stride(1), _hip.ptr(shg), gT, _hip.ptr(qpos),
               qpos.stride(0), qpos.stride(1), _hip.ptr(K), K.stride(0), K.stride(1), _hip.ptr(V), V.stride(0),
-              V.stride(1), S, _hip.ptr(lut), int(l2e), _hip.ptr(num), _hip.ptr(den), Z, gT, HD, _hip.stream_of(qg))
+              V.stride(1), S, _hip.ptr(lut), int(l2e), _hip.ptr(num), _hip.ptr(den), Z, gT, HD, _hip.ptr(tmp), tmpb,
+              _hip.stream_of(qg))
     return num, den
 
 
-def prefill(qg, shg, K, V, qpos, lut, l2e):
-    return _prefill(qg, shg, K, V, qpos, lut, int(l2e))
+def prefill(qg, shg, K, V, qpos, lut, l2e, planes=True):
+    """planes=True: K / V split into int8 limb planes once (scratch) and streamed into LDS by the main kernel;
+    False: the register-staged kernel (no scratch). Same integers."""
+    return _prefill(qg, shg, K, V, qpos, lut, int(l2e), bool(planes))

@@ -1401,6 +1401,289 @@ __global__ __launch_bounds__(256, HD == 64 ? 2 : 1) void attn_pre_kernel(AttnArg
   }
 }
 
+// ---- fused prefill attention, limb-plane form (contiguous int32 K / V, with a scratch buffer) ----
+// pre_split_kernel writes K and V once as int8 limb planes, padded with zeros to Sp (a multiple of 64 keys):
+// Kp [Z][3][Sp][HD] (key rows: the QK A operand) and Vp [Z][3][HD][Sp] (dim rows: the PV B operand), the keys of
+// every 64-key tile of Vp in MFMA k order: position 16 c + 4 kb + e holds key 16 kb + 4 c + e. That is the order in
+// which the transposed QK product leaves the weights in the lanes (below), so the weights go from registers
+// straight into the PV A operand.
+__device__ __forceinline__ int pre_vpos(int key) {   // tile key -> its Vp position
+  return ((key >> 2) & 3) * 16 + ((key >> 4) & 3) * 4 + (key & 3);
+}
+
+__global__ __launch_bounds__(256) void pre_split_kernel(AttnArgs p, int8_t* kp, int8_t* vp, int Z, int Sp, int HD) {
+  const int CR = HD / 16;
+  const int64_t nk = (int64_t)Z * Sp * CR;          // K units: (z, key, 16-dim chunk)
+  const int64_t nv = (int64_t)Z * (Sp / 4) * (HD / 4);   // V units: (z, 4 keys, 4 dims)
+  for (int64_t u = blockIdx.x * 256LL + threadIdx.x; u < nk + nv; u += (int64_t)gridDim.x * 256) {
+    if (u < nk) {
+      const int c = (int)(u % CR), s = (int)((u / CR) % Sp), z = (int)(u / ((int64_t)CR * Sp));
+      uint32_t l[3][4];
+#pragma unroll
+      for (int e4 = 0; e4 < 4; ++e4) {
+        const v4i v = s < p.S ? *(const v4i*)(p.K + (int64_t)z * p.sk_z + (int64_t)s * p.sk_s + c * 16 + e4 * 4)
+                              : v4i{0, 0, 0, 0};
+        split3(v, l[0][e4], l[1][e4], l[2][e4]);
+      }
+#pragma unroll
+      for (int j = 0; j < 3; ++j)
+        *(v4i*)(kp + (((int64_t)z * 3 + j) * Sp + s) * HD + c * 16) =
+            v4i{(int)l[j][0], (int)l[j][1], (int)l[j][2], (int)l[j][3]};
+    } else {
+      const int64_t w = u - nk;
+      const int d4 = (int)(w % (HD / 4)), s4 = (int)((w / (HD / 4)) % (Sp / 4)), z = (int)(w / ((int64_t)(HD / 4) * (Sp / 4)));
+      uint32_t l[4][3];   // [key m][plane j]: the 4 dims' limbs
+#pragma unroll
+      for (int m = 0; m < 4; ++m) {
+        const int s = s4 * 4 + m;
+        const v4i v = s < p.S ? *(const v4i*)(p.V + (int64_t)z * p.sv_z + (int64_t)s * p.sv_s + d4 * 4) : v4i{0, 0, 0, 0};
+        split3(v, l[m][0], l[m][1], l[m][2]);
+      }
+      const int key0 = (s4 * 4) & 63, tile0 = (s4 * 4) & ~63;
+      const int pos = tile0 + pre_vpos(key0);      // the 4 keys stay consecutive
+#pragma unroll
+      for (int j = 0; j < 3; ++j)
+#pragma unroll
+        for (int d = 0; d < 4; ++d) {
+          const uint32_t word = ((l[0][j] >> (8 * d)) & 255) | (((l[1][j] >> (8 * d)) & 255) << 8) |
+                                (((l[2][j] >> (8 * d)) & 255) << 16) | (((l[3][j] >> (8 * d)) & 255) << 24);
+          *(uint32_t*)(vp + (((int64_t)z * 3 + j) * HD + d4 * 4 + d) * Sp + pos) = word;
+        }
+    }
+  }
+}
+
+// attn_pre2_kernel: a block (8 waves at head_dim 64, 4 at 128) owns 16 rows per wave of consecutive query rows of
+// one group z, wave w rows 16 w .. 16 w + 15.
+// The 64-key tiles of the limb planes stream through an NS-stage LDS ring filled by buffer_load ... lds (1 KiB
+// per wave instruction; 16-byte chunks XOR-swizzled by row so the 16 rows an MFMA operand read touches fall in
+// distinct bank groups). QK is computed transposed: A = K limb plane j (16 keys x 64 dims), B = limb i of the
+// wave's 16 queries (registers), so lane l receives query l & 15's scores for keys 16 kb + 4 (l >> 4) + e; the
+// nine limb products accumulate by weight i + j in five int32 sets, joined in int64. Sweep 1 keeps the per-query
+// maxima. Sweep 2 forms the weights in the same lanes; their three limbs, packed in key order 4 kb + e, are the
+// PV A operand as they stand (16 queries x 64 keys in Vp's order), and B = V limb plane j (64 keys x 16 dims):
+// five int32 sets per 16-dim block (exact while S 3 2^14 < 2^31), joined in int64 at the end. The table loads of
+// a tile's 16 weights go out together, before the tile's next ring stage is requested.
+template <int HD>
+struct Pre2 {
+  static constexpr int KK = HD / 64, CR = HD / 16, DB = HD / 16;
+  static constexpr int NS = HD == 64 ? 3 : 2;        // ring stages
+  static constexpr int PB = 3 * 64 * HD;             // one operand's three planes of a tile (bytes)
+  static constexpr int STAGE = 2 * PB;               // K then V
+  static constexpr int KI = PB / 1024;               // 1 KiB instructions per operand
+  static constexpr int NW = HD == 64 ? 8 : 4;        // waves (16 query rows each): 2 per SIMD at HD 64, 1 at 128
+  static constexpr int LPK = (KI + NW - 1) / NW;     // sweep 1 (K only): instructions per issuing wave
+  static constexpr int LPT = 2 * KI / NW;            // sweep 2: instructions per wave
+  static constexpr size_t LDS = (size_t)NS * STAGE;
+};
+
+__device__ __forceinline__ int pre_swzk(int k, int HD) { return HD == 64 ? (k >> 2) & 3 : (k >> 1) & 7; }
+__device__ __forceinline__ int pre_swzv(int d) { return (d >> 2) & 3; }
+
+template <int HD>
+__global__ __launch_bounds__(64 * Pre2<HD>::NW, 1) void attn_pre2_kernel(AttnArgs p, const int8_t* planes, int Z,
+                                                                         int Sp) {
+  using C = Pre2<HD>;
+  constexpr int QR = 16 * C::NW;                     // query rows per block
+  constexpr int KK = C::KK, DB = C::DB, NS = C::NS;
+  extern __shared__ __align__(16) char smem[];
+  __shared__ int s_kend;
+  const int tiles = (p.nq + QR - 1) / QR;
+  const int z = blockIdx.x % Z, q0 = (tiles - 1 - blockIdx.x / Z) * QR;    // late (long) row tiles first
+  const int lane = threadIdx.x & 63, w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int kl = lane & 15, c = lane >> 4;
+  const auto rs = __builtin_amdgcn_make_buffer_rsrc(const_cast<int8_t*>(planes), (short)0, kBufRange, 0x00020000);
+  const int64_t vbase = (int64_t)Z * 3 * Sp * HD;
+
+  // the lane's query (B operand rows) and its position / exponent
+  const int qr = q0 + 16 * w + kl;
+  v4i qb[3][KK];
+  {
+    const int32_t* qp = p.q + (int64_t)z * p.sq_tile + (int64_t)min(qr, p.nq - 1) * p.sq_row;
+#pragma unroll
+    for (int kk = 0; kk < KK; ++kk) {
+      uint32_t l[3][4];
+#pragma unroll
+      for (int e4 = 0; e4 < 4; ++e4) split3(*(const v4i*)(qp + kk * 64 + c * 16 + e4 * 4), l[0][e4], l[1][e4], l[2][e4]);
+#pragma unroll
+      for (int i = 0; i < 3; ++i) qb[i][kk] = v4i{(int)l[i][0], (int)l[i][1], (int)l[i][2], (int)l[i][3]};
+    }
+  }
+  const bool live = qr < p.nq;
+  const int64_t my_qpos = live ? p.qpos[(z / p.qpos_div) * p.qpos_tile + (int64_t)qr * p.qpos_row] : -1;
+  const int64_t shift = live ? (int64_t)(kFK + 3 - kFZ) - p.sh[z * p.sh_tile + qr] : 0;
+  if (threadIdx.x == 0) s_kend = 0;
+  __syncthreads();
+  {
+    int64_t ke = wave_max64(my_qpos + 1);
+    if (lane == 0) atomicMax(&s_kend, (int)ke);
+  }
+  __syncthreads();
+  const int kend = min(s_kend, p.S);                 // keys [0, kend) are visible to some row of the block
+  const int ntile = (kend + 63) / 64;
+
+  // DMA offsets of the wave's instructions (tile 0) and their per-tile step
+  auto dma_off = [&](int n, int& off, int& step) {
+    if (n < C::KI) {
+      const int j = n / (C::KI / 3), o = (n % (C::KI / 3)) * 1024 + lane * 16;
+      const int k = o / HD, cc = ((o % HD) / 16) ^ pre_swzk(k, HD);
+      off = (int)((((int64_t)z * 3 + j) * Sp + k) * HD + cc * 16);
+      step = 64 * HD;
+    } else {
+      const int m = n - C::KI;
+      const int j = m / (C::KI / 3), o = (m % (C::KI / 3)) * 1024 + lane * 16;
+      const int d = o / 64, cc = ((o % 64) / 16) ^ pre_swzv(d);
+      off = (int)(vbase + (((int64_t)z * 3 + j) * HD + d) * Sp + cc * 16);
+      step = 64;
+    }
+  };
+  int off1[C::LPK], stp1[C::LPK], off2[C::LPT], stp2[C::LPT];
+#pragma unroll
+  for (int i = 0; i < C::LPK; ++i) dma_off(min(w * C::LPK + i, C::KI - 1), off1[i], stp1[i]);
+#pragma unroll
+  for (int i = 0; i < C::LPT; ++i) dma_off(w * C::LPT + i, off2[i], stp2[i]);
+  const bool k_issuer = w * C::LPK < C::KI;          // sweep 1: the waves that load K
+  auto issue1 = [&](int t) {
+    char* base = smem + (t % NS) * C::STAGE;
+#pragma unroll
+    for (int i = 0; i < C::LPK; ++i)
+      if (w * C::LPK + i < C::KI) buf_lds16(rs, base + (w * C::LPK + i) * 1024, off1[i] + t * stp1[i], 0);
+  };
+  auto issue2 = [&](int t) {
+    char* base = smem + (t % NS) * C::STAGE;
+#pragma unroll
+    for (int i = 0; i < C::LPT; ++i) buf_lds16(rs, base + (w * C::LPT + i) * 1024, off2[i] + t * stp2[i], 0);
+  };
+  // scores of 16-key block kb of the staged tile for the lane's query: keys 16 kb + 4 c + e
+  auto qk = [&](const int8_t* kbase, int kb, int64_t (&raw)[4]) {
+    v4i acc[5];
+#pragma unroll
+    for (int u = 0; u < 5; ++u) acc[u] = v4i{0, 0, 0, 0};
+    const int k = kb * 16 + kl;
+#pragma unroll
+    for (int kk = 0; kk < KK; ++kk)
+#pragma unroll
+      for (int j = 0; j < 3; ++j) {
+        const v4i a = *(const v4i*)(kbase + j * 64 * HD + k * HD + (((kk * 4 + c) ^ pre_swzk(k, HD)) * 16));
+#pragma unroll
+        for (int i = 0; i < 3; ++i) acc[i + j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a, qb[i][kk], acc[i + j], 0, 0, 0);
+      }
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      int64_t r = 0;
+#pragma unroll
+      for (int u = 0; u < 5; ++u) r += (int64_t)acc[u][e] << (8 * u);
+      raw[e] = r;
+    }
+  };
+
+  // ---- sweep 1: the lane's query maximum over its keys ----
+  int64_t mx = kNeg;
+#pragma unroll
+  for (int t = 0; t < NS - 1; ++t)
+    if (t < ntile) issue1(t);
+  for (int t = 0; t < ntile; ++t) {
+    if (k_issuer && t + NS - 2 < ntile)
+      ring_barrier<C::LPK * (NS - 2)>();
+    else
+      ring_barrier<0>();
+    if (t + NS - 1 < ntile) issue1(t + NS - 1);
+    const int8_t* kbase = (const int8_t*)smem + (t % NS) * C::STAGE;
+#pragma unroll
+    for (int kb = 0; kb < 4; ++kb) {
+      int64_t raw[4];
+      qk(kbase, kb, raw);
+#pragma unroll
+      for (int e = 0; e < 4; ++e)
+        if (t * 64 + kb * 16 + 4 * c + e <= my_qpos) mx = imax(mx, raw[e]);
+    }
+  }
+  mx = imax(mx, __shfl_xor(mx, 16, 64));
+  mx = imax(mx, __shfl_xor(mx, 32, 64));
+  ring_barrier<0>();                                 // every wave is done with the ring
+
+  // ---- sweep 2: weights, den, p V ----
+  int64_t den = 0;
+  v4i pacc[DB][5];
+#pragma unroll
+  for (int d = 0; d < DB; ++d)
+#pragma unroll
+    for (int u = 0; u < 5; ++u) pacc[d][u] = v4i{0, 0, 0, 0};
+#pragma unroll
+  for (int t = 0; t < NS - 1; ++t)
+    if (t < ntile) issue2(t);
+  for (int t = 0; t < ntile; ++t) {
+    if (t + NS - 2 < ntile)
+      ring_barrier<C::LPT * (NS - 2)>();
+    else
+      ring_barrier<0>();
+    const int8_t* kbase = (const int8_t*)smem + (t % NS) * C::STAGE;
+    const int8_t* vbs = kbase + C::PB;
+    int64_t raw[4][4];
+#pragma unroll
+    for (int kb = 0; kb < 4; ++kb) qk(kbase, kb, raw[kb]);
+    WeightAt wa[4][4];
+    int64_t ta[4][4], tb[4][4];
+#pragma unroll
+    for (int kb = 0; kb < 4; ++kb)
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        wa[kb][e] = weight_at(mx - raw[kb][e], shift, p.l2e);
+        ta[kb][e] = p.lut[wa[kb][e].idx];
+        tb[kb][e] = p.lut[wa[kb][e].idx + 1];
+      }
+    if (t + NS - 1 < ntile) issue2(t + NS - 1);      // after the table loads: waiting for them leaves it in flight
+    v4i pa[3] = {v4i{0, 0, 0, 0}, v4i{0, 0, 0, 0}, v4i{0, 0, 0, 0}};
+#pragma unroll
+    for (int kb = 0; kb < 4; ++kb) {
+      uint32_t wd[3] = {0, 0, 0};
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        int64_t pw = weight_of(wa[kb][e], ta[kb][e], tb[kb][e]);
+        if (t * 64 + kb * 16 + 4 * c + e > my_qpos) pw = 0;
+        den += pw;
+        int32_t x = (int32_t)pw;                     // 0 <= p <= 2^22: three limbs
+        const int32_t a0 = limb_lo(x);
+        x = (x - a0) >> 8;
+        const int32_t a1 = limb_lo(x);
+        x = (x - a1) >> 8;
+        wd[0] |= (uint32_t)(a0 & 255) << (8 * e);
+        wd[1] |= (uint32_t)(a1 & 255) << (8 * e);
+        wd[2] |= (uint32_t)(limb_lo(x) & 255) << (8 * e);
+      }
+#pragma unroll
+      for (int i = 0; i < 3; ++i) pa[i][kb] = (int)wd[i];
+    }
+#pragma unroll
+    for (int d = 0; d < DB; ++d) {
+      const int row = d * 16 + kl;
+#pragma unroll
+      for (int j = 0; j < 3; ++j) {
+        const v4i b = *(const v4i*)(vbs + j * HD * 64 + row * 64 + ((c ^ pre_swzv(row)) * 16));
+#pragma unroll
+        for (int i = 0; i < 3; ++i) pacc[d][i + j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(pa[i], b, pacc[d][i + j], 0, 0, 0);
+      }
+    }
+  }
+  den += __shfl_xor(den, 16, 64);
+  den += __shfl_xor(den, 32, 64);
+  // outputs: lane holds queries 4 c + e of the wave, dims 16 d + kl
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    const int qw = 4 * c + e, r = q0 + 16 * w + qw;
+    const int64_t dq = __shfl(den, qw, 64);
+    if (r >= p.nq) continue;
+#pragma unroll
+    for (int d = 0; d < DB; ++d) {
+      int64_t v = 0;
+#pragma unroll
+      for (int u = 0; u < 5; ++u) v += (int64_t)pacc[d][u][e] << (8 * u);
+      p.num[z * p.snum_tile + (int64_t)r * p.snum_row + d * 16 + kl] = v;
+    }
+    if (kl == 0) p.den[z * p.sden_tile + r] = dq;
+  }
+}
+
 // ---- KV store into the limb-plane cache (tri_paged.store, src/bitexact/vllm_plugin/tri_paged.py:311-335) ----
 template <typename T>
 __global__ __launch_bounds__(128) void kv_store_kernel(int8_t* cache, int64_t sc_nb, int64_t sc_h, int64_t sc_bs,
@@ -1574,11 +1857,21 @@ extern "C" int bx_int8_attn_paged(const int64_t* q, const int64_t* qpos, int64_t
                   : launch_dec<128>(p, R * HKV, max_keys, (hipStream_t)stream);
 }
 
+// the limb-plane form's scratch: K and V planes, 3 Z Sp HD bytes each (Sp = S rounded up to 64 keys)
+static int64_t pre2_scratch(int64_t Z, int64_t S, int64_t HD) { return 2 * 3 * Z * ((S + 63) / 64 * 64) * HD; }
+
+extern "C" int64_t bx_attn_prefill_scratch(int32_t Z, int32_t S, int32_t HD) {
+  if (Z <= 0 || S <= 0 || (HD != 64 && HD != 128)) return 0;
+  const int64_t b = pre2_scratch(Z, S, HD);
+  return b < kBufRange - 16 ? b : 0;                 // larger: the register-staged form (no scratch)
+}
+
 extern "C" int bx_exact_attn_prefill(const int32_t* qg, int64_t sq_z, int64_t sq_row, const int64_t* shg,
                                      int64_t ssh_z, const int64_t* qpos, int64_t sqpos_z, int64_t sqpos_row,
                                      const int32_t* K, int64_t sk_z, int64_t sk_s, const int32_t* V, int64_t sv_z,
                                      int64_t sv_s, int32_t S, const int64_t* lut, int64_t l2e, int64_t* num,
-                                     int64_t* den, int32_t Z, int32_t gT, int32_t HD, bx_stream_t stream) {
+                                     int64_t* den, int32_t Z, int32_t gT, int32_t HD, void* tmp, int64_t tmp_bytes,
+                                     bx_stream_t stream) {
   BX_REQUIRE(Z >= 0 && gT >= 0 && S >= 0, "negative size");
   BX_REQUIRE(HD == 64 || HD == 128, "head_dim must be 64 or 128");
   BX_REQUIRE(S < 43690, "keys must stay below 43690");
@@ -1597,8 +1890,28 @@ extern "C" int bx_exact_attn_prefill(const int32_t* qg, int64_t sq_z, int64_t sq
   p.num = num; p.den = den; p.snum_tile = (int64_t)gT * HD; p.snum_row = HD; p.sden_tile = gT;
   p.nsplit = 1;
   // keys visible to a query never exceed the cache length S: qpos beyond S - 1 is the caller's contract
-  const int tiles = (gT + 63) / 64;
   hipStream_t st = (hipStream_t)stream;
+  if (tmp != nullptr && S > 0) {
+    const int64_t need = pre2_scratch(Z, S, HD);
+    BX_REQUIRE(need < kBufRange - 16, "limb planes above 2 GiB: call without scratch");
+    BX_REQUIRE(tmp_bytes >= need && ((uintptr_t)tmp & 15) == 0, "scratch too small (%lld < %lld) or not 16-byte aligned",
+               (long long)tmp_bytes, (long long)need);
+    const int Sp = (S + 63) / 64 * 64;
+    int8_t* pl = (int8_t*)tmp;
+    const int64_t units = (int64_t)Z * Sp * (HD / 16) + (int64_t)Z * (Sp / 4) * (HD / 4);
+    pre_split_kernel<<<(int)std::min<int64_t>((units + 255) / 256, 8192), 256, 0, st>>>(p, pl, pl + (int64_t)Z * 3 * Sp * HD,
+                                                                                     Z, Sp, HD);
+    if (int rc = check_launch("pre_split_kernel")) return rc;
+    if (HD == 64) {
+      allow_lds_attn((const void*)attn_pre2_kernel<64>, Pre2<64>::LDS);
+      attn_pre2_kernel<64><<<Z * ((gT + 127) / 128), 512, Pre2<64>::LDS, st>>>(p, pl, Z, Sp);
+    } else {
+      allow_lds_attn((const void*)attn_pre2_kernel<128>, Pre2<128>::LDS);
+      attn_pre2_kernel<128><<<Z * ((gT + 63) / 64), 256, Pre2<128>::LDS, st>>>(p, pl, Z, Sp);
+    }
+    return check_launch("attn_pre2_kernel");
+  }
+  const int tiles = (gT + 63) / 64;
   if (HD == 64) {
     allow_lds_attn((const void*)attn_pre_kernel<64>, sizeof(PreSmem<64>));
     attn_pre_kernel<64><<<Z * tiles, 256, sizeof(PreSmem<64>), st>>>(p);

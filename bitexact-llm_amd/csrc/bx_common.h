@@ -160,6 +160,37 @@ __device__ __forceinline__ void split3(v4i v, uint32_t& l0, uint32_t& l1, uint32
   l2 = pack4(a2[0], a2[1], a2[2], a2[3]);
 }
 
+// Raw buffer loads (stride 0, byte range [0, kBufRange)): an offset at or past the range returns zero without
+// a memory access but still counts as an outstanding load, so a skipped step costs no traffic and the
+// compiler's wait counts stay the same on every path.
+constexpr int kBufRange = 0x7fffffff;
+constexpr int kBufSkip = 0x7fffffff;   // offset of a skipped load
+
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t buf_rsrc(const void* base) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, kBufRange, 0x00020000);
+}
+
+__device__ __forceinline__ v4i buf_load16(__amdgpu_buffer_rsrc_t r, int off) {
+  return __builtin_bit_cast(v4i, __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 0));
+}
+
+// Asynchronous 16-byte load per lane straight into LDS (buffer_load_dwordx4 ... lds): the wave's 64 lanes fill
+// 1 KiB at `lds` (M0 base), lane l at byte 16 l, from buffer offset voff + soff.
+__device__ __forceinline__ void buf_lds16(__amdgpu_buffer_rsrc_t r, void* lds, int voff, int soff) {
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (__attribute__((address_space(3))) void*)lds, 16, voff, soff, 0, 0);
+}
+
+// Ring-stage barrier: wait until at most n of this wave's vector memory operations (the asynchronous LDS
+// loads of later stages) are outstanding and all its LDS reads are done (gfx9 s_waitcnt encoding: vmcnt <= n,
+// lgkmcnt = 0), then a bare s_barrier. __syncthreads() would add a release fence, i.e. vmcnt(0), and drain
+// the whole ring every iteration; the memory clobber keeps the compiler from moving LDS accesses across.
+template <int n>
+__device__ __forceinline__ void ring_barrier() {
+  static_assert(n >= 0 && n < 64, "vmcnt range");
+  __builtin_amdgcn_s_waitcnt((n & 15) | ((n >> 4) << 14) | (7 << 4));
+  asm volatile("s_barrier" ::: "memory");
+}
+
 // ---- wavefront reductions (wave64) ----
 __device__ __forceinline__ int64_t wave_max64(int64_t v) {
 #pragma unroll

@@ -201,16 +201,6 @@ __device__ __forceinline__ void ws_add(const LinArgs& p, int m, int n, int64_t v
   atomicAdd((unsigned long long*)&p.ws[(int64_t)m * p.N + n], (unsigned long long)v);
 }
 
-// Ring-stage barrier: wait until at most n of this wave's vector memory operations (the asynchronous LDS
-// loads of later stages) are outstanding and all its LDS reads are done (gfx9 s_waitcnt encoding: vmcnt <= n,
-// lgkmcnt = 0), then a bare s_barrier. __syncthreads() would add a release fence, i.e. vmcnt(0), and drain
-// the whole ring every iteration; the memory clobber keeps the compiler from moving LDS accesses across.
-template <int n>
-__device__ __forceinline__ void ring_barrier() {
-  static_assert(n >= 0 && n < 64, "vmcnt range");
-  __builtin_amdgcn_s_waitcnt((n & 15) | ((n >> 4) << 14) | (7 << 4));
-  asm volatile("s_barrier" ::: "memory");
-}
 
 // =====================================================================================================
 // gemv kernel (decode)
@@ -223,19 +213,6 @@ __device__ __forceinline__ void ring_barrier() {
 // to RA, zero columns past kend.
 constexpr int kAB = 8;   // chunks per thread requested ahead of the weights
 
-// Raw buffer loads (stride 0, byte range [0, kBufRange)): an offset at or past the range returns zero without
-// a memory access but still counts as an outstanding load, so a skipped step costs no traffic and the
-// compiler's wait counts stay the same on every path.
-constexpr int kBufRange = 0x7fffffff;
-constexpr int kBufSkip = 0x7fffffff;   // offset of a skipped load
-
-__device__ __forceinline__ __amdgpu_buffer_rsrc_t buf_rsrc(const void* base) {
-  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, kBufRange, 0x00020000);
-}
-
-__device__ __forceinline__ v4i buf_load16(__amdgpu_buffer_rsrc_t r, int off) {
-  return __builtin_bit_cast(v4i, __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 0));
-}
 
 // floor(x / d) for 0 <= x < 2^21 from rcp ~ 1 / d (v_rcp_f32, relative error <= 2^-23): the quotient of
 // x + 1/2 is at least 1 / (2 d) away from an integer and its float error is below (x + 1/2) 2^-22 / d.
@@ -781,9 +758,6 @@ struct XtOps {
   v4i a[3][TM], b[3][TN];
 };
 
-__device__ __forceinline__ void buf_lds16(__amdgpu_buffer_rsrc_t r, void* lds, int voff, int soff) {
-  __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (__attribute__((address_space(3))) void*)lds, 16, voff, soff, 0, 0);
-}
 
 __device__ __forceinline__ void buf_lds4(__amdgpu_buffer_rsrc_t r, void* lds, int voff) {
   __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (__attribute__((address_space(3))) void*)lds, 4, voff, 0, 0, 0);

@@ -145,11 +145,17 @@ int bx_int8_attn_paged(const int64_t* q, const int64_t* qpos, int64_t sqpos_r, c
  * bmm(p, V)): qg int32 [Z, gT, HD] (strides sq_z, sq_row), shg int64 [Z, gT] (ssh_z = gT), qpos int64 [Z, gT]
  * (strides), K / V int32 [Z, S, HD] (strides; the integer Cache layout), outputs num int64 [Z, gT, HD],
  * den int64 [Z, gT]. The score matrix is never materialized. qg, K and V rows must be 16-byte aligned (base and
- * strides multiples of 4 elements); K / V values are taken as their three signed base-256 limbs. */
+ * strides multiples of 4 elements); K / V values are taken as their three signed base-256 limbs. tmp (16-byte
+ * aligned, at least bx_attn_prefill_scratch(Z, S, HD) bytes, no contents kept; null: the register-staged form, no
+ * scratch) receives K and V as int8 limb planes once per call, which the main kernel streams into LDS. */
 int bx_exact_attn_prefill(const int32_t* qg, int64_t sq_z, int64_t sq_row, const int64_t* shg, int64_t ssh_z,
                           const int64_t* qpos, int64_t sqpos_z, int64_t sqpos_row, const int32_t* K, int64_t sk_z,
                           int64_t sk_s, const int32_t* V, int64_t sv_z, int64_t sv_s, int32_t S, const int64_t* lut,
-                          int64_t l2e, int64_t* num, int64_t* den, int32_t Z, int32_t gT, int32_t HD, bx_stream_t stream);
+                          int64_t l2e, int64_t* num, int64_t* den, int32_t Z, int32_t gT, int32_t HD, void* tmp,
+                          int64_t tmp_bytes, bx_stream_t stream);
+/* Scratch bytes of bx_exact_attn_prefill's limb-plane form (0: not available for these sizes; pass null). No
+ * reference counterpart. */
+int64_t bx_attn_prefill_scratch(int32_t Z, int32_t S, int32_t HD);
 
 /* Replaces tri_paged.store (src/bitexact/vllm_plugin/tri_paged.py:311-335): K / V (int32 or int64 [N, HKV, HD] with
  * token / head strides) written as 3 int8 limb planes each at cache slots slot int64 [N]; slot < 0 is skipped.

@@ -148,7 +148,7 @@ def test_torch_ops_registered_with_meta_shapes():
     num, den = ops.attend_int8(m(2, 8, 4, 64), m(2, 4), m(9, 8, 16, 512, dt=i8), m(2, 4, dt=i32), m(4097, dt=i32), 1)
     assert num.shape == (2, 8, 4, 64)
     num, den = ops.attn_prefill(m(4, 12, 64, dt=i32), m(4, 12, 1), m(4, 3, 64, dt=i32), m(4, 3, 64, dt=i32),
-                                m(4, 12, 1), m(16385), 387270501)
+                                m(4, 12, 1), m(16385), 387270501, True)
     assert num.shape == (4, 12, 64)
     a, as_, sh, mant, e = ops.int8_quant_rows(m(5, 64), 2, True)
     assert a.shape == (10, 64) and mant.shape == (5,)

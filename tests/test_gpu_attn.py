@@ -141,7 +141,10 @@ def test_paged_attention_split_exchange(dev, monkeypatch, ticks, ns):
 
 
 @pytest.mark.parametrize("HD", [64, 128])
-def test_prefill_attention(dev, HD):
+@pytest.mark.parametrize("planes", [True, False])
+def test_prefill_attention(dev, HD, planes):
+    """Both prefill forms (limb planes streamed into LDS; register-staged) against the oracle's unfused
+    bmm -> softmax -> bmm, on a strided cache view with two sequence offsets."""
     from bitexact.exact.attention import prefill
     g = torch.Generator().manual_seed(3 + HD)
     B, HKV, grp, T, L = 2, 2, 4, 70, 96
@@ -159,8 +162,36 @@ def test_prefill_attention(dev, HD):
                                            R.exp2_table(), R.L2E28_HD[HD])
     kd = cache_k.to(dev)[:, :, :S].reshape(Z, S, HD)      # strided view of the cache (row stride L * HD)
     vd = cache_v.to(dev)[:, :, :S].reshape(Z, S, HD)
-    num, den = prefill(qg.to(dev), shg.to(dev), kd, vd, qpos.to(dev), _lut(dev), R.L2E28_HD[HD])
+    num, den = prefill(qg.to(dev), shg.to(dev), kd, vd, qpos.to(dev), _lut(dev), R.L2E28_HD[HD], planes=planes)
     assert np.array_equal(num.cpu().numpy(), ref_num) and np.array_equal(den.cpu().numpy(), ref_den)
+
+
+@pytest.mark.parametrize("HD,T,Z", [(64, 2048, 4), (128, 640, 2)])
+def test_prefill_attention_full_size(dev, HD, T, Z):
+    """Config 4's prefill shape (group 4, causal T = 2048) and a head_dim-128 case: the limb-plane form equals the
+    register-staged form on every row (two kernels with different tilings and operand orders), every row that
+    sees a key has den >= 2^22 (its own maximum's weight is 2^FP), and a sample of rows (first and last of each
+    head's block, the partial last tile) equals the oracle."""
+    from bitexact.exact.attention import prefill
+    g = torch.Generator().manual_seed(HD + T)
+    grp = 4
+    qg = torch.randint(-(1 << 22), (1 << 22) + 1, (Z, grp * T, HD), generator=g).to(torch.int32)
+    shg = torch.randint(-40, -25, (Z, grp * T, 1), generator=g)
+    K = torch.randint(-R.LIM3, R.LIM3 + 1, (Z, T, HD), generator=g).to(torch.int32)
+    V = torch.randint(-R.LIM3, R.LIM3 + 1, (Z, T, HD), generator=g).to(torch.int32)
+    qpos = torch.arange(T).repeat(grp).reshape(1, grp * T, 1).expand(Z, grp * T, 1).contiguous()
+    args = (qg.to(dev), shg.to(dev), K.to(dev), V.to(dev), qpos.to(dev), _lut(dev), R.L2E28_HD[HD])
+    n1, d1 = prefill(*args, planes=True)
+    n2, d2 = prefill(*args, planes=False)
+    assert torch.equal(n1, n2) and torch.equal(d1, d2)
+    assert bool((d1 >= 1 << 22).all())
+    rows = np.unique(np.concatenate([np.arange(0, 40), np.arange(T - 40, T + 40), np.arange(grp * T - 70, grp * T)]))
+    z = Z - 1
+    ref_num, ref_den = R.attention_prefill(qg[z:z + 1, rows].numpy(), shg[z:z + 1, rows].numpy(), K[z:z + 1].numpy(),
+                                           V[z:z + 1].numpy(), qpos[z:z + 1, rows].numpy(), R.exp2_table(),
+                                           R.L2E28_HD[HD])
+    assert np.array_equal(n1[z, rows].cpu().numpy(), ref_num[0]) and np.array_equal(d1[z, rows].cpu().numpy(),
+                                                                                     ref_den[0])
 
 
 def test_bmm_exact(dev):
