@@ -19,6 +19,7 @@
 #include "bx_common.h"
 
 #include <algorithm>
+#include <type_traits>
 
 namespace bx {
 
@@ -47,6 +48,23 @@ __device__ __forceinline__ WeightAt weight_at(int64_t z, int64_t zshift, int64_t
   w.n = t >> kFT2;
   w.idx = w.n < kZeroN ? (int)(f >> (kFT2 - kExp2Bits)) : 0;
   w.rr = f & ((1LL << (kFT2 - kExp2Bits)) - 1);
+  return w;
+}
+
+// weight_at for zshift >= 0, 0 <= l2e < 2^31 and 0 <= z < 2^62 (z = mx - raw of a visible key): zf = rshc(z, zshift)
+// is then >= 0 and at most 48 2^26 after the clamp, so zf l2e is one 32 x 32 -> 64-bit product below 3 2^61
+// and t, n, f come from 64-bit shifts of it; the same position as weight_at. Negative z (hidden keys, whose
+// weight is discarded) is clamped to 0, which keeps the position inside the table.
+__device__ __forceinline__ WeightAt weight_at_nn(int64_t z, int64_t zshift, int64_t l2e) {
+  int64_t zf = rshc(z, zshift);
+  zf = zf < 0 ? 0 : zf > (48LL << kFZ) ? (48LL << kFZ) : zf;
+  const uint64_t prod = (uint64_t)(uint32_t)zf * (uint64_t)(uint32_t)l2e;
+  const uint64_t t = (prod + (1ULL << (kFZ + 28 - kFT2 - 1))) >> (kFZ + 28 - kFT2);
+  const uint32_t f = (uint32_t)t & ((1u << kFT2) - 1);
+  WeightAt w;
+  w.n = (int64_t)(t >> kFT2);
+  w.idx = w.n < kZeroN ? (int)(f >> (kFT2 - kExp2Bits)) : 0;
+  w.rr = f & ((1u << (kFT2 - kExp2Bits)) - 1);
   return w;
 }
 
@@ -1510,7 +1528,9 @@ __global__ __launch_bounds__(64 * Pre2<HD>::NW, 1) void attn_pre2_kernel(AttnArg
     }
   }
   const bool live = qr < p.nq;
-  const int64_t my_qpos = live ? p.qpos[(z / p.qpos_div) * p.qpos_tile + (int64_t)qr * p.qpos_row] : -1;
+  // (positions past S - 1 see every key: the caller's contract keeps qpos < S, so the clamp changes nothing)
+  const int my_qpos =
+      live ? (int)imin(p.qpos[(z / p.qpos_div) * p.qpos_tile + (int64_t)qr * p.qpos_row], (int64_t)p.S) : -1;
   const int64_t shift = live ? (int64_t)(kFK + 3 - kFZ) - p.sh[z * p.sh_tile + qr] : 0;
   if (threadIdx.x == 0) s_kend = 0;
   __syncthreads();
@@ -1568,12 +1588,11 @@ __global__ __launch_bounds__(64 * Pre2<HD>::NW, 1) void attn_pre2_kernel(AttnArg
 #pragma unroll
         for (int i = 0; i < 3; ++i) acc[i + j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a, qb[i][kk], acc[i + j], 0, 0, 0);
       }
+    // |acc| <= 64 KK 2^14 = 2^(20 + KK - 1): the pairs acc0 + 2^8 acc1 and acc2 + 2^8 acc3 are exact in int32
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
-      int64_t r = 0;
-#pragma unroll
-      for (int u = 0; u < 5; ++u) r += (int64_t)acc[u][e] << (8 * u);
-      raw[e] = r;
+      const int32_t lo = acc[0][e] + (acc[1][e] << 8), mid = acc[2][e] + (acc[3][e] << 8);
+      raw[e] = (int64_t)lo + ((int64_t)mid << 16) + ((int64_t)acc[4][e] << 32);
     }
   };
 
@@ -1603,6 +1622,9 @@ __global__ __launch_bounds__(64 * Pre2<HD>::NW, 1) void attn_pre2_kernel(AttnArg
   ring_barrier<0>();                                 // every wave is done with the ring
 
   // ---- sweep 2: weights, den, p V ----
+  // (fast: no query of the wave has a negative exponent shift and l2e < 2^31, so no visible key's zf or zf l2e
+  // can wrap: weight_at_nn)
+  const bool fast = __builtin_amdgcn_ballot_w64(shift < 0) == 0 && p.l2e >= 0 && p.l2e < (1LL << 31);
   int64_t den = 0;
   v4i pacc[DB][5];
 #pragma unroll
@@ -1612,6 +1634,8 @@ __global__ __launch_bounds__(64 * Pre2<HD>::NW, 1) void attn_pre2_kernel(AttnArg
 #pragma unroll
   for (int t = 0; t < NS - 1; ++t)
     if (t < ntile) issue2(t);
+  auto sweep2 = [&](auto fast_t) {
+  constexpr bool kFast = decltype(fast_t)::value;
   for (int t = 0; t < ntile; ++t) {
     if (t + NS - 2 < ntile)
       ring_barrier<C::LPT * (NS - 2)>();
@@ -1622,13 +1646,18 @@ __global__ __launch_bounds__(64 * Pre2<HD>::NW, 1) void attn_pre2_kernel(AttnArg
     int64_t raw[4][4];
 #pragma unroll
     for (int kb = 0; kb < 4; ++kb) qk(kbase, kb, raw[kb]);
+    // every score's table position, then every table load, then the next stage's request
     WeightAt wa[4][4];
     int64_t ta[4][4], tb[4][4];
 #pragma unroll
     for (int kb = 0; kb < 4; ++kb)
 #pragma unroll
+      for (int e = 0; e < 4; ++e) wa[kb][e] = kFast ? weight_at_nn(mx - raw[kb][e], shift, p.l2e)
+                                                    : weight_at(mx - raw[kb][e], shift, p.l2e);
+#pragma unroll
+    for (int kb = 0; kb < 4; ++kb)
+#pragma unroll
       for (int e = 0; e < 4; ++e) {
-        wa[kb][e] = weight_at(mx - raw[kb][e], shift, p.l2e);
         ta[kb][e] = p.lut[wa[kb][e].idx];
         tb[kb][e] = p.lut[wa[kb][e].idx + 1];
       }
@@ -1639,17 +1668,15 @@ __global__ __launch_bounds__(64 * Pre2<HD>::NW, 1) void attn_pre2_kernel(AttnArg
       uint32_t wd[3] = {0, 0, 0};
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
-        int64_t pw = weight_of(wa[kb][e], ta[kb][e], tb[kb][e]);
-        if (t * 64 + kb * 16 + 4 * c + e > my_qpos) pw = 0;
-        den += pw;
-        int32_t x = (int32_t)pw;                     // 0 <= p <= 2^22: three limbs
-        const int32_t a0 = limb_lo(x);
-        x = (x - a0) >> 8;
-        const int32_t a1 = limb_lo(x);
-        x = (x - a1) >> 8;
-        wd[0] |= (uint32_t)(a0 & 255) << (8 * e);
-        wd[1] |= (uint32_t)(a1 & 255) << (8 * e);
-        wd[2] |= (uint32_t)(limb_lo(x) & 255) << (8 * e);
+        // 0 <= p <= 2^22: signed base-256 limbs; limb_lo(x) as a byte is x & 255 and (x - limb_lo(x)) >> 8 is
+        // (x + 128) >> 8
+        const int32_t x = t * 64 + kb * 16 + 4 * c + e <= my_qpos ? (int32_t)weight_of(wa[kb][e], ta[kb][e], tb[kb][e])
+                                                                   : 0;
+        den += x;
+        const int32_t x1 = (x + 128) >> 8, x2 = (x1 + 128) >> 8;
+        wd[0] |= (uint32_t)(x & 255) << (8 * e);
+        wd[1] |= (uint32_t)(x1 & 255) << (8 * e);
+        wd[2] |= (uint32_t)(x2 & 255) << (8 * e);
       }
 #pragma unroll
       for (int i = 0; i < 3; ++i) pa[i][kb] = (int)wd[i];
@@ -1665,6 +1692,11 @@ __global__ __launch_bounds__(64 * Pre2<HD>::NW, 1) void attn_pre2_kernel(AttnArg
       }
     }
   }
+  };
+  if (fast)
+    sweep2(std::true_type{});
+  else
+    sweep2(std::false_type{});
   den += __shfl_xor(den, 16, 64);
   den += __shfl_xor(den, 32, 64);
   // outputs: lane holds queries 4 c + e of the wave, dims 16 d + kl

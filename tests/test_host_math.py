@@ -35,3 +35,5 @@ def test_div_round_short_form_matches_long_division():
     assert taken.sum() > n // 4
     ref = R.div_round(a[taken], p[taken], r[taken])
     assert np.array_equal(got[taken], ref)
+
+
