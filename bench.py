@@ -38,8 +38,8 @@ sys.path.insert(0, os.path.join(HERE, "bitexact-llm_amd"))
 HBM_PEAK_GBS = 8000.0
 # HBM bytes per decode launch (average over the step's 6 GEMMs) from rocprofv3 --pmc FETCH_SIZE and WRITE_SIZE
 # runs of `bench.py --eager --no-prefill --no-attn --no-cpu --no-engine`, each scaled by what the same counter reads
-# for a plain 1 GiB device copy (profiles/decode_gemv_config2_hbm_traffic.txt).
-DECODE_TRAFFIC_PER_LAUNCH = 30040422
+# for a plain 1 GiB device copy (profiles/decode_gemm_config2_hbm_traffic.txt).
+DECODE_TRAFFIC_PER_LAUNCH = 30033462
 INT8_PEAK_TOPS = 5000.0
 # The reference's int8 MLP issues gate and up as one GEMM over wgu = cat(gate, up) [2 x 8192, 2048]
 # (src/bitexact/int8/consts.py:68, src/bitexact/int8/model.py:106), then down; the step follows that call pattern.
@@ -461,7 +461,7 @@ def main():
 
     def r(x, n):
         return None if x is None else round(x, n)
-    # roofline of the dominant kernel: every decode launch is one gemv_kernel; algorithmic bytes per launch
+    # roofline of the decode launches (each one kernel); algorithmic bytes per launch
     # over its average duration (graph replay timed with HIP events on the launch stream)
     per_launch_s = sec / args.steps / launches
     achieved = None if value is None else step_bytes / launches / per_launch_s / 1e9
@@ -475,7 +475,8 @@ def main():
                                   "output",
                       "gemms_per_step": launches, "bytes_per_step": step_bytes, "weight_rotation": ">=1 GiB/shape"},
            "roofline": {"bound": "hbm",
-                        "kernel": "decode GEMM launches (staged_kernel M=1, gemv_kernel, tile_kernel T_DEC M=64 gate|up)",
+                        "kernel": "decode GEMM launches (stream_kernel gate|up at M=1/8/64, staged_kernel M=1 down, "
+                                  "gemv_kernel M=8/64 down)",
                         "achieved": r(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                         "frac": r(None if achieved is None else achieved / HBM_PEAK_GBS, 4),
                         "traffic": DECODE_TRAFFIC_PER_LAUNCH, "algorithmic_bytes_per_launch": step_bytes // launches,
