@@ -1429,12 +1429,19 @@ __device__ __forceinline__ int pre_vpos(int key) {   // tile key -> its Vp posit
   return ((key >> 2) & 3) * 16 + ((key >> 4) & 3) * 4 + (key & 3);
 }
 
-__global__ __launch_bounds__(256) void pre_split_kernel(AttnArgs p, int8_t* kp, int8_t* vp, int Z, int Sp, int HD) {
+__global__ __launch_bounds__(256) void pre_split_kernel(AttnArgs p, int8_t* kp, int8_t* vp, int64_t* tab2, int Z, int Sp,
+                                                        int HD) {
   const int CR = HD / 16;
   const int64_t nk = (int64_t)Z * Sp * CR;          // K units: (z, key, 16-dim chunk)
   const int64_t nv = (int64_t)Z * (Sp / 4) * (HD / 4);   // V units: (z, 4 keys, 4 dims)
-  for (int64_t u = blockIdx.x * 256LL + threadIdx.x; u < nk + nv; u += (int64_t)gridDim.x * 256) {
-    if (u < nk) {
+  const int64_t nt = 1 << kExp2Bits;                 // table pairs: (lut[i], lut[i + 1] - lut[i])
+  for (int64_t u = blockIdx.x * 256LL + threadIdx.x; u < nk + nv + nt; u += (int64_t)gridDim.x * 256) {
+    if (u >= nk + nv) {
+      const int64_t i = u - nk - nv;
+      const int64_t a = p.lut[i];
+      tab2[2 * i] = a;
+      tab2[2 * i + 1] = p.lut[i + 1] - a;
+    } else if (u < nk) {
       const int c = (int)(u % CR), s = (int)((u / CR) % Sp), z = (int)(u / ((int64_t)CR * Sp));
       uint32_t l[3][4];
 #pragma unroll
@@ -1500,7 +1507,7 @@ __device__ __forceinline__ int pre_swzv(int d) { return (d >> 2) & 3; }
 
 template <int HD>
 __global__ __launch_bounds__(64 * Pre2<HD>::NW, 1) void attn_pre2_kernel(AttnArgs p, const int8_t* planes, int Z,
-                                                                         int Sp) {
+                                                                         int Sp, const char* tab2) {
   using C = Pre2<HD>;
   constexpr int QR = 16 * C::NW;                     // query rows per block
   constexpr int KK = C::KK, DB = C::DB, NS = C::NS;
@@ -1624,7 +1631,8 @@ __global__ __launch_bounds__(64 * Pre2<HD>::NW, 1) void attn_pre2_kernel(AttnArg
   // ---- sweep 2: weights, den, p V ----
   // (fast: no query of the wave has a negative exponent shift and l2e < 2^31, so no visible key's zf or zf l2e
   // can wrap: weight_at_nn)
-  const bool fast = __builtin_amdgcn_ballot_w64(shift < 0) == 0 && p.l2e >= 0 && p.l2e < (1LL << 31);
+  const bool fast = tab2 != nullptr && __builtin_amdgcn_ballot_w64(shift < 0) == 0 && p.l2e >= 0 &&
+                    p.l2e < (1LL << 31);
   int64_t den = 0;
   v4i pacc[DB][5];
 #pragma unroll
@@ -1634,35 +1642,76 @@ __global__ __launch_bounds__(64 * Pre2<HD>::NW, 1) void attn_pre2_kernel(AttnArg
 #pragma unroll
   for (int t = 0; t < NS - 1; ++t)
     if (t < ntile) issue2(t);
-  auto sweep2 = [&](auto fast_t) {
-  constexpr bool kFast = decltype(fast_t)::value;
-  for (int t = 0; t < ntile; ++t) {
-    if (t + NS - 2 < ntile)
-      ring_barrier<C::LPT * (NS - 2)>();
-    else
-      ring_barrier<0>();
+  // fast: zf = rshc(mx - raw, s) = (cz - raw) >> s with cz = mx + 2^(s - 1) (wrapping, as rshc's add), s clamped
+  // to 62 as rshc clamps it; the weight's interpolation reads the (entry, next - entry) pair table in one load
+  const int s62 = (int)imin(imax(shift, 0), 62);
+  const int64_t cz = add_wrap(mx, s62 > 0 ? (1LL << (s62 - 1)) : 0);
+  const int wmin_qpos = (int)-wave_max64(-(int64_t)my_qpos);      // the wave's smallest position
+  auto tile2 = [&](int t, auto fast_t, auto full_t) {
+    constexpr bool kFast = decltype(fast_t)::value, kFull = decltype(full_t)::value;   // kFull: every key visible
     const int8_t* kbase = (const int8_t*)smem + (t % NS) * C::STAGE;
     const int8_t* vbs = kbase + C::PB;
     int64_t raw[4][4];
 #pragma unroll
     for (int kb = 0; kb < 4; ++kb) qk(kbase, kb, raw[kb]);
     // every score's table position, then every table load, then the next stage's request
-    WeightAt wa[4][4];
-    int64_t ta[4][4], tb[4][4];
+    int32_t x[4][4];
+    if constexpr (kFast) {
+      int idx[4][4], n[4][4], rr[4][4];
 #pragma unroll
-    for (int kb = 0; kb < 4; ++kb)
+      for (int kb = 0; kb < 4; ++kb)
 #pragma unroll
-      for (int e = 0; e < 4; ++e) wa[kb][e] = kFast ? weight_at_nn(mx - raw[kb][e], shift, p.l2e)
-                                                    : weight_at(mx - raw[kb][e], shift, p.l2e);
+        for (int e = 0; e < 4; ++e) {
+          uint64_t zf = (uint64_t)((cz - raw[kb][e]) >> s62);
+          zf = zf < (48ULL << kFZ) ? zf : (48ULL << kFZ);     // hidden keys (negative) clamp too: inside the table
+          const uint64_t prod = (uint64_t)(uint32_t)zf * (uint64_t)(uint32_t)p.l2e + (1ULL << 27);
+          n[kb][e] = (int)(prod >> (28 + kFT2));
+          const uint32_t f = (uint32_t)(prod >> 28) & ((1u << kFT2) - 1);
+          idx[kb][e] = n[kb][e] < kZeroN ? (int)(f >> (kFT2 - kExp2Bits)) : 0;
+          rr[kb][e] = (int)(f & ((1u << (kFT2 - kExp2Bits)) - 1));
+        }
+      v4i tv[4][4];
 #pragma unroll
-    for (int kb = 0; kb < 4; ++kb)
+      for (int kb = 0; kb < 4; ++kb)
 #pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        ta[kb][e] = p.lut[wa[kb][e].idx];
-        tb[kb][e] = p.lut[wa[kb][e].idx + 1];
-      }
-    if (t + NS - 1 < ntile) issue2(t + NS - 1);      // after the table loads: waiting for them leaves it in flight
+        for (int e = 0; e < 4; ++e) tv[kb][e] = *(const v4i*)(tab2 + idx[kb][e] * 16);
+      if (t + NS - 1 < ntile) issue2(t + NS - 1);    // after the table loads: waiting for them leaves it in flight
+#pragma unroll
+      for (int kb = 0; kb < 4; ++kb)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const int64_t av = (int64_t)(((uint64_t)(uint32_t)tv[kb][e][1] << 32) | (uint32_t)tv[kb][e][0]);
+          const int64_t dv = (int64_t)(((uint64_t)(uint32_t)tv[kb][e][3] << 32) | (uint32_t)tv[kb][e][2]);
+          const int64_t v = av + ((dv * rr[kb][e] + (1LL << (kFT2 - kExp2Bits - 1))) >> (kFT2 - kExp2Bits));
+          // rshc(v, 38 + n) for 0 <= v < 2^61: ((v >> (s - 1)) + 1) >> 1 with s = min(38 + n, 62)
+          const int sh2 = min(kExp2One - kFP + n[kb][e], 62) - 1;
+          int32_t w = ((int32_t)(v >> sh2) + 1) >> 1;
+          if (!kFull && t * 64 + kb * 16 + 4 * c + e > my_qpos) w = 0;
+          x[kb][e] = w;
+        }
+    } else {
+      WeightAt wa[4][4];
+      int64_t ta[4][4], tb[4][4];
+#pragma unroll
+      for (int kb = 0; kb < 4; ++kb)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) wa[kb][e] = weight_at(mx - raw[kb][e], shift, p.l2e);
+#pragma unroll
+      for (int kb = 0; kb < 4; ++kb)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          ta[kb][e] = p.lut[wa[kb][e].idx];
+          tb[kb][e] = p.lut[wa[kb][e].idx + 1];
+        }
+      if (t + NS - 1 < ntile) issue2(t + NS - 1);
+#pragma unroll
+      for (int kb = 0; kb < 4; ++kb)
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+          x[kb][e] = t * 64 + kb * 16 + 4 * c + e <= my_qpos ? (int32_t)weight_of(wa[kb][e], ta[kb][e], tb[kb][e]) : 0;
+    }
     v4i pa[3] = {v4i{0, 0, 0, 0}, v4i{0, 0, 0, 0}, v4i{0, 0, 0, 0}};
+    int32_t dt = 0;                                   // the tile's weight sum: <= 64 2^22, exact in int32
 #pragma unroll
     for (int kb = 0; kb < 4; ++kb) {
       uint32_t wd[3] = {0, 0, 0};
@@ -1670,17 +1719,17 @@ __global__ __launch_bounds__(64 * Pre2<HD>::NW, 1) void attn_pre2_kernel(AttnArg
       for (int e = 0; e < 4; ++e) {
         // 0 <= p <= 2^22: signed base-256 limbs; limb_lo(x) as a byte is x & 255 and (x - limb_lo(x)) >> 8 is
         // (x + 128) >> 8
-        const int32_t x = t * 64 + kb * 16 + 4 * c + e <= my_qpos ? (int32_t)weight_of(wa[kb][e], ta[kb][e], tb[kb][e])
-                                                                   : 0;
-        den += x;
-        const int32_t x1 = (x + 128) >> 8, x2 = (x1 + 128) >> 8;
-        wd[0] |= (uint32_t)(x & 255) << (8 * e);
+        const int32_t x0 = x[kb][e];
+        dt += x0;
+        const int32_t x1 = (x0 + 128) >> 8, x2 = (x1 + 128) >> 8;
+        wd[0] |= (uint32_t)(x0 & 255) << (8 * e);
         wd[1] |= (uint32_t)(x1 & 255) << (8 * e);
         wd[2] |= (uint32_t)(x2 & 255) << (8 * e);
       }
 #pragma unroll
       for (int i = 0; i < 3; ++i) pa[i][kb] = (int)wd[i];
     }
+    den += dt;
 #pragma unroll
     for (int d = 0; d < DB; ++d) {
       const int row = d * 16 + kl;
@@ -1691,7 +1740,18 @@ __global__ __launch_bounds__(64 * Pre2<HD>::NW, 1) void attn_pre2_kernel(AttnArg
         for (int i = 0; i < 3; ++i) pacc[d][i + j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(pa[i], b, pacc[d][i + j], 0, 0, 0);
       }
     }
-  }
+  };
+  auto sweep2 = [&](auto fast_t) {
+    for (int t = 0; t < ntile; ++t) {
+      if (t + NS - 2 < ntile)
+        ring_barrier<C::LPT * (NS - 2)>();
+      else
+        ring_barrier<0>();
+      if (t * 64 + 63 <= wmin_qpos)               // wave-uniform: every key of the tile is visible to every query
+        tile2(t, fast_t, std::true_type{});
+      else
+        tile2(t, fast_t, std::false_type{});
+    }
   };
   if (fast)
     sweep2(std::true_type{});
@@ -1890,7 +1950,8 @@ extern "C" int bx_int8_attn_paged(const int64_t* q, const int64_t* qpos, int64_t
 }
 
 // the limb-plane form's scratch: K and V planes, 3 Z Sp HD bytes each (Sp = S rounded up to 64 keys)
-static int64_t pre2_scratch(int64_t Z, int64_t S, int64_t HD) { return 2 * 3 * Z * ((S + 63) / 64 * 64) * HD; }
+static int64_t pre2_planes(int64_t Z, int64_t S, int64_t HD) { return 2 * 3 * Z * ((S + 63) / 64 * 64) * HD; }
+static int64_t pre2_scratch(int64_t Z, int64_t S, int64_t HD) { return pre2_planes(Z, S, HD) + (16LL << kExp2Bits); }
 
 extern "C" int64_t bx_attn_prefill_scratch(int32_t Z, int32_t S, int32_t HD) {
   if (Z <= 0 || S <= 0 || (HD != 64 && HD != 128)) return 0;
@@ -1930,16 +1991,17 @@ extern "C" int bx_exact_attn_prefill(const int32_t* qg, int64_t sq_z, int64_t sq
                (long long)tmp_bytes, (long long)need);
     const int Sp = (S + 63) / 64 * 64;
     int8_t* pl = (int8_t*)tmp;
-    const int64_t units = (int64_t)Z * Sp * (HD / 16) + (int64_t)Z * (Sp / 4) * (HD / 4);
-    pre_split_kernel<<<(int)std::min<int64_t>((units + 255) / 256, 8192), 256, 0, st>>>(p, pl, pl + (int64_t)Z * 3 * Sp * HD,
-                                                                                     Z, Sp, HD);
+    const int64_t units = (int64_t)Z * Sp * (HD / 16) + (int64_t)Z * (Sp / 4) * (HD / 4) + (1LL << kExp2Bits);
+    int64_t* tab2 = (int64_t*)(pl + pre2_planes(Z, S, HD));
+    pre_split_kernel<<<(int)std::min<int64_t>((units + 255) / 256, 8192), 256, 0, st>>>(
+        p, pl, pl + (int64_t)Z * 3 * Sp * HD, tab2, Z, Sp, HD);
     if (int rc = check_launch("pre_split_kernel")) return rc;
     if (HD == 64) {
       allow_lds_attn((const void*)attn_pre2_kernel<64>, Pre2<64>::LDS);
-      attn_pre2_kernel<64><<<Z * ((gT + 127) / 128), 512, Pre2<64>::LDS, st>>>(p, pl, Z, Sp);
+      attn_pre2_kernel<64><<<Z * ((gT + 127) / 128), 512, Pre2<64>::LDS, st>>>(p, pl, Z, Sp, (const char*)tab2);
     } else {
       allow_lds_attn((const void*)attn_pre2_kernel<128>, Pre2<128>::LDS);
-      attn_pre2_kernel<128><<<Z * ((gT + 63) / 64), 256, Pre2<128>::LDS, st>>>(p, pl, Z, Sp);
+      attn_pre2_kernel<128><<<Z * ((gT + 63) / 64), 256, Pre2<128>::LDS, st>>>(p, pl, Z, Sp, (const char*)tab2);
     }
     return check_launch("attn_pre2_kernel");
   }

@@ -141,16 +141,17 @@ def test_paged_attention_split_exchange(dev, monkeypatch, ticks, ns):
 
 
 @pytest.mark.parametrize("HD", [64, 128])
-@pytest.mark.parametrize("planes", [True, False])
-def test_prefill_attention(dev, HD, planes):
+@pytest.mark.parametrize("planes,shr", [(True, (-40, -10)), (False, (-40, -10)), (True, (-9, 7))])
+def test_prefill_attention(dev, HD, planes, shr):
     """Both prefill forms (limb planes streamed into LDS; register-staged) against the oracle's unfused
-    bmm -> softmax -> bmm, on a strided cache view with two sequence offsets."""
+    bmm -> softmax -> bmm, on a strided cache view with two sequence offsets. Query exponents from -9 up give
+    negative score shifts for some rows (the limb-plane kernel's general weight path)."""
     from bitexact.exact.attention import prefill
     g = torch.Generator().manual_seed(3 + HD)
     B, HKV, grp, T, L = 2, 2, 4, 70, 96
     Z = B * HKV
     qg = torch.randint(-(1 << 22), (1 << 22) + 1, (Z, grp * T, HD), generator=g).to(torch.int32)
-    shg = torch.randint(-40, -10, (Z, grp * T, 1), generator=g)
+    shg = torch.randint(shr[0], shr[1], (Z, grp * T, 1), generator=g)
     cache_k = torch.randint(-R.LIM3, R.LIM3 + 1, (B, HKV, L, HD), generator=g).to(torch.int32)
     cache_v = torch.randint(-R.LIM3, R.LIM3 + 1, (B, HKV, L, HD), generator=g).to(torch.int32)
     pos = torch.arange(T)[None].expand(B, T) + torch.tensor([[0], [20]])           # two sequences, offsets
