@@ -28,6 +28,9 @@ SIGNATURES = {
     "bx_exact_linear_workspace": (I64, [I32, I32, I32]),
     "bx_exact_linear_scratch": (I64, [I32, I32, I32]),
     "bx_exact_linear_plan": (ctypes.c_int, [I32, I32, I32, P]),
+    "bx_exact_linear_planes_plan": (ctypes.c_int, [I32, I32, I32, P]),
+    "bx_exact_linear_planes_workspace": (I64, [I32, I32, I32]),
+    "bx_exact_linear_reads_planes": (I32, [I32, I32, I32]),
     "bx_int8_gemm_plan": (ctypes.c_int, [I32, I32, I32, I32, P]),
     "bx_exact_linear_noalloc": (ctypes.c_int, [P, I64, P, P, I64, I64, P, P, P, P, P, I32, P, I32, I32, I32, I32,
                                                I32, P, P]),

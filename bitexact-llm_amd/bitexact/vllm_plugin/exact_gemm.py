@@ -13,20 +13,22 @@ from bitexact.exact.consts import FR
 
 
 def needs_planes(M, N, K):
-    """Whether the exact linear at this shape reads q as int8 limb planes (then a caller that has them, from
-    ops.add_norm_y(planes=True), saves the split launch by passing them as q_planes)."""
-    return _hip.lib().bx_exact_linear_scratch(M, N, K) > 0
+    """Whether the exact linear at this shape, given q's int8 limb planes, reads them (then a caller that can
+    produce them, e.g. ops.add_norm_y(planes=True), should pass them as q_planes: no split launch, and at some
+    narrow shapes a faster kernel than without them)."""
+    return _hip.lib().bx_exact_linear_reads_planes(M, N, K) > 0
 
 
 KERNELS = {1: "gemv", 2: "wide", 3: "tile", 5: "stream"}
 TILES = {0: "128x128", 1: "64x128", 2: "64x32", 3: "64x64-int8", 4: "64x64", -1: None}
 
 
-def plan(M, N, K):
-    """Which kernel the exact linear runs at (M, N, K): (kernel, tile, k_splits, blocks_per_split)."""
+def plan(M, N, K, planes=False):
+    """Which kernel the exact linear runs at (M, N, K) (planes: given q's limb planes): (kernel, tile, k_splits,
+    blocks_per_split)."""
     import ctypes
     out = (ctypes.c_int32 * 4)()
-    _hip.call("bx_exact_linear_plan", M, N, K, out)
+    _hip.call("bx_exact_linear_planes_plan" if planes else "bx_exact_linear_plan", M, N, K, out)
     return KERNELS[out[0]], TILES[out[1]], out[2], out[3]
 
 
@@ -45,9 +47,9 @@ def _exact_linear(q, sh, limbs, d, g, cnt, ec, ev, R, flag, checked, fr, q_plane
     if checked:
         assert flag is not None and flag.dtype == torch.int32
     y = torch.empty(M, N, dtype=torch.long, device=q.device)
-    ws, wsb = _hip.workspace(q.device, _hip.lib().bx_exact_linear_workspace(M, N, K))
     sh = sh.contiguous()
     if q_planes is not None:
+        ws, wsb = _hip.workspace(q.device, _hip.lib().bx_exact_linear_planes_workspace(M, N, K))
         _hip.require_cuda(q_planes)
         assert q_planes.dtype == torch.int8 and q_planes.shape == (3, M, K) and q_planes.is_contiguous()
         _hip.call("bx_exact_linear_planes", _hip.ptr(q), q.stride(0), _hip.ptr(sh), _hip.ptr(limbs), limbs.stride(0),
@@ -55,6 +57,7 @@ def _exact_linear(q, sh, limbs, d, g, cnt, ec, ev, R, flag, checked, fr, q_plane
                   _hip.ptr(ec) if R else None, _hip.ptr(ev) if R else None, R, _hip.ptr(y), M, N, K, fr,
                   int(checked), _hip.ptr(flag), _hip.ptr(ws), wsb, _hip.ptr(q_planes), _hip.stream_of(q))
         return y
+    ws, wsb = _hip.workspace(q.device, _hip.lib().bx_exact_linear_workspace(M, N, K))
     tmp, tmpb = _hip.scratch(q.device, _hip.lib().bx_exact_linear_scratch(M, N, K))
     _hip.call("bx_exact_linear", _hip.ptr(q), q.stride(0), _hip.ptr(sh), _hip.ptr(limbs), limbs.stride(0),
               limbs.stride(1), _hip.ptr(d), _hip.ptr(g), _hip.ptr(cnt) if R else None,

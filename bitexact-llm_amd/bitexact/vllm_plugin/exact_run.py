@@ -74,8 +74,9 @@ class ExactEngine:
         qpos = pos.view(-1, 1).expand(-1, G).contiguous()
         fl = self.fl
         x, q, sh, _ = ops.embed_norm(self.emb, ids, *self.ga[0], flag=fl)
+        pl = None                             # q's limb planes, when the layer-end norm wrote them
         for i in range(self.L):
-            y = self.fused[i, "wqkv"](q, sh, fl, False)
+            y = self.fused[i, "wqkv"](q, sh, fl, False, q_planes=pl)
             if kvs is None:
                 ops.qkv_y(y, pos.view(N, 1), self.cos, self.sin, N, 1, (self.H, HKV, HD), flag=fl)
                 num = torch.zeros(N, HKV, G, HD, dtype=torch.long, device=y.device)
@@ -104,7 +105,11 @@ class ExactEngine:
                 q, sh, _ = ops.gu_silu_y(y, self.exp2, flag=fl)
                 yd = wd(q, sh, fl, True)
             nxt = self.ga[i + 1] if i + 1 < self.L else (None, None)
-            x, q, sh, _ = ops.add_norm_y(yd, x, *nxt, flag=fl)
+            pl = None
+            if nxt[0] is not None and self.fused[i + 1, "wqkv"].needs_planes(N):
+                x, (q, pl), sh, _ = ops.add_norm_y(yd, x, *nxt, flag=fl, planes=True)
+            else:
+                x, q, sh, _ = ops.add_norm_y(yd, x, *nxt, flag=fl)
         return x
 
     def logits(self, h):

@@ -1524,6 +1524,7 @@ static const TileShape kTileExact = {4, 2, 1, 2, 64, 2};
 
 struct Plan {
   int stream;                     // stream kernel: activation row blocks RBM (0: none)
+  int nwv;                        // stream kernel: waves per block (16 columns each)
   int wide;                       // wide kernel configuration (0: none)
   int staged;                     // staged kernel configuration (0: none)
   bool gemv;
@@ -1629,19 +1630,30 @@ static int staged_cfg(int rows_a, int N, int K, bool exact, int cus) {
 // 16 us), so those shapes keep them. Exact mode at M = 32: N = 16384: 26.5 vs 39.1 us (wide kernel), N = 128256:
 // 203 vs 289 us; narrow N splits K over the zeroed workspace when every block keeps >= 1024 k (N = 2048, K = 8192:
 // 24.3 vs 30.4 us on the 64 x 64 tile); at K = 2048 (8 splits of 256 k: 16.4 vs 11.7 us) the gemv stays.
-static bool stream_plan(int rows_a, int M_out, int N, int K, bool exact, int cus, Plan& s) {
+static bool stream_plan(int rows_a, int M_out, int N, int K, bool exact, bool planes, int cus, Plan& s) {
   static const int on = getenv("BX_STREAM") ? atoi(getenv("BX_STREAM")) : 1;
   if (!on || rows_a > 128 || rows_a < (exact ? 49 : 1) || K % kStBK != 0) return false;
   s.tiles_x = (N + kStC - 1) / kStC;
   s.tiles_y = 1;
   s.split = 1;
+  s.nwv = 4;
   if (s.tiles_x < cus) {   // exact only: K split until the tiles cover the chip
     if (!exact) return false;
     const int nch = K / kStBK;
     const int want = std::min(nch, (cus + s.tiles_x - 1) / s.tiles_x);
     const int per = (nch + want - 1) / want;
-    if (per < 8) return false;   // under 1024 k per block the split's fixed costs lose to the gemv
-    s.split = (nch + per - 1) / per;
+    if (per < 8) {
+      // under 1024 k per block the split's fixed costs lose to the gemv, unless the caller brings q's limb
+      // planes (no split launch) and 65..96 limb rows: then 32-column blocks, K split in at most as many parts
+      // as keep every block resident at once (M = 32, N = 3072, K = 2048: 14.6 vs 18.9 us for the gemv)
+      if (!planes || rows_a <= 64 || rows_a > 96) return false;
+      s.nwv = 2;
+      s.tiles_x = (N + 31) / 32;
+      s.split = std::max(1, std::min(cus / s.tiles_x, nch / 4));
+      if (s.tiles_x * s.split > cus || 2 * s.tiles_x * s.split < cus) return false;   // one round, half the chip
+    } else {
+      s.split = (nch + per - 1) / per;
+    }
   }
   s.stream = rows_a <= 16 ? 1 : rows_a <= 32 ? 2 : rows_a <= 64 ? 4 : (exact && rows_a <= 96) ? 6 : 8;
   s.kbytes = (K / kStBK + s.split - 1) / s.split * kStBK;
@@ -1650,11 +1662,12 @@ static bool stream_plan(int rows_a, int M_out, int N, int K, bool exact, int cus
   return true;
 }
 
-static Plan make_plan(int rows_a, int M_out, int N, int K, int nb, int na, bool exact) {
+// planes: the caller supplies q's limb planes (exact mode), so a plane-reading kernel costs no split launch
+static Plan make_plan(int rows_a, int M_out, int N, int K, int nb, int na, bool exact, bool planes = false) {
   Plan s = {};
   const int cus = device_cus();
   const int nst = (K + 63) / 64;
-  if (stream_plan(rows_a, M_out, N, K, exact, cus, s)) return s;
+  if (stream_plan(rows_a, M_out, N, K, exact, planes, cus, s)) return s;
   s.wide = wide_cfg(rows_a, N, K, exact);
   s.staged = staged_cfg(rows_a, N, K, exact, cus);
   if (s.staged != S_NONE) {
@@ -1902,6 +1915,7 @@ static int launch_stream(LinArgs& p, const Plan& s, hipStream_t st) {
     if (s.stream == 1) return launch_stream_cfg<1, 3, 4, MODE>(p, s, st);
     if (s.stream == 2) return launch_stream_cfg<2, 3, 4, MODE>(p, s, st);
     if (s.stream == 4) return launch_stream_cfg<4, 3, 4, MODE>(p, s, st);
+    if (s.nwv == 2) return launch_stream_cfg<6, 3, 4, MODE, 2>(p, s, st);   // 65..96 rows (planner)
     if (s.stream == 6) return launch_stream_cfg<6, 3, 4, MODE>(p, s, st);
     return launch_stream_cfg<8, 3, 3, MODE>(p, s, st);
   }
@@ -1939,7 +1953,7 @@ static int exact_common(LinArgs& p, int mode, int64_t ws_bytes, void* tmp, int64
   if (p.M == 0 || p.N == 0) return BX_OK;
   BX_REQUIRE(p.K > 0, "K == 0");
   p.rows_a = 3 * p.M;
-  Plan s = make_plan(p.rows_a, p.M, p.N, p.K, 3, 3, true);
+  Plan s = make_plan(p.rows_a, p.M, p.N, p.K, 3, 3, true, planes != nullptr);
   if (planes != nullptr) s.tmp_bytes = 0;   // the caller's limb planes replace the scratch
   if (int rc = need_ws(p, s, ws_bytes, tmp, tmp_bytes)) return rc;
   if (s.gemv) return mode == EXACT ? launch_gemv<3, EXACT>(p, s, st) : launch_gemv<3, WMM_T>(p, s, st);
@@ -2013,6 +2027,16 @@ extern "C" int64_t bx_exact_linear_scratch(int32_t M, int32_t N, int32_t K) {
   return make_plan(3 * M, M, N, K, 3, 3, true).tmp_bytes;
 }
 
+extern "C" int64_t bx_exact_linear_planes_workspace(int32_t M, int32_t N, int32_t K) {
+  if (M <= 0 || N <= 0 || K <= 0) return 0;
+  return make_plan(3 * M, M, N, K, 3, 3, true, true).ws_bytes;
+}
+
+extern "C" int32_t bx_exact_linear_reads_planes(int32_t M, int32_t N, int32_t K) {
+  if (M <= 0 || N <= 0 || K <= 0) return 0;
+  return make_plan(3 * M, M, N, K, 3, 3, true, true).gemv ? 0 : 1;
+}
+
 static int int8_common(LinArgs& p, int mode, int64_t ws_bytes, hipStream_t st) {
   BX_REQUIRE(p.M >= 0 && p.N >= 0 && p.K >= 0, "negative size");
   BX_REQUIRE(p.K % 16 == 0, "K %% 16 != 0 (K=%d)", p.K);
@@ -2059,14 +2083,22 @@ extern "C" int64_t bx_int8_gemm_workspace(int32_t M, int32_t N, int32_t K, int32
 // Which kernel bx_exact_linear launches for (M, N, K) (tests use it to prove they reach every configuration):
 // out[0] = 1 gemv, 2 wide, 3 tile, 5 stream; out[1] = tile configuration (0 T_BIG, 1 T_MID, 2 T_NARROW, 3 T_DEC,
 // 4 T_SMALL; -1 otherwise); out[2] = K splits; out[3] = blocks per split.
-extern "C" int bx_exact_linear_plan(int32_t M, int32_t N, int32_t K, int32_t* out) {
-  BX_REQUIRE(out && M > 0 && N > 0 && K > 0, "bad plan query");
-  const Plan s = make_plan(3 * M, M, N, K, 3, 3, true);
+static int exact_plan_out(const Plan& s, int32_t* out) {
   out[0] = s.stream ? 5 : s.gemv ? 1 : s.wide ? 2 : 3;
   out[1] = (s.gemv || s.wide || s.stream) ? -1 : s.tile;
   out[2] = s.split;
   out[3] = s.gemv ? s.tiles_x * s.parts : s.tiles_x * s.tiles_y;
   return BX_OK;
+}
+
+extern "C" int bx_exact_linear_plan(int32_t M, int32_t N, int32_t K, int32_t* out) {
+  BX_REQUIRE(out && M > 0 && N > 0 && K > 0, "bad plan query");
+  return exact_plan_out(make_plan(3 * M, M, N, K, 3, 3, true), out);
+}
+
+extern "C" int bx_exact_linear_planes_plan(int32_t M, int32_t N, int32_t K, int32_t* out) {
+  BX_REQUIRE(out && M > 0 && N > 0 && K > 0, "bad plan query");
+  return exact_plan_out(make_plan(3 * M, M, N, K, 3, 3, true, true), out);
 }
 
 // The int8 GEMM's plan for M output rows of nl stacked limbs (nl = 0: the raw int32 GEMM of M stacked rows):

@@ -63,6 +63,12 @@ int bx_exact_linear_planes(const int32_t* q, int64_t ldq, const int64_t* sh, con
                            int64_t ws_bytes, const int8_t* q_planes, bx_stream_t stream);
 int64_t bx_exact_linear_workspace(int32_t M, int32_t N, int32_t K);
 int64_t bx_exact_linear_scratch(int32_t M, int32_t N, int32_t K);
+/* Planner queries for bx_exact_linear_planes, which may take another kernel than bx_exact_linear at the same shape
+ * (q's limb planes at hand make a plane-reading kernel cheaper): its workspace size, and whether it reads the
+ * planes at all (1) or streams q itself (0), so a caller knows when producing the planes pays. No reference
+ * counterpart (see bx_exact_linear_planes). */
+int64_t bx_exact_linear_planes_workspace(int32_t M, int32_t N, int32_t K);
+int32_t bx_exact_linear_reads_planes(int32_t M, int32_t N, int32_t K);
 /* No counterpart in the reference. For callers that cannot allocate device memory (code under HIP graph capture,
  * tight serving loops, harnesses that forbid hipMalloc): bx_exact_linear with its split-K workspace and limb-plane
  * scratch taken from a static device array of bx_exact_linear_noalloc_limit() bytes (32 MiB: 8 MiB workspace,
@@ -79,6 +85,8 @@ int64_t bx_exact_linear_noalloc_limit(void);
  * out int32 [4] = {kernel: 1 gemv, 2 wide, 3 tile, 5 stream; tile config: 0 128x128, 1 64x128, 2 64x32, 3 64x64 int8 decode,
  * 4 64x64 exact, -1 none; K splits; blocks per split}. Tests use it to show every configuration is reached. */
 int bx_exact_linear_plan(int32_t M, int32_t N, int32_t K, int32_t* out);
+/* The same for bx_exact_linear_planes. */
+int bx_exact_linear_planes_plan(int32_t M, int32_t N, int32_t K, int32_t* out);
 
 /* Replaces wmm_triton / wmm_cublas / wmm_cpu (src/bitexact/exact/wmm.py:79-121): the exact dense product
  * T int64 [M, N] = q W^T (one slice of the reference's [split, M, N] partials). */

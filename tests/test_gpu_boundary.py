@@ -140,6 +140,7 @@ def test_wmm_entry_names(dev):
 
 def test_opcheck_operators(dev):
     """torch.library.opcheck (schema, fake tensor, dispatch) on representative operators."""
+    import bitexact.bmm  # noqa: F401  (registers bitexact_hip::bmm)
     from bitexact.exact.consts import decompose
     N, K, M = 64, 128, 5
     w = (torch.randn(N, K, generator=torch.Generator().manual_seed(1)) * 0.02).to(torch.bfloat16)

@@ -338,6 +338,40 @@ def test_exact_linear_norm_planes(dev, M, N):
     assert np.array_equal(yb.cpu().numpy(), ref) and bool(f2.item()) == rflag
 
 
+@pytest.mark.parametrize("M,N", [(32, 3072), (22, 3000), (32, 2048)])
+def test_exact_linear_narrow_planes(dev, M, N):
+    """Narrow N at K = 2048 with q's limb planes given: 32-column stream blocks with the K split over the zeroed
+    workspace (without planes the gemv serves the shape); same y and flag as the gemv, and y matches the oracle
+    (partial last column tile at N = 3000, forced residual entries, 66 and 96 limb rows)."""
+    from bitexact.exact import ops
+    from bitexact.vllm_plugin.exact_gemm import exact_linear, needs_planes, plan
+    K = 2048
+    assert plan(M, N, K)[0] == "gemv"
+    kern, _, split, blocks = plan(M, N, K, planes=True)
+    assert kern == "stream" and split > 1 and blocks == -(-N // 32), plan(M, N, K, planes=True)
+    assert needs_planes(M, N, K)
+    g = torch.Generator().manual_seed(M * N)
+    x = torch.randint(-(1 << 33), 1 << 33, (M, K), generator=g)
+    y = torch.randint(-(1 << 32), 1 << 32, (M, K), generator=g)
+    gm, ge = torch.randint(-255, 256, (K,), generator=g), torch.randint(-14, -6, (K,), generator=g)
+    _, (q, pl), sh, _ = ops.add_norm_y(y.to(dev), x.to(dev), gm.to(dev), ge.to(dev), planes=True)
+    dec = _dec(_bf16(N, K, 11))
+    limbs = torch.from_numpy(dec["limbs"]).to(dev)
+    d, gg = torch.from_numpy(dec["d"]).to(dev), torch.from_numpy(dec["g"]).to(dev)
+    cnt, ec, ev, Rr = _ell(dec, N, dev)
+    f1 = torch.zeros(1, dtype=torch.int32, device=dev)
+    f2 = torch.zeros(1, dtype=torch.int32, device=dev)
+    ya = exact_linear(q, sh, limbs, d, gg, cnt, ec, ev, Rr, f1, True)
+    for _ in range(2):                                # the second call finds the workspace zeroed again
+        f2.zero_()
+        yb = exact_linear(q, sh, limbs, d, gg, cnt, ec, ev, Rr, f2, True, q_planes=pl)
+        assert torch.equal(ya, yb) and f1.item() == f2.item()
+    qn, shn = q.cpu().numpy().astype(np.int64), sh.cpu().numpy()
+    ref, rflag, _ = R.epilogue(R.wmm_f64(qn, dec["W"]), R.residual(qn, dec["rr"], dec["rc"], dec["rv"], N),
+                               dec["d"], dec["g"], shn, R.FR, True)
+    assert np.array_equal(yb.cpu().numpy(), ref) and bool(f2.item()) == rflag
+
+
 @pytest.mark.parametrize("M", [22, 32])
 def test_exact_linear_silu_planes(dev, M):
     """The SiLU stage's limb planes fed to the exact linear at K = 8192 (MFMA tiles with K split) give the same q,
