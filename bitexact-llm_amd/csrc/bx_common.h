@@ -202,6 +202,41 @@ __device__ __forceinline__ int64_t wave_sum64(int64_t v) {
   for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
   return v;
 }
+// DPP forms: a row rotation (row_ror:n, dpp_ctrl 0x120 + n) of both 32-bit halves; rotations by 1, 2, 4 and 8
+// leave every lane of a 16-lane row with the row's reduction, and the four rows meet through readlane, so the
+// result is wave-uniform without any LDS traffic (the shuffles above go through the LDS crossbar). Every lane of
+// the wave must be active.
+template <int CTRL>
+__device__ __forceinline__ int64_t dpp64(int64_t v) {
+  const int lo = __builtin_amdgcn_update_dpp((int)v, (int)v, CTRL, 0xF, 0xF, false);
+  const int hi = __builtin_amdgcn_update_dpp((int)(v >> 32), (int)(v >> 32), CTRL, 0xF, 0xF, false);
+  return (int64_t)(((uint64_t)(uint32_t)hi << 32) | (uint32_t)lo);
+}
+__device__ __forceinline__ int64_t readlane64(int64_t v, int l) {
+  const int lo = __builtin_amdgcn_readlane((int)v, l), hi = __builtin_amdgcn_readlane((int)(v >> 32), l);
+  return (int64_t)(((uint64_t)(uint32_t)hi << 32) | (uint32_t)lo);
+}
+template <bool MAX>
+__device__ __forceinline__ int64_t op64(int64_t a, int64_t b) { return MAX ? imax(a, b) : add_wrap(a, b); }
+template <bool MAX>
+__device__ __forceinline__ int64_t wave_reduce64_dpp(int64_t v) {
+  v = op64<MAX>(v, dpp64<0x121>(v));
+  v = op64<MAX>(v, dpp64<0x122>(v));
+  v = op64<MAX>(v, dpp64<0x124>(v));
+  v = op64<MAX>(v, dpp64<0x128>(v));
+  return op64<MAX>(op64<MAX>(readlane64(v, 0), readlane64(v, 16)), op64<MAX>(readlane64(v, 32), readlane64(v, 48)));
+}
+// Block reduction over NW waves with an LDS-only barrier (no wait for outstanding global loads or stores);
+// `slot` (NW entries) must not be reused by another reduction before every wave has passed this one.
+template <bool MAX, int NW>
+__device__ __forceinline__ int64_t block_reduce64_dpp(int64_t v, int64_t* slot, int64_t identity) {
+  v = wave_reduce64_dpp<MAX>(v);
+  const int lane = threadIdx.x & 63;
+  if (lane == 0) slot[threadIdx.x >> 6] = v;
+  __builtin_amdgcn_s_waitcnt(0xc07f);   // lgkmcnt(0)
+  asm volatile("s_barrier" ::: "memory");
+  return wave_reduce64_dpp<MAX>(lane < NW ? slot[lane] : identity);
+}
 __device__ __forceinline__ int wave_or(int v) {
 #pragma unroll
   for (int o = 32; o > 0; o >>= 1) v |= __shfl_xor(v, o, 64);

@@ -16,26 +16,30 @@ constexpr int kQB = 22;                        // |q| <= 2^22
 constexpr int kRowThreads = 1024;
 constexpr int kRowU = 4;   // elements per thread whose loads are issued together
 
+// Block reductions (every thread of the block calls them, sbuf holds 16 entries): wave reductions in DPP and
+// LDS-only barriers (a __syncthreads would also wait for every outstanding global load and store); the leading
+// barrier keeps a reduction's sbuf writes behind the previous reduction's reads.
+__device__ __forceinline__ void lds_sync() {
+  __builtin_amdgcn_s_waitcnt(0xc07f);   // lgkmcnt(0)
+  asm volatile("s_barrier" ::: "memory");
+}
+
 __device__ __forceinline__ int64_t block_max64(int64_t v, int64_t* sbuf) {
-  v = wave_max64(v);
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  __syncthreads();
-  if (lane == 0) sbuf[wave] = v;
-  __syncthreads();
-  int64_t r = sbuf[0];
-  for (int i = 1; i < (int)(blockDim.x >> 6); ++i) r = imax(r, sbuf[i]);
-  return r;
+  v = wave_reduce64_dpp<true>(v);
+  const int lane = threadIdx.x & 63;
+  lds_sync();
+  if (lane == 0) sbuf[threadIdx.x >> 6] = v;
+  lds_sync();
+  return wave_reduce64_dpp<true>(lane < (int)(blockDim.x >> 6) ? sbuf[lane] : INT64_MIN);
 }
 
 __device__ __forceinline__ int64_t block_sum64(int64_t v, int64_t* sbuf) {
-  v = wave_sum64(v);
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  __syncthreads();
-  if (lane == 0) sbuf[wave] = v;
-  __syncthreads();
-  int64_t r = 0;
-  for (int i = 0; i < (int)(blockDim.x >> 6); ++i) r += sbuf[i];
-  return r;
+  v = wave_reduce64_dpp<false>(v);
+  const int lane = threadIdx.x & 63;
+  lds_sync();
+  if (lane == 0) sbuf[threadIdx.x >> 6] = v;
+  lds_sync();
+  return wave_reduce64_dpp<false>(lane < (int)(blockDim.x >> 6) ? sbuf[lane] : 0);
 }
 
 // floor(sqrt(x)) for 0 <= x < 2^62, exact (float estimate, then integer corrections; intops.isqrt's value)
@@ -113,32 +117,46 @@ struct NormArgs {
   int64_t plane;    // M D
 };
 
+// One block of kNormThreads per row (a decode row of 2048 is 4 elements a thread, all loads in flight at once):
+// fewer waves make the three block reductions cheap (wave reductions in DPP, one LDS-only barrier each), and
+// the gamma loads go out with the row's loads rather than after the reductions.
+constexpr int kNormThreads = 512, kNormU = 4;
 template <int SRC>
-__global__ __launch_bounds__(kRowThreads) void norm_quant_kernel(NormArgs p) {
+__global__ __launch_bounds__(kNormThreads) void norm_quant_kernel(NormArgs p) {
+  constexpr int NT = kNormThreads, U = kNormU, NW = NT / 64;
   extern __shared__ __align__(16) char smem[];
   int64_t* Xs = (int64_t*)smem;
   int64_t* Ps = Xs + p.D;
-  __shared__ int64_t sbuf[16];
+  __shared__ int64_t sbuf[3][NW];
   const int D = p.D;
   int64_t* xr = p.x + (int64_t)blockIdx.x * p.ldx;
   const int32_t* er_row = nullptr;
   if (SRC == SRC_EMB) er_row = p.emb + p.ids[blockIdx.x] * (int64_t)D;
-  int64_t amax = 0;
-  // kRowU elements per thread at a time, every load issued before the first store (the write-back to x could
-  // alias later loads, which would otherwise wait for it one element at a time)
   const int64_t* yr = SRC == SRC_ADD ? p.y + (int64_t)blockIdx.x * p.ldy : nullptr;
-  for (int i0 = threadIdx.x; i0 < D; i0 += kRowU * kRowThreads) {
-    int64_t v[kRowU];
+  int64_t amax = 0;
+  int64_t gmv0[U], gev0[U];   // the first group's gamma pairs, requested with the row
+  // U elements per thread at a time, every load issued before the first store (the write-back to x could
+  // alias later loads, which would otherwise wait for it one element at a time)
+  for (int i0 = threadIdx.x; i0 < D; i0 += U * NT) {
+    int64_t v[U];
 #pragma unroll
-    for (int k = 0; k < kRowU; ++k) {
-      const int i = min(i0 + k * kRowThreads, D - 1);
+    for (int k = 0; k < U; ++k) {
+      const int i = min(i0 + k * NT, D - 1);
       if (SRC == SRC_EMB) v[k] = er_row[i];
       else if (SRC == SRC_ADD) v[k] = add_wrap(xr[i], yr[i]);
       else v[k] = xr[i];
     }
+    if (i0 == (int)threadIdx.x && p.gm != nullptr) {
 #pragma unroll
-    for (int k = 0; k < kRowU; ++k) {
-      const int i = i0 + k * kRowThreads;
+      for (int k = 0; k < U; ++k) {
+        const int i = min(i0 + k * NT, D - 1);
+        gmv0[k] = p.gm[i];
+        gev0[k] = p.ge[i];
+      }
+    }
+#pragma unroll
+    for (int k = 0; k < U; ++k) {
+      const int i = i0 + k * NT;
       if (i < D) {
         if (SRC != SRC_X) xr[i] = v[k];
         Xs[i] = v[k];
@@ -146,16 +164,16 @@ __global__ __launch_bounds__(kRowThreads) void norm_quant_kernel(NormArgs p) {
       }
     }
   }
-  amax = block_max64(amax, sbuf);
+  amax = block_reduce64_dpp<true, NW>(amax, sbuf[0], 0);
   if (threadIdx.x == 0 && amax >= (1LL << 40)) p.err[0] = 1;
   if (p.gm == nullptr) return;
   const int64_t shx = imax(bitlen(imax(amax, 1)) - 25, -6);
   int64_t S = 0;
-  for (int i = threadIdx.x; i < D; i += kRowThreads) {
+  for (int i = threadIdx.x; i < D; i += NT) {
     const int64_t xs = rshc(Xs[i], shx);
     S = add_wrap(S, mul_wrap(xs, xs));
   }
-  S = block_sum64(S, sbuf);
+  S = block_reduce64_dpp<false, NW>(S, sbuf[1], 0);
   const int64_t T = add_wrap(S, rshc(kEps60 * (int64_t)D, 60 - 2 * (p.FR - shx)));
   const int64_t m = fdiv(62 + p.lg - bitlen(T), 2);
   const int64_t s = 2 * m - p.lg;
@@ -163,17 +181,17 @@ __global__ __launch_bounds__(kRowThreads) void norm_quant_kernel(NormArgs p) {
   const int64_t r = isqrt64(V), er = shx - p.FR - m;
   const double rinv = 1.0 / (double)r;
   int64_t emax = kNegBig;
-  for (int i0 = threadIdx.x; i0 < D; i0 += kRowU * kRowThreads) {
-    int64_t gmv[kRowU], gev[kRowU];
+  for (int i0 = threadIdx.x; i0 < D; i0 += U * NT) {
+    int64_t gmv[U], gev[U];
 #pragma unroll
-    for (int k = 0; k < kRowU; ++k) {
-      const int i = min(i0 + k * kRowThreads, D - 1);
-      gmv[k] = p.gm[i];
-      gev[k] = p.ge[i];
+    for (int k = 0; k < U; ++k) {
+      const int i = min(i0 + k * NT, D - 1);
+      gmv[k] = i0 == (int)threadIdx.x ? gmv0[k] : p.gm[i];
+      gev[k] = i0 == (int)threadIdx.x ? gev0[k] : p.ge[i];
     }
 #pragma unroll
-    for (int k = 0; k < kRowU; ++k) {
-      const int i = i0 + k * kRowThreads;
+    for (int k = 0; k < U; ++k) {
+      const int i = i0 + k * NT;
       if (i < D) {
         const int64_t P = div_round64(mul_wrap(Xs[i], gmv[k]), gev[k] - p.FR - er + p.FN, r, rinv);
         Ps[i] = P;
@@ -181,9 +199,9 @@ __global__ __launch_bounds__(kRowThreads) void norm_quant_kernel(NormArgs p) {
       }
     }
   }
-  emax = block_max64(emax, sbuf);
+  emax = block_reduce64_dpp<true, NW>(emax, sbuf[2], kNegBig);
   const int64_t shr = imax(emax - kQB, kNegBig);
-  for (int i = threadIdx.x; i < D; i += kRowThreads) {
+  for (int i = threadIdx.x; i < D; i += NT) {
     const int32_t qv = (int32_t)rshc(Ps[i], shr + p.FN);
     p.q[(int64_t)blockIdx.x * p.ldq + i] = qv;
     if (p.planes != nullptr) {   // the limb split of the exact GEMM's activation planes (split_q_kernel's)
@@ -527,9 +545,9 @@ static int launch_norm(NormArgs& p, int src, int32_t M, bx_stream_t stream) {
                   : src == SRC_EMB ? (const void*)norm_quant_kernel<SRC_EMB> : (const void*)norm_quant_kernel<SRC_X>;
   allow_lds_rows(k, lds);
   hipStream_t st = (hipStream_t)stream;
-  if (src == SRC_ADD) norm_quant_kernel<SRC_ADD><<<M, kRowThreads, lds, st>>>(p);
-  else if (src == SRC_EMB) norm_quant_kernel<SRC_EMB><<<M, kRowThreads, lds, st>>>(p);
-  else norm_quant_kernel<SRC_X><<<M, kRowThreads, lds, st>>>(p);
+  if (src == SRC_ADD) norm_quant_kernel<SRC_ADD><<<M, kNormThreads, lds, st>>>(p);
+  else if (src == SRC_EMB) norm_quant_kernel<SRC_EMB><<<M, kNormThreads, lds, st>>>(p);
+  else norm_quant_kernel<SRC_X><<<M, kNormThreads, lds, st>>>(p);
   return check_launch("norm_quant_kernel");
 }
 
