@@ -288,7 +288,7 @@ def _gu_silu(y, lut, flag, split, planes):
     assert split or not planes, "limb planes come from the column-chunked path"
     pl = torch.empty((3, M, ff) if planes else (0,), dtype=torch.int8, device=y.device)
     if split and M > 0:
-        tmp, tmpb = _hip.scratch(y.device, _hip.lib().bx_silu_quant_scratch(M, ff))
+        tmp, tmpb = _hip.workspace(y.device, _hip.lib().bx_silu_quant_scratch(M, ff))   # zero-filled, kept so
         _hip.call("bx_silu_quant_ws", _hip.ptr(y), y.stride(0), ff, _hip.ptr(lut), FR, _hip.ptr(q), ff, _hip.ptr(sh),
                   _hip.ptr(pl) if planes else None, M, _hip.ptr(flag), _hip.ptr(tmp), tmpb, _hip.stream_of(y))
         return q, pl, sh

@@ -492,14 +492,6 @@ struct DecWs {
 __host__ __device__ __forceinline__ int64_t dec_ws_bytes(int64_t T, int64_t NS, int HD) {
   return T * NS * 4 * 8 * (2 + HD) + T * 4 + 256;
 }
-// Workspace slots are written by one block and read by another, possibly on another XCD (whose L2 is its own):
-// agent-scope relaxed atomic stores and loads keep them coherent without a cache-wide fence.
-__device__ __forceinline__ void ws_store(int64_t* a, int64_t v) {
-  __hip_atomic_store(a, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-__device__ __forceinline__ int64_t ws_load(int64_t* a) {
-  return __hip_atomic_load(a, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
 
 __device__ __forceinline__ DecWs dec_ws(const AttnArgs& p, int T, int NS, int HD) {
   const int64_t slots = (int64_t)T * NS * 4;

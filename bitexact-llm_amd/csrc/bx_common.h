@@ -191,6 +191,15 @@ __device__ __forceinline__ void ring_barrier() {
   asm volatile("s_barrier" ::: "memory");
 }
 
+// Workspace slots are written by one block and read by another, possibly on another XCD (whose L2 is its own):
+// agent-scope relaxed atomic stores and loads keep them coherent without a cache-wide fence.
+__device__ __forceinline__ void ws_store(int64_t* a, int64_t v) {
+  __hip_atomic_store(a, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ int64_t ws_load(int64_t* a) {
+  return __hip_atomic_load(a, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
 // ---- wavefront reductions (wave64) ----
 __device__ __forceinline__ int64_t wave_max64(int64_t v) {
 #pragma unroll

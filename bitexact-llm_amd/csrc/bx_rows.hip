@@ -396,15 +396,22 @@ __global__ __launch_bounds__(kRowThreads) void attn_out_kernel(const int64_t* nu
 }
 
 // The same stage split over column chunks for few rows (one block per row would leave most CUs idle while each
-// streams its 16 ff bytes of gate | up): silu_part_kernel, grid (M, C), writes P (int64 [M, ff]) and each chunk's
-// exponent maximum (slot [M, C]) to scratch; silu_fin_kernel, grid (M, C), takes the row's maximum over its C
-// slots and writes q for its chunk (and sh from chunk 0). The kernel boundary orders the two; the integers are
-// silu_quant_kernel's.
+// streams its 16 ff bytes of gate | up): grid (M, C), chunks of about 1024 columns.
 constexpr int kSiluPartThreads = 256;
-__global__ __launch_bounds__(kSiluPartThreads) void silu_part_kernel(const int64_t* gu, int64_t ldgu, int ff,
-                                                                     int chunk, const int64_t* lut, int FR,
-                                                                     int64_t* P, int64_t* slots, int32_t* err) {
+// Block (m, c) keeps its chunk's P in LDS, publishes the chunk's exponent maximum
+// (as emax - kNegBig + 1; 0 = not yet published) and waits for the other chunks of its row for at most `ticks` of
+// the 100 MHz real-time counter. A block that has not seen them all by then forms the row's maximum itself from
+// gu (the same integers, slower), so the wait always ends. The row's last block to finish reading resets its
+// slots and counter: the zero-filled workspace is left as it was found.
+constexpr uint64_t kSiluTicks = 20000;   // 200 us
+__global__ __launch_bounds__(kSiluPartThreads) void silu_fused_kernel(const int64_t* gu, int64_t ldgu, int ff,
+                                                                      int chunk, const int64_t* lut, int FR,
+                                                                      int64_t* slots, int32_t* cnt, uint64_t ticks,
+                                                                      int32_t* q, int64_t ldq, int64_t* sh,
+                                                                      int8_t* planes, int32_t* err) {
+  extern __shared__ __align__(16) int64_t Ps[];   // [chunk]
   __shared__ int64_t sbuf[16];
+  __shared__ int64_t s_row;
   const int m = blockIdx.x, c = blockIdx.y, C = gridDim.y;
   const int64_t* row = gu + (int64_t)m * ldgu;
   const int i_lo = c * chunk, i_hi = min(ff, i_lo + chunk);
@@ -431,29 +438,52 @@ __global__ __launch_bounds__(kSiluPartThreads) void silu_part_kernel(const int64
       const int i = i0 + k * kSiluPartThreads;
       if (i >= i_hi) continue;
       const int64_t v = silu_elem(gv[k], uv[k], la[k], lb[k], FR, bad);
-      P[(int64_t)m * ff + i] = v;
+      Ps[i - i_lo] = v;
       if (v != 0) emax = imax(emax, bitlen(v < 0 ? (int64_t)(0 - (uint64_t)v) : v) + eps);
     }
   }
   if (bad) err[0] = 1;
   emax = block_max64(emax, sbuf);
-  if (threadIdx.x == 0) slots[(int64_t)m * C + c] = emax;
-}
-
-__global__ __launch_bounds__(kSiluPartThreads) void silu_fin_kernel(const int64_t* P, const int64_t* slots, int ff,
-                                                                    int chunk, int FR, int32_t* q, int64_t ldq,
-                                                                    int64_t* sh, int8_t* planes) {
-  const int m = blockIdx.x, c = blockIdx.y, C = gridDim.y;
-  int64_t emax = kNegBig;
-  for (int j = 0; j < C; ++j) emax = imax(emax, slots[(int64_t)m * C + j]);
-  const int64_t shr = imax(emax - kQB, kNegBig);
-  const int eps = -2 * (int)FR;
-  const int i_lo = c * chunk, i_hi = min(ff, i_lo + chunk);
+  if (threadIdx.x == 0) {
+    s_row = emax;
+    ws_store(&slots[(int64_t)m * C + c], emax - kNegBig + 1);
+  }
+  lds_sync();
+  bool seen = true;
+  if ((int)threadIdx.x < C && (int)threadIdx.x != c) {
+    int64_t* a = &slots[(int64_t)m * C + threadIdx.x];
+    const uint64_t t0 = __builtin_amdgcn_s_memrealtime();
+    int64_t v = ws_load(a);
+    while (v == 0 && __builtin_amdgcn_s_memrealtime() - t0 < ticks) {
+      __builtin_amdgcn_s_sleep(1);
+      v = ws_load(a);
+    }
+    seen = v != 0;
+    if (seen) atomicMax((long long*)&s_row, (long long)(v - 1 + kNegBig));
+  }
+  const bool all = __syncthreads_and(seen);
+  if (threadIdx.x == 0 && atomicAdd(&cnt[m], 1) == C - 1) {   // every block of the row has read the slots
+    for (int j = 0; j < C; ++j) ws_store(&slots[(int64_t)m * C + j], 0);
+    atomicExch(&cnt[m], 0);
+  }
+  int64_t rmax = s_row;
+  if (!all) {   // the row's maximum from gu (blocks of the row that did not run alongside this one)
+    int64_t e2 = kNegBig;
+    int bad2 = 0;
+    for (int i = threadIdx.x; i < ff; i += kSiluPartThreads) {
+      const int64_t g = row[i];
+      const int idx = silu_index(g, FR);
+      const int64_t v = silu_elem(g, row[ff + i], lut[idx], lut[idx + 1], FR, bad2);
+      if (v != 0) e2 = imax(e2, bitlen(v < 0 ? (int64_t)(0 - (uint64_t)v) : v) + eps);
+    }
+    rmax = block_max64(e2, sbuf);
+  }
+  const int64_t shr = imax(rmax - kQB, kNegBig);
   const int64_t plane = (int64_t)gridDim.x * ff;
   for (int i = i_lo + threadIdx.x; i < i_hi; i += kSiluPartThreads) {
-    const int32_t qv = (int32_t)rshc(P[(int64_t)m * ff + i], shr - eps);
+    const int32_t qv = (int32_t)rshc(Ps[i - i_lo], shr - eps);
     q[(int64_t)m * ldq + i] = qv;
-    if (planes != nullptr) {   // q's signed int8 limb planes [3][M][ff] for the exact GEMM (split_q_kernel's split)
+    if (planes != nullptr) {
       int32_t r = qv;
 #pragma unroll
       for (int l = 0; l < 3; ++l) {
@@ -465,6 +495,7 @@ __global__ __launch_bounds__(kSiluPartThreads) void silu_fin_kernel(const int64_
   }
   if (c == 0 && threadIdx.x == 0) sh[m] = shr;
 }
+
 
 // first_argmax split over column chunks for few rows (one block per row streams the whole row on one CU):
 // argmax_part_kernel, grid (M, C), writes each chunk's (maximum, its first index) to scratch slots; argmax_fin_kernel
@@ -604,7 +635,7 @@ static int silu_chunks(int ff) { return std::min(64, std::max(1, (ff + 1023) / 1
 
 extern "C" int64_t bx_silu_quant_scratch(int32_t M, int32_t ff) {
   if (M <= 0 || ff <= 0) return 0;
-  return (int64_t)M * ff * 8 + (int64_t)M * silu_chunks(ff) * 8;
+  return (int64_t)M * silu_chunks(ff) * 8 + (int64_t)M * 4;
 }
 
 extern "C" int bx_silu_quant_ws(const int64_t* gu, int64_t ldgu, int32_t ff, const int64_t* lut, int32_t FR, int32_t* q,
@@ -618,13 +649,15 @@ extern "C" int bx_silu_quant_ws(const int64_t* gu, int64_t ldgu, int32_t ff, con
              "scratch too small (%lld < %lld)", (long long)tmp_bytes, (long long)bx_silu_quant_scratch(M, ff));
   BX_REQUIRE(!planes || ff % 16 == 0, "limb planes need ff %% 16 == 0");
   const int C = silu_chunks(ff), chunk = (ff + C - 1) / C;
-  int64_t* P = (int64_t*)tmp;
-  int64_t* slots = P + (int64_t)M * ff;
-  const dim3 grid(M, C);
-  silu_part_kernel<<<grid, kSiluPartThreads, 0, (hipStream_t)stream>>>(gu, ldgu, ff, chunk, lut, FR, P, slots, err);
-  if (int rc = check_launch("silu_part_kernel")) return rc;
-  silu_fin_kernel<<<grid, kSiluPartThreads, 0, (hipStream_t)stream>>>(P, slots, ff, chunk, FR, q, ldq, sh, planes);
-  return check_launch("silu_fin_kernel");
+  BX_REQUIRE((int64_t)chunk * 8 <= 64 * 1024, "ff too large for the one-launch form");
+  int64_t* slots = (int64_t*)tmp;
+  int32_t* cnt = (int32_t*)(slots + (int64_t)M * C);
+  // BX_SILU_TICKS (tests): a shorter wait, down to 0, where blocks form the row maximum they have not seen
+  const char* et = getenv("BX_SILU_TICKS");
+  const uint64_t ticks = et ? (uint64_t)strtoull(et, nullptr, 10) : kSiluTicks;
+  silu_fused_kernel<<<dim3(M, C), kSiluPartThreads, (size_t)chunk * 8, (hipStream_t)stream>>>(
+      gu, ldgu, ff, chunk, lut, FR, slots, cnt, ticks, q, ldq, sh, planes, err);
+  return check_launch("silu_fused_kernel");
 }
 
 extern "C" int bx_first_argmax(const int64_t* v, int64_t ldv, int32_t M, int32_t N, int64_t* out, bx_stream_t stream) {

@@ -216,8 +216,9 @@ int bx_silu_quant(const int64_t* gu, int64_t ldgu, int32_t ff, const int64_t* lu
                   int64_t* sh, int32_t M, int32_t* err, bx_stream_t stream);
 
 /* bx_silu_quant split over column chunks of about 1024 elements, for few rows (one block per row leaves most CUs
- * idle): two launches on `stream`, with P and the chunk maxima in the caller's scratch (tmp, 8-byte aligned, at
- * least bx_silu_quant_scratch(M, ff) bytes; no contents kept). Same rule, outputs and flag as bx_silu_quant, the
+ * idle): one launch on `stream`; the chunks of a row exchange their maxima through the caller's workspace (tmp,
+ * 8-byte aligned, at least bx_silu_quant_scratch(M, ff) bytes, zero-filled before its first use and left
+ * zero-filled by every call; ff <= 524288). Same rule, outputs and flag as bx_silu_quant, the
  * reference stage it replaces (src/bitexact/exact/segs.py:120-128, 180-182). planes (optional, ff % 16 == 0): q's
  * signed int8 limb planes [3][M][ff] for bx_exact_linear_planes. */
 int bx_silu_quant_ws(const int64_t* gu, int64_t ldgu, int32_t ff, const int64_t* lut, int32_t FR, int32_t* q,

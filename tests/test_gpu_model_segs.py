@@ -142,6 +142,28 @@ def test_gu_silu_split(dev, M, ff):
     assert bool(ops.gu_silu_y(bad.to(dev), L, split=True)[2]) and R.gu_silu_y(bad.numpy(), lut)[2]
 
 
+@pytest.mark.parametrize("ticks", ["0", "1"])
+def test_gu_silu_split_exchange_fallback(dev, monkeypatch, ticks):
+    """The column chunks of a row exchange their maxima with a bounded wait; with the wait cut to 0 / 1 tick
+    (forced from the host), blocks that have not seen every chunk form the row maximum from gu themselves: same
+    q, sh and flag, on three calls in a row (the workspace's slots and counters are left zeroed)."""
+    from bitexact.exact import ops
+    M, ff = 32, 8192
+    g = torch.Generator().manual_seed(11)
+    gu = torch.randint(-(1 << 31), 1 << 31, (M, 2 * ff), generator=g)
+    gu[1, :ff] >>= 12
+    lut = R.exp2_table()
+    q, sh, flag = R.gu_silu_y(gu.numpy(), lut)
+    L = torch.from_numpy(lut).to(dev)
+    monkeypatch.setenv("BX_SILU_TICKS", ticks)
+    for _ in range(3):
+        qa, sha, ea = ops.gu_silu_y(gu.to(dev), L, split=True)
+        assert np.array_equal(qa.cpu().numpy(), q) and np.array_equal(sha.cpu().numpy(), sh) and bool(ea) == flag
+    monkeypatch.delenv("BX_SILU_TICKS")
+    qa, sha, _ = ops.gu_silu_y(gu.to(dev), L, split=True)
+    assert np.array_equal(qa.cpu().numpy(), q) and np.array_equal(sha.cpu().numpy(), sh)
+
+
 @pytest.mark.parametrize("split", [False, True])
 @pytest.mark.parametrize("M,N", [(1, 128256), (5, 1000), (3, 7), (32, 128256), (4, 40000)])
 def test_first_argmax(dev, M, N, split):
