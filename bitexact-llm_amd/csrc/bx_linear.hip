@@ -118,24 +118,51 @@ struct ColCtx {
   const int64_t* evp;
 };
 
-__device__ __forceinline__ ColCtx col_ctx(const LinArgs& p, int n) {
-  ColCtx c;
+// The column's raw context, loaded with no value-dependent step (a kernel requests it before its main loop and
+// forms the ColCtx after it, so the loads' latency hides behind the loop): the first min(kRes, R) list slots
+// are read whatever the count, and col_ctx_from masks them.
+struct ColPre {
+  int64_t d, g;
+  int32_t cnt;
+  int32_t ec[kRes];
+  int64_t ev[kRes];
+};
+
+__device__ __forceinline__ ColPre col_pre(const LinArgs& p, int n) {
+  ColPre c;
   const int nn = min(n, p.N - 1);
   c.d = p.d[nn];
-  c.gdr = p.g[nn] - c.d + p.FR;
+  c.g = p.g[nn];
+  c.cnt = p.R > 0 ? p.cnt[nn] : 0;
+#pragma unroll
+  for (int j = 0; j < kRes; ++j) {
+    const bool slot = j < p.R;   // uniform
+    c.ec[j] = slot ? p.ecol[(int64_t)nn * p.R + j] : 0;
+    c.ev[j] = slot ? p.eval[(int64_t)nn * p.R + j] : 0;
+  }
+  return c;
+}
+
+__device__ __forceinline__ ColCtx col_ctx_from(const LinArgs& p, int n, const ColPre& r) {
+  ColCtx c;
+  const int nn = min(n, p.N - 1);
+  c.d = r.d;
+  c.gdr = r.g - r.d + p.FR;
   c.corrupt = false;
-  c.cnt = p.R > 0 ? kcnt(p, p.cnt[nn], c.corrupt) : 0;   // entries stay inside the row's R slots
+  c.cnt = p.R > 0 ? kcnt(p, r.cnt, c.corrupt) : 0;   // entries stay inside the row's R slots
   c.wmax = (int)wave_max64(c.cnt);
   c.ecp = p.ecol + (int64_t)nn * p.R;
   c.evp = p.eval + (int64_t)nn * p.R;
 #pragma unroll
   for (int j = 0; j < kRes; ++j) {
     const bool has = j < c.cnt;
-    c.ec[j] = has ? kcol(p, c.ecp[j], c.corrupt) : 0;
-    c.ev[j] = has ? c.evp[j] : 0;
+    c.ec[j] = has ? kcol(p, r.ec[j], c.corrupt) : 0;
+    c.ev[j] = has ? r.ev[j] : 0;
   }
   return c;
 }
+
+__device__ __forceinline__ ColCtx col_ctx(const LinArgs& p, int n) { return col_ctx_from(p, n, col_pre(p, n)); }
 
 // The residuals of NR rows of the lane's column, gathered together: one wave-uniform branch per residual entry
 // with NR independent loads under it, so a column costs about wmax load latencies instead of NR wmax (per-row
@@ -1115,6 +1142,9 @@ __global__ __launch_bounds__(64 * NWV) void stream_kernel(LinArgs p) {
 
   const auto ra = __builtin_amdgcn_make_buffer_rsrc(const_cast<int8_t*>(p.a), (short)0, kBufRange, 0x00020000);
   const auto rw = __builtin_amdgcn_make_buffer_rsrc(const_cast<int8_t*>(p.w), (short)0, kBufRange, 0x00020000);
+  // exact: the epilogue context of the thread's column (tid % C), requested before the ring
+  ColPre cpre;
+  if constexpr (MODE == EXACT) cpre = col_pre(p, n0 + tid % C);
   int voff[LPW];
 #pragma unroll
   for (int i = 0; i < LPW; ++i) {
@@ -1225,7 +1255,7 @@ __global__ __launch_bounds__(64 * NWV) void stream_kernel(LinArgs p) {
     const int c = tid % C, rg = tid / C, n = n0 + c;
     const bool split = gridDim.y > 1;
     ColCtx cc;
-    if constexpr (MODE == EXACT) cc = col_ctx(p, n);
+    if constexpr (MODE == EXACT) cc = col_ctx_from(p, n, cpre);
     auto finish8 = [&](int m0, const int (&mrow)[8], const int64_t (&v)[8]) {
       int64_t B[8];
       if constexpr (MODE == EXACT) residual_rows<8>(p, cc, mrow, B, corrupt);
