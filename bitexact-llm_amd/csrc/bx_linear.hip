@@ -1674,13 +1674,14 @@ static bool stream_plan(int rows_a, int M_out, int N, int K, bool exact, bool pl
     const int per = (nch + want - 1) / want;
     if (per < 8) {
       // under 1024 k per block the split's fixed costs lose to the gemv, unless the caller brings q's limb
-      // planes (no split launch) and 65..96 limb rows: then 32-column blocks, K split in at most as many parts
-      // as keep every block resident at once (M = 32, N = 3072, K = 2048: 14.6 vs 18.9 us for the gemv)
+      // planes (no split launch) and 65..96 limb rows: then 32-column blocks, >= 1024 k each, in one round of
+      // blocks that covers at least 3/4 of the chip (M = 32, N = 3072, K = 2048: 14.1 vs 18.8 us for the gemv;
+      // N = 2048 stays on the gemv: 12.8 us with 256 blocks of 512 k, 14.1 with 128 blocks, vs 11.9)
       if (!planes || rows_a <= 64 || rows_a > 96) return false;
       s.nwv = 2;
       s.tiles_x = (N + 31) / 32;
-      s.split = std::max(1, std::min(cus / s.tiles_x, nch / 4));
-      if (s.tiles_x * s.split > cus || 2 * s.tiles_x * s.split < cus) return false;   // one round, half the chip
+      s.split = std::max(1, std::min(cus / s.tiles_x, nch / 8));
+      if (s.tiles_x * s.split > cus || 4 * s.tiles_x * s.split < 3 * cus) return false;
     } else {
       s.split = (nch + per - 1) / per;
     }

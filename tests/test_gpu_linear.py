@@ -338,14 +338,16 @@ def test_exact_linear_norm_planes(dev, M, N):
     assert np.array_equal(yb.cpu().numpy(), ref) and bool(f2.item()) == rflag
 
 
-@pytest.mark.parametrize("M,N", [(32, 3072), (22, 3000), (32, 2048)])
+@pytest.mark.parametrize("M,N", [(32, 3072), (22, 3080), (32, 4096)])
 def test_exact_linear_narrow_planes(dev, M, N):
     """Narrow N at K = 2048 with q's limb planes given: 32-column stream blocks with the K split over the zeroed
     workspace (without planes the gemv serves the shape); same y and flag as the gemv, and y matches the oracle
-    (partial last column tile at N = 3000, forced residual entries, 66 and 96 limb rows)."""
+    (partial last column tile at N = 3080, forced residual entries, 66 and 96 limb rows). N = 2048 keeps the gemv
+    either way."""
     from bitexact.exact import ops
     from bitexact.vllm_plugin.exact_gemm import exact_linear, needs_planes, plan
     K = 2048
+    assert plan(32, 2048, K, planes=True)[0] == "gemv" and not needs_planes(32, 2048, K)
     assert plan(M, N, K)[0] == "gemv"
     kern, _, split, blocks = plan(M, N, K, planes=True)
     assert kern == "stream" and split > 1 and blocks == -(-N // 32), plan(M, N, K, planes=True)
