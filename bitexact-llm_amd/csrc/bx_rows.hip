@@ -1,6 +1,7 @@
-// Row-wise integer stages around the GEMMs and the attention, one block per row (1024 threads: a decode step has
-// few rows, so each row spreads over a whole CU; softmax rows use 256) with wavefront
-// int64 reductions: RMSNorm + per-row quantization (segs.norm_quant, optionally after the residual add or the
+// Row-wise integer stages around the GEMMs and the attention, one block per row (1024 threads, 512 for the norm:
+// a decode step has few rows, so each row spreads over a whole CU; softmax rows use 256; the SiLU stage of few rows
+// goes over column chunks) with DPP wavefront int64 reductions: RMSNorm + per-row quantization (segs.norm_quant,
+// optionally after the residual add or the
 // embedding gather), SiLU gating + quantization (segs.silu_y + quant_silu), the masked softmax weights
 // (segs.softmax), and the attention output rule (segs.attn_out = div_round + regroup + quant).
 #include "bx_common.h"
