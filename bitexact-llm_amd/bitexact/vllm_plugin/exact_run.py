@@ -70,7 +70,7 @@ class ExactEngine:
         at FR (src/bitexact/vllm_plugin/exact_run.py:55-128 with the fused stages of its 130-155)."""
         N, G, HKV, HD = ids.shape[0], self.G, self.HKV, self.HD
         pos = pos.long().contiguous()
-        slot = torch.where(slot < 0, torch.zeros_like(slot), slot).long()
+        slot = slot.long().clamp(min=0)    # padding (slot < 0) -> the null block 0; one launch
         qpos = pos.view(-1, 1).expand(-1, G).contiguous()
         fl = self.fl
         x, q, sh, _ = ops.embed_norm(self.emb, ids, *self.ga[0], flag=fl)
