@@ -58,8 +58,29 @@ def _norm_quant(x, gm, ge, flag):
     return q, sh
 
 
-def norm_quant(x, gm, ge, err=None, flag=None):
+@op("norm_planes(Tensor x, Tensor gm, Tensor ge, Tensor(a!) flag) -> (Tensor, Tensor, Tensor)",
+    lambda x, gm, ge, flag: (empty(x.shape, torch.int32, x), empty((3, *x.shape), torch.int8, x),
+                             empty(x.shape[:1], torch.long, x)))
+def _norm_planes(x, gm, ge, flag):
+    _hip.require_cuda(x, gm, ge)
+    assert x.dtype == torch.int64 and x.stride(-1) == 1 and x.dim() == 2
+    M, D = x.shape
+    q = torch.empty(M, D, dtype=torch.int32, device=x.device)
+    pl = torch.empty(3, M, D, dtype=torch.int8, device=x.device)
+    sh = torch.empty(M, dtype=torch.long, device=x.device)
+    gm, ge = gm.contiguous().long(), ge.contiguous().long()
+    _hip.call("bx_add_rmsnorm_quant_planes", _hip.ptr(x), x.stride(0), None, 0, _hip.ptr(gm), _hip.ptr(ge),
+              _hip.ptr(q), D, _hip.ptr(sh), _hip.ptr(pl), M, D, FR, FN, _hip.ptr(flag), _hip.stream_of(x))
+    return q, pl, sh
+
+
+def norm_quant(x, gm, ge, err=None, flag=None, planes=False):
+    """segs.norm_quant -> (q, sh, err); planes=True: q is returned as (q, limb planes int8 [3, M, D]) for
+    exact_linear's q_planes."""
     fl = _flag(x.device, flag)
+    if planes:
+        q, pl, sh = _norm_planes(x, gm, ge, fl)
+        return (q, pl), sh, _or(err, fl, flag)
     q, sh = _norm_quant(x, gm, ge, fl)
     return q, sh, _or(err, fl, flag)
 

@@ -114,8 +114,12 @@ class ExactEngine:
 
     def logits(self, h):
         """Final residual rows [M, D] -> logits int64 [M, V] at FR (exact_run.py:157-175)."""
+        lm = self.fused["lm"]
+        if lm.needs_planes(h.shape[0]):   # the norm kernel writes q's limb planes: no split launch
+            (q, pl), sh, _ = ops.norm_quant(h, *self.gf, flag=self.fl, planes=True)
+            return lm(q, sh, self.fl, True, q_planes=pl)
         q, sh, _ = ops.norm_quant(h, *self.gf, flag=self.fl)
-        return self.fused["lm"](q, sh, self.fl, True)
+        return lm(q, sh, self.fl, True)
 
     def greedy(self, logits):
         """The greedy token of each logits row: its first maximum."""

@@ -603,11 +603,11 @@ extern "C" int bx_add_rmsnorm_quant_planes(int64_t* x, int64_t ldx, const int64_
                                            const int64_t* ge, int32_t* q, int64_t ldq, int64_t* sh, int8_t* planes,
                                            int32_t M, int32_t D, int32_t FR, int32_t FN, int32_t* err,
                                            bx_stream_t stream) {
-  BX_REQUIRE(y && ldy >= D, "y: null or ldy too small");
+  BX_REQUIRE(!y || ldy >= D, "ldy too small");
   BX_REQUIRE(gm && ge && q && sh && planes, "null pointer");
   BX_REQUIRE(D % 16 == 0, "D %% 16 != 0 (the limb planes are the exact GEMM's K-major operand)");
   NormArgs p = {x, ldx, y, ldy, nullptr, nullptr, gm, ge, q, ldq, sh, D, 0, FR, FN, err, planes, (int64_t)M * D};
-  return launch_norm(p, SRC_ADD, M, stream);
+  return launch_norm(p, y ? SRC_ADD : SRC_X, M, stream);   // y null: the norm of x as it is (x not written)
 }
 
 extern "C" int bx_embed_rmsnorm_quant(const int32_t* emb, const int64_t* ids, int64_t* x, int64_t ldx,

@@ -196,7 +196,9 @@ int bx_add_rmsnorm_quant(int64_t* x, int64_t ldx, const int64_t* y, int64_t ldy,
 
 /* bx_add_rmsnorm_quant (gm required) that also writes the new q's signed int8 limb planes (planes int8
  * [3][M][D], limb i of q[m][k] at i M D + m D + k) for bx_exact_linear_planes. D % 16 == 0. Replaces the same
- * reference stage (exact_fuse.add_norm, src/bitexact/vllm_plugin/exact_fuse.py:361-364). */
+ * reference stage (exact_fuse.add_norm, src/bitexact/vllm_plugin/exact_fuse.py:361-364). y null: no add, the
+ * norm of x as it is (bx_rmsnorm_quant with the planes; x is not written), e.g. the final norm before lm_head
+ * (segs.norm_quant, src/bitexact/exact/segs.py:59-63). */
 int bx_add_rmsnorm_quant_planes(int64_t* x, int64_t ldx, const int64_t* y, int64_t ldy, const int64_t* gm,
                                 const int64_t* ge, int32_t* q, int64_t ldq, int64_t* sh, int8_t* planes, int32_t M,
                                 int32_t D, int32_t FR, int32_t FN, int32_t* err, bx_stream_t stream);

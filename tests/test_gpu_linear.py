@@ -338,6 +338,36 @@ def test_exact_linear_norm_planes(dev, M, N):
     assert np.array_equal(yb.cpu().numpy(), ref) and bool(f2.item()) == rflag
 
 
+def test_norm_quant_planes(dev):
+    """The norm without an add (the final norm before lm_head) writing q's limb planes: same q and sh as
+    norm_quant, x left as it was, planes = the signed base-256 split of q; the exact linear on them = without."""
+    from bitexact.exact import ops
+    from bitexact.vllm_plugin.exact_gemm import exact_linear, needs_planes
+    M, K, N = 32, 512, 16384
+    g = torch.Generator().manual_seed(8)
+    x = torch.randint(-(1 << 35), 1 << 35, (M, K), generator=g).to(dev)
+    gm, ge = torch.randint(-255, 256, (K,), generator=g).to(dev), torch.randint(-14, -6, (K,), generator=g).to(dev)
+    x0 = x.clone()
+    q1, sh1, e1 = ops.norm_quant(x, gm, ge)
+    (q2, pl), sh2, e2 = ops.norm_quant(x, gm, ge, planes=True)
+    assert torch.equal(x, x0) and torch.equal(q1, q2) and torch.equal(sh1, sh2) and bool(e1) == bool(e2)
+    r = q1.long()
+    for i in range(3):
+        lo = ((r + 128) & 255) - 128
+        assert torch.equal(pl[i].long(), lo)
+        r = (r - lo) >> 8
+    assert needs_planes(M, N, K)
+    dec = _dec(_bf16(N, K, 12))
+    limbs = torch.from_numpy(dec["limbs"]).to(dev)
+    d, gg = torch.from_numpy(dec["d"]).to(dev), torch.from_numpy(dec["g"]).to(dev)
+    cnt, ec, ev, Rr = _ell(dec, N, dev)
+    f1 = torch.zeros(1, dtype=torch.int32, device=dev)
+    f2 = torch.zeros(1, dtype=torch.int32, device=dev)
+    ya = exact_linear(q1, sh1, limbs, d, gg, cnt, ec, ev, Rr, f1, True)
+    yb = exact_linear(q2, sh2, limbs, d, gg, cnt, ec, ev, Rr, f2, True, q_planes=pl)
+    assert torch.equal(ya, yb) and f1.item() == f2.item()
+
+
 @pytest.mark.parametrize("M,N", [(32, 3072), (22, 3080), (32, 4096)])
 def test_exact_linear_narrow_planes(dev, M, N):
     """Narrow N at K = 2048 with q's limb planes given: 32-column stream blocks with the K split over the zeroed
