@@ -54,6 +54,7 @@ SIGNATURES = {
     "bx_add_rmsnorm_quant": (ctypes.c_int, [P, I64, P, I64, P, P, P, I64, P, I32, I32, I32, I32, P, P]),
     "bx_add_rmsnorm_quant_planes": (ctypes.c_int, [P, I64, P, I64, P, P, P, I64, P, P, I32, I32, I32, I32, P, P]),
     "bx_embed_rmsnorm_quant": (ctypes.c_int, [P, P, P, I64, P, P, P, I64, P, I32, I32, I32, I32, P, P]),
+    "bx_embed_rmsnorm_quant_planes": (ctypes.c_int, [P, P, P, I64, P, P, P, I64, P, P, I32, I32, I32, I32, P, P]),
     "bx_silu_quant": (ctypes.c_int, [P, I64, I32, P, I32, P, I64, P, I32, P, P]),
     "bx_silu_quant_ws": (ctypes.c_int, [P, I64, I32, P, I32, P, I64, P, P, I32, P, P, I64, P]),
     "bx_silu_quant_scratch": (I64, [I32, I32]),

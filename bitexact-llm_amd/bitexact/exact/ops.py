@@ -266,6 +266,26 @@ def _embed_fake(emb, ids, gm, ge, flag):
     return empty((M, D), torch.long, emb), empty((M, D), torch.int32, emb), empty((M,), torch.long, emb)
 
 
+@op("embed_norm_planes(Tensor emb, Tensor ids, Tensor gm, Tensor ge, Tensor(a!) flag) -> (Tensor, Tensor, Tensor, "
+    "Tensor)", lambda emb, ids, gm, ge, flag: (*_embed_fake(emb, ids, gm, ge, flag)[:2],
+                                               empty((3, ids.numel(), emb.shape[1]), torch.int8, emb),
+                                               empty((ids.numel(),), torch.long, emb)))
+def _embed_norm_planes(emb, ids, gm, ge, flag):
+    _hip.require_cuda(emb, ids, gm, ge)
+    assert emb.dtype == torch.int32 and emb.is_contiguous()
+    ids = ids.reshape(-1).contiguous().long()
+    M, D = ids.shape[0], emb.shape[1]
+    x = torch.empty(M, D, dtype=torch.long, device=emb.device)
+    q = torch.empty(M, D, dtype=torch.int32, device=emb.device)
+    pl = torch.empty(3, M, D, dtype=torch.int8, device=emb.device)
+    sh = torch.empty(M, dtype=torch.long, device=emb.device)
+    gm, ge = gm.contiguous().long(), ge.contiguous().long()
+    _hip.call("bx_embed_rmsnorm_quant_planes", _hip.ptr(emb), _hip.ptr(ids), _hip.ptr(x), D, _hip.ptr(gm),
+              _hip.ptr(ge), _hip.ptr(q), D, _hip.ptr(sh), _hip.ptr(pl), M, D, FR, FN, _hip.ptr(flag),
+              _hip.stream_of(emb))
+    return x, q, pl, sh
+
+
 @op("embed_norm(Tensor emb, Tensor ids, Tensor gm, Tensor ge, Tensor(a!) flag) -> (Tensor, Tensor, Tensor)",
     _embed_fake)
 def _embed_norm(emb, ids, gm, ge, flag):
@@ -282,9 +302,13 @@ def _embed_norm(emb, ids, gm, ge, flag):
     return x, q, sh
 
 
-def embed_norm(emb, ids, gm, ge, err=None, flag=None):
-    """x = emb[ids].long() (emb int32 [V, D]) and its pre_norm (src/bitexact/exact/model.py:130-132) -> (x, q, sh, err)."""
+def embed_norm(emb, ids, gm, ge, err=None, flag=None, planes=False):
+    """x = emb[ids].long() (emb int32 [V, D]) and its pre_norm (src/bitexact/exact/model.py:130-132) -> (x, q, sh, err);
+    planes=True: q is returned as (q, limb planes int8 [3, M, D]) for exact_linear's q_planes."""
     fl = _flag(emb.device, flag)
+    if planes:
+        x, q, pl, sh = _embed_norm_planes(emb, ids, gm, ge, fl)
+        return x, (q, pl), sh, _or(err, fl, flag)
     x, q, sh = _embed_norm(emb, ids, gm, ge, fl)
     return x, q, sh, _or(err, fl, flag)
 

@@ -73,8 +73,11 @@ class ExactEngine:
         slot = slot.long().clamp(min=0)    # padding (slot < 0) -> the null block 0; one launch
         qpos = pos.view(-1, 1).expand(-1, G).contiguous()
         fl = self.fl
-        x, q, sh, _ = ops.embed_norm(self.emb, ids, *self.ga[0], flag=fl)
-        pl = None                             # q's limb planes, when the layer-end norm wrote them
+        pl = None                             # q's limb planes, when the norm before the layer wrote them
+        if self.fused[0, "wqkv"].needs_planes(N):
+            x, (q, pl), sh, _ = ops.embed_norm(self.emb, ids, *self.ga[0], flag=fl, planes=True)
+        else:
+            x, q, sh, _ = ops.embed_norm(self.emb, ids, *self.ga[0], flag=fl)
         for i in range(self.L):
             y = self.fused[i, "wqkv"](q, sh, fl, False, q_planes=pl)
             if kvs is None:

@@ -618,6 +618,16 @@ extern "C" int bx_embed_rmsnorm_quant(const int32_t* emb, const int64_t* ids, in
   return launch_norm(p, SRC_EMB, M, stream);
 }
 
+extern "C" int bx_embed_rmsnorm_quant_planes(const int32_t* emb, const int64_t* ids, int64_t* x, int64_t ldx,
+                                             const int64_t* gm, const int64_t* ge, int32_t* q, int64_t ldq,
+                                             int64_t* sh, int8_t* planes, int32_t M, int32_t D, int32_t FR,
+                                             int32_t FN, int32_t* err, bx_stream_t stream) {
+  BX_REQUIRE(emb && ids && gm && ge && q && sh && planes, "null pointer");
+  BX_REQUIRE(D % 16 == 0, "D %% 16 != 0 (the limb planes are the exact GEMM's K-major operand)");
+  NormArgs p = {x, ldx, nullptr, 0, emb, ids, gm, ge, q, ldq, sh, D, 0, FR, FN, err, planes, (int64_t)M * D};
+  return launch_norm(p, SRC_EMB, M, stream);
+}
+
 extern "C" int bx_silu_quant(const int64_t* gu, int64_t ldgu, int32_t ff, const int64_t* lut, int32_t FR, int32_t* q,
                              int64_t ldq, int64_t* sh, int32_t M, int32_t* err, bx_stream_t stream) {
   BX_REQUIRE(M >= 0 && ff > 0 && ldgu >= 2 * (int64_t)ff && ldq >= ff, "bad sizes");

@@ -209,6 +209,11 @@ int bx_add_rmsnorm_quant_planes(int64_t* x, int64_t ldx, const int64_t* y, int64
 int bx_embed_rmsnorm_quant(const int32_t* emb, const int64_t* ids, int64_t* x, int64_t ldx, const int64_t* gm,
                            const int64_t* ge, int32_t* q, int64_t ldq, int64_t* sh, int32_t M, int32_t D, int32_t FR,
                            int32_t FN, int32_t* err, bx_stream_t stream);
+/* bx_embed_rmsnorm_quant (gm required) that also writes q's signed int8 limb planes (as
+ * bx_add_rmsnorm_quant_planes, D % 16 == 0) for the first layer's bx_exact_linear_planes. Same reference stage. */
+int bx_embed_rmsnorm_quant_planes(const int32_t* emb, const int64_t* ids, int64_t* x, int64_t ldx, const int64_t* gm,
+                                  const int64_t* ge, int32_t* q, int64_t ldq, int64_t* sh, int8_t* planes, int32_t M,
+                                  int32_t D, int32_t FR, int32_t FN, int32_t* err, bx_stream_t stream);
 
 /* Replaces Segs.gu_silu_y = segs.silu_y + quant_silu (src/bitexact/exact/segs.py:120-128, 180-182) over
  * ops.silu_mul (src/bitexact/exact/ops.py:119-130): gu int64 [M, 2 ff] = [gate | up] at FR; q int32 [M, ff],

@@ -340,7 +340,8 @@ def test_exact_linear_norm_planes(dev, M, N):
 
 def test_norm_quant_planes(dev):
     """The norm without an add (the final norm before lm_head) writing q's limb planes: same q and sh as
-    norm_quant, x left as it was, planes = the signed base-256 split of q; the exact linear on them = without."""
+    norm_quant, x left as it was, planes = the signed base-256 split of q; the exact linear on them = without. The
+    embedding norm's planes likewise."""
     from bitexact.exact import ops
     from bitexact.vllm_plugin.exact_gemm import exact_linear, needs_planes
     M, K, N = 32, 512, 16384
@@ -366,6 +367,17 @@ def test_norm_quant_planes(dev):
     ya = exact_linear(q1, sh1, limbs, d, gg, cnt, ec, ev, Rr, f1, True)
     yb = exact_linear(q2, sh2, limbs, d, gg, cnt, ec, ev, Rr, f2, True, q_planes=pl)
     assert torch.equal(ya, yb) and f1.item() == f2.item()
+    # the embedding norm's planes (the first layer's input)
+    emb = torch.randint(-(1 << 30), 1 << 30, (300, K), generator=g, dtype=torch.int64).to(torch.int32).to(dev)
+    ids = torch.randint(0, 300, (M,), generator=g).to(dev)
+    xa, qa, sha, ea = ops.embed_norm(emb, ids, gm, ge)
+    xb, (qb, plb), shb, eb = ops.embed_norm(emb, ids, gm, ge, planes=True)
+    assert torch.equal(xa, xb) and torch.equal(qa, qb) and torch.equal(sha, shb) and bool(ea) == bool(eb)
+    r = qa.long()
+    for i in range(3):
+        lo = ((r + 128) & 255) - 128
+        assert torch.equal(plb[i].long(), lo)
+        r = (r - lo) >> 8
 
 
 @pytest.mark.parametrize("M,N", [(32, 3072), (22, 3080), (32, 4096)])
