@@ -197,14 +197,16 @@ def bench_prefill(dev, reps=10):
         gw = torch.Generator(device=dev).manual_seed(N + K)
         w = (torch.randn(N, K, generator=gw, device=dev) * 0.02).to(torch.bfloat16)
         dec = decompose(w)
-        del w
         q, sh = quant40(torch.randn(M, K, generator=gc, dtype=torch.float64).to(dev))
         flag = torch.zeros(1, dtype=torch.int32, device=dev)
+        outs = {}
 
         def run(i):
-            exact_linear(q, sh, dec["limbs"], dec["d"], dec["g"], dec["ell_cnt"], dec["ell_col"], dec["ell_val"],
-                         dec["R"], flag, True)
+            outs[0] = exact_linear(q, sh, dec["limbs"], dec["d"], dec["g"], dec["ell_cnt"], dec["ell_col"],
+                                   dec["ell_val"], dec["R"], flag, True)
         s = time_graph(run, 2, reps, stream) / reps
+        check_prefill_sample(name, w, q, sh, outs[0], flag)
+        del w
         ops = 9 * 2 * M * N * K
         tops = ops / s / 1e12
         res.append({"gemm": name, "M": M, "N": N, "K": K, "us": round(s * 1e6, 1), "TOPS": round(tops, 1),
@@ -216,6 +218,26 @@ def bench_prefill(dev, reps=10):
         del dec, q
         torch.cuda.empty_cache()
     return res, tot_ops / tot_s / 1e12
+
+
+def check_prefill_sample(name, w, q, sh, y, flag, nrows=4, ncols=64):
+    """The timed output against oracle/bxref.py's exact linear on a sample: nrows rows (first, last, two seeded)
+    x ncols columns (first, last, seeded). The decomposition is row-local, so the oracle decomposes only the
+    sampled weight rows. Raises if any sampled output or the flag differs."""
+    import numpy as np
+    import torch
+    sys.path.insert(0, HERE)
+    from oracle import bxref as R
+    M, N = y.shape
+    rng = np.random.default_rng(M + N)
+    rows = np.unique(np.concatenate([[0, M - 1], rng.integers(0, M, nrows - 2)]))
+    cols = np.unique(np.concatenate([[0, N - 1], rng.integers(0, N, ncols - 2)]))
+    dec = R.decompose(w[torch.from_numpy(cols).to(w.device)].cpu().view(torch.int16).numpy())
+    ref, rflag = R.exact_linear(q[torch.from_numpy(rows).to(q.device)].cpu().long().numpy(),
+                                dec, sh[torch.from_numpy(rows).to(sh.device)].cpu().numpy())
+    got = y.cpu().numpy()[np.ix_(rows, cols)]
+    if not np.array_equal(got, ref) or (rflag and not bool(flag.item())):
+        raise AssertionError(f"exact prefill {name}: sampled outputs differ from the oracle")
 
 
 def bench_attention(dev, reps=20):
@@ -365,7 +387,7 @@ def _blas_threads():
     return max([i.get("num_threads", 1) for i in threadpool_info()] or [1])
 
 
-def cpu_baseline(budget_s=10.0):
+def cpu_baseline(budget_s=6.0):
     """oracle/bxref.py's float64 restatement of the int8 GEMM (the reference's CPU path imm,
     src/bitexact/int8/ops.py:87-90) on the config-2 shapes at M = 8, on the host cores; GB/s of the same
     algorithmic bytes as the GPU figure."""
@@ -390,7 +412,7 @@ def cpu_baseline(budget_s=10.0):
                       f"{t_tot:.1f} s of GEMM time"}
 
 
-def cpu_baseline_exact(budget_s=8.0):
+def cpu_baseline_exact(budget_s=6.0):
     """The exact linear on the host cores as the reference's CPU path computes it: oracle/bxref.py's float64
     wmm_f64 + residual + epilogue (src/bitexact/exact/wmm.py:117-150) on config 1 (M = 8, K = N = 2048) and on
     config 3's q/o shape (M = 2048, K = N = 2048); effective limb-op TOPS (9 x 2 M N K per call), as the GPU's."""

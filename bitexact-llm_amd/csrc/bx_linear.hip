@@ -1681,6 +1681,8 @@ static bool stream_plan(int rows_a, int M_out, int N, int K, bool exact, bool pl
       s.nwv = 2;
       s.tiles_x = (N + 31) / 32;
       s.split = std::max(1, std::min(cus / s.tiles_x, nch / 8));
+      const int per_split = (nch + s.split - 1) / s.split;   // k chunks per block; no block left without k
+      s.split = (nch + per_split - 1) / per_split;
       if (s.tiles_x * s.split > cus || 4 * s.tiles_x * s.split < 3 * cus) return false;
     } else {
       s.split = (nch + per - 1) / per;
@@ -2133,7 +2135,7 @@ extern "C" int bx_exact_linear_planes_plan(int32_t M, int32_t N, int32_t K, int3
 }
 
 // The int8 GEMM's plan for M output rows of nl stacked limbs (nl = 0: the raw int32 GEMM of M stacked rows):
-// out[0] = 1 gemv, 3 tile, 4 staged; out[1] = tile configuration (-1 otherwise); out[2] = K splits; out[3] =
+// out[0] = 1 gemv, 3 tile, 4 staged, 5 stream; out[1] = tile configuration (-1 otherwise); out[2] = K splits; out[3] =
 // blocks per split; out[4] = gemv column groups (16 columns each); out[5] = gemv row parts.
 extern "C" int bx_int8_gemm_plan(int32_t M, int32_t N, int32_t K, int32_t nl, int32_t* out) {
   BX_REQUIRE(out && M > 0 && N > 0 && K > 0 && nl >= 0 && nl <= 3, "bad plan query");

@@ -397,7 +397,7 @@ __global__ __launch_bounds__(kRowThreads) void attn_out_kernel(const int64_t* nu
 }
 
 // The same stage split over column chunks for few rows (one block per row would leave most CUs idle while each
-// streams its 16 ff bytes of gate | up): grid (M, C), chunks of about 1024 columns.
+// streams its 16 ff bytes of gate | up): grid (C, M), chunk index fastest, chunks of about 1024 columns.
 constexpr int kSiluPartThreads = 256;
 // Block (m, c) keeps its chunk's P in LDS, publishes the chunk's exponent maximum
 // (as emax - kNegBig + 1; 0 = not yet published) and waits for the other chunks of its row for at most `ticks` of
@@ -413,7 +413,7 @@ __global__ __launch_bounds__(kSiluPartThreads) void silu_fused_kernel(const int6
   extern __shared__ __align__(16) int64_t Ps[];   // [chunk]
   __shared__ int64_t sbuf[16];
   __shared__ int64_t s_row;
-  const int m = blockIdx.x, c = blockIdx.y, C = gridDim.y;
+  const int m = blockIdx.y, c = blockIdx.x, C = gridDim.x;   // chunk index fastest: a row's chunks run together
   const int64_t* row = gu + (int64_t)m * ldgu;
   const int i_lo = c * chunk, i_hi = min(ff, i_lo + chunk);
   const int eps = -2 * (int)FR;
@@ -463,7 +463,10 @@ __global__ __launch_bounds__(kSiluPartThreads) void silu_fused_kernel(const int6
     if (seen) atomicMax((long long*)&s_row, (long long)(v - 1 + kNegBig));
   }
   const bool all = __syncthreads_and(seen);
-  if (threadIdx.x == 0 && atomicAdd(&cnt[m], 1) == C - 1) {   // every block of the row has read the slots
+  // The counter bump releases this block's own publish (thread 0's slot store lands before the count does) and
+  // the last block acquires before it clears: no publish can arrive after the row's slots were reset.
+  if (threadIdx.x == 0 &&
+      __hip_atomic_fetch_add(&cnt[m], 1, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT) == C - 1) {
     for (int j = 0; j < C; ++j) ws_store(&slots[(int64_t)m * C + j], 0);
     atomicExch(&cnt[m], 0);
   }
@@ -480,7 +483,7 @@ __global__ __launch_bounds__(kSiluPartThreads) void silu_fused_kernel(const int6
     rmax = block_max64(e2, sbuf);
   }
   const int64_t shr = imax(rmax - kQB, kNegBig);
-  const int64_t plane = (int64_t)gridDim.x * ff;
+  const int64_t plane = (int64_t)gridDim.y * ff;
   for (int i = i_lo + threadIdx.x; i < i_hi; i += kSiluPartThreads) {
     const int32_t qv = (int32_t)rshc(Ps[i - i_lo], shr - eps);
     q[(int64_t)m * ldq + i] = qv;
@@ -660,13 +663,14 @@ extern "C" int bx_silu_quant_ws(const int64_t* gu, int64_t ldgu, int32_t ff, con
              "scratch too small (%lld < %lld)", (long long)tmp_bytes, (long long)bx_silu_quant_scratch(M, ff));
   BX_REQUIRE(!planes || ff % 16 == 0, "limb planes need ff %% 16 == 0");
   const int C = silu_chunks(ff), chunk = (ff + C - 1) / C;
-  BX_REQUIRE((int64_t)chunk * 8 <= 64 * 1024, "ff too large for the one-launch form");
+  // dynamic LDS (the chunk's products) plus the kernel's static LDS must stay within the default 64 KiB
+  BX_REQUIRE((int64_t)chunk * 8 <= 63 * 1024, "ff too large for the one-launch form");
   int64_t* slots = (int64_t*)tmp;
   int32_t* cnt = (int32_t*)(slots + (int64_t)M * C);
   // BX_SILU_TICKS (tests): a shorter wait, down to 0, where blocks form the row maximum they have not seen
   const char* et = getenv("BX_SILU_TICKS");
   const uint64_t ticks = et ? (uint64_t)strtoull(et, nullptr, 10) : kSiluTicks;
-  silu_fused_kernel<<<dim3(M, C), kSiluPartThreads, (size_t)chunk * 8, (hipStream_t)stream>>>(
+  silu_fused_kernel<<<dim3(C, M), kSiluPartThreads, (size_t)chunk * 8, (hipStream_t)stream>>>(
       gu, ldgu, ff, chunk, lut, FR, slots, cnt, ticks, q, ldq, sh, planes, err);
   return check_launch("silu_fused_kernel");
 }

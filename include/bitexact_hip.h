@@ -116,7 +116,7 @@ int bx_int8_gemm(const int8_t* a, const int8_t* w, int32_t* c, int32_t R, int32_
 int bx_int8_gemm_join(const int8_t* a, const int8_t* w, int64_t* y, int32_t M, int32_t N, int32_t K, int32_t nl,
                       void* ws, int64_t ws_bytes, bx_stream_t stream);
 /* Introspection, no reference counterpart: the int8 GEMM's kernel for M rows of nl limbs (nl = 0: raw int32 GEMM of M
- * stacked rows). out int32 [6] = {kernel: 1 gemv, 3 tile, 4 staged; tile config or -1; K splits; blocks per split;
+ * stacked rows). out int32 [6] = {kernel: 1 gemv, 3 tile, 4 staged, 5 stream; tile config or -1; K splits; blocks per split;
  * gemv column groups; gemv row parts}. */
 int bx_int8_gemm_plan(int32_t M, int32_t N, int32_t K, int32_t nl, int32_t* out);
 int64_t bx_int8_gemm_workspace(int32_t M, int32_t N, int32_t K, int32_t nl); /* raw int_mm: M = R, nl = 1 */
