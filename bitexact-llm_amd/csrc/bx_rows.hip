@@ -463,10 +463,11 @@ __global__ __launch_bounds__(kSiluPartThreads) void silu_fused_kernel(const int6
     if (seen) atomicMax((long long*)&s_row, (long long)(v - 1 + kNegBig));
   }
   const bool all = __syncthreads_and(seen);
-  // The counter bump releases this block's own publish (thread 0's slot store lands before the count does) and
-  // the last block acquires before it clears: no publish can arrive after the row's slots were reset.
-  if (threadIdx.x == 0 &&
-      __hip_atomic_fetch_add(&cnt[m], 1, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT) == C - 1) {
+  // Thread 0's own publish (an agent-scope store) is complete before its count (s_waitcnt), so no publish can
+  // arrive after the row's last block has reset the slots. (An agent-scope release / acquire fence would write back
+  // and invalidate the whole L2 on this chip; the waits on the coherent stores are all that is needed.)
+  if (threadIdx.x == 0) __builtin_amdgcn_s_waitcnt(0);
+  if (threadIdx.x == 0 && atomicAdd(&cnt[m], 1) == C - 1) {
     for (int j = 0; j < C; ++j) ws_store(&slots[(int64_t)m * C + j], 0);
     atomicExch(&cnt[m], 0);
   }
