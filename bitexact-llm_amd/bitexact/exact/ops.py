@@ -1,4 +1,7 @@
-"""Exact-mode row stages on HIP (src/bitexact/exact/segs.py, src/bitexact/exact/ops.py).
+"""Exact-mode integer primitives and row stages on HIP (src/bitexact/exact/ops.py, src/bitexact/exact/segs.py).
+
+The reference's primitives, same names and contracts (device tensors; the integers of the reference's CPU tensors):
+rshc, div_round, combine, shift_round_hl, quant, rms, exp2neg_lut, silu_mul, softmax_w.
 
 Stages with a bound check return err (a bool tensor, or'ed into the caller's `err`); with flag= (an int32 [1]
 device tensor) they set that flag instead and pass err through, so a caller chaining many stages keeps one flag
@@ -15,16 +18,96 @@ gu_silu_y(y, lut, err)          Segs.gu_silu_y: silu(gate) up + quantization at 
 
 import torch
 
-from bitexact import _hip
+from bitexact import _elem, _hip
 from bitexact._ops import empty, op
 from bitexact.exact.consts import FR
 
-FN = 40
+QB = 22                         # activation rows: |q| <= 2^22 (3 int8 limbs)
+FN = 40                         # normalized activations before quantization
 FK, FV, FP = 17, 19, 22
 FT = 30                         # cos / sin fractional bits (src/bitexact/exact/consts.py:24)
-FZ = 26
-L2E28 = 387270501
+FT2 = 26                        # exponent argument t of 2^-t
+FZ = 26                         # softmax z = score - max
+L2E28 = 387270501               # round(log2(e) 2^28)
+L2E30 = 1549082005              # round(log2(e) 2^30)
 L2E28_HD = {64: L2E28, 128: 273841598}
+EPS60 = 11529215046068          # round(1e-5 2^60)
+NEG_BIG = -(1 << 20)
+
+
+# ---- integer primitives (src/bitexact/exact/ops.py:25-143), element-wise and row kernels of csrc/bx_elem.hip ----
+def rshc(x, s):
+    """round(x / 2^s) for a tensor or int s (s <= 0: x 2^-s), shifts clamped to [-62, 62]
+    (src/bitexact/exact/ops.py:25-34)."""
+    return _elem.elem(_elem.RSHC, x, s)[0]
+
+
+def div_round(a, p, r, chunk=28):
+    """round(a 2^p / r), exact, for |a| < 2^62, 0 < r < 2^34 (src/bitexact/exact/ops.py:37-57: the 28-bit long
+    division's value; the kernel takes its short form where that cannot wrap)."""
+    assert chunk == 28, "the long division runs in 28-bit chunks"
+    return _elem.elem(_elem.DIVROUND, a, p, r)[0]
+
+
+def combine(T, d, B):
+    """(H, L) with H 2^32 + L = T 2^d + B, 0 <= L < 2^32 (src/bitexact/exact/ops.py:60-66)."""
+    H, L = _elem.elem(_elem.COMBINE, T, d, B)
+    return H, L
+
+
+def shift_round_hl(H, L, p):
+    """round((H 2^32 + L) 2^p), 0 <= L < 2^32 (src/bitexact/exact/ops.py:69-79)."""
+    return _elem.elem(_elem.SHRHL, H, L, p)[0]
+
+
+def quant(P, eps):
+    """Per-row power-of-two quantization of P 2^eps (P int64 [..., K], eps an int or a tensor broadcastable to P)
+    -> (q int64, |q| <= 2^22, sh [...]) (src/bitexact/exact/ops.py:82-89)."""
+    K = P.shape[-1]
+    lead = P.shape[:-1]
+    P2 = P.reshape(-1, K)
+    if torch.is_tensor(eps):
+        eps = eps.expand(P.shape).reshape(P2.shape)
+    q, sh = _elem.row(_elem.R_QUANT, P2, eps)
+    return q.view(P.shape), sh.view(lead)
+
+
+def rms(x):
+    """sqrt(mean(x^2) + 1e-5) of each row of x int64 [M, D] at FR as (r, er): r 2^er, 2^30 <= r < 2^31; D a power of
+    two <= 4096 (src/bitexact/exact/ops.py:92-105)."""
+    D = x.shape[-1]
+    lg = D.bit_length() - 1
+    assert D == 1 << lg and lg <= 12, "row length a power of two <= 4096"
+    r, er = _elem.row(_elem.R_RMS, x, ia=(FR,))
+    return r, er
+
+
+def exp2neg_lut(t, lut, out_bits):
+    """2^-t at out_bits for t >= 0 at FT2 bits: the 2^-f table (step 2^-14, at 2^60) and linear interpolation
+    (src/bitexact/exact/ops.py:108-116)."""
+    return _elem.elem(_elem.EXP2NEG, t, lut=lut, iarg=out_bits)[0]
+
+
+def silu_mul(g, u, lut):
+    """silu(g) u for g, u at FR -> (P, eps, ok): value P 2^eps, ok a bool device scalar (every |silu| |u| < 2^62 and
+    |g| <= 2^32) (src/bitexact/exact/ops.py:119-130)."""
+    fl = _elem.flag_for(g.device)
+    P = _elem.elem(_elem.SILU_MUL, g, u, lut=lut, iarg=FR, flag=fl)[0]
+    return P, -2 * FR, fl[0] == 0
+
+
+def softmax_w(raw, ok, sh, kbits, lut, fp, l2e=None):
+    """Attention weights at fp bits from exact scores raw [..., S] (value raw 2^(sh - kbits - 3), sh per row
+    [..., 1]); ok marks visible keys -> (p int64 [..., S], 0 where masked, row sums [..., 1])
+    (src/bitexact/exact/ops.py:133-143)."""
+    S = raw.shape[-1]
+    lead = raw.shape[:-1]
+    r2 = raw.reshape(-1, S)
+    okb = ok.expand(raw.shape).reshape(r2.shape)
+    shb = sh.expand(*lead, 1).reshape(-1, 1) if torch.is_tensor(sh) else sh
+    p, den = _elem.row(_elem.R_SOFTMAX_W, r2, okb, shb, lut=lut,
+                       ia=(kbits, fp, L2E28 if l2e is None else int(l2e)))
+    return p.view(raw.shape), den.view(*lead, 1)
 
 
 def _flag(dev, flag):

@@ -14,9 +14,10 @@ integers are the same either way.
 
 import torch
 
+from bitexact import _elem
 from bitexact.exact import ops
 from bitexact.exact import wmm
-from bitexact.exact.consts import FR
+from bitexact.exact.consts import FR, LIM3
 
 H, HKV, HD = 32, 8, 64                                      # Llama-3.2-1B attention geometry (default dm)
 FK, FV, FP = ops.FK, ops.FV, ops.FP
@@ -66,7 +67,98 @@ def attn_out(num, den, T, hkv):
     return ops.attn_out(num, den, T, hkv)
 
 
-STAGES = ("lin_y", "lin_add", "add_y", "norm_quant", "softmax", "qkv_y", "gu_silu_y", "attn_out")
+def rms(x, err):
+    """ops.rms plus the |x| < 2^40 bound (segs.py:44-46) -> (r, er, err)."""
+    r, er = ops.rms(x)
+    fl = _elem.flag_for(x.device)
+    _elem.elem(_elem.ABSFLAG, x, iarg=(1 << 40) - 1, flag=fl)
+    return r, er, err | (fl[0] != 0)
+
+
+def ndiv(x, gm, ge, r, er):
+    """x gamma / rms at FN, one rounding per element (segs.py:49-51)."""
+    return _elem.elem(_elem.NDIV, x, gm, r[:, None], ge, er[:, None], iarg=ops.FN - FR)[0]
+
+
+def quant(P, eps):
+    """ops.quant with q as int32 (segs.py:54-56)."""
+    q, sh = ops.quant(P, eps)
+    return q.to(torch.int32), sh
+
+
+def _rope_full(x, c, s, shift=0):
+    """(x1 c - x2 s, x2 c + x1 s) over the two halves of the last axis, each rounded by `shift` bits (segs.py:66-69
+    with the caller's rshc)."""
+    hd = x.shape[-1]
+    x1, x2 = x[..., :hd // 2], x[..., hd // 2:]
+    lo = _elem.elem(_elem.MULSUB, x1, c, x2, s, iarg=shift)[0]
+    hi = _elem.elem(_elem.MULADD, x2, c, x1, s, iarg=shift)[0]
+    return torch.cat([lo, hi], -1)
+
+
+def rope_y(y, pos, cos, sin, B, T, dm):
+    """The qkv linear's output y [B T, (H + 2 HKV) HD] at FR -> (Pq at FR + FT [B, T, H, HD], k at FK, v at FV
+    [B, T, HKV, HD], y [B, T, .]) (segs.py:78-86)."""
+    h, hkv, hd = dm
+    y = y.view(B, T, -1)
+    c, s = cos[pos][:, :, None], sin[pos][:, :, None]
+    Pq = _rope_full(y[..., :h * hd].reshape(B, T, h, hd), c, s)
+    k = _rope_full(y[..., h * hd:(h + hkv) * hd].reshape(B, T, hkv, hd), c, s, FR + ops.FT - FK)
+    v = ops.rshc(y[..., (h + hkv) * hd:].reshape(B, T, hkv, hd), FR - FV)
+    return Pq, k, v, y
+
+
+def lin_rope(C, rs, d, g, sh, pos, cos, sin, B, T, dm):
+    """qkv linear + RoPE (segs.py:72-75)."""
+    return rope_y(lin_y(C, rs, d, g, sh), pos, cos, sin, B, T, dm)
+
+
+def q_group(Pq, k, v, y, err):
+    """q quantized per (token, head) and grouped by KV head -> ([B HKV, g T, HD] int32, exponents [.., 1], err)
+    (segs.py:89-99)."""
+    B, T, h, hd = Pq.shape
+    hkv = k.shape[2]
+    qi, shq = ops.quant(Pq, -(FR + ops.FT))
+    g = h // hkv
+    qg = qi.view(B, T, hkv, g, hd).permute(0, 2, 3, 1, 4).reshape(B * hkv, g * T, hd).to(torch.int32)
+    shg = shq.view(B, T, hkv, g).permute(0, 2, 3, 1).reshape(B * hkv, g * T, 1)
+    fl = _elem.flag_for(Pq.device)
+    _elem.elem(_elem.ABSFLAG, y, iarg=(1 << 31) - 1, flag=fl)
+    _elem.elem(_elem.ABSFLAG, k, iarg=LIM3, flag=fl)
+    _elem.elem(_elem.ABSFLAG, v, iarg=LIM3, flag=fl)
+    _elem.elem(_elem.GTFLAG, shq, iarg=FK + 3 - ops.FZ, flag=fl)
+    return qg, shg, err | (fl[0] != 0)
+
+
+def attn_div(num, den, T, hkv):
+    """num [B HKV, g T, HD] at FV + FP, den [B HKV, g T, 1] -> o at FR [B T, H HD], one rounding (segs.py:108-113)."""
+    Z, gT, hd = num.shape
+    B, g = Z // hkv, gT // T
+    o = ops.div_round(num, FR - FV, den)
+    return o.view(B, hkv, g, T, hd).permute(0, 3, 1, 2, 4).reshape(B * T, hkv * g * hd)
+
+
+def silu_y(gu, lut):
+    """silu(gate) up at 2 FR from gu = [gate | up] (segs.py:120-123) -> (P, ok)."""
+    ff = gu.shape[1] // 2
+    P, _, ok = ops.silu_mul(gu[:, :ff], gu[:, ff:], lut)
+    return P, ok
+
+
+def lin_silu(C, rs, d, g, sh, lut):
+    """gate|up linear + silu_y (segs.py:116-117)."""
+    return silu_y(lin_y(C, rs, d, g, sh), lut)
+
+
+def quant_silu(P, ok, err):
+    """quantization of the gated product at -2 FR (segs.py:126-128) -> (q int32, sh, err)."""
+    q, sh = ops.quant(P, -2 * FR)
+    return q.to(torch.int32), sh, err | ~ok
+
+
+# the reference's stage table (segs.py:131-132); Segs.s binds them (compiled or not)
+STAGES = ("lin_y", "lin_add", "rms", "ndiv", "quant", "lin_rope", "q_group", "softmax", "attn_div",
+          "lin_silu", "quant_silu", "rope_y", "add_y", "silu_y", "norm_quant")
 
 
 class Segs:
@@ -85,6 +177,9 @@ class Segs:
             torch._dynamo.config.cache_size_limit = max(torch._dynamo.config.cache_size_limit, 64)
             for name in self.METHODS:
                 setattr(self, name, torch.compile(getattr(self, name), fullgraph=True, backend="aot_eager"))
+        # the reference's per-stage table (segs.py:140-146); compiled stages trace through the registered operators
+        wrap = (lambda f: torch.compile(f, backend="aot_eager")) if compiled else (lambda f: f)
+        self.s = type("S", (), {n: staticmethod(wrap(globals()[n])) for n in STAGES})
 
     def norm_q(self, x, gm, ge, err):
         return norm_quant(x, gm, ge, err)

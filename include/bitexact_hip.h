@@ -303,6 +303,36 @@ int bx_int8_post(const int64_t* acc, int64_t ldacc, const int64_t* m, int32_t fm
                  const int64_t* e, int32_t FR, int64_t* y, int64_t ldy, int32_t M, int32_t N, int32_t* flag,
                  bx_stream_t stream);
 
+/* ---- the reference's Python helper rules, element-wise and per row ---- */
+
+/* Replaces the element-wise rules of intops (src/bitexact/intops.py:14-87: bitlen, rsh, fdiv, rdiv, isqrt,
+ * split_limbs, stack_limbs, join_limbs), exact ops (src/bitexact/exact/ops.py:25-130: rshc, div_round, combine,
+ * shift_round_hl, exp2neg_lut, silu_mul), int8 ops (src/bitexact/int8/ops.py:38-108: bitlen32, rdiv32, norm24,
+ * exp_of, silu) and the RoPE / division / bound steps of exact segs (src/bitexact/exact/segs.py:49-113) and int8
+ * segs (src/bitexact/int8/segs.py:70-118). `op` selects the rule (csrc/bx_elem.hip ElemOp, 1..28); operand j
+ * (j < nin <= 5) is element (r, c) of the [rows, inner] output grid at ptrs[j] + r desc[4j] + c desc[4j+1] with
+ * desc[4j+3] bytes per element (1, 2, 4, 8; signed), or the constant desc[4j+2] when ptrs[j] is null. Outputs are
+ * contiguous [rows, inner] with ob0 / ob1 bytes per element; lut is the rule's table (lut_len entries); iarg /
+ * iarg2 its integer parameters; rule violations (a zero divisor, a table index past the end, a failed bound) set
+ * flag[0] = 1 when flag is given. */
+int bx_int_elementwise(int32_t op, int32_t nin, const void* const* ptrs, const int64_t* desc, void* out0, int32_t ob0,
+                       void* out1, int32_t ob1, int64_t rows, int64_t inner, const int64_t* lut, int64_t lut_len,
+                       int64_t iarg, int64_t iarg2, int32_t* flag, bx_stream_t stream);
+
+/* Replaces the per-row rules exact ops.quant / ops.rms / ops.softmax_w (src/bitexact/exact/ops.py:82-143) and int8
+ * ops.rms / ops.quant_rows (src/bitexact/int8/ops.py:24-35, 76-84), int8 segs.pre_norm / segs.softmax
+ * (src/bitexact/int8/segs.py:47-52, 90-99) and a row max |x|, one block per row of x int64 [rows, ldx] (D
+ * columns). Operands as for bx_int_elementwise over the [rows, D] grid (nin <= 3); iargs[6] the rule's integer
+ * parameters; outputs out0..out3 per rule (csrc/bx_elem.hip RowOp). */
+int bx_int_rowop(int32_t op, int32_t nin, const void* const* ptrs, const int64_t* desc, const int64_t* x, int64_t ldx,
+                 int64_t rows, int64_t D, void* out0, void* out1, void* out2, void* out3, const int64_t* lut,
+                 int64_t lut_len, const int64_t* iargs, int32_t* flag, bx_stream_t stream);
+
+/* No counterpart in the reference: a measurement probe for the decode GEMMs' roofline. Streams `bytes` from src
+ * (16-byte nontemporal loads, grid-stride over blocks x threads) and discards them: the practical read ceiling of
+ * one launch at that size. sink: an int32 [1] device word (practically never written). */
+int bx_stream_read(const void* src, int64_t bytes, int32_t blocks, int32_t threads, int32_t* sink, bx_stream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -687,6 +687,121 @@ def paged_attend_int8(q, qpos, c32, bt, expt):
 
 
 
+# ---- int8-mode RMSNorm front, SiLU and the remaining int8 segments (src/bitexact/int8/ops.py:76-108,
+# src/bitexact/int8/segs.py:47-118) ----
+FG8, FT8, FV8 = 12, 16, 14
+SILU_LIM8 = 32
+EPS40 = 10995116                                # round(1e-5 2^40) (src/bitexact/int8/ops.py:18)
+
+
+def int8_rms(x, FR_=FR8):
+    """int8 ops.rms (src/bitexact/int8/ops.py:76-84): (r, shx) with rms = r 2^(shx - FR)."""
+    x = _a(x)
+    d = x.shape[-1]
+    amax = np.maximum(np.abs(x).max(-1), 1)
+    shx = bitlen(amax) - 24
+    xs = rsh(x, shx[:, None])
+    ms = (xs * xs).sum(-1) // d
+    eps = rsh(np.full_like(shx, EPS40), 40 - 2 * (FR_ - shx))
+    return isqrt(ms + eps), shx
+
+
+def int8_pre_norm(x, gamma, nl, FR_=FR8, FG_=FG8):
+    """int8 segs.pre_norm (src/bitexact/int8/segs.py:47-52): RMSNorm + quant_rows of x gamma, and the row scale
+    norm24(rdiv(as_ << 30, r), sh - FG - shx - 30) -> (q, mant, e)."""
+    x = _a(x)
+    r, shx = int8_rms(x, FR_)
+    q, as_, sh = quant_rows(x * _a(gamma), nl)
+    mant, e = norm24(rdiv(as_ << I64(30), r), sh - FG_ - shx - 30)
+    return q, mant, e
+
+
+def int8_pre_plain(x, nl, FR_=FR8):
+    """int8 segs.pre_plain (src/bitexact/int8/segs.py:56-59) -> (q, mant, e)."""
+    q, as_, sh = quant_rows(x, nl)
+    mant, e = norm24(as_, sh - FR_)
+    return q, mant, e
+
+
+def int8_silu_table():
+    """SiLU(x) at FR bits, x in [-SILU_LIM, SILU_LIM] at step 2^-FA (src/bitexact/int8/consts.py:79-80), with torch's
+    float64 exp on the CPU as the reference's offline build calls it."""
+    import torch
+    xs = torch.arange(-SILU_LIM8 << FA8, (SILU_LIM8 << FA8) + 1, dtype=torch.float64) / (1 << FA8)
+    return torch.round(xs / (1.0 + torch.exp(-xs)) * (1 << FR8)).long().numpy()
+
+
+def int8_exp_of(z, lut):
+    """int8 ops.exp_of (src/bitexact/int8/ops.py:93-97): e^z at FE bits, 0 below EXP_MIN."""
+    idx = _a(z) - I64(EXP_MIN8 << FA8)
+    val = _a(lut)[np.maximum(idx, 0)]
+    return np.where(idx < 0, I64(0), val)
+
+
+def int8_silu(g, lut, FR_=FR8):
+    """int8 ops.silu (src/bitexact/int8/ops.py:100-108): table at step 2^-FA with linear interpolation, identity
+    above the table and 0 below it."""
+    g, lut = _a(g), _a(lut)
+    lo, hi = -SILU_LIM8 << FA8, SILU_LIM8 << FA8
+    gi = g >> I64(FR_ - FA8)
+    r = g - (gi << I64(FR_ - FA8))
+    i = np.clip(gi, lo, hi - 1) - lo
+    a = lut[i]
+    v = a + rsh((lut[i + 1] - a) * r, FR_ - FA8)
+    return np.where(gi >= hi, g, np.where(gi < lo, I64(0), v))
+
+
+def _amax8(z):
+    return I64(np.abs(_a(z)).max()) if np.size(z) else I64(0)
+
+
+def int8_silu_mul(gu, lut, nl, FR_=FR8):
+    """int8 segs.silu_mul (src/bitexact/int8/segs.py:112-118) -> (q, mant, e, flag); the flag compares the wrapped
+    int64 product of the two maxima with 2^62, as the reference's int64 tensors do."""
+    gu = _a(gu)
+    ff = gu.shape[1] // 2
+    g, u = gu[:, :ff], gu[:, ff:]
+    sg = int8_silu(g, lut, FR_)
+    with np.errstate(over="ignore"):
+        flag = bool(_amax8(sg) * _amax8(u) >= I64(1 << 62))
+    q, mant, e = int8_pre_plain(rsh(sg * u, FR_), nl, FR_)
+    return q, mant, e, flag
+
+
+def _rope8(x, c, s, FR_=FR8):
+    h = x.shape[-1] // 2
+    x1, x2 = x[..., :h], x[..., h:]
+    sh = FT8 + FR_ - FQ8
+    return np.concatenate([rsh(x1 * c - x2 * s, sh), rsh(x2 * c + x1 * s, sh)], -1)
+
+
+def int8_qkv(y, c, s, dm, FR_=FR8):
+    """int8 segs.qkv (src/bitexact/int8/segs.py:77-87): y [B, T, (H + 2 HKV) HD] at FR, c / s [B, T, 1, HD / 2]
+    -> (qg [B HKV, g T, HD], k, v [B, T, HKV, HD], flag)."""
+    H, HKV, HD = dm
+    y, c, s = _a(y), _a(c), _a(s)
+    B, T = y.shape[0], y.shape[1]
+    D = H * HD
+    q = _rope8(y[..., :D].reshape(B, T, H, HD), c, s, FR_)
+    k = _rope8(y[..., D:D + HKV * HD].reshape(B, T, HKV, HD), c, s, FR_)
+    v = rsh(y[..., D + HKV * HD:].reshape(B, T, HKV, HD), FR_ - FV8)
+    g = H // HKV
+    qg = q.reshape(B, T, HKV, g, HD).transpose(0, 2, 3, 1, 4).reshape(B * HKV, g * T, HD)
+    flag = bool(_amax8(q) > LIM3 or _amax8(k) > LIM3 or _amax8(v) > LIM3)
+    return qg, k, v, flag
+
+
+def int8_attn_out(num, den, T, nl, dm, FR_=FR8):
+    """int8 segs.attn_out (src/bitexact/int8/segs.py:102-109): rdiv(num << (FR - FV), den), regrouped, pre_plain."""
+    H, HKV, HD = dm
+    num = _a(num)
+    B = num.shape[0]
+    g = H // HKV
+    o = rdiv(num << I64(FR_ - FV8), _a(den))
+    o = o.reshape(B, HKV, g, T, HD).transpose(0, 3, 1, 2, 4).reshape(B * T, H * HD)
+    return int8_pre_plain(o, nl, FR_)
+
+
 # ---- the exact decode engine (src/bitexact/vllm_plugin/exact_run.py:60-128, src/bitexact/exact/model.py:95-148) ----
 def engine_constants(emb_bits, lin_bits, gammas, cos, sin, L):
     """Oracle-side model from raw bf16 bits: emb_bits [V, D], lin_bits {(i, name) or "lm": bits [N, K]},

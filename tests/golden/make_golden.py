@@ -1,6 +1,7 @@
 """Writes tests/golden/reference_vectors.npz: input/output vectors of the reference's CPU integer rules that
 closed forms do not pin bit for bit (ops.rms, ops.exp2neg_lut, ops.softmax_w, segs.norm_quant, ops.div_round,
-int8 ops.quant_rows, int8 segs.softmax, ops.silu_mul, segs.silu_y + quant_silu, llama.digest). Run in the development container only, where the reference checkout is present:
+int8 ops.quant_rows, int8 segs.softmax, ops.silu_mul, segs.silu_y + quant_silu, llama.digest; int8 ops.rms, norm24,
+exp_of, silu and segs.pre_norm, pre_plain, silu_mul, qkv, attn_out). Run in the development container only, where the reference checkout is present:
 
     python tests/golden/make_golden.py /root/reference
 
@@ -124,6 +125,68 @@ def main(ref_root):
         if torch.is_tensor(v):
             out["dg_" + k] = v.numpy()
     out["dg_sha"] = np.frombuffer(bytes.fromhex(digest(cdict)), np.uint8)
+
+    # int8 RMSNorm front and the other int8 segments (src/bitexact/int8/ops.py:70-108, src/bitexact/int8/segs.py:47-118)
+    gi = torch.Generator().manual_seed(20261202)
+    x = torch.randint(-(1 << 26), 1 << 26, (9, 512), generator=gi)
+    x = x >> torch.randint(0, 20, (9, 1), generator=gi)
+    x[3] = 0
+    x[3, 5] = -7
+    x[4] = (1 << 40) - 1
+    gamma = torch.randint(1, 1 << 13, (512,), generator=gi)
+    r, shx = iops.rms(x)
+    out["i8rms_x"], out["i8rms_r"], out["i8rms_shx"] = x.numpy(), r.numpy(), shx.numpy()
+    out["i8pn_gamma"] = gamma.numpy()
+    for nl in (1, 2, 3):
+        q, mant, e = isegs.pre_norm(x, gamma, nl)
+        out[f"i8pn{nl}_q"], out[f"i8pn{nl}_mant"], out[f"i8pn{nl}_e"] = q.numpy(), mant.numpy(), e.numpy()
+        q, mant, e = isegs.pre_plain(x, nl)
+        out[f"i8pp{nl}_q"], out[f"i8pp{nl}_mant"], out[f"i8pp{nl}_e"] = q.numpy(), mant.numpy(), e.numpy()
+    mant = torch.randint(1, 1 << 40, (500,), generator=gi) >> torch.randint(0, 40, (500,), generator=gi)
+    ee = torch.randint(-60, 20, (500,), generator=gi)
+    m2, e2 = iops.norm24(mant, ee)
+    out["n24_m"], out["n24_e"], out["n24_mo"], out["n24_eo"] = mant.numpy(), ee.numpy(), m2.numpy(), e2.numpy()
+    z = torch.cat([torch.randint(-(40 << 12), 1, (3000,), generator=gi), torch.tensor([0, -1, -(32 << 12),
+                                                                                       -(32 << 12) - 1])])
+    out["i8eo_z"], out["i8eo_v"] = z.numpy(), iops.exp_of(z, expt).numpy()
+    xs = torch.arange(-iconsts.SILU_LIM << iconsts.FA, (iconsts.SILU_LIM << iconsts.FA) + 1,
+                      dtype=torch.float64) / (1 << iconsts.FA)
+    silu_t = torch.round(xs / (1.0 + torch.exp(-xs)) * (1 << iconsts.FR)).long()
+    out["i8silu_sha256"] = np.frombuffer(hashlib.sha256(silu_t.numpy().astype("<i8").tobytes()).digest(), np.uint8)
+    gg = torch.cat([torch.randint(-(40 << 16), 40 << 16, (3000,), generator=gi),
+                    torch.tensor([0, 1, -1, 32 << 16, (32 << 16) - 1, -(32 << 16), -(32 << 16) - 1])])
+    out["i8silu_g"], out["i8silu_v"] = gg.numpy(), iops.silu(gg, silu_t).numpy()
+    gu = torch.randint(-(1 << 22), 1 << 22, (5, 1024), generator=gi)
+    gu[1] >>= 10
+    gu[2, :512] = torch.randint(-(40 << 16), 40 << 16, (512,), generator=gi)
+    for nl in (1, 2):
+        q, mant, e, flag = isegs.silu_mul(gu, silu_t, nl)
+        out[f"i8sm{nl}_q"], out[f"i8sm{nl}_mant"], out[f"i8sm{nl}_e"] = q.numpy(), mant.numpy(), e.numpy()
+        out[f"i8sm{nl}_flag"] = np.array(bool(flag))
+    out["i8sm_gu"] = gu.numpy()
+    big = gu.clone()
+    big[0, 0] = 1 << 40
+    big[0, 600] = 1 << 30
+    out["i8sm_big_gu"] = big.numpy()
+    out["i8sm_big_flag"] = np.array(bool(isegs.silu_mul(big, silu_t, 2)[3]))
+    B, T, dm = 2, 5, (8, 2, 16)
+    y = torch.randint(-(1 << 30), 1 << 30, (B, T, (8 + 4) * 16), generator=gi)
+    ang = torch.rand(B, T, 1, 8, generator=gi, dtype=torch.float64) * 6.283
+    c = torch.round(torch.cos(ang) * (1 << 16)).long()
+    sn = torch.round(torch.sin(ang) * (1 << 16)).long()
+    qg, k, v, flag = isegs.qkv(y, c, sn, dm)
+    out["i8qkv_y"], out["i8qkv_c"], out["i8qkv_s"] = y.numpy(), c.numpy(), sn.numpy()
+    out["i8qkv_qg"], out["i8qkv_k"], out["i8qkv_v"], out["i8qkv_flag"] = qg.numpy(), k.numpy(), v.numpy(), \
+        np.array(bool(flag))
+    y2 = y.clone()
+    y2[0, 0, 0] = 1 << 40
+    out["i8qkv_big_flag"] = np.array(bool(isegs.qkv(y2, c, sn, dm)[3]))
+    num = torch.randint(-(1 << 50), 1 << 50, (B, 2, 4 * T, 16), generator=gi)
+    den = torch.randint(1 << 20, 1 << 30, (B, 2, 4 * T, 1), generator=gi)
+    for nl in (1, 2):
+        q, mant, e = isegs.attn_out(num, den, T, nl, dm)
+        out[f"i8ao{nl}_q"], out[f"i8ao{nl}_mant"], out[f"i8ao{nl}_e"] = q.numpy(), mant.numpy(), e.numpy()
+    out["i8ao_num"], out["i8ao_den"] = num.numpy(), den.numpy()
 
     path = os.path.join(os.path.dirname(os.path.abspath(__file__)), "reference_vectors.npz")
     np.savez_compressed(path, **out)

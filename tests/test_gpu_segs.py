@@ -60,11 +60,11 @@ def test_int8_quant_rows(dev, nl):
         z = torch.randint(-(1 << 40), 1 << 40, (M, K), generator=g)
         z = z >> torch.randint(0, 40, (M, 1), generator=g)
         z[0, :] = 0                                      # amax clamps to 1
-        a, as_, sh = segs.quant_rows(z.to(dev), nl)
+        a, as_, sh = segs.quant_rows_limbs(z.to(dev), nl)
         rq, ras, rsh_ = R.quant_rows(z.numpy(), nl)
         assert np.array_equal(a.cpu().numpy(), R.stack_limbs(rq, nl)[:nl * M].astype(np.int8))
         assert np.array_equal(as_.cpu().numpy(), ras) and np.array_equal(sh.cpu().numpy(), rsh_)
-        a2, mant, e = segs.pre_plain(z.to(dev), nl)
+        a2, mant, e = segs.pre_plain_limbs(z.to(dev), nl)
         rm, re = R.norm24(ras, rsh_ - R.FR8)
         assert torch.equal(a, a2)
         assert np.array_equal(mant.cpu().numpy(), rm) and np.array_equal(e.cpu().numpy(), re)

@@ -1,6 +1,7 @@
 """The oracle against vectors the reference's own CPU rules produced (tests/golden/make_golden.py):
 ops.rms, segs.norm_quant, ops.exp2neg_lut, ops.softmax_w (head_dim 64 and 128), ops.div_round, int8 quant_rows,
-int8 segs.softmax (head_dim 64 and 128), ops.silu_mul and the gate/up stage (segs.silu_y + quant_silu)."""
+int8 segs.softmax (head_dim 64 and 128), ops.silu_mul and the gate/up stage (segs.silu_y + quant_silu); int8 ops.rms,
+norm24, exp_of, silu (and its table) and int8 segs.pre_norm, pre_plain, silu_mul, qkv, attn_out."""
 
 import os
 
@@ -66,3 +67,50 @@ def test_silu_mul_and_gate_up_stage():
     assert R.silu_mul(bad, GOLD["silu_u"], lut)[2] == bool(GOLD["silu_bad_ok"])
     q, sh, err = R.gu_silu_y(np.concatenate([GOLD["silu_g"], GOLD["silu_u"]], 1), lut)
     assert np.array_equal(q, GOLD["gus_q"]) and np.array_equal(sh, GOLD["gus_sh"]) and err == bool(GOLD["gus_err"])
+
+
+# ---- int8 RMSNorm front and the other int8 segments (src/bitexact/int8/ops.py:70-108, segs.py:47-118) ----
+def test_int8_rms_pre_norm_pre_plain():
+    x = GOLD["i8rms_x"]
+    r, shx = R.int8_rms(x)
+    assert np.array_equal(r, GOLD["i8rms_r"]) and np.array_equal(shx, GOLD["i8rms_shx"])
+    for nl in (1, 2, 3):
+        for got, key in zip(R.int8_pre_norm(x, GOLD["i8pn_gamma"], nl), ("q", "mant", "e")):
+            assert np.array_equal(got, GOLD[f"i8pn{nl}_{key}"]), (nl, key)
+        for got, key in zip(R.int8_pre_plain(x, nl), ("q", "mant", "e")):
+            assert np.array_equal(got, GOLD[f"i8pp{nl}_{key}"]), (nl, key)
+
+
+def test_int8_norm24_exp_of():
+    m, e = R.norm24(GOLD["n24_m"], GOLD["n24_e"])
+    assert np.array_equal(m, GOLD["n24_mo"]) and np.array_equal(e, GOLD["n24_eo"])
+    assert np.array_equal(R.int8_exp_of(GOLD["i8eo_z"], R.int8_exp_table()), GOLD["i8eo_v"])
+
+
+def test_int8_silu_table_and_silu():
+    import hashlib
+    t = R.int8_silu_table()
+    assert hashlib.sha256(t.astype("<i8").tobytes()).digest() == GOLD["i8silu_sha256"].tobytes()
+    assert np.array_equal(R.int8_silu(GOLD["i8silu_g"], t), GOLD["i8silu_v"])
+
+
+def test_int8_silu_mul():
+    t = R.int8_silu_table()
+    for nl in (1, 2):
+        q, mant, e, flag = R.int8_silu_mul(GOLD["i8sm_gu"], t, nl)
+        assert np.array_equal(q, GOLD[f"i8sm{nl}_q"]) and np.array_equal(mant, GOLD[f"i8sm{nl}_mant"])
+        assert np.array_equal(e, GOLD[f"i8sm{nl}_e"]) and flag == bool(GOLD[f"i8sm{nl}_flag"])
+    assert R.int8_silu_mul(GOLD["i8sm_big_gu"], t, 2)[3] == bool(GOLD["i8sm_big_flag"])
+
+
+def test_int8_qkv_attn_out():
+    dm = (8, 2, 16)
+    qg, k, v, flag = R.int8_qkv(GOLD["i8qkv_y"], GOLD["i8qkv_c"], GOLD["i8qkv_s"], dm)
+    assert np.array_equal(qg, GOLD["i8qkv_qg"]) and np.array_equal(k, GOLD["i8qkv_k"])
+    assert np.array_equal(v, GOLD["i8qkv_v"]) and flag == bool(GOLD["i8qkv_flag"])
+    y2 = GOLD["i8qkv_y"].copy()
+    y2[0, 0, 0] = 1 << 40
+    assert R.int8_qkv(y2, GOLD["i8qkv_c"], GOLD["i8qkv_s"], dm)[3] == bool(GOLD["i8qkv_big_flag"])
+    for nl in (1, 2):
+        for got, key in zip(R.int8_attn_out(GOLD["i8ao_num"], GOLD["i8ao_den"], 5, nl, dm), ("q", "mant", "e")):
+            assert np.array_equal(got, GOLD[f"i8ao{nl}_{key}"]), (nl, key)
