@@ -185,6 +185,38 @@ def bench_decode(dev, steps, warmup):
     return sec, step_bytes, len(plan), per
 
 
+def bench_read_ceiling(dev, reps=64):
+    """The practical read ceiling at the decode GEMMs' sizes: a bare streaming-read kernel (bx_stream_read: 16-byte
+    nontemporal loads, grid-stride, nothing computed) over 16.8 MB (a down GEMM's weights) and 33.6 MB (gate|up),
+    rotating over >= 1 GiB of buffers so every launch reads HBM, graph-replayed and timed with HIP events on the
+    launch stream like the GEMMs. Best of a few launch shapes."""
+    import ctypes
+    import torch
+    from bitexact import _hip
+    sink = torch.zeros(1, dtype=torch.int32, device=dev)
+    stream = torch.cuda.Stream(dev)
+    out = {}
+    for name, nbytes in (("16.8MB", 2048 * 8192), ("33.6MB", 16384 * 2048)):
+        n = max(4, -(-(1 << 30) // nbytes))
+        bufs = [torch.empty(nbytes, dtype=torch.uint8, device=dev) for _ in range(n)]
+        for b in bufs:
+            b.fill_(1)
+        best = None
+        for blocks, threads in ((256, 512), (512, 256), (1024, 256)):
+            def run(i, blocks=blocks, threads=threads):
+                _hip.call("bx_stream_read", ctypes.c_void_p(bufs[i % n].data_ptr()), nbytes, blocks, threads,
+                          _hip.ptr(sink), _hip.stream_of(sink))
+            sec = time_graph(run, 8, reps, stream) / reps
+            if best is None or sec < best[0]:
+                best = (sec, blocks, threads)
+        out[name] = {"bytes": nbytes, "us": round(best[0] * 1e6, 3), "GBps": round(nbytes / best[0] / 1e9, 1),
+                     "frac_hbm": round(nbytes / best[0] / 1e9 / HBM_PEAK_GBS, 4), "blocks": best[1],
+                     "threads": best[2]}
+        del bufs
+        torch.cuda.empty_cache()
+    return out
+
+
 def bench_prefill(dev, reps=10):
     import torch
     from bitexact.exact.consts import decompose
@@ -292,6 +324,43 @@ def bench_attention(dev, reps=20):
             "prefill_ms": round(s_pre * 1e3, 3), "prefill_limb_ops": ops,
             "prefill_TOPS": round(ops / s_pre / 1e12, 2),
             "prefill_frac_int8_peak": round(ops / s_pre / 1e12 / INT8_PEAK_TOPS, 4)}
+
+
+def bench_bmm(dev, reps=5):
+    """bitexact.bmm.bmm (the reference model's unfused attention products) at config 4's shapes: q.k
+    [32, 8192, 64] x [32, 64, 2048] (int64 scores, 4.3 GB written: HBM-write bound) and p.v [32, 8192, 2048] x
+    [32, 2048, 64] (3-limb weights and values: MFMA bound). Limb-op TOPS = 9 x 2 Z M N K per call."""
+    import torch
+    from bitexact.bmm import bmm
+    g = torch.Generator(device=dev).manual_seed(21)
+    Z, gT, S, HD = 32, 8192, 2048, 64
+    lim = 8355711
+    qg = torch.randint(-(1 << 22), (1 << 22) + 1, (Z, gT, HD), device=dev, generator=g).to(torch.int32)
+    Kc = torch.randint(-lim, lim + 1, (Z, S, HD), device=dev, generator=g).to(torch.int32)
+    stream = torch.cuda.Stream(dev)
+    outs = {}
+    s_qk = time_graph(lambda i: outs.__setitem__(0, bmm(qg, Kc.transpose(1, 2))), 1, reps, stream) / reps
+    # a row sample of q.k against the oracle's exact product
+    sys.path.insert(0, HERE)
+    from oracle import bxref as R
+    import numpy as np
+    zs, rows = [0, Z - 1], [0, 4097, gT - 1]
+    for z in zs:
+        ref = R.bmm(qg[z, rows].cpu().numpy()[None], Kc[z].cpu().numpy().T[None])[0]
+        if not np.array_equal(outs[0][z, rows].cpu().numpy(), ref):
+            raise AssertionError("bmm q.k differs from the oracle")
+    del outs[0]
+    torch.cuda.empty_cache()
+    p = torch.randint(0, 1 << 22, (Z, gT, S), device=dev, generator=g).to(torch.int32)
+    V = torch.randint(-lim, lim + 1, (Z, S, HD), device=dev, generator=g).to(torch.int32)
+    s_pv = time_graph(lambda i: outs.__setitem__(1, bmm(p, V)), 1, reps, stream) / reps
+    ops_qk = 9 * 2 * Z * gT * S * HD
+    return {"workload": "config 4 shapes: q.k [32, 8192, 64] x [32, 64, 2048], p.v [32, 8192, 2048] x [32, 2048, 64]",
+            "qk_us": round(s_qk * 1e6, 1), "qk_TOPS": round(ops_qk / s_qk / 1e12, 1),
+            "qk_write_GBps": round(8 * Z * gT * S / s_qk / 1e9, 1),
+            "qk_frac_hbm": round(8 * Z * gT * S / s_qk / 1e9 / HBM_PEAK_GBS, 4),
+            "pv_us": round(s_pv * 1e6, 1), "pv_TOPS": round(ops_qk / s_pv / 1e12, 1),
+            "pv_frac_int8_peak": round(ops_qk / s_pv / 1e12 / INT8_PEAK_TOPS, 4)}
 
 
 def bench_engine(dev, steps, warmup, B=32, ctx=1024, bs=16):
@@ -504,6 +573,17 @@ def main():
                         "traffic": DECODE_TRAFFIC_PER_LAUNCH, "algorithmic_bytes_per_launch": step_bytes // launches,
                         "launch_us": round(per_launch_s * 1e6, 3)},
            "per_gemm": per}
+    if value is not None:
+        log("read ceiling ...")
+        ceil = bench_read_ceiling(dev)
+        # the step at the measured ceiling rates: each GEMM's algorithmic bytes at its size's bare-read rate
+        rate = {2048: ceil["16.8MB"]["GBps"], 16384: ceil["33.6MB"]["GBps"]}
+        step_at_ceiling = sum((N * K + 2 * M * K + 8 * M * N) / (rate[N] * 1e9)
+                              for M in DECODE_M for _, N, K in DECODE_SHAPES)
+        ceil["step_us_at_ceiling"] = round(step_at_ceiling * 1e6, 2)
+        ceil["step_GBps_at_ceiling"] = round(step_bytes / step_at_ceiling / 1e9, 1)
+        ceil["frac_of_ceiling"] = round(step_at_ceiling / (sec / args.steps), 4)
+        out["read_ceiling"] = ceil
     if not args.no_prefill:
         log("exact prefill GEMMs ...")
         res, tops = bench_prefill(dev)
@@ -514,6 +594,9 @@ def main():
     if not args.no_attn:
         log("attention ...")
         out["exact_attention"] = bench_attention(dev)
+    if not args.no_attn:
+        log("bmm ...")
+        out["bmm"] = bench_bmm(dev)
     if not args.no_engine:
         log("exact decode engine (config 5) ...")
         out["exact_engine"] = bench_engine(dev, args.engine_steps, 3)

@@ -1,69 +1,146 @@
-// Exact batched integer matrix product (bitexact.bmm.bmm, src/bitexact/bmm.py:27-102):
-// c int64 [Z, M, N] = a [Z, M, K] @ b [Z, K, N] for int32 or int64 operands with arbitrary strides, each operand
-// taken as its first na / nb signed base-256 digits (what the reference's limb split keeps; identical for
-// values within the limbs). 64 x 64 output tiles per 256-thread block, 32-deep K tiles in LDS, exact int64
-// multiply-adds (every product of two 3-limb values is below 2^47, K < 43690 keeps the sums below 2^63).
+// Exact batched integer matrix product (bitexact.bmm.bmm, src/bitexact/bmm.py:27-102) on int8 MFMA:
+// c int64 [Z, M, N] = a [Z, M, K] @ b [Z, K, N] for int32 or int64 operands with arbitrary strides, each operand taken
+// as its first na / nb signed base-256 digits (what the reference's limb split keeps; identical for values within
+// the limbs).
+//
+// A 256-thread block owns a 64 x 64 output tile and walks K in 64-deep steps. Each step's operand tiles are loaded
+// four k values per thread (the thread-to-element map follows whichever of the operand's strides is 1, so the loads
+// coalesce for q.k with K^T and for p.v alike), split into signed int8 limbs and written to LDS as limb planes
+// [limb][row][64 k] (16-byte k chunks XOR-swizzled by row so the MFMA operand reads are conflict-free); the next
+// step's values are loaded into registers while the current step's MFMAs run. Wave w computes rows 16 w .. 16 w + 15
+// against all 64 columns with v_mfma_i32_16x16x64_i8: limb pair (i, j) accumulates into the int32 set of weight
+// s = i + j (|sum| <= 3 K 2^14 < 2^31 for K < 43690, the reference's bound), and the int64 result sum_s c_s 2^(8 s)
+// is formed once, in registers, before the store.
 #include "bx_common.h"
 
 namespace bx {
 
-__device__ __forceinline__ int64_t keep_limbs(int64_t x, int n) {
-  int64_t r = x, v = 0;
+constexpr int kBT = 64;                 // output tile edge, k step
+constexpr int kPlane = kBT * kBT;       // bytes of one limb plane of a tile (64 rows x 64 k)
+
+__device__ __forceinline__ int swz(int row, int chunk) { return row * kBT + ((chunk ^ ((row >> 2) & 3)) << 4); }
+
+template <typename T>
+__device__ __forceinline__ int64_t ldv(const T* p, int64_t off, bool ok) { return ok ? (int64_t)p[off] : 0; }
+
+// The four values (row r, k = k0 + 4 q .. + 3) of one operand; rows past R or k past K read as 0.
+template <typename T>
+__device__ __forceinline__ void load4(const T* base, int64_t sr, int64_t sk, int r, int R, int k, int K, int64_t v[4]) {
 #pragma unroll
-  for (int i = 0; i < 3; ++i) {
-    if (i < n) {
-      const int64_t lo = limb_lo64(r);
-      v += lo << (8 * i);
-      r = (r - lo) >> 8;
+  for (int e = 0; e < 4; ++e) v[e] = ldv(base, (int64_t)r * sr + (int64_t)(k + e) * sk, r < R && k + e < K);
+}
+
+// Signed limbs of four values, packed by k into one 32-bit word per limb, written to the n limb planes.
+__device__ __forceinline__ void store4(int8_t* planes, int n, int row, int q, const int64_t v[4]) {
+  int64_t r[4] = {v[0], v[1], v[2], v[3]};
+  for (int l = 0; l < n; ++l) {
+    uint32_t w = 0;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const int64_t lo = limb_lo64(r[e]);
+      w |= (uint32_t)(lo & 255) << (8 * e);
+      r[e] = (r[e] - lo) >> 8;
+    }
+    *(uint32_t*)(planes + l * kPlane + swz(row, q >> 2) + (q & 3) * 4) = w;
+  }
+}
+
+template <typename TA, typename TB, int NA, int NB>
+__global__ __launch_bounds__(256) void bmm_mfma_kernel(const TA* a, int64_t saz, int64_t sam, int64_t sak, const TB* b,
+                                                       int64_t sbz, int64_t sbk, int64_t sbn, int64_t* c, int64_t scz,
+                                                       int64_t scm, int64_t scn, int M, int N, int K) {
+  constexpr int NS = NA + NB - 1;
+  __shared__ __align__(16) int8_t As[NA * kPlane];
+  __shared__ __align__(16) int8_t Bs[NB * kPlane];
+  const int64_t z = blockIdx.z;
+  const int m0 = blockIdx.y * kBT, n0 = blockIdx.x * kBT;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const TA* ab = a + z * saz;
+  const TB* bb = b + z * sbz;
+  // thread -> (row, k quad) of the four load groups; k-major when k is the contiguous stride
+  const bool a_k = sak == 1, b_k = sbk == 1;
+  int ar[4], aq[4], br[4], bq[4];
+#pragma unroll
+  for (int g = 0; g < 4; ++g) {
+    const int idx = tid + 256 * g;
+    ar[g] = a_k ? idx / 16 : idx % 64;
+    aq[g] = a_k ? idx % 16 : idx / 64;
+    br[g] = b_k ? idx / 16 : idx % 64;
+    bq[g] = b_k ? idx % 16 : idx / 64;
+  }
+  int64_t va[4][4], vb[4][4];
+  auto fetch = [&](int k0) {
+#pragma unroll
+    for (int g = 0; g < 4; ++g) {
+      load4(ab, sam, sak, m0 + ar[g], M, k0 + 4 * aq[g], K, va[g]);
+      load4(bb, sbn, sbk, n0 + br[g], N, k0 + 4 * bq[g], K, vb[g]);
+    }
+  };
+  v4i acc[NS][4];
+#pragma unroll
+  for (int s = 0; s < NS; ++s)
+#pragma unroll
+    for (int cb = 0; cb < 4; ++cb) acc[s][cb] = v4i{0, 0, 0, 0};
+  fetch(0);
+  const int r16 = lane & 15, ch = lane >> 4;
+  for (int k0 = 0; k0 < K; k0 += kBT) {
+#pragma unroll
+    for (int g = 0; g < 4; ++g) {
+      store4(As, NA, ar[g], aq[g], va[g]);
+      store4(Bs, NB, br[g], bq[g], vb[g]);
+    }
+    __syncthreads();
+    if (k0 + kBT < K) fetch(k0 + kBT);   // the next step's values travel while this step's MFMAs run
+    v4i af[NA];
+#pragma unroll
+    for (int i = 0; i < NA; ++i) af[i] = *(const v4i*)(As + i * kPlane + swz(16 * wave + r16, ch));
+#pragma unroll
+    for (int cb = 0; cb < 4; ++cb)
+#pragma unroll
+      for (int j = 0; j < NB; ++j) {
+        const v4i bf = *(const v4i*)(Bs + j * kPlane + swz(16 * cb + r16, ch));
+#pragma unroll
+        for (int i = 0; i < NA; ++i)
+          acc[i + j][cb] = __builtin_amdgcn_mfma_i32_16x16x64_i8(af[i], bf, acc[i + j][cb], 0, 0, 0);
+      }
+    __syncthreads();
+  }
+  // lane l holds column 16 cb + l % 16, rows 4 (l / 16) + e of the wave's 16-row block
+#pragma unroll
+  for (int cb = 0; cb < 4; ++cb) {
+    const int n = n0 + 16 * cb + r16;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const int m = m0 + 16 * wave + 4 * ch + e;
+      int64_t v = 0;
+#pragma unroll
+      for (int s = 0; s < NS; ++s) v += (int64_t)acc[s][cb][e] << (8 * s);
+      if (m < M && n < N) c[z * scz + (int64_t)m * scm + (int64_t)n * scn] = v;
     }
   }
-  return v;
+}
+
+template <typename TA, typename TB, int NA>
+static void launch_nb(int nb, dim3 grid, hipStream_t st, const TA* a, int64_t saz, int64_t sam, int64_t sak,
+                      const TB* b, int64_t sbz, int64_t sbk, int64_t sbn, int64_t* c, int64_t scz, int64_t scm,
+                      int64_t scn, int M, int N, int K) {
+  if (nb == 1)
+    bmm_mfma_kernel<TA, TB, NA, 1><<<grid, 256, 0, st>>>(a, saz, sam, sak, b, sbz, sbk, sbn, c, scz, scm, scn, M, N, K);
+  else if (nb == 2)
+    bmm_mfma_kernel<TA, TB, NA, 2><<<grid, 256, 0, st>>>(a, saz, sam, sak, b, sbz, sbk, sbn, c, scz, scm, scn, M, N, K);
+  else
+    bmm_mfma_kernel<TA, TB, NA, 3><<<grid, 256, 0, st>>>(a, saz, sam, sak, b, sbz, sbk, sbn, c, scz, scm, scn, M, N, K);
 }
 
 template <typename TA, typename TB>
-__global__ __launch_bounds__(256) void bmm_kernel(const TA* a, int64_t saz, int64_t sam, int64_t sak, const TB* b,
-                                                  int64_t sbz, int64_t sbk, int64_t sbn, int64_t* c, int64_t scz,
-                                                  int64_t scm, int64_t scn, int M, int N, int K, int na, int nb) {
-  __shared__ int32_t As[32][65];   // [k][m]
-  __shared__ int32_t Bs[32][65];   // [k][n]
-  const int64_t z = blockIdx.z;
-  const int m0 = blockIdx.y * 64, n0 = blockIdx.x * 64;
-  const int tid = threadIdx.x, tm = tid / 16, tn = tid % 16;   // 4 x 4 outputs per thread
-  int64_t acc[4][4];
-#pragma unroll
-  for (int i = 0; i < 4; ++i)
-#pragma unroll
-    for (int j = 0; j < 4; ++j) acc[i][j] = 0;
-  for (int k0 = 0; k0 < K; k0 += 32) {
-    __syncthreads();
-    for (int u = tid; u < 32 * 64; u += 256) {
-      const int kk = u / 64, mm = u % 64;
-      const int m = m0 + mm, k = k0 + kk;
-      As[kk][mm] = (m < M && k < K) ? (int32_t)keep_limbs((int64_t)a[z * saz + (int64_t)m * sam + (int64_t)k * sak], na) : 0;
-      const int n = n0 + mm;
-      Bs[kk][mm] = (n < N && k < K) ? (int32_t)keep_limbs((int64_t)b[z * sbz + (int64_t)k * sbk + (int64_t)n * sbn], nb) : 0;
-    }
-    __syncthreads();
-#pragma unroll 4
-    for (int kk = 0; kk < 32; ++kk) {
-      int64_t av[4], bv[4];
-#pragma unroll
-      for (int i = 0; i < 4; ++i) av[i] = As[kk][tm + 16 * i];
-#pragma unroll
-      for (int j = 0; j < 4; ++j) bv[j] = Bs[kk][tn + 16 * j];
-#pragma unroll
-      for (int i = 0; i < 4; ++i)
-#pragma unroll
-        for (int j = 0; j < 4; ++j) acc[i][j] += av[i] * bv[j];
-    }
-  }
-#pragma unroll
-  for (int i = 0; i < 4; ++i)
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const int m = m0 + tm + 16 * i, n = n0 + tn + 16 * j;
-      if (m < M && n < N) c[z * scz + (int64_t)m * scm + (int64_t)n * scn] = acc[i][j];
-    }
+static void launch_na(int na, int nb, dim3 grid, hipStream_t st, const void* a, int64_t saz, int64_t sam, int64_t sak,
+                      const void* b, int64_t sbz, int64_t sbk, int64_t sbn, int64_t* c, int64_t scz, int64_t scm,
+                      int64_t scn, int M, int N, int K) {
+  const TA* A = (const TA*)a;
+  const TB* B = (const TB*)b;
+  if (na == 1) launch_nb<TA, TB, 1>(nb, grid, st, A, saz, sam, sak, B, sbz, sbk, sbn, c, scz, scm, scn, M, N, K);
+  else if (na == 2) launch_nb<TA, TB, 2>(nb, grid, st, A, saz, sam, sak, B, sbz, sbk, sbn, c, scz, scm, scn, M, N, K);
+  else launch_nb<TA, TB, 3>(nb, grid, st, A, saz, sam, sak, B, sbz, sbk, sbn, c, scz, scm, scn, M, N, K);
 }
 
 }  // namespace bx
@@ -81,19 +158,20 @@ extern "C" int bx_limb_bmm(const void* a, int32_t a_bytes, int64_t saz, int64_t 
   BX_REQUIRE(Z <= 65535, "Z <= 65535");
   if (Z == 0 || M == 0 || N == 0) return BX_OK;
   BX_REQUIRE(a && b && c, "null pointer");
-  dim3 grid((N + 63) / 64, (M + 63) / 64, Z);
+  const dim3 grid((N + kBT - 1) / kBT, (M + kBT - 1) / kBT, Z);
   hipStream_t st = (hipStream_t)stream;
+  if (K == 0) {   // an empty sum: zeros (one step over a zero-length K reads nothing)
+    bmm_mfma_kernel<int32_t, int32_t, 1, 1><<<grid, 256, 0, st>>>((const int32_t*)a, saz, sam, sak, (const int32_t*)b,
+                                                                  sbz, sbk, sbn, c, scz, scm, scn, M, N, 0);
+    return check_launch("bmm_mfma_kernel");
+  }
   if (a_bytes == 4 && b_bytes == 4)
-    bmm_kernel<int32_t, int32_t><<<grid, 256, 0, st>>>((const int32_t*)a, saz, sam, sak, (const int32_t*)b, sbz, sbk,
-                                                      sbn, c, scz, scm, scn, M, N, K, na, nb);
+    launch_na<int32_t, int32_t>(na, nb, grid, st, a, saz, sam, sak, b, sbz, sbk, sbn, c, scz, scm, scn, M, N, K);
   else if (a_bytes == 4)
-    bmm_kernel<int32_t, int64_t><<<grid, 256, 0, st>>>((const int32_t*)a, saz, sam, sak, (const int64_t*)b, sbz, sbk,
-                                                      sbn, c, scz, scm, scn, M, N, K, na, nb);
+    launch_na<int32_t, int64_t>(na, nb, grid, st, a, saz, sam, sak, b, sbz, sbk, sbn, c, scz, scm, scn, M, N, K);
   else if (b_bytes == 4)
-    bmm_kernel<int64_t, int32_t><<<grid, 256, 0, st>>>((const int64_t*)a, saz, sam, sak, (const int32_t*)b, sbz, sbk,
-                                                      sbn, c, scz, scm, scn, M, N, K, na, nb);
+    launch_na<int64_t, int32_t>(na, nb, grid, st, a, saz, sam, sak, b, sbz, sbk, sbn, c, scz, scm, scn, M, N, K);
   else
-    bmm_kernel<int64_t, int64_t><<<grid, 256, 0, st>>>((const int64_t*)a, saz, sam, sak, (const int64_t*)b, sbz, sbk,
-                                                      sbn, c, scz, scm, scn, M, N, K, na, nb);
-  return check_launch("bmm_kernel");
+    launch_na<int64_t, int64_t>(na, nb, grid, st, a, saz, sam, sak, b, sbz, sbk, sbn, c, scz, scm, scn, M, N, K);
+  return check_launch("bmm_mfma_kernel");
 }

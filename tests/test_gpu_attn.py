@@ -209,6 +209,32 @@ def test_bmm_exact(dev):
     a = torch.randint(-128, 128, (2, 9, 33), generator=g)
     b = torch.randint(-R.LIM3, R.LIM3 + 1, (2, 33, 11), generator=g)
     assert np.array_equal(bmm(a.to(dev), b.to(dev), na=1).cpu().numpy(), R.bmm(a.numpy(), b.numpy()))
+    for na, nb in ((1, 2), (2, 3), (3, 1), (2, 2)):
+        la, lb = (-128, 127) if na == 1 else (-R.LIM[na], R.LIM[na]), (-128, 127) if nb == 1 else (-R.LIM[nb], R.LIM[nb])
+        a = torch.randint(la[0], la[1] + 1, (3, 70, 150), generator=g)
+        b = torch.randint(lb[0], lb[1] + 1, (3, 150, 66), generator=g)
+        assert np.array_equal(bmm(a.to(dev), b.to(dev), na=na, nb=nb).cpu().numpy(), R.bmm(a.numpy(), b.numpy()))
+    # A transposed in memory (m contiguous), both int32
+    a = torch.randint(-R.LIM3, R.LIM3 + 1, (2, 67, 100), generator=g).to(torch.int32)
+    b = torch.randint(-R.LIM3, R.LIM3 + 1, (2, 100, 65), generator=g).to(torch.int32)
+    at = a.to(dev).transpose(1, 2).contiguous().transpose(1, 2)
+    assert np.array_equal(bmm(at, b.to(dev)).cpu().numpy(), R.bmm(a.numpy(), b.numpy()))
+
+
+def test_bmm_int32_bound(dev):
+    """The int32 limb-weight sums at the reference's bound (K < 43690): every limb -128, the largest K, and a
+    mixed-sign case, against Python-int products."""
+    from bitexact.bmm import bmm
+    K = 43689
+    x = -128 - 128 * 256 - 128 * 65536                  # three limbs of -128
+    a = torch.full((1, 3, K), x, dtype=torch.long)
+    b = torch.full((1, K, 5), x, dtype=torch.int32)
+    got = bmm(a.to(dev), b.to(dev)).cpu().numpy()
+    assert (got == x * x * K).all()
+    b2 = b.clone()
+    b2[0, ::2] = R.LIM3                                  # three limbs of 127
+    got = bmm(a.to(dev), b2.to(dev)).cpu().numpy()
+    assert (got == x * x * (K // 2) + x * R.LIM3 * ((K + 1) // 2)).all()
 
 
 def test_unfused_equals_fused_attention(dev):
