@@ -3,8 +3,9 @@
 // as its first na / nb signed base-256 digits (what the reference's limb split keeps; identical for values within
 // the limbs).
 //
-// A 256-thread block owns a 64 x 64 output tile and walks K in 64-deep steps. Each step's operand tiles are loaded
-// four k values per thread (the thread-to-element map follows whichever of the operand's strides is 1, so the loads
+// A 256-thread block owns 64 rows x up to 4 consecutive 64-column tiles and walks each tile's K in 64-deep steps
+// (one flattened sequence, so the next tile's loads overlap this tile's stores). Each step's operand tiles are
+// loaded four k values per thread (the thread-to-element map follows whichever of the operand's strides is 1, so the loads
 // coalesce for q.k with K^T and for p.v alike), split into signed int8 limbs and written to LDS as limb planes
 // [limb][row][64 k] (16-byte k chunks XOR-swizzled by row so the MFMA operand reads are conflict-free); the next
 // step's values are loaded into registers while the current step's MFMAs run. Wave w computes rows 16 w .. 16 w + 15
@@ -30,20 +31,22 @@ __device__ __forceinline__ void load4(const T* base, int64_t sr, int64_t sk, int
   for (int e = 0; e < 4; ++e) v[e] = ldv(base, (int64_t)r * sr + (int64_t)(k + e) * sk, r < R && k + e < K);
 }
 
-// Signed limbs of four values, packed by k into one 32-bit word per limb, written to the n limb planes.
+// Signed limbs of four values, packed by k into one 32-bit word per limb, written to the n limb planes. The first
+// n signed base-256 digits of any v are the bytes of v + 0x808080 (mod 2^(8 n)) less 128 each (adding 128 at every
+// digit position turns the signed split's floor steps into plain byte extraction), so each plane word is one byte
+// gather of the four biased values and an xor.
 __device__ __forceinline__ void store4(int8_t* planes, int n, int row, int q, const int64_t v[4]) {
-  int64_t r[4] = {v[0], v[1], v[2], v[3]};
+  const uint32_t u0 = (uint32_t)v[0] + 0x808080u, u1 = (uint32_t)v[1] + 0x808080u;
+  const uint32_t u2 = (uint32_t)v[2] + 0x808080u, u3 = (uint32_t)v[3] + 0x808080u;
+  int8_t* dst = planes + swz(row, q >> 2) + (q & 3) * 4;
   for (int l = 0; l < n; ++l) {
-    uint32_t w = 0;
-#pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      const int64_t lo = limb_lo64(r[e]);
-      w |= (uint32_t)(lo & 255) << (8 * e);
-      r[e] = (r[e] - lo) >> 8;
-    }
-    *(uint32_t*)(planes + l * kPlane + swz(row, q >> 2) + (q & 3) * 4) = w;
+    const uint32_t sel = (uint32_t)l | ((uint32_t)(4 + l) << 8) | 0x0c0c0000u;   // [x.b_l, y.b_l, 0, 0]
+    const uint32_t lo = __builtin_amdgcn_perm(u1, u0, sel), hi = __builtin_amdgcn_perm(u3, u2, sel);
+    *(uint32_t*)(dst + l * kPlane) = __builtin_amdgcn_perm(hi, lo, 0x05040100u) ^ 0x80808080u;
   }
 }
+
+constexpr int kNTI = 4;   // column tiles per block, walked in sequence (the next tile's loads overlap this one's stores)
 
 template <typename TA, typename TB, int NA, int NB>
 __global__ __launch_bounds__(256) void bmm_mfma_kernel(const TA* a, int64_t saz, int64_t sam, int64_t sak, const TB* b,
@@ -53,7 +56,7 @@ __global__ __launch_bounds__(256) void bmm_mfma_kernel(const TA* a, int64_t saz,
   __shared__ __align__(16) int8_t As[NA * kPlane];
   __shared__ __align__(16) int8_t Bs[NB * kPlane];
   const int64_t z = blockIdx.z;
-  const int m0 = blockIdx.y * kBT, n0 = blockIdx.x * kBT;
+  const int m0 = blockIdx.y * kBT, nb0 = blockIdx.x * kBT * kNTI;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const TA* ab = a + z * saz;
   const TB* bb = b + z * sbz;
@@ -68,12 +71,17 @@ __global__ __launch_bounds__(256) void bmm_mfma_kernel(const TA* a, int64_t saz,
     br[g] = b_k ? idx / 16 : idx % 64;
     bq[g] = b_k ? idx % 16 : idx / 64;
   }
+  // steps: (column tile j, k step) flattened, j outer
+  const int ksteps = max(1, (K + kBT - 1) / kBT);
+  const int ntile = min(kNTI, (N - nb0 + kBT - 1) / kBT);
+  const int nsteps = ntile * ksteps;
   int64_t va[4][4], vb[4][4];
-  auto fetch = [&](int k0) {
+  auto fetch = [&](int st) {
+    const int j = st / ksteps, k0 = (st % ksteps) * kBT;
 #pragma unroll
     for (int g = 0; g < 4; ++g) {
       load4(ab, sam, sak, m0 + ar[g], M, k0 + 4 * aq[g], K, va[g]);
-      load4(bb, sbn, sbk, n0 + br[g], N, k0 + 4 * bq[g], K, vb[g]);
+      load4(bb, sbn, sbk, nb0 + j * kBT + br[g], N, k0 + 4 * bq[g], K, vb[g]);
     }
   };
   v4i acc[NS][4];
@@ -83,14 +91,14 @@ __global__ __launch_bounds__(256) void bmm_mfma_kernel(const TA* a, int64_t saz,
     for (int cb = 0; cb < 4; ++cb) acc[s][cb] = v4i{0, 0, 0, 0};
   fetch(0);
   const int r16 = lane & 15, ch = lane >> 4;
-  for (int k0 = 0; k0 < K; k0 += kBT) {
+  for (int st = 0; st < nsteps; ++st) {
 #pragma unroll
     for (int g = 0; g < 4; ++g) {
       store4(As, NA, ar[g], aq[g], va[g]);
       store4(Bs, NB, br[g], bq[g], vb[g]);
     }
     __syncthreads();
-    if (k0 + kBT < K) fetch(k0 + kBT);   // the next step's values travel while this step's MFMAs run
+    if (st + 1 < nsteps) fetch(st + 1);   // the next step's values travel while this step's MFMAs run
     v4i af[NA];
 #pragma unroll
     for (int i = 0; i < NA; ++i) af[i] = *(const v4i*)(As + i * kPlane + swz(16 * wave + r16, ch));
@@ -104,18 +112,22 @@ __global__ __launch_bounds__(256) void bmm_mfma_kernel(const TA* a, int64_t saz,
           acc[i + j][cb] = __builtin_amdgcn_mfma_i32_16x16x64_i8(af[i], bf, acc[i + j][cb], 0, 0, 0);
       }
     __syncthreads();
-  }
-  // lane l holds column 16 cb + l % 16, rows 4 (l / 16) + e of the wave's 16-row block
+    if (st % ksteps != ksteps - 1) continue;
+    // the column tile is complete: lane l holds column 16 cb + l % 16, rows 4 (l / 16) + e of the wave's 16 rows
+    const int n0 = nb0 + (st / ksteps) * kBT;
 #pragma unroll
-  for (int cb = 0; cb < 4; ++cb) {
-    const int n = n0 + 16 * cb + r16;
+    for (int cb = 0; cb < 4; ++cb) {
+      const int n = n0 + 16 * cb + r16;
 #pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      const int m = m0 + 16 * wave + 4 * ch + e;
-      int64_t v = 0;
+      for (int e = 0; e < 4; ++e) {
+        const int m = m0 + 16 * wave + 4 * ch + e;
+        int64_t v = 0;
 #pragma unroll
-      for (int s = 0; s < NS; ++s) v += (int64_t)acc[s][cb][e] << (8 * s);
-      if (m < M && n < N) c[z * scz + (int64_t)m * scm + (int64_t)n * scn] = v;
+        for (int s = 0; s < NS; ++s) v += (int64_t)acc[s][cb][e] << (8 * s);
+        if (m < M && n < N) c[z * scz + (int64_t)m * scm + (int64_t)n * scn] = v;
+      }
+#pragma unroll
+      for (int s = 0; s < NS; ++s) acc[s][cb] = v4i{0, 0, 0, 0};
     }
   }
 }
@@ -158,9 +170,9 @@ extern "C" int bx_limb_bmm(const void* a, int32_t a_bytes, int64_t saz, int64_t 
   BX_REQUIRE(Z <= 65535, "Z <= 65535");
   if (Z == 0 || M == 0 || N == 0) return BX_OK;
   BX_REQUIRE(a && b && c, "null pointer");
-  const dim3 grid((N + kBT - 1) / kBT, (M + kBT - 1) / kBT, Z);
+  const dim3 grid((N + kBT * kNTI - 1) / (kBT * kNTI), (M + kBT - 1) / kBT, Z);
   hipStream_t st = (hipStream_t)stream;
-  if (K == 0) {   // an empty sum: zeros (one step over a zero-length K reads nothing)
+  if (K == 0) {   // an empty sum: zeros (one step per column tile over a zero-length K reads nothing)
     bmm_mfma_kernel<int32_t, int32_t, 1, 1><<<grid, 256, 0, st>>>((const int32_t*)a, saz, sam, sak, (const int32_t*)b,
                                                                   sbz, sbk, sbn, c, scz, scm, scn, M, N, 0);
     return check_launch("bmm_mfma_kernel");
