@@ -188,15 +188,15 @@ def bench_decode(dev, steps, warmup):
 def bench_read_ceiling(dev, reps=64):
     """The practical read ceiling at the decode GEMMs' sizes: a bare streaming-read kernel (bx_stream_read: 16-byte
     nontemporal loads, grid-stride, nothing computed) over 16.8 MB (a down GEMM's weights) and 33.6 MB (gate|up),
-    rotating over >= 1 GiB of buffers so every launch reads HBM, graph-replayed and timed with HIP events on the
-    launch stream like the GEMMs. Best of a few launch shapes."""
+    and 268 MB for the large-read asymptote, rotating over >= 1 GiB of buffers so every launch reads HBM,
+    graph-replayed and timed with HIP events on the launch stream like the GEMMs. Best of a few launch shapes."""
     import ctypes
     import torch
     from bitexact import _hip
     sink = torch.zeros(1, dtype=torch.int32, device=dev)
     stream = torch.cuda.Stream(dev)
     out = {}
-    for name, nbytes in (("16.8MB", 2048 * 8192), ("33.6MB", 16384 * 2048)):
+    for name, nbytes in (("16.8MB", 2048 * 8192), ("33.6MB", 16384 * 2048), ("268MB", 1 << 28)):
         n = max(4, -(-(1 << 30) // nbytes))
         bufs = [torch.empty(nbytes, dtype=torch.uint8, device=dev) for _ in range(n)]
         for b in bufs:
