@@ -55,7 +55,7 @@ struct LinArgs {
   int spw;               // gemv: k steps per wave
   int nla;               // gemv: stacked activation groups (exact 3, JOIN nl, RAW32 1); rows_a = nla M
   int tiles, parts_lg, mp;   // gemv: column tiles, log2 of the row parts per tile, output rows per part
-  int xcd_remap;             // xtile: XCD-grouped tile order (tile count a multiple of 8, row tiles of 4)
+  int xcd_remap;             // xtile: XCD-grouped tile order, row tiles per group (0: off; tile count a multiple of 8)
 };
 
 // Residual column index. Valid ELL data is always in [0, K) with counts in [0, R]; a corrupt index or count
@@ -817,9 +817,10 @@ __global__ __launch_bounds__(WM * WN * 64) void xtile_kernel(LinArgs p) {
   if (p.xcd_remap) {
     const int T = gridDim.x * gridDim.y, b = blockIdx.y * gridDim.x + blockIdx.x;
     const int v = (b & 7) * (T >> 3) + (b >> 3);
-    const int grp = v / (4 * gridDim.x), in = v - grp * 4 * gridDim.x;
-    ty = grp * 4 + (in & 3);
-    tx = in >> 2;
+    const int R = p.xcd_remap;
+    const int grp = v / (R * gridDim.x), in = v - grp * R * gridDim.x;
+    ty = grp * R + in % R;
+    tx = in / R;
   }
   const int m0 = ty * BM, n0 = tx * BN;
   const int nk = p.K / BK;                                  // K % 64 == 0 and no K split (planner)
@@ -1864,9 +1865,9 @@ static int launch_tile(LinArgs& p, const Plan& s, hipStream_t st) {
     if constexpr (NA * NB == 9 && (MODE == EXACT || MODE == WMM_T)) {
       // BX_XTILE=0 / BX_XCD=0 switch the pipelined tile / its XCD-grouped order off (the same integers either way)
       static const int xt = getenv("BX_XTILE") ? atoi(getenv("BX_XTILE")) : 1;
-      static const int xcd = getenv("BX_XCD") ? atoi(getenv("BX_XCD")) : 1;
+      static const int xcd = getenv("BX_XCD") ? atoi(getenv("BX_XCD")) : 4;   // row tiles per XCD group
       if (xt && xtile_fits(p, s)) {
-        p.xcd_remap = xcd && (s.tiles_x * s.tiles_y) % 8 == 0 && s.tiles_y % 4 == 0;
+        p.xcd_remap = (xcd > 0 && (s.tiles_x * s.tiles_y) % 8 == 0 && s.tiles_y % xcd == 0) ? xcd : 0;
         allow_lds(xtile_kernel<MODE, 4, 2, 1, 2>, kXtLds);
         xtile_kernel<MODE, 4, 2, 1, 2><<<dim3(s.tiles_x, s.tiles_y, 1), 512, kXtLds, st>>>(p);
         return check_launch("xtile_kernel");
