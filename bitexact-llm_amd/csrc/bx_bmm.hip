@@ -14,6 +14,9 @@
 // is formed once, in registers, before the store.
 #include "bx_common.h"
 
+#include <algorithm>
+#include <cstdlib>
+
 namespace bx {
 
 constexpr int kBT = 64;                 // output tile edge, k step
@@ -22,11 +25,12 @@ constexpr int kPlane = kBT * kBT;       // bytes of one limb plane of a tile (64
 __device__ __forceinline__ int swz(int row, int chunk) { return row * kBT + ((chunk ^ ((row >> 2) & 3)) << 4); }
 
 template <typename T>
-__device__ __forceinline__ int64_t ldv(const T* p, int64_t off, bool ok) { return ok ? (int64_t)p[off] : 0; }
+__device__ __forceinline__ uint32_t ldv(const T* p, int64_t off, bool ok) { return ok ? (uint32_t)p[off] : 0u; }
 
-// The four values (row r, k = k0 + 4 q .. + 3) of one operand; rows past R or k past K read as 0.
+// The low 32 bits of the four values (row r, k = k0 + 4 q .. + 3) of one operand (the limb split below reads only
+// the low 24); rows past R or k past K read as 0.
 template <typename T>
-__device__ __forceinline__ void load4(const T* base, int64_t sr, int64_t sk, int r, int R, int k, int K, int64_t v[4]) {
+__device__ __forceinline__ void load4(const T* base, int64_t sr, int64_t sk, int r, int R, int k, int K, uint32_t v[4]) {
 #pragma unroll
   for (int e = 0; e < 4; ++e) v[e] = ldv(base, (int64_t)r * sr + (int64_t)(k + e) * sk, r < R && k + e < K);
 }
@@ -35,9 +39,8 @@ __device__ __forceinline__ void load4(const T* base, int64_t sr, int64_t sk, int
 // n signed base-256 digits of any v are the bytes of v + 0x808080 (mod 2^(8 n)) less 128 each (adding 128 at every
 // digit position turns the signed split's floor steps into plain byte extraction), so each plane word is one byte
 // gather of the four biased values and an xor.
-__device__ __forceinline__ void store4(int8_t* planes, int n, int row, int q, const int64_t v[4]) {
-  const uint32_t u0 = (uint32_t)v[0] + 0x808080u, u1 = (uint32_t)v[1] + 0x808080u;
-  const uint32_t u2 = (uint32_t)v[2] + 0x808080u, u3 = (uint32_t)v[3] + 0x808080u;
+__device__ __forceinline__ void store4(int8_t* planes, int n, int row, int q, const uint32_t v[4]) {
+  const uint32_t u0 = v[0] + 0x808080u, u1 = v[1] + 0x808080u, u2 = v[2] + 0x808080u, u3 = v[3] + 0x808080u;
   int8_t* dst = planes + swz(row, q >> 2) + (q & 3) * 4;
   for (int l = 0; l < n; ++l) {
     const uint32_t sel = (uint32_t)l | ((uint32_t)(4 + l) << 8) | 0x0c0c0000u;   // [x.b_l, y.b_l, 0, 0]
@@ -46,17 +49,17 @@ __device__ __forceinline__ void store4(int8_t* planes, int n, int row, int q, co
   }
 }
 
-constexpr int kNTI = 4;   // column tiles per block, walked in sequence (the next tile's loads overlap this one's stores)
+constexpr int kNTI = 8;   // default column tiles per block, walked in sequence (the next tile's loads overlap this one's stores)
 
 template <typename TA, typename TB, int NA, int NB>
 __global__ __launch_bounds__(256) void bmm_mfma_kernel(const TA* a, int64_t saz, int64_t sam, int64_t sak, const TB* b,
                                                        int64_t sbz, int64_t sbk, int64_t sbn, int64_t* c, int64_t scz,
-                                                       int64_t scm, int64_t scn, int M, int N, int K) {
+                                                       int64_t scm, int64_t scn, int M, int N, int K, int nti) {
   constexpr int NS = NA + NB - 1;
   __shared__ __align__(16) int8_t As[NA * kPlane];
   __shared__ __align__(16) int8_t Bs[NB * kPlane];
   const int64_t z = blockIdx.z;
-  const int m0 = blockIdx.y * kBT, nb0 = blockIdx.x * kBT * kNTI;
+  const int m0 = blockIdx.y * kBT, nb0 = blockIdx.x * kBT * nti;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const TA* ab = a + z * saz;
   const TB* bb = b + z * sbz;
@@ -73,9 +76,9 @@ __global__ __launch_bounds__(256) void bmm_mfma_kernel(const TA* a, int64_t saz,
   }
   // steps: (column tile j, k step) flattened, j outer
   const int ksteps = max(1, (K + kBT - 1) / kBT);
-  const int ntile = min(kNTI, (N - nb0 + kBT - 1) / kBT);
+  const int ntile = min(nti, (N - nb0 + kBT - 1) / kBT);
   const int nsteps = ntile * ksteps;
-  int64_t va[4][4], vb[4][4];
+  uint32_t va[4][4], vb[4][4];
   auto fetch = [&](int st) {
     const int j = st / ksteps, k0 = (st % ksteps) * kBT;
 #pragma unroll
@@ -135,24 +138,24 @@ __global__ __launch_bounds__(256) void bmm_mfma_kernel(const TA* a, int64_t saz,
 template <typename TA, typename TB, int NA>
 static void launch_nb(int nb, dim3 grid, hipStream_t st, const TA* a, int64_t saz, int64_t sam, int64_t sak,
                       const TB* b, int64_t sbz, int64_t sbk, int64_t sbn, int64_t* c, int64_t scz, int64_t scm,
-                      int64_t scn, int M, int N, int K) {
+                      int64_t scn, int M, int N, int K, int nti) {
   if (nb == 1)
-    bmm_mfma_kernel<TA, TB, NA, 1><<<grid, 256, 0, st>>>(a, saz, sam, sak, b, sbz, sbk, sbn, c, scz, scm, scn, M, N, K);
+    bmm_mfma_kernel<TA, TB, NA, 1><<<grid, 256, 0, st>>>(a, saz, sam, sak, b, sbz, sbk, sbn, c, scz, scm, scn, M, N, K, nti);
   else if (nb == 2)
-    bmm_mfma_kernel<TA, TB, NA, 2><<<grid, 256, 0, st>>>(a, saz, sam, sak, b, sbz, sbk, sbn, c, scz, scm, scn, M, N, K);
+    bmm_mfma_kernel<TA, TB, NA, 2><<<grid, 256, 0, st>>>(a, saz, sam, sak, b, sbz, sbk, sbn, c, scz, scm, scn, M, N, K, nti);
   else
-    bmm_mfma_kernel<TA, TB, NA, 3><<<grid, 256, 0, st>>>(a, saz, sam, sak, b, sbz, sbk, sbn, c, scz, scm, scn, M, N, K);
+    bmm_mfma_kernel<TA, TB, NA, 3><<<grid, 256, 0, st>>>(a, saz, sam, sak, b, sbz, sbk, sbn, c, scz, scm, scn, M, N, K, nti);
 }
 
 template <typename TA, typename TB>
 static void launch_na(int na, int nb, dim3 grid, hipStream_t st, const void* a, int64_t saz, int64_t sam, int64_t sak,
                       const void* b, int64_t sbz, int64_t sbk, int64_t sbn, int64_t* c, int64_t scz, int64_t scm,
-                      int64_t scn, int M, int N, int K) {
+                      int64_t scn, int M, int N, int K, int nti) {
   const TA* A = (const TA*)a;
   const TB* B = (const TB*)b;
-  if (na == 1) launch_nb<TA, TB, 1>(nb, grid, st, A, saz, sam, sak, B, sbz, sbk, sbn, c, scz, scm, scn, M, N, K);
-  else if (na == 2) launch_nb<TA, TB, 2>(nb, grid, st, A, saz, sam, sak, B, sbz, sbk, sbn, c, scz, scm, scn, M, N, K);
-  else launch_nb<TA, TB, 3>(nb, grid, st, A, saz, sam, sak, B, sbz, sbk, sbn, c, scz, scm, scn, M, N, K);
+  if (na == 1) launch_nb<TA, TB, 1>(nb, grid, st, A, saz, sam, sak, B, sbz, sbk, sbn, c, scz, scm, scn, M, N, K, nti);
+  else if (na == 2) launch_nb<TA, TB, 2>(nb, grid, st, A, saz, sam, sak, B, sbz, sbk, sbn, c, scz, scm, scn, M, N, K, nti);
+  else launch_nb<TA, TB, 3>(nb, grid, st, A, saz, sam, sak, B, sbz, sbk, sbn, c, scz, scm, scn, M, N, K, nti);
 }
 
 }  // namespace bx
@@ -170,20 +173,23 @@ extern "C" int bx_limb_bmm(const void* a, int32_t a_bytes, int64_t saz, int64_t 
   BX_REQUIRE(Z <= 65535, "Z <= 65535");
   if (Z == 0 || M == 0 || N == 0) return BX_OK;
   BX_REQUIRE(a && b && c, "null pointer");
-  const dim3 grid((N + kBT * kNTI - 1) / (kBT * kNTI), (M + kBT - 1) / kBT, Z);
+  // BX_BMM_NTI: column tiles per block (experiments; the same integers for any value)
+  static const int nti_env = getenv("BX_BMM_NTI") ? atoi(getenv("BX_BMM_NTI")) : kNTI;
+  const int nti = std::max(1, std::min(nti_env, 64));
+  const dim3 grid((N + kBT * nti - 1) / (kBT * nti), (M + kBT - 1) / kBT, Z);
   hipStream_t st = (hipStream_t)stream;
   if (K == 0) {   // an empty sum: zeros (one step per column tile over a zero-length K reads nothing)
     bmm_mfma_kernel<int32_t, int32_t, 1, 1><<<grid, 256, 0, st>>>((const int32_t*)a, saz, sam, sak, (const int32_t*)b,
-                                                                  sbz, sbk, sbn, c, scz, scm, scn, M, N, 0);
+                                                                  sbz, sbk, sbn, c, scz, scm, scn, M, N, 0, nti);
     return check_launch("bmm_mfma_kernel");
   }
   if (a_bytes == 4 && b_bytes == 4)
-    launch_na<int32_t, int32_t>(na, nb, grid, st, a, saz, sam, sak, b, sbz, sbk, sbn, c, scz, scm, scn, M, N, K);
+    launch_na<int32_t, int32_t>(na, nb, grid, st, a, saz, sam, sak, b, sbz, sbk, sbn, c, scz, scm, scn, M, N, K, nti);
   else if (a_bytes == 4)
-    launch_na<int32_t, int64_t>(na, nb, grid, st, a, saz, sam, sak, b, sbz, sbk, sbn, c, scz, scm, scn, M, N, K);
+    launch_na<int32_t, int64_t>(na, nb, grid, st, a, saz, sam, sak, b, sbz, sbk, sbn, c, scz, scm, scn, M, N, K, nti);
   else if (b_bytes == 4)
-    launch_na<int64_t, int32_t>(na, nb, grid, st, a, saz, sam, sak, b, sbz, sbk, sbn, c, scz, scm, scn, M, N, K);
+    launch_na<int64_t, int32_t>(na, nb, grid, st, a, saz, sam, sak, b, sbz, sbk, sbn, c, scz, scm, scn, M, N, K, nti);
   else
-    launch_na<int64_t, int64_t>(na, nb, grid, st, a, saz, sam, sak, b, sbz, sbk, sbn, c, scz, scm, scn, M, N, K);
+    launch_na<int64_t, int64_t>(na, nb, grid, st, a, saz, sam, sak, b, sbz, sbk, sbn, c, scz, scm, scn, M, N, K, nti);
   return check_launch("bmm_mfma_kernel");
 }
