@@ -476,6 +476,54 @@ __global__ void stream_read_kernel(const v4i* __restrict__ src, int64_t n16, int
   if (acc == 0x5eed5eed) sink[0] = acc;   // keeps the loads; practically never taken
 }
 
+// Back-to-back int8 MFMAs from registers (CH independent accumulator chains per wave, no memory traffic in the
+// loop): the dense int8 rate the matrix cores sustain, for the prefill kernels' roofline. SHAPE 0:
+// v_mfma_i32_32x32x32_i8 (65536 ops), 1: v_mfma_i32_16x16x64_i8 (32768 ops). RND: the operands take fresh
+// pseudo-random bytes every iteration (a 32-bit LCG per dword, 16 VALU per 4 MFMAs), as a GEMM's limbs do; the
+// matrix cores' clock under load depends on how many operand bits switch, so constant operands overstate the rate
+// (mul = 1, inc = 0 runs the same instructions on constant operands: the control).
+template <int SHAPE, bool RND>
+__global__ void mfma_rate_kernel(int iters, int32_t mul, int32_t inc, int32_t* sink) {
+  constexpr int CH = 4;
+  const int lane = threadIdx.x & 63;
+  v4i a = {lane, lane * 3, lane ^ 5, 7}, b = {lane * 5, 1, lane + 2, lane ^ 9};
+  int32_t x = 0;
+  if constexpr (SHAPE == 0) {
+    v16i acc[CH];
+#pragma unroll
+    for (int c = 0; c < CH; ++c)
+#pragma unroll
+      for (int e = 0; e < 16; ++e) acc[c][e] = c;
+    for (int it = 0; it < iters; ++it) {
+#pragma unroll
+      for (int c = 0; c < CH; ++c) acc[c] = __builtin_amdgcn_mfma_i32_32x32x32_i8(a, b, acc[c], 0, 0, 0);
+      if (RND) {
+        a = a * mul + inc;
+        b = b * mul + (inc ^ 0x55555555);
+      }
+    }
+#pragma unroll
+    for (int c = 0; c < CH; ++c)
+#pragma unroll
+      for (int e = 0; e < 16; ++e) x ^= acc[c][e];
+  } else {
+    v4i acc[CH];
+#pragma unroll
+    for (int c = 0; c < CH; ++c) acc[c] = v4i{c, c, c, c};
+    for (int it = 0; it < iters; ++it) {
+#pragma unroll
+      for (int c = 0; c < CH; ++c) acc[c] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a, b, acc[c], 0, 0, 0);
+      if (RND) {
+        a = a * mul + inc;
+        b = b * mul + (inc ^ 0x55555555);
+      }
+    }
+#pragma unroll
+    for (int c = 0; c < CH; ++c) x ^= acc[c][0] ^ acc[c][1] ^ acc[c][2] ^ acc[c][3];
+  }
+  if (x == 0x5eed5eed) sink[0] = x;   // keeps the MFMAs; practically never taken
+}
+
 static int fill_operands(Operand* o, int nin, const void* const* ptrs, const int64_t* desc) {
   BX_REQUIRE(nin >= 0 && nin <= kMaxIn, "at most %d operands", kMaxIn);
   for (int j = 0; j < kMaxIn; ++j) o[j] = Operand{nullptr, 0, 0, 0, 8};
@@ -547,4 +595,17 @@ extern "C" int bx_stream_read(const void* src, int64_t bytes, int32_t blocks, in
   BX_REQUIRE(blocks > 0 && threads > 0 && threads <= 1024 && threads % 64 == 0, "bad launch shape");
   stream_read_kernel<<<blocks, threads, 0, (hipStream_t)stream>>>((const v4i*)src, bytes / 16, sink);
   return check_launch("stream_read_kernel");
+}
+
+extern "C" int bx_mfma_rate(int32_t shape, int32_t iters, int32_t blocks, int32_t threads, int32_t* sink,
+                            bx_stream_t stream) {
+  BX_REQUIRE(sink && shape >= 0 && shape <= 5 && iters > 0, "bad mfma-rate arguments");
+  BX_REQUIRE(blocks > 0 && threads > 0 && threads <= 1024 && threads % 64 == 0, "bad launch shape");
+  const hipStream_t st = (hipStream_t)stream;
+  const int32_t mul = shape >= 4 ? 1 : 1664525, inc = shape >= 4 ? 0 : 1013904223;
+  if (shape == 0) mfma_rate_kernel<0, false><<<blocks, threads, 0, st>>>(iters, mul, inc, sink);
+  else if (shape == 1) mfma_rate_kernel<1, false><<<blocks, threads, 0, st>>>(iters, mul, inc, sink);
+  else if (shape % 2 == 0) mfma_rate_kernel<0, true><<<blocks, threads, 0, st>>>(iters, mul, inc, sink);
+  else mfma_rate_kernel<1, true><<<blocks, threads, 0, st>>>(iters, mul, inc, sink);
+  return check_launch("mfma_rate_kernel");
 }

@@ -333,6 +333,14 @@ int bx_int_rowop(int32_t op, int32_t nin, const void* const* ptrs, const int64_t
  * one launch at that size. sink: an int32 [1] device word (practically never written). */
 int bx_stream_read(const void* src, int64_t bytes, int32_t blocks, int32_t threads, int32_t* sink, bx_stream_t stream);
 
+/* No counterpart in the reference: a measurement probe for the prefill kernels' roofline. Each of blocks x threads
+ * lanes' waves issues iters x 4 independent int8 MFMAs from registers (shape 0: v_mfma_i32_32x32x32_i8, 65536 ops;
+ * 1: v_mfma_i32_16x16x64_i8, 32768 ops; 2 and 3: the same with fresh pseudo-random operand bytes every iteration;
+ * 4 and 5: the instructions of 2 and 3 with the operands held constant)
+ * with no memory traffic: the dense int8 rate the matrix cores sustain.
+ * sink: an int32 [1] device word (practically never written). */
+int bx_mfma_rate(int32_t shape, int32_t iters, int32_t blocks, int32_t threads, int32_t* sink, bx_stream_t stream);
+
 #ifdef __cplusplus
 }
 #endif
