@@ -1133,6 +1133,11 @@ __global__ __launch_bounds__(64 * NWV) void stream_kernel(LinArgs p) {
   constexpr int RP = RBM < 2 ? 32 : 16 * RBM, BK = kStBK, C = 16 * NWV, NT = 64 * NWV;   // loaded rows: x 32
   constexpr int SA = RP * BK, STAGE = SA + NB * C * BK;
   constexpr int LA = RP / 8, LT = LA + NB * C / 8, LPW = LT / NWV;   // 1 KiB load instructions per stage / wave
+  // RS: at 128 rows and one weight plane a wave owns two 16-row blocks x every column of the tile, not 16 columns x
+  // every row: a k chunk's LDS operand reads per block drop from 4 x (128 + 16) rows to 4 x (32 + 64)
+  constexpr bool RS = RBM == 2 * NWV && NB == 1 && MODE != EXACT && MODE != WMM_T;
+  constexpr int CB = C / 16;
+  static_assert(!RS || RBM == 2 * CB, "RS layout: as many accumulators as the row-block layout");
   static_assert(LT % NWV == 0, "load instructions per stage must split over the waves");
   extern __shared__ __align__(16) char smem[];
   const int tid = threadIdx.x, lane = tid & 63;
@@ -1190,6 +1195,26 @@ __global__ __launch_bounds__(64 * NWV) void stream_kernel(LinArgs p) {
 #pragma unroll
     for (int h = 0; h < 2; ++h) {
       const int c = 4 * h + (lane >> 4);
+      if constexpr (RS) {
+        // wave w: row blocks w and w + NWV, every column block of the tile (acc[q CB + cb])
+        v4i b[CB], a[2];
+#pragma unroll
+        for (int cb = 0; cb < CB; ++cb) {
+          const int brow = cb * 16 + r16;
+          b[cb] = *(const v4i*)(base + SA + brow * BK + ((c ^ ((brow >> 1) & 7)) << 4));
+        }
+#pragma unroll
+        for (int q = 0; q < 2; ++q) {
+          const int arow = (wave + NWV * q) * 16 + r16;
+          a[q] = *(const v4i*)(base + arow * BK + ((c ^ ((arow >> 1) & 7)) << 4));
+        }
+#pragma unroll
+        for (int q = 0; q < 2; ++q)
+#pragma unroll
+          for (int cb = 0; cb < CB; ++cb)
+            acc[q * CB + cb][0] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a[q], b[cb], acc[q * CB + cb][0], 0, 0, 0);
+        continue;
+      }
       v4i b[NB];
 #pragma unroll
       for (int j = 0; j < NB; ++j)
@@ -1210,9 +1235,25 @@ __global__ __launch_bounds__(64 * NWV) void stream_kernel(LinArgs p) {
   ring_barrier<0>();
   bool bad = false, corrupt = false;
   const int Mo = MODE == RAW32 ? rows : p.M;                   // output rows
+  if constexpr (RS) {
+    // JOIN at M = 64 with two limbs: limb rows m and 64 + m sit in the lane's row blocks w and w + 4
+    if (MODE == JOIN && p.M == 64 && p.nl == 2) {   // block-uniform
+#pragma unroll
+      for (int cb = 0; cb < CB; ++cb) {
+        const int n = n0 + cb * 16 + (lane & 15);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const int64_t v = (int64_t)acc[cb][0][e] + ((int64_t)acc[CB + cb][0][e] << 8);
+          const int m = wave * 16 + (lane >> 4) * 4 + e;
+          if (n < p.N) ((int64_t*)p.out)[(int64_t)m * p.N + n] = v;
+        }
+      }
+      return;
+    }
+  }
   // ---- JOIN with whole 16-row limb blocks (M % 16 == 0): limb row i M + m sits in block m / 16 + i M / 16 of the
   // same lane and element, so the join is done in registers ----
-  if constexpr (MODE == JOIN && NB == 1) {
+  if constexpr (MODE == JOIN && NB == 1 && !RS) {
     if (p.M % 16 == 0 && p.nl * p.M <= RP) {   // block-uniform
       const int n = n0 + wave * 16 + (lane & 15), bm = p.M >> 4;
 #pragma unroll
@@ -1238,13 +1279,23 @@ __global__ __launch_bounds__(64 * NWV) void stream_kernel(LinArgs p) {
   // four row groups of a store land in different banks) ----
   constexpr int CP = C + 1;
   int32_t* Cs = (int32_t*)smem;
+  if constexpr (RS) {
 #pragma unroll
-  for (int r = 0; r < RBM; ++r)
+    for (int q = 0; q < 2; ++q)
 #pragma unroll
-    for (int j = 0; j < NB; ++j)
+      for (int cb = 0; cb < CB; ++cb)
 #pragma unroll
-      for (int e = 0; e < 4; ++e)
-        Cs[(j * RP + r * 16 + (lane >> 4) * 4 + e) * CP + wave * 16 + (lane & 15)] = acc[r][j][e];
+        for (int e = 0; e < 4; ++e)
+          Cs[((wave + NWV * q) * 16 + (lane >> 4) * 4 + e) * CP + cb * 16 + (lane & 15)] = acc[q * CB + cb][0][e];
+  } else {
+#pragma unroll
+    for (int r = 0; r < RBM; ++r)
+#pragma unroll
+      for (int j = 0; j < NB; ++j)
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+          Cs[(j * RP + r * 16 + (lane >> 4) * 4 + e) * CP + wave * 16 + (lane & 15)] = acc[r][j][e];
+  }
   __syncthreads();
   const int nla = MODE == JOIN ? p.nl : MODE == RAW32 ? 1 : 3;
   if constexpr (MODE == EXACT || MODE == WMM_T) {
