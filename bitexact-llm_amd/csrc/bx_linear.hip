@@ -56,6 +56,7 @@ struct LinArgs {
   int nla;               // gemv: stacked activation groups (exact 3, JOIN nl, RAW32 1); rows_a = nla M
   int tiles, parts_lg, mp;   // gemv: column tiles, log2 of the row parts per tile, output rows per part
   int xcd_remap;             // xtile: XCD-grouped tile order, row tiles per group (0: off; tile count a multiple of 8)
+  int xt_pre;                // xtile: ring stages requested before the epilogue context is written (1..3)
 };
 
 // Residual column index. Valid ELL data is always in [0, K) with counts in [0, R]; a corrupt index or count
@@ -825,20 +826,68 @@ __global__ __launch_bounds__(WM * WN * 64) void xtile_kernel(LinArgs p) {
   const int m0 = ty * BM, n0 = tx * BN;
   const int nk = p.K / BK;                                  // K % 64 == 0 and no K split (planner)
 
-  // ---- epilogue context (threads 0 - 255, before their ring loads) ----
+  // ---- epilogue context, requested first (threads 0 - 255: a column's d, g, count and first kRes list slots,
+  // or a row's exponent, into registers), then the ring fill goes out behind it, then the context is written to
+  // LDS from registers while the ring lands: the start costs one round trip, not three in a row ----
   int E = 0;
   bool ctx_corrupt = false;             // a residual index or count of the block's columns is out of range
+  int64_t cx_a = 0, cx_b = 0;           // d and g of the column, or the row exponent
+  int32_t cx_cnt = 0;
+  int32_t cx_ec[kRes];
+  int64_t cx_ev[kRes];
   if (EX && tid < 256) {
     const int c = tid & 127;
     if (tid < 128) {
       const int n = min(n0 + c, p.N - 1);
-      const int64_t dn = p.d[n];
-      const int cnt = p.R > 0 ? kcnt(p, p.cnt[n], ctx_corrupt) : 0;
-      s_d[c] = dn;
-      s_gdr[c] = p.g[n] - dn + p.FR;
+      cx_a = p.d[n];
+      cx_b = p.g[n];
+      cx_cnt = p.R > 0 ? p.cnt[n] : 0;
+#pragma unroll
+      for (int j = 0; j < kRes; ++j) {
+        const bool slot = j < p.R;   // uniform
+        cx_ec[j] = slot ? p.ecol[(int64_t)n * p.R + j] : 0;
+        cx_ev[j] = slot ? p.eval[(int64_t)n * p.R + j] : 0;
+      }
+    } else {
+      cx_a = p.sh[min(m0 + c, p.M - 1)];
+    }
+  }
+
+  // ---- ring loads: the first half of the waves load the A planes, the second half the B planes; instruction i of
+  // a wave covers 16 rows x 64 bytes (lane: row lane / 4, 16-byte chunk lane % 4, swizzled) ----
+  const int lrow = lane >> 2, lch = ((lane & 3) ^ swz<BK>(lrow)) << 4;
+  const bool isA = wave < NW / 2;
+  const __amdgpu_buffer_rsrc_t rsrc = isA ? __builtin_amdgcn_make_buffer_rsrc(const_cast<int8_t*>(p.a), (short)0,
+                                                                               kBufRange, 0x00020000)
+                                          : __builtin_amdgcn_make_buffer_rsrc(const_cast<int8_t*>(p.w), (short)0,
+                                                                               kBufRange, 0x00020000);
+  int voff[LPW];
+#pragma unroll
+  for (int i = 0; i < LPW; ++i) {
+    const int inst = (wave % (NW / 2)) * LPW + i, pl = inst >> 3, row = (inst & 7) * 16 + lrow;
+    voff[i] = isA ? pl * p.M * p.K + min(m0 + row, p.M - 1) * p.K + lch
+                  : pl * (int)p.ld_plane + min(n0 + row, p.N - 1) * (int)p.ld_row + lch;
+  }
+  auto issue = [&](int kt, int stage) {
+    char* sbase = smem + stage * STAGE + wave * LPW * 1024;
+#pragma unroll
+    for (int i = 0; i < LPW; ++i) buf_lds16(rsrc, sbase + i * 1024, voff[i], kt * BK);
+  };
+
+  // The first LDS write waits for every LDS DMA in flight (the compiler cannot tell the context area from the
+  // ring), so p.xt_pre stages go out before the context is written and the rest after it.
+  for (int t = 0; t < p.xt_pre; ++t)
+    if (t < nk) issue(t, t);
+
+  if (EX && tid < 256) {
+    const int c = tid & 127;
+    if (tid < 128) {
+      const int cnt = p.R > 0 ? kcnt(p, cx_cnt, ctx_corrupt) : 0;
+      s_d[c] = cx_a;
+      s_gdr[c] = cx_b - cx_a + p.FR;
       s_cs[c] = n0 + c < p.N ? cnt : 0;
     } else {
-      const int64_t v = p.sh[min(m0 + c, p.M - 1)];
+      const int64_t v = cx_a;
       s_sh[c] = v;
       int64_t lo = v, hi = v;
 #pragma unroll
@@ -871,32 +920,17 @@ __global__ __launch_bounds__(WM * WN * 64) void xtile_kernel(LinArgs p) {
   if (EX && tid < 128 && E <= kXtEmax) {                    // the compact list: (k, v) of every entry
     const int c = tid, n = min(n0 + c, p.N - 1);
     const int e0 = s_cs[c], e1 = s_cs[c + 1];
-    for (int e = e0; e < e1; ++e) {
+#pragma unroll
+    for (int j = 0; j < kRes; ++j)
+      if (e0 + j < e1) {
+        s_ek[e0 + j] = kcol(p, cx_ec[j], ctx_corrupt);
+        s_ev[e0 + j] = cx_ev[j];
+      }
+    for (int e = e0 + kRes; e < e1; ++e) {                  // rare: more entries than the registers hold
       s_ek[e] = kcol(p, p.ecol[(int64_t)n * p.R + (e - e0)], ctx_corrupt);
       s_ev[e] = p.eval[(int64_t)n * p.R + (e - e0)];
     }
   }
-
-  // ---- ring loads: the first half of the waves load the A planes, the second half the B planes; instruction i of
-  // a wave covers 16 rows x 64 bytes (lane: row lane / 4, 16-byte chunk lane % 4, swizzled) ----
-  const int lrow = lane >> 2, lch = ((lane & 3) ^ swz<BK>(lrow)) << 4;
-  const bool isA = wave < NW / 2;
-  const __amdgpu_buffer_rsrc_t rsrc = isA ? __builtin_amdgcn_make_buffer_rsrc(const_cast<int8_t*>(p.a), (short)0,
-                                                                               kBufRange, 0x00020000)
-                                          : __builtin_amdgcn_make_buffer_rsrc(const_cast<int8_t*>(p.w), (short)0,
-                                                                               kBufRange, 0x00020000);
-  int voff[LPW];
-#pragma unroll
-  for (int i = 0; i < LPW; ++i) {
-    const int inst = (wave % (NW / 2)) * LPW + i, pl = inst >> 3, row = (inst & 7) * 16 + lrow;
-    voff[i] = isA ? pl * p.M * p.K + min(m0 + row, p.M - 1) * p.K + lch
-                  : pl * (int)p.ld_plane + min(n0 + row, p.N - 1) * (int)p.ld_row + lch;
-  }
-  auto issue = [&](int kt, int stage) {
-    char* sbase = smem + stage * STAGE + wave * LPW * 1024;
-#pragma unroll
-    for (int i = 0; i < LPW; ++i) buf_lds16(rsrc, sbase + i * 1024, voff[i], kt * BK);
-  };
 
   auto load_ops = [&](XtOps<TM, TN>& o, int stage, int h) {
     const char* base = smem + stage * STAGE;
@@ -953,8 +987,7 @@ __global__ __launch_bounds__(WM * WN * 64) void xtile_kernel(LinArgs p) {
     }
   };
 
-#pragma unroll
-  for (int t = 0; t < S; ++t)
+  for (int t = p.xt_pre; t < S; ++t)
     if (t < nk) issue(t, t);
   // first k tile landed (later stages may still be in flight) and visible to every wave
   if (S - 1 < nk)
@@ -1919,6 +1952,8 @@ static int launch_tile(LinArgs& p, const Plan& s, hipStream_t st) {
       static const int xcd = getenv("BX_XCD") ? atoi(getenv("BX_XCD")) : 4;   // row tiles per XCD group
       if (xt && xtile_fits(p, s)) {
         p.xcd_remap = (xcd > 0 && (s.tiles_x * s.tiles_y) % 8 == 0 && s.tiles_y % xcd == 0) ? xcd : 0;
+        static const int pre = getenv("BX_XT_PRE") ? atoi(getenv("BX_XT_PRE")) : 1;
+        p.xt_pre = std::max(0, std::min(pre, kXtS));
         allow_lds(xtile_kernel<MODE, 4, 2, 1, 2>, kXtLds);
         xtile_kernel<MODE, 4, 2, 1, 2><<<dim3(s.tiles_x, s.tiles_y, 1), 512, kXtLds, st>>>(p);
         return check_launch("xtile_kernel");
