@@ -972,10 +972,10 @@ __global__ __launch_bounds__(WM * WN * 64) void xtile_kernel(LinArgs p) {
       for (int t = 0; t < TN; ++t)
 #pragma unroll
         for (int e = 0; e < 16; ++e) acc[s2][a2][t][e] = 0;
-  // the nine limb products, A-limb major: an A operand stays on the matrix core's inputs for 2 TN MFMAs in a row (fewer
-  // operand bits switch, which the clock under load rewards: +1 % on config 3); products into one accumulator are
-  // still at least four MFMAs apart
-  // the nine limb products, ordered so that products into one accumulator are at least two MFMAs apart
+
+  // the nine limb products, A-limb major: an A operand stays on the matrix core's inputs for 3 TN MFMAs in a row
+  // (fewer operand bits switch, which the clock under load rewards: +1 % on the M = 2048 prefill shapes); products
+  // into one accumulator are still at least four MFMAs apart
   auto mfmas = [&](const XtOps<TM, TN>& o) {
 #pragma unroll
     for (int u = 0; u < 9; ++u) {
