@@ -246,6 +246,116 @@ def bench_mfma_rate(dev, reps=8, iters=4096):
     return out
 
 
+def _phase_table(name):
+    """The measurement build's phase table of one source file (bx_phases_<name>): int64 [4, 1024, 8] ticks."""
+    import ctypes
+    import numpy as np
+    from bitexact import _hip
+    buf = np.zeros(4 * 1024 * 8, dtype=np.uint64)
+    if _hip.lib()["bx_phases_" + name](ctypes.c_void_p(buf.ctypes.data)) != 0:
+        raise RuntimeError("the phase timers need the measurement build: BX_PHASES=1 (libbitexact_hip_phases.so)")
+    return buf.reshape(4, 1024, 8).astype(np.int64)
+
+
+def _phase_summary(t, nblocks, names):
+    """Mean / min / max (us) of each phase between consecutive marks over the first nblocks blocks (100 MHz ticks),
+    and the span from the first block's start to the last block's last mark."""
+    t = t[:nblocks]
+    out = {}
+    for k, nm in enumerate(names):
+        d = (t[:, k + 1] - t[:, k]) / 100.0
+        out[nm] = {"mean": round(float(d.mean()), 2), "min": round(float(d.min()), 2), "max": round(float(d.max()), 2)}
+    out["block_total_mean"] = round(float(((t[:, len(names)] - t[:, 0]) / 100.0).mean()), 2)
+    out["launch_span"] = round(float((t[:, len(names)].max() - t[:, 0].min()) / 100.0), 2)
+    out["blocks"] = int(nblocks)
+    return out
+
+
+def bench_phases(dev):
+    """Phase timestamps of the main kernels (the measurement build, BX_PHASES=1): the exact prefill tile at
+    lm_head / q-o / down shapes (M = 2048), the exact decode stream kernel at the engine's gate|up shape (M = 32
+    with q's limb planes), the split decode attention at config 4, the one-block decode attention at the engine's
+    shape (batch 32, context 1024), and the add + norm at the engine's shape (32 rows of 2048). Each is launched a
+    few times over rotating copies of its weights / cache (>= 400 MB, beyond the 256 MB last-level cache, so the
+    timed launch reads HBM); the table holds the last launch's first 1024 blocks."""
+    import torch
+    from bitexact.exact import ops
+    from bitexact.exact.consts import decompose, exp2_table
+    from bitexact.vllm_plugin import tri_exact_attn
+    from bitexact.vllm_plugin.exact_gemm import exact_linear
+    res = {}
+    flag = torch.zeros(1, dtype=torch.int32, device=dev)
+    for name, M, N, K in (("xtile lm_head 2048x128256x2048", 2048, 128256, 2048),
+                          ("xtile q_o 2048x2048x2048", 2048, 2048, 2048),
+                          ("xtile down 2048x2048x8192", 2048, 2048, 8192),
+                          ("stream gate|up 32x16384x2048 (engine)", 32, 16384, 2048)):
+        ncop = max(1, min(4, -(-(400 << 20) // (3 * N * K))))   # weight copies: each launch reads HBM
+        decs = []
+        for c in range(ncop):
+            w = (torch.randn(N, K, generator=torch.Generator(device=dev).manual_seed(N + K + c), device=dev) *
+                 0.02).to(torch.bfloat16)
+            decs.append(decompose(w))
+            del w
+        q, sh = quant40(torch.randn(M, K, generator=torch.Generator().manual_seed(5), dtype=torch.float64).to(dev))
+        pl = None
+        if M == 32:
+            pl = torch.empty(3, M, K, dtype=torch.int8, device=dev)
+            v = q.to(torch.int64)
+            for i in range(3):
+                lo = ((v + 128) & 255) - 128
+                pl[i] = lo.to(torch.int8)
+                v = (v - lo) >> 8
+        for i in range(max(3, ncop)):
+            dec = decs[i % ncop]
+            exact_linear(q, sh, dec["limbs"], dec["d"], dec["g"], dec["ell_cnt"], dec["ell_col"], dec["ell_val"],
+                         dec["R"], flag, False, q_planes=pl)
+        torch.cuda.synchronize()
+        t = _phase_table("linear")
+        if M == 32:
+            res[name] = _phase_summary(t[1], (N + 63) // 64, ["fill+chunk0", "chunks 1..", "epilogue"])
+        else:
+            res[name] = _phase_summary(t[0], min(1024, ((N + 127) // 128) * ((M + 127) // 128)),
+                                       ["context", "first stage", "loop", "gathers", "epilogue"])
+        del decs, dec, q, sh
+        torch.cuda.empty_cache()
+    lut = exp2_table(dev)
+    g = torch.Generator(device=dev).manual_seed(77)
+    for name, B, S, nsplit, slot, names in (
+            ("decode attention split (config 4: B=4, ctx 2048)", 4, 2048, None, 0,
+             ["K/V + scores", "maxima exchange", "weights + pV", "finish"]),
+            ("decode attention one block (engine: B=32, ctx 1024)", 32, 1024, 1, 1,
+             ["prologue", "K sweep", "V request", "V sweep", "finish"])):
+        HKV, grp, HD, bs = 8, 4, 64, 16
+        nblk = S // bs
+        nb = B * nblk
+        ncop = -(-(400 << 20) // (nb * HKV * bs * 8 * HD))           # cache copies: each launch reads HBM
+        caches = [torch.randint(-128, 128, (nb, HKV, bs, 8 * HD), dtype=torch.int8, device=dev, generator=g)
+                  for _ in range(ncop)]
+        bt = torch.randperm(nb, device=dev, generator=g).to(torch.int32).reshape(B, nblk)
+        rmap = torch.arange(B, device=dev)
+        qa = torch.randint(-(1 << 22), (1 << 22) + 1, (B, HKV, grp, HD), device=dev, generator=g).to(torch.int32)
+        sha = torch.randint(-40, -25, (B, HKV, grp), device=dev, generator=g)
+        qpos = torch.full((B, grp), S - 1, dtype=torch.long, device=dev)
+        for i in range(max(3, ncop)):
+            tri_exact_attn.attend(qa, sha, qpos, caches[i % ncop], bt, rmap, lut, 387270501, nsplit=nsplit)
+        torch.cuda.synchronize()
+        t = _phase_table("attn")
+        nblocks = B * HKV * (8 if nsplit is None else 1)
+        res[name] = _phase_summary(t[slot], min(1024, nblocks), names)
+        del caches
+        torch.cuda.empty_cache()
+    x = torch.randint(-(1 << 36), 1 << 36, (32, 2048), device=dev, generator=g)
+    y = torch.randint(-(1 << 36), 1 << 36, (32, 2048), device=dev, generator=g)
+    gm = torch.randint(1 << 7, 1 << 8, (2048,), device=dev, generator=g)
+    ge = torch.full((2048,), -7, dtype=torch.long, device=dev)
+    for _ in range(3):
+        ops.add_norm_y(y, x.clone(), gm, ge, flag=flag, planes=True)
+    torch.cuda.synchronize()
+    res["add + norm (engine: 32 rows of 2048)"] = _phase_summary(_phase_table("rows")[0], 32,
+                                                                ["row loaded", "divisor", "quotients", "quantize"])
+    return res
+
+
 def bench_prefill(dev, reps=10):
     import torch
     from bitexact.exact.consts import decompose
@@ -557,9 +667,13 @@ def main():
     ap.add_argument("--engine-steps", type=int, default=20)
     ap.add_argument("--eager", action="store_true")
     ap.add_argument("--copy-calibrate", action="store_true")
+    ap.add_argument("--phases", action="store_true",
+                    help="phase timestamps of the main kernels (loads the measurement build, BX_PHASES=1)")
     args = ap.parse_args()
     global EAGER
     EAGER = args.eager
+    if args.phases:
+        os.environ["BX_PHASES"] = "1"          # before the library loads: the measurement build
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py: this build runs on one GPU only (the hot path has no collectives); use --gpus 1",
               file=sys.stderr)
@@ -571,6 +685,9 @@ def main():
     dev = torch.device("cuda:0")
     if args.copy_calibrate:
         copy_calibrate(dev)
+        return
+    if args.phases:
+        print(json.dumps({"phases": bench_phases(dev), "unit": "us (100 MHz real-time counter)"}), flush=True)
         return
     if args.no_decode:
         sec, step_bytes, launches, per, value = 1.0, 0, 1, [], None

@@ -11,7 +11,9 @@ import threading
 
 import torch
 
-_LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "_lib", "libbitexact_hip.so")
+# BX_PHASES=1 loads the measurement build (the same kernels with phase timestamps; bench.py --phases)
+_LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "_lib",
+                         "libbitexact_hip_phases.so" if os.environ.get("BX_PHASES") == "1" else "libbitexact_hip.so")
 _lib = None
 _lock = threading.Lock()
 
@@ -77,6 +79,9 @@ SIGNATURES = {
     "bx_int_rowop": (ctypes.c_int, [I32, I32, P, P, P, I64, I64, I64, P, P, P, P, P, I64, P, P, P]),
     "bx_stream_read": (ctypes.c_int, [P, I64, I32, I32, P, P]),
     "bx_mfma_rate": (ctypes.c_int, [I32, I32, I32, I32, P, P]),
+    "bx_phases_linear": (ctypes.c_int, [P]),
+    "bx_phases_attn": (ctypes.c_int, [P]),
+    "bx_phases_rows": (ctypes.c_int, [P]),
 }
 
 

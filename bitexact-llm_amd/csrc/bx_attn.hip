@@ -23,6 +23,8 @@
 
 namespace bx {
 
+BX_PHASE_TABLE
+
 constexpr int kFK = 17, kFZ = 26, kFP = 22, kFT2 = 26, kExp2Bits = 14, kExp2One = 60;
 
 // A weight is exactly 0 once n >= FP + 2: the interpolated table value v lies in [0, 2^60] (the table falls
@@ -891,6 +893,7 @@ __device__ __forceinline__ int64_t dec_score_k(const v4i (&qa)[HD / 64], const v
 constexpr int kDecDepth = 3;
 template <int HD>
 __global__ __launch_bounds__(kDecWaves * 64) void attn_dec_raw_kernel(AttnArgs p) {
+  BX_PHASE(1, 0);
   __shared__ DecSmem<HD> sm;
   extern __shared__ __align__(16) int64_t raw_cache[];     // [4][p.S] scores, then the block-table entries
   constexpr int KK = HD / 64, DR = kDecDepth;
@@ -921,6 +924,7 @@ __global__ __launch_bounds__(kDecWaves * 64) void attn_dec_raw_kernel(AttnArgs p
   v4i qa[KK];
   dec_q_limbs<HD>(qv, lane, qa);
   const int nb16 = (kend + 15) / 16;
+  BX_PHASE(1, 1);
   auto rows = [&](int i, int first, v4i (&r)[3][KK]) {
     const int s = min(i * 16 + kl, kend - 1);
     dec_planes<HD>(p, spg[s / p.bs], h, s, first, r);
@@ -950,6 +954,7 @@ __global__ __launch_bounds__(kDecWaves * 64) void attn_dec_raw_kernel(AttnArgs p
     for (int o = 1; o < 16; o <<= 1) best = imax(best, __shfl_xor(best, o, 64));
     if (kl == 0) atomicMax((long long*)&sm.mx[qo], (long long)best);
   }
+  BX_PHASE(1, 2);
   // the first V rows go out before the maxima are complete
   v4i vr[DR][3][KK];
 #pragma unroll
@@ -958,6 +963,7 @@ __global__ __launch_bounds__(kDecWaves * 64) void attn_dec_raw_kernel(AttnArgs p
   __builtin_amdgcn_s_waitcnt(0xc07f);             // LDS only (lgkmcnt(0)): the V loads stay in flight
   asm volatile("s_barrier" ::: "memory");
 
+  BX_PHASE(1, 3);
   // ---- sweep 2: V, weights from the kept scores, den, p V ----
   const int64_t mx = sm.mx[qo];
   int64_t den = 0;
@@ -982,7 +988,9 @@ __global__ __launch_bounds__(kDecWaves * 64) void attn_dec_raw_kernel(AttnArgs p
       }
     }
   }
+  BX_PHASE(1, 4);
   dec_finish<HD>(p, sm, DecWs{}, den, num, tile, 0, 1, group, q0, nvalid);
+  BX_PHASE(1, 5);
 }
 
 // ---- paged decode attention, key splits in one launch ----
@@ -997,6 +1005,7 @@ __global__ __launch_bounds__(kDecWaves * 64) void attn_dec_raw_kernel(AttnArgs p
 // so K and V are each read once.
 template <int HD, int NBW>
 __global__ __launch_bounds__(kDecWaves * 64) void attn_dec_exch_kernel(AttnArgs p) {
+  BX_PHASE(0, 0);
   __shared__ DecSmem<HD> sm;
   __shared__ int64_t s_best[kDecWaves][4];
   constexpr int KK = HD / 64;
@@ -1053,6 +1062,7 @@ __global__ __launch_bounds__(kDecWaves * 64) void attn_dec_exch_kernel(AttnArgs 
   for (int o = 1; o < 16; o <<= 1) best = imax(best, __shfl_xor(best, o, 64));
   if (kl == 0) s_best[w][qo] = best;
   __syncthreads();
+  BX_PHASE(0, 1);
   if (threadIdx.x < 4) {
     int64_t m = kNeg;
     for (int ww = 0; ww < kDecWaves; ++ww) m = imax(m, s_best[ww][threadIdx.x]);
@@ -1087,6 +1097,7 @@ __global__ __launch_bounds__(kDecWaves * 64) void attn_dec_exch_kernel(AttnArgs 
     __syncthreads();
   }
 
+  BX_PHASE(0, 2);
   // weights (every table load first), den, p V
   const int64_t mx = sm.mx[qo];
   int64_t pw[NBW];
@@ -1153,7 +1164,9 @@ __global__ __launch_bounds__(kDecWaves * 64) void attn_dec_exch_kernel(AttnArgs 
     __builtin_amdgcn_s_waitcnt(0xc07f);
     __builtin_amdgcn_wave_barrier();
   }
+  BX_PHASE(0, 3);
   dec_finish<HD>(p, sm, ws, den, num, tile, sp, NS, group, q0, nvalid);
+  BX_PHASE(0, 4);
 }
 
 // ---- fused prefill attention on MFMA (contiguous int32 K / V) ----
@@ -2025,3 +2038,5 @@ extern "C" int bx_kv_store(int8_t* cache, int64_t sc_nb, int64_t sc_h, int64_t s
                                                                    skn, skh, (const int32_t*)v, svn, svh, HD, bs);
   return check_launch("kv_store_kernel");
 }
+
+BX_PHASE_DEFINE(attn)

@@ -254,6 +254,33 @@ __device__ __forceinline__ int wave_or(int v) {
 
 }  // namespace bx
 
+// Phase timers (measurement builds only: compiled with -DBX_PHASES, a separate library): BX_PHASE(kid, k) records
+// the 100 MHz real-time counter for phase boundary k (0..7) of kernel slot kid (0..3) in block b (< 1024) of the
+// launch, thread 0 only. BX_PHASE_DEFINE(name) gives a source file its table and the exported reader
+// bx_phases_<name>(host): the table as uint64 [4][1024][8]; without -DBX_PHASES the reader returns BX_EINVAL and
+// the marks compile to nothing.
+#ifdef BX_PHASES
+#define BX_PHASE(kid, k)                                                                   \
+  do {                                                                                     \
+    if (threadIdx.x == 0) {                                                                \
+      const unsigned bx_b_ = blockIdx.x + blockIdx.y * gridDim.x;                          \
+      if (bx_b_ < 1024) g_bx_phase[kid][bx_b_][k] = __builtin_amdgcn_s_memrealtime();      \
+    }                                                                                      \
+  } while (0)
+#define BX_PHASE_TABLE static __device__ uint64_t g_bx_phase[4][1024][8];
+#define BX_PHASE_DEFINE(name)                                                                              \
+  extern "C" int bx_phases_##name(uint64_t* host) {                                                        \
+    return hipMemcpyFromSymbol(host, HIP_SYMBOL(g_bx_phase), sizeof(g_bx_phase)) == hipSuccess ? BX_OK : BX_EINVAL; \
+  }
+#else
+#define BX_PHASE(kid, k) \
+  do {                   \
+  } while (0)
+#define BX_PHASE_TABLE
+#define BX_PHASE_DEFINE(name) \
+  extern "C" int bx_phases_##name(uint64_t*) { return BX_EINVAL; }
+#endif
+
 #define BX_REQUIRE(cond, ...)          \
   do {                                 \
     if (!(cond)) {                     \

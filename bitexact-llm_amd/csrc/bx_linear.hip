@@ -28,6 +28,8 @@
 
 namespace bx {
 
+BX_PHASE_TABLE
+
 enum Mode { RAW32 = 0, JOIN = 1, WMM_T = 2, EXACT = 3 };
 
 struct LinArgs {
@@ -796,6 +798,7 @@ __device__ __forceinline__ void buf_lds4(__amdgpu_buffer_rsrc_t r, void* lds, in
 // per MFMA, but the compiler then moves the 320 accumulators between AGPRs and VGPRs inside the loop.
 template <int MODE, int WM, int WN, int TM, int TN>
 __global__ __launch_bounds__(WM * WN * 64) void xtile_kernel(LinArgs p) {
+  BX_PHASE(0, 0);
   constexpr int NW = WM * WN, BM = kXtBM, BN = kXtBN, BK = kXtBK, S = kXtS, STAGE = kXtStage;
   static_assert(32 * WM * TM == BM && 32 * WN * TN == BN, "wave layout");
   constexpr int SA = 3 * BM * BK, LPW = 48 / NW;            // 1 KiB load instructions per wave per stage
@@ -989,6 +992,7 @@ __global__ __launch_bounds__(WM * WN * 64) void xtile_kernel(LinArgs p) {
     }
   };
 
+  BX_PHASE(0, 1);
   for (int t = p.xt_pre; t < S; ++t)
     if (t < nk) issue(t, t);
   // first k tile landed (later stages may still be in flight) and visible to every wave
@@ -997,6 +1001,7 @@ __global__ __launch_bounds__(WM * WN * 64) void xtile_kernel(LinArgs p) {
   else
     ring_barrier<0>();
 
+  BX_PHASE(0, 2);
   XtOps<TM, TN> cur, nxt;
   if (nk > 0) load_ops(cur, 0, 0);
   // One k tile: the second half-step's operands are read during the first half-step's MFMAs, the ring barrier,
@@ -1062,12 +1067,14 @@ __global__ __launch_bounds__(WM * WN * 64) void xtile_kernel(LinArgs p) {
     mfmas(cur);
     mfmas(nxt);
   }
+  BX_PHASE(0, 3);
   if (gat && gbase == nullptr) {        // short K: the ring was never retired, gather into stage 0 now
     ring_barrier<0>();
     gbase = smem;
     gather(gbase);
   }
   ring_barrier<0>();                    // gathers landed; context visible
+  BX_PHASE(0, 4);
 
   // ---- epilogue: lane (l % 32) owns column (wn TN + t) 32 + l % 32 of each 32-column block t and rows
   // wm 32 + (e / 4) 8 + (l / 32) 4 + e % 4 of the 32 x 32 MFMA block ----
@@ -1148,6 +1155,7 @@ __global__ __launch_bounds__(WM * WN * 64) void xtile_kernel(LinArgs p) {
     }
   }
   if (EX) write_flag(p, bad, corrupt);
+  BX_PHASE(0, 5);
 }
 
 // =====================================================================================================
@@ -1165,6 +1173,7 @@ constexpr int kStBK = 128, kStC = 64;
 
 template <int RBM, int NB, int S, int MODE, int NWV = 4>
 __global__ __launch_bounds__(64 * NWV) void stream_kernel(LinArgs p) {
+  BX_PHASE(1, 0);
   constexpr int RP = RBM < 2 ? 32 : 16 * RBM, BK = kStBK, C = 16 * NWV, NT = 64 * NWV;   // loaded rows: x 32
   constexpr int SA = RP * BK, STAGE = SA + NB * C * BK;
   constexpr int LA = RP / 8, LT = LA + NB * C / 8, LPW = LT / NWV;   // 1 KiB load instructions per stage / wave
@@ -1225,6 +1234,7 @@ __global__ __launch_bounds__(64 * NWV) void stream_kernel(LinArgs p) {
       ring_barrier<LPW * (S - 2)>();
     else
       ring_barrier<0>();
+    if (it == 1) BX_PHASE(1, 1);
     if (it + S - 1 < nks) issue(it + S - 1, (it + S - 1) % S);
     const char* base = smem + (it % S) * STAGE;
 #pragma unroll
@@ -1268,6 +1278,7 @@ __global__ __launch_bounds__(64 * NWV) void stream_kernel(LinArgs p) {
   }
 
   ring_barrier<0>();
+  BX_PHASE(1, 2);
   bool bad = false, corrupt = false;
   const int Mo = MODE == RAW32 ? rows : p.M;                   // output rows
   if constexpr (RS) {
@@ -1389,6 +1400,7 @@ __global__ __launch_bounds__(64 * NWV) void stream_kernel(LinArgs p) {
       }
     }
     if (MODE == EXACT) write_flag(p, bad, corrupt);
+    BX_PHASE(1, 3);
     return;
   }
   for (int o = tid; o < Mo * C; o += NT) {
@@ -2304,3 +2316,4 @@ extern "C" int bx_exact_linear_noalloc(const int32_t* q, int64_t ldq, const int6
                          checked, flag, base, kNoAllocWs, (int8_t*)base + kNoAllocWs, kNoAllocTmp, stream);
 }
 
+BX_PHASE_DEFINE(linear)

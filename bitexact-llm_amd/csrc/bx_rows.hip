@@ -11,6 +11,8 @@
 
 namespace bx {
 
+BX_PHASE_TABLE
+
 
 constexpr int kRowThreads = 1024;
 constexpr int kRowU = 4;   // elements per thread whose loads are issued together
@@ -48,6 +50,7 @@ struct NormArgs {
 constexpr int kNormThreads = 512, kNormU = 4;
 template <int SRC>
 __global__ __launch_bounds__(kNormThreads) void norm_quant_kernel(NormArgs p) {
+  BX_PHASE(0, 0);
   constexpr int NT = kNormThreads, U = kNormU, NW = NT / 64;
   extern __shared__ __align__(16) char smem[];
   int64_t* Xs = (int64_t*)smem;
@@ -89,6 +92,7 @@ __global__ __launch_bounds__(kNormThreads) void norm_quant_kernel(NormArgs p) {
       }
     }
   }
+  BX_PHASE(0, 1);
   amax = block_reduce64_dpp<true, NW>(amax, sbuf[0], 0);
   if (threadIdx.x == 0 && amax >= (1LL << 40)) p.err[0] = 1;
   if (p.gm == nullptr) return;
@@ -105,6 +109,7 @@ __global__ __launch_bounds__(kNormThreads) void norm_quant_kernel(NormArgs p) {
   const int64_t V = s >= 0 ? shl(T, s) : sar(T, -s);
   const int64_t r = isqrt64(V), er = shx - p.FR - m;
   const double rinv = 1.0 / (double)r;
+  BX_PHASE(0, 2);
   int64_t emax = kNegBig;
   for (int i0 = threadIdx.x; i0 < D; i0 += U * NT) {
     int64_t gmv[U], gev[U];
@@ -124,6 +129,7 @@ __global__ __launch_bounds__(kNormThreads) void norm_quant_kernel(NormArgs p) {
       }
     }
   }
+  BX_PHASE(0, 3);
   emax = block_reduce64_dpp<true, NW>(emax, sbuf[2], kNegBig);
   const int64_t shr = imax(emax - kQB, kNegBig);
   for (int i = threadIdx.x; i < D; i += NT) {
@@ -141,6 +147,7 @@ __global__ __launch_bounds__(kNormThreads) void norm_quant_kernel(NormArgs p) {
     }
   }
   if (threadIdx.x == 0) p.sh[blockIdx.x] = shr;
+  BX_PHASE(0, 4);
 }
 
 // ---- segs.silu_y + segs.quant_silu (src/bitexact/exact/segs.py:120-128) over ops.silu_mul
@@ -612,3 +619,5 @@ extern "C" int bx_attn_out(const int64_t* num, int64_t sn_group, int64_t sn_quer
                                                           FV, q, ldq, sh);
   return check_launch("attn_out_kernel");
 }
+
+BX_PHASE_DEFINE(rows)

@@ -341,6 +341,18 @@ int bx_stream_read(const void* src, int64_t bytes, int32_t blocks, int32_t threa
  * sink: an int32 [1] device word (practically never written). */
 int bx_mfma_rate(int32_t shape, int32_t iters, int32_t blocks, int32_t threads, int32_t* sink, bx_stream_t stream);
 
+/* No counterpart in the reference: phase timers of the measurement build (libbitexact_hip_phases.so, compiled
+ * with -DBX_PHASES). Each copies its source file's table, uint64 [4 kernel slots][1024 blocks][8 marks] of the
+ * 100 MHz real-time counter as the kernels last wrote them, into host memory: linear (slot 0 the exact prefill
+ * tile: start, context built, first stage landed, loop end, gathers landed, end; slot 1 the stream kernel:
+ * start, chunk 1, loop end, end), attn (slot 0 the split decode attention: start, scores, maxima exchanged,
+ * weights and p V, end; slot 1 the one-block decode attention: start, prologue, K sweep, V requested, V sweep,
+ * end), rows (slot 0 the norm: start, row loaded, divisor, quotients, end). The product library returns
+ * BX_EINVAL. */
+int bx_phases_linear(uint64_t* host);
+int bx_phases_attn(uint64_t* host);
+int bx_phases_rows(uint64_t* host);
+
 #ifdef __cplusplus
 }
 #endif
