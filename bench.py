@@ -540,7 +540,7 @@ def bench_engine(dev, steps, warmup, B=32, ctx=1024, bs=16):
         pos = torch.full((b,), ctx, device=dev, dtype=torch.long)
         rmap = torch.arange(b, device=dev)
         slot = bt[rmap, pos // bs].long() * bs + pos % bs
-        x = eng.forward(kvs, first[:b], pos, slot, bt, rmap)
+        x = eng.forward(kvs, first[:b], pos, slot, bt, rmap, one_per_seq=True)
         shas[b] = logits_sha(eng.logits(x)[0])
     # timed decode: static inputs updated on the device by each step
     ids = first.clone()
@@ -549,7 +549,7 @@ def bench_engine(dev, steps, warmup, B=32, ctx=1024, bs=16):
     slot = bt[rmap, pos // bs].long() * bs + pos % bs
 
     def step(i):
-        x = eng.forward(kvs, ids, pos, slot, bt, rmap)
+        x = eng.forward(kvs, ids, pos, slot, bt, rmap, one_per_seq=True)
         ids.copy_(eng.greedy(eng.logits(x)))
         pos.add_(1)
         slot.copy_(bt[rmap, pos // bs].long() * bs + pos % bs)

@@ -45,6 +45,8 @@ SIGNATURES = {
     "bx_int8_gemm_workspace": (I64, [I32, I32, I32, I32]),
     "bx_exact_attn_paged": (ctypes.c_int, [P, P, P, I64, P, I64, I64, I64, I32, P, I64, I32, P, P, I64, P, P, I32, I32,
                                            I32, I32, I32, P, I64, P]),
+    "bx_exact_attn_paged_rope": (ctypes.c_int, [P, I64, P, I64, P, P, I32, I32, I32, I32, I32, I32, I32, P, P, I64, I64,
+                                                I64, I32, P, I64, I32, P, P, I64, P, P, I32, I32, I32, P, P]),
     "bx_attn_paged_workspace": (I64, [I32, I32, I32, I32]),
     "bx_exact_attn_prefill": (ctypes.c_int, [P, I64, I64, P, I64, P, I64, I64, P, I64, I64, P, I64, I64, I32, P, I64,
                                              P, P, I32, I32, I32, P, I64, P]),

@@ -63,11 +63,14 @@ class ExactEngine:
         return [torch.zeros(nblocks, self.HKV, bs, 8 * self.HD, dtype=torch.int8, device=self.dev)
                 for _ in range(self.L)]
 
-    def forward(self, kvs, ids, pos, slot, bt, rmap):
+    def forward(self, kvs, ids, pos, slot, bt, rmap, one_per_seq=False):
         """ids, pos, slot [N]: the step's tokens (slot < 0: padding, redirected to the null block 0); bt [*, nblk]
         int32 block table and rmap [N] the table row of each token. kvs None: no cache (the reference's memory
         profiling run): nothing is stored and the attention output is 0. Returns the residual stream [N, D] int64
-        at FR (src/bitexact/vllm_plugin/exact_run.py:55-128 with the fused stages of its 130-155)."""
+        at FR (src/bitexact/vllm_plugin/exact_run.py:55-128 with the fused stages of its 130-155).
+        one_per_seq: every token is the only one of its sequence in this step (a decode step), so each layer's
+        RoPE + KV store and attention run as one launch (tri_exact_attn.rope_attend) where the shapes allow; the
+        integers are the same either way."""
         N, G, HKV, HD = ids.shape[0], self.G, self.HKV, self.HD
         pos = pos.long().contiguous()
         slot = slot.long().clamp(min=0)    # padding (slot < 0) -> the null block 0; one launch
@@ -78,9 +81,14 @@ class ExactEngine:
             x, (q, pl), sh, _ = ops.embed_norm(self.emb, ids, *self.ga[0], flag=fl, planes=True)
         else:
             x, q, sh, _ = ops.embed_norm(self.emb, ids, *self.ga[0], flag=fl)
+        fuse = (one_per_seq and kvs is not None and
+                tri_exact_attn.rope_fusable(N, HKV, self.H, bt.shape[1], kvs[0].shape[2]))
         for i in range(self.L):
             y = self.fused[i, "wqkv"](q, sh, fl, False, q_planes=pl)
-            if kvs is None:
+            if fuse:
+                num, den = tri_exact_attn.rope_attend(y, pos, self.cos, self.sin, (self.H, HKV, HD), kvs[i], slot, bt,
+                                                      rmap, self.exp2, self.l2e, fl)
+            elif kvs is None:
                 ops.qkv_y(y, pos.view(N, 1), self.cos, self.sin, N, 1, (self.H, HKV, HD), flag=fl)
                 num = torch.zeros(N, HKV, G, HD, dtype=torch.long, device=y.device)
                 den = torch.ones(N, HKV, G, 1, dtype=torch.long, device=y.device)

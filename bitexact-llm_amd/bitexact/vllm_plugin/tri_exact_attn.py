@@ -54,3 +54,48 @@ def attend(q, sh, qpos, cache, bt, rmap, lut, l2e, nsplit=None, bn=64, warps=4):
     if nsplit is None:
         nsplit = default_nsplit(q.shape[0], q.shape[1], bt.shape[1], cache.shape[2])
     return _attend(q, sh, qpos, cache, bt, rmap, lut, int(l2e), int(nsplit))
+
+
+def rope_fusable(N, HKV, H, nblk, bs):
+    """Whether a decode step of N tokens (one per sequence) can take rope_attend: the attention would run
+    unsplit (default_nsplit == 1), over at most 2048 keys per row, with at most 4 q heads per KV head."""
+    return default_nsplit(N, HKV, nblk, bs) == 1 and nblk * bs <= 2048 and H % HKV == 0 and H // HKV <= 4
+
+
+def _rope_attend_fake(y, pos, cos, sin, H, HKV, HD, cache, slot, bt, rmap, lut, l2e, flag):
+    N = y.shape[0]
+    G = H // HKV
+    return empty((N, HKV, G, HD), torch.long, y), empty((N, HKV, G, 1), torch.long, y)
+
+
+@op("attend_exact_rope(Tensor y, Tensor pos, Tensor cos, Tensor sin, int H, int HKV, int HD, Tensor(a!) cache, "
+    "Tensor slot, Tensor bt, Tensor rmap, Tensor lut, int l2e, Tensor(b!) flag) -> (Tensor, Tensor)", _rope_attend_fake)
+def _rope_attend(y, pos, cos, sin, H, HKV, HD, cache, slot, bt, rmap, lut, l2e, flag):
+    from bitexact.exact.ops import FK, FR, FT, FV, FZ
+    _hip.require_cuda(y, pos, cos, sin, cache, slot, bt, rmap, lut, flag)
+    N = y.shape[0]
+    G = H // HKV
+    assert y.dtype == torch.int64 and y.stride(-1) == 1 and y.shape[1] >= (H + 2 * HKV) * HD
+    assert cache.dtype == torch.int8 and cache.dim() == 4 and cache.shape[1] == HKV and cache.shape[3] >= 6 * HD
+    assert cache.stride(3) == 1 and bt.dtype == torch.int32 and flag.dtype == torch.int32
+    pos = pos.reshape(-1).contiguous().long()
+    slot = slot.reshape(-1).contiguous().long()
+    assert pos.shape[0] == N and slot.shape[0] == N
+    cos, sin = cos.contiguous().long(), sin.contiguous().long()
+    rmap, lut = rmap.contiguous().long(), lut.contiguous().long()
+    num = torch.empty(N, HKV, G, HD, dtype=torch.long, device=y.device)
+    den = torch.empty(N, HKV, G, 1, dtype=torch.long, device=y.device)
+    _hip.call("bx_exact_attn_paged_rope", _hip.ptr(y), y.stride(0), _hip.ptr(pos), 1, _hip.ptr(cos), _hip.ptr(sin),
+              cos.shape[0], H, FR, FT, FK, FV, FZ, _hip.ptr(slot), _hip.ptr(cache), cache.stride(0), cache.stride(1),
+              cache.stride(2), cache.shape[2], _hip.ptr(bt), bt.stride(0), bt.shape[1], _hip.ptr(rmap), _hip.ptr(lut),
+              int(l2e), _hip.ptr(num), _hip.ptr(den), N, HKV, HD, _hip.ptr(flag), _hip.stream_of(y))
+    return num, den
+
+
+def rope_attend(y, pos, cos, sin, dm, cache, slot, bt, rmap, lut, l2e, flag):
+    """A decode step's exact_fuse.qkv (RoPE, q grouping, K / V into the cache at slot) and attend in one launch, for
+    steps where every token is its own sequence's only one (rope_fusable). y int64 [N, (H + 2 HKV) HD] at FR, pos /
+    slot int64 [N], dm = (H, HKV, HD) -> (num int64 [N, HKV, G, HD], den int64 [N, HKV, G, 1]); bound violations
+    set flag[0]. The same integers as qkv_y(..., store=(cache, slot)) followed by attend(...)."""
+    H, HKV, HD = (int(v) for v in dm)
+    return _rope_attend(y, pos, cos, sin, H, HKV, HD, cache, slot, bt, rmap, lut, int(l2e), flag)

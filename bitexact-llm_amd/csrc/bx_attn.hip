@@ -17,6 +17,7 @@
 // same queries for p V, so query-indexed LDS reads are wave-uniform broadcasts and key/dim-indexed reads
 // hit distinct banks (rows padded by one word).
 #include "bx_common.h"
+#include "bx_rope.h"
 
 #include <algorithm>
 #include <type_traits>
@@ -890,9 +891,14 @@ __device__ __forceinline__ int64_t dec_score_k(const v4i (&qa)[HD / 64], const v
 // memory round trip. Each wave keeps the limb rows of its next DR 16-key blocks in flight (a register ring, the
 // loop unrolled by DR). Sweep 1 streams K, keeps every score in LDS and the per-query maxima; sweep 2 streams V
 // and forms weights and p V from the kept scores, so K and V are each read once.
+// RP (decode steps with one token per sequence): the block first runs the rope kernel's work for its (token, KV
+// head): waves 0 .. nq - 1 RoPE and quantize the group's q heads into LDS, waves 4 and 5 RoPE the k head and
+// store the k and v limbs at the token's cache slot (each waits for its stores before the barrier, so the
+// sweeps read them back). The launch then replaces the standalone rope kernel.
 constexpr int kDecDepth = 3;
-template <int HD>
-__global__ __launch_bounds__(kDecWaves * 64) void attn_dec_raw_kernel(AttnArgs p) {
+template <int HD, bool RP = false>
+__global__ __launch_bounds__(kDecWaves * 64) void attn_dec_raw_kernel(AttnArgs p, RopeArgs r) {
+  static_assert(!RP || kDecWaves >= 6, "the rope prologue uses waves 0-3 (q heads), 4 (k) and 5 (v)");
   BX_PHASE(1, 0);
   __shared__ DecSmem<HD> sm;
   extern __shared__ __align__(16) int64_t raw_cache[];     // [4][p.S] scores, then the block-table entries
@@ -906,21 +912,58 @@ __global__ __launch_bounds__(kDecWaves * 64) void attn_dec_raw_kernel(AttnArgs p
   const int lane = threadIdx.x & 63, w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int kl = lane & 15, qo = lane >> 4;
   int32_t* spg = (int32_t*)(raw_cache + 4 * (int64_t)p.S);
+  __shared__ int32_t s_q[RP ? 4 : 1][RP ? HD : 1];
+  __shared__ int64_t s_shq[4];
 
   DecQ<HD> qv;
-  dec_q_load<HD>(p, group, q0, nvalid, lane, qv);
+  if constexpr (!RP) dec_q_load<HD>(p, group, q0, nvalid, lane, qv);
   // the block-table row (every entry the launch may reach: p.S / bs + 1), independent of the positions
   const int npg = p.S / p.bs + 1 < p.nblk ? p.S / p.bs + 1 : p.nblk;
   for (int i = threadIdx.x; i < npg; i += kDecWaves * 64) spg[i] = p.bt[brow * p.sbt + i];
   int64_t qp[4];
+  if constexpr (RP) {
+    // token group / hkv, KV head h, its nq q heads h nq ..; one position for the group (the token's)
+    const int n = group / p.hkv;
+    const int64_t pos_raw = r.pos[(int64_t)n * r.spb];
+    bool bad = pos_raw < 0 || pos_raw >= r.npos;        // the reference's table index would fail: flagged
+    const int64_t pos = imin(imax(pos_raw, 0), r.npos - 1);
+    int64_t out[KK];
+    if (w < nvalid) {
+      rope_row<HD>(r, n, h * p.nq + w, pos, lane, out, bad);
+      const int64_t shq = rope_q_shift<HD>(r, out, bad);
 #pragma unroll
-  for (int i = 0; i < 4; ++i)
-    qp[i] = i < nvalid ? p.qpos[(group / p.qpos_div) * p.qpos_tile + (int64_t)(q0 + i) * p.qpos_row] : -1;
+      for (int e = 0; e < KK; ++e) s_q[w][lane + 64 * e] = (int32_t)rshc(out[e], shq + r.FR + r.FT);
+      if (lane == 0) s_shq[w] = shq;
+    } else if (w == 4 || w == 5) {
+      const int hr = r.H + (w - 4) * r.HKV + h;
+      rope_row<HD>(r, n, hr, pos, lane, out, bad);
+      rope_kv_store<HD>(r, n, hr, lane, out, bad);
+      __builtin_amdgcn_s_waitcnt(0);                     // the cache stores are complete before the barrier
+    }
+    if (wave_or(bad ? 1 : 0) && lane == 0) r.err[0] = 1;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) qp[i] = i < nvalid ? pos_raw : -1;
+  } else {
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+      qp[i] = i < nvalid ? p.qpos[(group / p.qpos_div) * p.qpos_tile + (int64_t)(q0 + i) * p.qpos_row] : -1;
+  }
   const int kend = (int)imin(imax(imax(qp[0], qp[1]), imax(qp[2], qp[3])) + 1, p.S);   // qpos < nblk bs <= p.S
   const int64_t my_qpos = qo == 0 ? qp[0] : qo == 1 ? qp[1] : qo == 2 ? qp[2] : qp[3];
   if (threadIdx.x < 4) sm.mx[threadIdx.x] = kNeg;
-  const int64_t shift = qo < nvalid && p.sh ? (int64_t)(kFK + 3 - kFZ) - p.sh[group * p.sh_tile + q0 + qo] : 0;
+  int64_t shift = 0;
+  if constexpr (!RP) shift = qo < nvalid && p.sh ? (int64_t)(kFK + 3 - kFZ) - p.sh[group * p.sh_tile + q0 + qo] : 0;
   __syncthreads();
+  if constexpr (RP) {
+    // the queries from LDS in dec_q_load's lane layout: query (lane & 15) >> 2, dims 16 (lane >> 4) + e
+    const int m = lane & 15, qi = m >> 2, c = lane >> 4;
+    const bool live = qi < nvalid && (m & 3) < 3;
+#pragma unroll
+    for (int kk = 0; kk < KK; ++kk)
+#pragma unroll
+      for (int e = 0; e < 16; ++e) qv.x[kk][e] = live ? s_q[qi][kk * 64 + c * 16 + e] : 0;
+    shift = qo < nvalid ? (int64_t)(kFK + 3 - kFZ) - s_shq[qo] : 0;
+  }
   v4i qa[KK];
   dec_q_limbs<HD>(qv, lane, qa);
   const int nb16 = (kend + 15) / 16;
@@ -1856,7 +1899,7 @@ static int launch_dec(AttnArgs& p, int groups, int64_t max_keys, hipStream_t st)
     const size_t lds = (size_t)4 * p.S * 8 + ((size_t)p.S / p.bs + 2) * 4;   // scores + block-table entries
     hipFuncSetAttribute((const void*)attn_dec_raw_kernel<HD>, hipFuncAttributeMaxDynamicSharedMemorySize,
                         (int)(4 * kDecRawKeys * 8 + (kDecRawKeys + 2) * 4));
-    attn_dec_raw_kernel<HD><<<grid, kDecWaves * 64, lds, st>>>(p);
+    attn_dec_raw_kernel<HD><<<grid, kDecWaves * 64, lds, st>>>(p, RopeArgs{});
     return check_launch("attn_dec_raw_kernel");
   }
   attn_dec_kernel<HD, 1, false><<<grid, kDecWaves * 64, 0, st>>>(p);
@@ -1914,6 +1957,50 @@ extern "C" int bx_exact_attn_paged(const int32_t* q, const int64_t* sh, const in
   const int64_t max_keys = (int64_t)nblk * bs;     // qpos < nblk bs: the block table's reach
   return HD == 64 ? launch_dec<64>(p, R * HKV, max_keys, (hipStream_t)stream)
                   : launch_dec<128>(p, R * HKV, max_keys, (hipStream_t)stream);
+}
+
+extern "C" int bx_exact_attn_paged_rope(const int64_t* y, int64_t ldy, const int64_t* pos, int64_t spos,
+                                        const int64_t* cos, const int64_t* sin, int32_t npos, int32_t H, int32_t FR,
+                                        int32_t FT, int32_t FK, int32_t FV, int32_t FZ, const int64_t* slot,
+                                        int8_t* cache, int64_t sc_nb, int64_t sc_h, int64_t sc_bs, int32_t bs,
+                                        const int32_t* bt, int64_t sbt, int32_t nblk, const int64_t* rmap,
+                                        const int64_t* lut, int64_t l2e, int64_t* num, int64_t* den, int32_t R,
+                                        int32_t HKV, int32_t HD, int32_t* err, bx_stream_t stream) {
+  BX_REQUIRE(R >= 0 && HKV > 0 && H % HKV == 0 && H / HKV >= 1 && H / HKV <= 4, "need 1 <= H / HKV <= 4");
+  BX_REQUIRE(HD == 64 || HD == 128, "head_dim must be 64 or 128");
+  BX_REQUIRE(FK == kFK && FZ == kFZ, "the attention's fixed-point formats (FK, FZ) are compiled in");
+  BX_REQUIRE((int64_t)nblk * bs <= kDecRawKeys, "the fused form takes at most %d keys per row", kDecRawKeys);
+  BX_REQUIRE(ldy >= (int64_t)(H + 2 * HKV) * HD && npos > 0, "bad qkv rows or rope tables");
+  BX_REQUIRE(sc_bs >= 6 * HD && sc_nb % 16 == 0 && sc_h % 16 == 0 && sc_bs % 16 == 0 && ((uintptr_t)cache & 15) == 0,
+             "cache rows must hold the 6 HD limb bytes, 16-byte aligned");
+  BX_REQUIRE(sc_h >= (int64_t)bs * sc_bs && sc_nb >= (int64_t)HKV * sc_h, "cache strides");
+  BX_REQUIRE(y && pos && cos && sin && slot && bt && rmap && lut && num && den && err, "null pointer");
+  if (R == 0) return BX_OK;
+  const int M = H / HKV;
+  AttnArgs p = {};
+  p.nq = M;
+  p.cache = cache; p.sc_nb = sc_nb; p.sc_h = sc_h; p.sc_bs = sc_bs; p.bt = bt; p.sbt = sbt; p.rmap = rmap;
+  p.bs = bs; p.hkv = HKV; p.nblk = nblk;
+  p.lut = lut; p.l2e = l2e;
+  p.num = num; p.den = den; p.snum_tile = (int64_t)M * HD; p.snum_row = HD; p.sden_tile = M;
+  p.nsplit = 1;
+  RopeArgs r = {y, ldy, pos, spos, 0, cos, sin, npos, R, 1, H, HKV, HD, FR, FT, FK, FV, FZ, nullptr, nullptr, nullptr,
+                nullptr, err, cache, sc_nb, sc_h, sc_bs, slot, bs};
+  const int64_t max_keys = (int64_t)nblk * bs;
+  p.S = (int)((max_keys + 15) / 16 * 16);
+  const size_t lds = (size_t)4 * p.S * 8 + ((size_t)p.S / p.bs + 2) * 4;   // scores + block-table entries
+  const dim3 grid(R * HKV, 1);
+  hipStream_t st = (hipStream_t)stream;
+  if (HD == 64) {
+    hipFuncSetAttribute((const void*)attn_dec_raw_kernel<64, true>, hipFuncAttributeMaxDynamicSharedMemorySize,
+                        (int)(4 * kDecRawKeys * 8 + (kDecRawKeys + 2) * 4));
+    attn_dec_raw_kernel<64, true><<<grid, kDecWaves * 64, lds, st>>>(p, r);
+  } else {
+    hipFuncSetAttribute((const void*)attn_dec_raw_kernel<128, true>, hipFuncAttributeMaxDynamicSharedMemorySize,
+                        (int)(4 * kDecRawKeys * 8 + (kDecRawKeys + 2) * 4));
+    attn_dec_raw_kernel<128, true><<<grid, kDecWaves * 64, lds, st>>>(p, r);
+  }
+  return check_launch("attn_dec_raw_kernel(rope)");
 }
 
 extern "C" int bx_int8_attn_paged(const int64_t* q, const int64_t* qpos, int64_t sqpos_r, const int8_t* cache,

@@ -6,11 +6,10 @@
 //    src/bitexact/intops.py:73-79), and the linear post-segment (int8.segs.post, src/bitexact/int8/segs.py:62-67).
 // All arithmetic is int64 with the reference's wrapping and shift rules; every reduction is a maximum.
 #include "bx_common.h"
+#include "bx_rope.h"
 
 namespace bx {
 
-constexpr int64_t kSegNegBig = -(1LL << 20);   // ops.NEG_BIG
-constexpr int kSegQB = 22;                     // |q| <= 2^22
 
 // intops.rdiv (src/bitexact/intops.py:41-43): floor((2a + b) / (2b)), b > 0.
 __device__ __forceinline__ int64_t rdiv64(int64_t a, int64_t b) { return fdiv(add_wrap(2 * a, b), 2 * b); }
@@ -26,109 +25,31 @@ __device__ __forceinline__ int64_t seg_block_max(int64_t v, int64_t* sbuf) {
   return r;
 }
 
-struct RopeArgs {
-  const int64_t* y;        // [B T, ldy] at FR: q heads, k heads, v heads (H + 2 HKV) HD columns
-  int64_t ldy;
-  const int64_t* pos;      // [B, T] (strides spb, spt)
-  int64_t spb, spt;
-  const int64_t* cos;      // [n_pos, HD / 2] at FT
-  const int64_t* sin;
-  int npos;
-  int B, T, H, HKV, HD;
-  int FR, FT, FK, FV, FZ;
-  int32_t* qg;             // [B HKV, g T, HD]
-  int64_t* shg;            // [B HKV, g T]
-  int64_t* k;              // [B, T, HKV, HD] (null: not written)
-  int64_t* v;
-  int32_t* err;
-  int8_t* cache;           // paged limb-plane cache [nb][HKV][bs][8 HD] (null: no store)
-  int64_t sc_nb, sc_h, sc_bs;
-  const int64_t* slot;     // [B T] cache slot of each token (< 0: not stored)
-  int bs;
-};
-
-// The three int8 limbs of a K (plane 0) or V (plane 3) value into the paged cache at the token's slot, as the
-// reference's fused qkv kernel stores them (src/bitexact/vllm_plugin/exact_fuse.py:223-236; tri_paged.store's
-// layout, src/bitexact/vllm_plugin/tri_paged.py:311-335): limb i at byte (plane + i) HD + d of the slot's row.
-__device__ __forceinline__ void store_limbs(const RopeArgs& p, int token, int h, int plane, int d, int64_t x) {
-  if (!p.cache) return;
-  const int64_t sl = p.slot[token];
-  if (sl < 0) return;                                  // dummy / padded tokens carry slot -1
-  int8_t* base = p.cache + (sl / p.bs) * p.sc_nb + h * p.sc_h + (sl % p.bs) * p.sc_bs + (int64_t)plane * p.HD + d;
-  int32_t r = (int32_t)x;                              // |x| <= 8355711: three signed base-256 limbs
-#pragma unroll
-  for (int i = 0; i < 3; ++i) {
-    const int32_t l = limb_lo(r);
-    base[i * p.HD] = (int8_t)l;
-    r = (r - l) >> 8;
-  }
-}
-
 // Grid (token, head-row group of 4): wave w of block (token, j) takes head row 4 j + w (one row per wave, so the
 // rows' loads are in flight together instead of one row after another); lane l holds dims l + 64 e.
 template <int HD>
 __global__ __launch_bounds__(256) void rope_qgroup_kernel(RopeArgs p) {
-  constexpr int E = HD / 64, HALF = HD / 2;
+  constexpr int E = HD / 64;
   const int token = blockIdx.x, b = token / p.T, t = token - b * p.T;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  const int64_t* yr = p.y + (int64_t)token * p.ldy;
   const int64_t pos_raw = p.pos[(int64_t)b * p.spb + (int64_t)t * p.spt];
   bool bad = pos_raw < 0 || pos_raw >= p.npos;          // the reference's table index would fail: flagged
   const int64_t pos = imin(imax(pos_raw, 0), p.npos - 1);
-  const int64_t* cr = p.cos + pos * HALF;
-  const int64_t* sr = p.sin + pos * HALF;
   const int g = p.H / p.HKV, rows = p.H + 2 * p.HKV;
   const int64_t eps = -(int64_t)(p.FR + p.FT);
   for (int hr = blockIdx.y * 4 + wave; hr < rows && hr < (int)blockIdx.y * 4 + 4; hr += 4) {
-    const int64_t* x = yr + (int64_t)hr * HD;
     int64_t out[E];
-    int64_t emax = kSegNegBig;
-#pragma unroll
-    for (int e = 0; e < E; ++e) {
-      const int d = lane + 64 * e;
-      const int64_t xv = x[d];
-      bad |= (xv >= (1LL << 31)) || (xv <= -(1LL << 31));
-      if (hr < p.H + p.HKV) {
-        // _rope_full (src/bitexact/exact/segs.py:66-69): (x1 c - x2 s, x2 c + x1 s)
-        const int dd = d < HALF ? d : d - HALF;
-        const int64_t xp = x[d < HALF ? d + HALF : d - HALF];
-        const int64_t c = cr[dd], s = sr[dd];
-        out[e] = d < HALF ? add_wrap(mul_wrap(xv, c), -mul_wrap(xp, s)) : add_wrap(mul_wrap(xv, c), mul_wrap(xp, s));
-      } else {
-        out[e] = xv;
-      }
-    }
+    rope_row<HD>(p, token, hr, pos, lane, out, bad);
     if (hr < p.H) {
-      // q head: ops.quant(Pq, -(FR + FT)) over the head's HD values, stored at its grouped row
-#pragma unroll
-      for (int e = 0; e < E; ++e)
-        if (out[e] != 0) emax = imax(emax, bitlen(out[e] < 0 ? -out[e] : out[e]) + eps);
-      emax = wave_max64(emax);
-      const int64_t shq = imax(emax - kSegQB, kSegNegBig);
-      bad |= shq > p.FK + 3 - p.FZ;
+      // q head: quantized, stored at its grouped row
+      const int64_t shq = rope_q_shift<HD>(p, out, bad);
       const int kvh = hr / g, gi = hr - kvh * g;
       const int64_t row = ((int64_t)b * p.HKV + kvh) * ((int64_t)g * p.T) + (int64_t)gi * p.T + t;
 #pragma unroll
       for (int e = 0; e < E; ++e) p.qg[row * HD + lane + 64 * e] = (int32_t)rshc(out[e], shq - eps);
       if (lane == 0) p.shg[row] = shq;
-    } else if (hr < p.H + p.HKV) {
-      const int kh = hr - p.H;
-#pragma unroll
-      for (int e = 0; e < E; ++e) {
-        const int64_t kv = rshc(out[e], p.FR + p.FT - p.FK);
-        bad |= kv > kLim3 || kv < -kLim3;
-        if (p.k) p.k[((int64_t)token * p.HKV + kh) * HD + lane + 64 * e] = kv;
-        store_limbs(p, token, kh, 0, lane + 64 * e, kv);
-      }
     } else {
-      const int vh = hr - p.H - p.HKV;
-#pragma unroll
-      for (int e = 0; e < E; ++e) {
-        const int64_t vv = rshc(out[e], p.FR - p.FV);
-        bad |= vv > kLim3 || vv < -kLim3;
-        if (p.v) p.v[((int64_t)token * p.HKV + vh) * HD + lane + 64 * e] = vv;
-        store_limbs(p, token, vh, 3, lane + 64 * e, vv);
-      }
+      rope_kv_store<HD>(p, token, hr, lane, out, bad);
     }
   }
   if (wave_or(bad ? 1 : 0) && lane == 0) p.err[0] = 1;

@@ -135,6 +135,21 @@ int bx_exact_attn_paged(const int32_t* q, const int64_t* sh, const int64_t* qpos
                         int32_t nblk, const int64_t* rmap, const int64_t* lut, int64_t l2e, int64_t* num, int64_t* den,
                         int32_t R, int32_t HKV, int32_t M, int32_t HD, int32_t nsplit, void* ws, int64_t ws_bytes,
                         bx_stream_t stream);
+
+/* Replaces the decode step's exact_fuse.qkv + tri_exact_attn.attend pair (src/bitexact/vllm_plugin/exact_fuse.py:
+ * 372-386, tri_exact_attn.py:138-165) when every token of the step belongs to its own sequence (decode): one launch
+ * does the rope kernel's work (bx_rope_qgroup_store: RoPE of the q and k heads of y int64 [R, >= (H + 2 HKV) HD]
+ * (row stride ldy) at pos int64 [R] (stride spos) with the cos / sin tables [npos, HD / 2], the per-head
+ * quantization of q, the k / v limbs stored at slot int64 [R] of the cache, bound violations to err[0]) and then
+ * the attention of bx_exact_attn_paged with M = H / HKV <= 4 queries per (token, KV head) at qpos = pos, over at
+ * most 2048 keys per row, no key split. Outputs num int64 [R, HKV, M, HD], den int64 [R, HKV, M]; the grouped
+ * queries are not written. FK and FZ must be the compiled formats (17, 26). */
+int bx_exact_attn_paged_rope(const int64_t* y, int64_t ldy, const int64_t* pos, int64_t spos, const int64_t* cos,
+                             const int64_t* sin, int32_t npos, int32_t H, int32_t FR, int32_t FT, int32_t FK,
+                             int32_t FV, int32_t FZ, const int64_t* slot, int8_t* cache, int64_t sc_nb, int64_t sc_h,
+                             int64_t sc_bs, int32_t bs, const int32_t* bt, int64_t sbt, int32_t nblk,
+                             const int64_t* rmap, const int64_t* lut, int64_t l2e, int64_t* num, int64_t* den,
+                             int32_t R, int32_t HKV, int32_t HD, int32_t* err, bx_stream_t stream);
 /* Workspace bytes of the paged attentions (exact and int8) for up to min(64, 4096 / T) key splits, T = R HKV
  * ceil(M / 4) query tiles; a call with more splits than the workspace holds is rejected. */
 int64_t bx_attn_paged_workspace(int32_t R, int32_t HKV, int32_t M, int32_t HD);

@@ -278,3 +278,55 @@ def test_int8_paged_attention(dev, HD):
                 num, den = tri_paged.attend(q.to(dev), qpos.to(dev), cl, bt.to(dev), ptab, nsplit=ns)
                 assert np.array_equal(num.cpu().numpy(), ref_num), (Rr, M, ns, lim)
                 assert np.array_equal(den.cpu().numpy(), ref_den), (Rr, M, ns, lim)
+
+
+@pytest.mark.parametrize("HD,H,HKV", [(64, 32, 8), (128, 8, 2), (64, 6, 2)])
+def test_rope_attend_equals_store_then_attend(dev, HD, H, HKV):
+    """The decode step's fused launch (tri_exact_attn.rope_attend: RoPE, q quantization and the K / V store as the
+    attention's prologue) against the two-launch path it replaces (ops.qkv_y with the cache store, then attend
+    unsplit): the same num / den, the same cache bytes and the same flag, one token per sequence at different
+    context lengths, with a padding token (slot -1 keeps the cache unchanged) and the key at the token's own
+    position read back from the slot the prologue just wrote."""
+    from bitexact.exact import ops
+    from bitexact.exact.consts import FT, llama3_inv_freq, rope_tables
+    from bitexact.vllm_plugin import tri_exact_attn
+    g = torch.Generator().manual_seed(HD + H)
+    N, bs, nblk = 6, 16, 20
+    cos, sin = rope_tables(400, FT, llama3_inv_freq(HD))
+    cos, sin = cos.to(dev), sin.to(dev)
+    W = (H + 2 * HKV) * HD
+    y = torch.randint(-(1 << 30), 1 << 30, (N, W), generator=g)
+    y[1, :HD] >>= 24                                   # a small q head: exponent near NEG_BIG
+    pos = torch.tensor([0, 17, 100, 255, 319, 5])
+    nb = 1 + N * nblk
+    bt = (1 + torch.randperm(N * nblk, generator=g)).to(torch.int32).view(N, nblk)
+    rmap = torch.arange(N)
+    slot = bt[rmap, pos // bs].long() * bs + pos % bs
+    slot[5] = -1                                       # padding: nothing stored
+    c0 = torch.randint(-128, 128, (nb, HKV, bs, 8 * HD), dtype=torch.int8, generator=g).to(dev)
+    lut = _lut(dev)
+    l2e = R.L2E28_HD[HD]
+    ca, cb = c0.clone(), c0.clone()
+    fa = torch.zeros(1, dtype=torch.int32, device=dev)
+    qg, shg, _, _, _ = ops.qkv_y(y.to(dev), pos.view(N, 1).to(dev), cos, sin, N, 1, (H, HKV, HD), flag=fa,
+                                 store=(ca, slot.to(dev)))
+    G = H // HKV
+    qpos = pos.view(-1, 1).expand(-1, G).contiguous().to(dev)
+    na, da = tri_exact_attn.attend(qg.view(N, HKV, G, HD), shg.view(N, HKV, G), qpos, ca, bt.to(dev), rmap.to(dev),
+                                   lut, l2e, nsplit=1)
+    fb = torch.zeros(1, dtype=torch.int32, device=dev)
+    nb_, db = tri_exact_attn.rope_attend(y.to(dev), pos.to(dev), cos, sin, (H, HKV, HD), cb, slot.to(dev),
+                                         bt.to(dev), rmap.to(dev), lut, l2e, fb)
+    torch.cuda.synchronize()
+    assert torch.equal(ca, cb), "cache bytes differ"
+    assert torch.equal(na, nb_) and torch.equal(da, db)
+    assert int(fa.item()) == int(fb.item())
+    # a position past the rope tables flags in both forms
+    pos2 = pos.clone()
+    pos2[2] = 400
+    fa2, fb2 = torch.zeros(1, dtype=torch.int32, device=dev), torch.zeros(1, dtype=torch.int32, device=dev)
+    ops.qkv_y(y.to(dev), pos2.view(N, 1).to(dev), cos, sin, N, 1, (H, HKV, HD), flag=fa2, store=(c0.clone(),
+                                                                                                     slot.to(dev)))
+    tri_exact_attn.rope_attend(y.to(dev), pos2.to(dev), cos, sin, (H, HKV, HD), c0.clone(), slot.to(dev), bt.to(dev),
+                               rmap.to(dev), lut, l2e, fb2)
+    assert int(fa2.item()) == 1 and int(fb2.item()) == 1

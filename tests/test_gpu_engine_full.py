@@ -52,7 +52,7 @@ def test_full_geometry_batch_invariance_and_lm_head(dev, engine):
         p = torch.full((b,), CTX, device=dev, dtype=torch.long)
         rm = torch.arange(b, device=dev)
         sl = bt[rm, p // BS].long() * BS + p % BS
-        h = eng.forward(kvs, first[:b], p, sl, bt, rm)
+        h = eng.forward(kvs, first[:b], p, sl, bt, rm, one_per_seq=True)   # b = 32: the fused rope + attention
         lg = eng.logits(h)
         shas[b] = logits_sha(lg[0])
         if b == B:
