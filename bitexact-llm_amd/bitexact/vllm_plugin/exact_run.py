@@ -69,8 +69,8 @@ class ExactEngine:
         profiling run): nothing is stored and the attention output is 0. Returns the residual stream [N, D] int64
         at FR (src/bitexact/vllm_plugin/exact_run.py:55-128 with the fused stages of its 130-155).
         one_per_seq: every token is the only one of its sequence in this step (a decode step), so each layer's
-        RoPE + KV store and attention run as one launch (tri_exact_attn.rope_attend) where the shapes allow; the
-        integers are the same either way."""
+        RoPE + KV store, attention and attention output stage run as one launch (tri_exact_attn.rope_attend_out)
+        where the shapes allow; the integers are the same either way."""
         N, G, HKV, HD = ids.shape[0], self.G, self.HKV, self.HD
         pos = pos.long().contiguous()
         slot = slot.long().clamp(min=0)    # padding (slot < 0) -> the null block 0; one launch
@@ -85,9 +85,9 @@ class ExactEngine:
                 tri_exact_attn.rope_fusable(N, HKV, self.H, bt.shape[1], kvs[0].shape[2]))
         for i in range(self.L):
             y = self.fused[i, "wqkv"](q, sh, fl, False, q_planes=pl)
-            if fuse:
-                num, den = tri_exact_attn.rope_attend(y, pos, self.cos, self.sin, (self.H, HKV, HD), kvs[i], slot, bt,
-                                                      rmap, self.exp2, self.l2e, fl)
+            if fuse:   # RoPE + KV store + attention + the attention output stage in one launch
+                qo, sho = tri_exact_attn.rope_attend_out(y, pos, self.cos, self.sin, (self.H, HKV, HD), kvs[i], slot,
+                                                         bt, rmap, self.exp2, self.l2e, fl)
             elif kvs is None:
                 ops.qkv_y(y, pos.view(N, 1), self.cos, self.sin, N, 1, (self.H, HKV, HD), flag=fl)
                 num = torch.zeros(N, HKV, G, HD, dtype=torch.long, device=y.device)
@@ -97,7 +97,8 @@ class ExactEngine:
                                              flag=fl, store=(kvs[i], slot))   # K / V into the cache (exact_fuse.qkv)
                 num, den = tri_exact_attn.attend(qg.view(N, HKV, G, HD), shg.view(N, HKV, G), qpos, kvs[i], bt,
                                                  rmap, self.exp2, self.l2e)
-            qo, sho = ops.attn_out(num.view(N * HKV, G, HD), den.view(N * HKV, G, 1), 1, HKV)
+            if not fuse:
+                qo, sho = ops.attn_out(num.view(N * HKV, G, HD), den.view(N * HKV, G, 1), 1, HKV)
             wgu = self.fused[i, "wgu"]
             if wgu.needs_planes(N):   # the norm kernel also writes q's limb planes for the MFMA path
                 x, (q, pl), sh, _ = ops.add_norm_y(self.fused[i, "wo"](qo, sho, fl, True), x, *self.gm[i], flag=fl,

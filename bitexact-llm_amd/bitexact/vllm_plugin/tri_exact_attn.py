@@ -99,3 +99,42 @@ def rope_attend(y, pos, cos, sin, dm, cache, slot, bt, rmap, lut, l2e, flag):
     set flag[0]. The same integers as qkv_y(..., store=(cache, slot)) followed by attend(...)."""
     H, HKV, HD = (int(v) for v in dm)
     return _rope_attend(y, pos, cos, sin, H, HKV, HD, cache, slot, bt, rmap, lut, int(l2e), flag)
+
+
+def _rope_attend_out_fake(y, pos, cos, sin, H, HKV, HD, cache, slot, bt, rmap, lut, l2e, flag):
+    N = y.shape[0]
+    return empty((N, H * HD), torch.int32, y), empty((N,), torch.long, y)
+
+
+@op("attend_exact_rope_out(Tensor y, Tensor pos, Tensor cos, Tensor sin, int H, int HKV, int HD, Tensor(a!) cache, "
+    "Tensor slot, Tensor bt, Tensor rmap, Tensor lut, int l2e, Tensor(b!) flag) -> (Tensor, Tensor)",
+    _rope_attend_out_fake)
+def _rope_attend_out(y, pos, cos, sin, H, HKV, HD, cache, slot, bt, rmap, lut, l2e, flag):
+    from bitexact.exact.ops import FK, FR, FT, FV, FZ
+    _hip.require_cuda(y, pos, cos, sin, cache, slot, bt, rmap, lut, flag)
+    N = y.shape[0]
+    assert y.dtype == torch.int64 and y.stride(-1) == 1 and y.shape[1] >= (H + 2 * HKV) * HD
+    assert cache.dtype == torch.int8 and cache.dim() == 4 and cache.shape[1] == HKV and cache.shape[3] >= 6 * HD
+    assert cache.stride(3) == 1 and bt.dtype == torch.int32 and flag.dtype == torch.int32
+    pos = pos.reshape(-1).contiguous().long()
+    slot = slot.reshape(-1).contiguous().long()
+    assert pos.shape[0] == N and slot.shape[0] == N
+    cos, sin = cos.contiguous().long(), sin.contiguous().long()
+    rmap, lut = rmap.contiguous().long(), lut.contiguous().long()
+    qo = torch.empty(N, H * HD, dtype=torch.int32, device=y.device)
+    sho = torch.empty(N, dtype=torch.long, device=y.device)
+    ws, wsb = _hip.workspace(y.device, _hip.lib().bx_attn_rope_out_workspace(N))
+    tmp, tmpb = _hip.scratch(y.device, _hip.lib().bx_attn_rope_out_scratch(N, H, HD))
+    _hip.call("bx_exact_attn_paged_rope_out", _hip.ptr(y), y.stride(0), _hip.ptr(pos), 1, _hip.ptr(cos),
+              _hip.ptr(sin), cos.shape[0], H, FR, FT, FK, FV, FZ, _hip.ptr(slot), _hip.ptr(cache), cache.stride(0),
+              cache.stride(1), cache.stride(2), cache.shape[2], _hip.ptr(bt), bt.stride(0), bt.shape[1],
+              _hip.ptr(rmap), _hip.ptr(lut), int(l2e), _hip.ptr(qo), qo.stride(0), _hip.ptr(sho), N, HKV, HD,
+              _hip.ptr(flag), _hip.ptr(ws), wsb, _hip.ptr(tmp), tmpb, _hip.stream_of(y))
+    return qo, sho
+
+
+def rope_attend_out(y, pos, cos, sin, dm, cache, slot, bt, rmap, lut, l2e, flag):
+    """rope_attend with the attention output stage fused too (ops.attn_out over its num / den): -> (q int32
+    [N, H HD], sh int64 [N]), the wo linear's input; the same integers as rope_attend then ops.attn_out."""
+    H, HKV, HD = (int(v) for v in dm)
+    return _rope_attend_out(y, pos, cos, sin, H, HKV, HD, cache, slot, bt, rmap, lut, int(l2e), flag)

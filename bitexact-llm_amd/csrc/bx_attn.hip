@@ -18,6 +18,7 @@
 // hit distinct banks (rows padded by one word).
 #include "bx_common.h"
 #include "bx_rope.h"
+#include "bx_introws.h"
 
 #include <algorithm>
 #include <type_traits>
@@ -656,6 +657,75 @@ __device__ __forceinline__ void dec_finish(const AttnArgs& p, DecSmem<HD>& sm, c
   if (threadIdx.x < nvalid) p.den[group * p.sden_tile + q0 + threadIdx.x] = fin[4 * HD + threadIdx.x];
 }
 
+// The decode step's attention output stage (segs.attn_out: div_round + regroup + quant, src/bitexact/exact/segs.py
+// and ops.py; the standalone form is attn_out_kernel in csrc/bx_rows.hip) fused into the one-block decode
+// attention: ws_p int64 [R, H HD] (scratch) and ws_e int64 [R] / cnt int32 [R] (zero-filled workspace, left zero)
+// are the exchange, q int32 [R, ldq] and sh int64 [R] the outputs.
+struct AoArgs {
+  int64_t* ws_p;
+  int64_t* ws_e;
+  int32_t* cnt;
+  int32_t* q;
+  int64_t ldq;
+  int64_t* sh;
+  int FR, FV;
+};
+
+// The block's sums as dec_finish forms them (waves in order), then its queries' quotients P = div_round(num, FR -
+// FV, den) (0 where den = 0), their exponent maximum into the token's slot (atomicMax of emax - kNegBig + 1) and the
+// quotients into the token's row of ws_p (agent-scope stores, complete before the count); the token's last block
+// quantizes the whole row against the row maximum (rshc(P, shr + FR), shr = max(emax - kQB, NEG_BIG)) and resets
+// the slot and the count. No block waits for another.
+template <int HD>
+__device__ __forceinline__ void dec_finish_ao(const AttnArgs& p, const AoArgs& ao, DecSmem<HD>& sm, int64_t den,
+                                              int64_t (&num)[4][HD / 64], int group, int nvalid) {
+  constexpr int KK = HD / 64, NT = kDecWaves * 64;
+  __shared__ int64_t s_den[4];
+  __shared__ int64_t s_red[NT / 64];
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6, kl = lane & 15, qo = lane >> 4;
+#pragma unroll
+  for (int o = 1; o < 16; o <<= 1) den += __shfl_xor(den, o, 64);
+  if (kl == 0) sm.den[w][qo] = den;
+  __syncthreads();                                 // red overlays the waves' V rows
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+#pragma unroll
+    for (int kk = 0; kk < KK; ++kk) sm.red[w][i][lane + 64 * kk] = num[i][kk];
+  if (threadIdx.x < 4) {
+    int64_t t = 0;
+    for (int ww = 0; ww < kDecWaves; ++ww) t += sm.den[ww][threadIdx.x];
+    s_den[threadIdx.x] = t;
+  }
+  __syncthreads();
+  const int n = group / p.hkv, h = group % p.hkv, G = p.nq;
+  const int64_t W = (int64_t)p.hkv * G * HD;
+  int64_t emax = kNegBig;
+  for (int u = threadIdx.x; u < nvalid * HD; u += NT) {
+    const int i = u / HD, d = u % HD;
+    int64_t t = 0;
+    for (int ww = 0; ww < kDecWaves; ++ww) t += sm.red[ww][i][d];
+    const int64_t dn = s_den[i];                   // >= 1 whenever the query sees a key (itself)
+    const int64_t v = dn > 0 ? div_round64(t, ao.FR - ao.FV, dn, 1.0 / (double)dn) : 0;
+    ws_store(&ao.ws_p[n * W + (int64_t)(h * G + i) * HD + d], v);
+    if (v != 0) emax = imax(emax, bitlen(v < 0 ? -v : v) - ao.FR);
+  }
+  emax = block_max64(emax, s_red);
+  if (threadIdx.x == 0) atomicMax((unsigned long long*)&ao.ws_e[n], (unsigned long long)(emax - kNegBig + 1));
+  __builtin_amdgcn_s_waitcnt(0);                   // this thread's stores and atomic are complete before the count
+  __syncthreads();
+  if (threadIdx.x == 0) sm.s_last = atomicAdd(&ao.cnt[n], 1) == p.hkv - 1;
+  __syncthreads();
+  if (!sm.s_last) return;
+  const int64_t em = (int64_t)ws_load(&ao.ws_e[n]) + kNegBig - 1;
+  const int64_t shr = imax(em - kQB, kNegBig);
+  for (int64_t c = threadIdx.x; c < W; c += NT) ao.q[n * ao.ldq + c] = (int32_t)rshc(ws_load(&ao.ws_p[n * W + c]), shr + ao.FR);
+  if (threadIdx.x == 0) {
+    ao.sh[n] = shr;
+    ws_store(&ao.ws_e[n], 0);
+    atomicExch(&ao.cnt[n], 0);
+  }
+}
+
 // RAW (single launch only): sweep 1 keeps every score of the block's key range (p.S >= hi - lo of them per
 // query) in dynamic LDS and sweep 2 reads them back, so K is read once.
 template <int HD, int PHASE, bool RAW>
@@ -896,8 +966,8 @@ __device__ __forceinline__ int64_t dec_score_k(const v4i (&qa)[HD / 64], const v
 // store the k and v limbs at the token's cache slot (each waits for its stores before the barrier, so the
 // sweeps read them back). The launch then replaces the standalone rope kernel.
 constexpr int kDecDepth = 3;
-template <int HD, bool RP = false>
-__global__ __launch_bounds__(kDecWaves * 64) void attn_dec_raw_kernel(AttnArgs p, RopeArgs r) {
+template <int HD, bool RP = false, bool AO = false>
+__global__ __launch_bounds__(kDecWaves * 64) void attn_dec_raw_kernel(AttnArgs p, RopeArgs r, AoArgs ao) {
   static_assert(!RP || kDecWaves >= 6, "the rope prologue uses waves 0-3 (q heads), 4 (k) and 5 (v)");
   BX_PHASE(1, 0);
   __shared__ DecSmem<HD> sm;
@@ -1032,7 +1102,10 @@ __global__ __launch_bounds__(kDecWaves * 64) void attn_dec_raw_kernel(AttnArgs p
     }
   }
   BX_PHASE(1, 4);
-  dec_finish<HD>(p, sm, DecWs{}, den, num, tile, 0, 1, group, q0, nvalid);
+  if constexpr (AO)
+    dec_finish_ao<HD>(p, ao, sm, den, num, group, nvalid);
+  else
+    dec_finish<HD>(p, sm, DecWs{}, den, num, tile, 0, 1, group, q0, nvalid);
   BX_PHASE(1, 5);
 }
 
@@ -1899,7 +1972,7 @@ static int launch_dec(AttnArgs& p, int groups, int64_t max_keys, hipStream_t st)
     const size_t lds = (size_t)4 * p.S * 8 + ((size_t)p.S / p.bs + 2) * 4;   // scores + block-table entries
     hipFuncSetAttribute((const void*)attn_dec_raw_kernel<HD>, hipFuncAttributeMaxDynamicSharedMemorySize,
                         (int)(4 * kDecRawKeys * 8 + (kDecRawKeys + 2) * 4));
-    attn_dec_raw_kernel<HD><<<grid, kDecWaves * 64, lds, st>>>(p, RopeArgs{});
+    attn_dec_raw_kernel<HD><<<grid, kDecWaves * 64, lds, st>>>(p, RopeArgs{}, AoArgs{});
     return check_launch("attn_dec_raw_kernel");
   }
   attn_dec_kernel<HD, 1, false><<<grid, kDecWaves * 64, 0, st>>>(p);
@@ -1959,13 +2032,12 @@ extern "C" int bx_exact_attn_paged(const int32_t* q, const int64_t* sh, const in
                   : launch_dec<128>(p, R * HKV, max_keys, (hipStream_t)stream);
 }
 
-extern "C" int bx_exact_attn_paged_rope(const int64_t* y, int64_t ldy, const int64_t* pos, int64_t spos,
-                                        const int64_t* cos, const int64_t* sin, int32_t npos, int32_t H, int32_t FR,
-                                        int32_t FT, int32_t FK, int32_t FV, int32_t FZ, const int64_t* slot,
-                                        int8_t* cache, int64_t sc_nb, int64_t sc_h, int64_t sc_bs, int32_t bs,
-                                        const int32_t* bt, int64_t sbt, int32_t nblk, const int64_t* rmap,
-                                        const int64_t* lut, int64_t l2e, int64_t* num, int64_t* den, int32_t R,
-                                        int32_t HKV, int32_t HD, int32_t* err, bx_stream_t stream) {
+static int attn_rope_common(const int64_t* y, int64_t ldy, const int64_t* pos, int64_t spos, const int64_t* cos,
+                            const int64_t* sin, int32_t npos, int32_t H, int32_t FR, int32_t FT, int32_t FK, int32_t FV,
+                            int32_t FZ, const int64_t* slot, int8_t* cache, int64_t sc_nb, int64_t sc_h, int64_t sc_bs,
+                            int32_t bs, const int32_t* bt, int64_t sbt, int32_t nblk, const int64_t* rmap,
+                            const int64_t* lut, int64_t l2e, int64_t* num, int64_t* den, int32_t R, int32_t HKV,
+                            int32_t HD, int32_t* err, const AoArgs* ao, hipStream_t st) {
   BX_REQUIRE(R >= 0 && HKV > 0 && H % HKV == 0 && H / HKV >= 1 && H / HKV <= 4, "need 1 <= H / HKV <= 4");
   BX_REQUIRE(HD == 64 || HD == 128, "head_dim must be 64 or 128");
   BX_REQUIRE(FK == kFK && FZ == kFZ, "the attention's fixed-point formats (FK, FZ) are compiled in");
@@ -1974,7 +2046,8 @@ extern "C" int bx_exact_attn_paged_rope(const int64_t* y, int64_t ldy, const int
   BX_REQUIRE(sc_bs >= 6 * HD && sc_nb % 16 == 0 && sc_h % 16 == 0 && sc_bs % 16 == 0 && ((uintptr_t)cache & 15) == 0,
              "cache rows must hold the 6 HD limb bytes, 16-byte aligned");
   BX_REQUIRE(sc_h >= (int64_t)bs * sc_bs && sc_nb >= (int64_t)HKV * sc_h, "cache strides");
-  BX_REQUIRE(y && pos && cos && sin && slot && bt && rmap && lut && num && den && err, "null pointer");
+  BX_REQUIRE(y && pos && cos && sin && slot && bt && rmap && lut && err, "null pointer");
+  BX_REQUIRE(ao != nullptr || (num && den), "null pointer");
   if (R == 0) return BX_OK;
   const int M = H / HKV;
   AttnArgs p = {};
@@ -1990,17 +2063,64 @@ extern "C" int bx_exact_attn_paged_rope(const int64_t* y, int64_t ldy, const int
   p.S = (int)((max_keys + 15) / 16 * 16);
   const size_t lds = (size_t)4 * p.S * 8 + ((size_t)p.S / p.bs + 2) * 4;   // scores + block-table entries
   const dim3 grid(R * HKV, 1);
-  hipStream_t st = (hipStream_t)stream;
-  if (HD == 64) {
-    hipFuncSetAttribute((const void*)attn_dec_raw_kernel<64, true>, hipFuncAttributeMaxDynamicSharedMemorySize,
-                        (int)(4 * kDecRawKeys * 8 + (kDecRawKeys + 2) * 4));
-    attn_dec_raw_kernel<64, true><<<grid, kDecWaves * 64, lds, st>>>(p, r);
-  } else {
-    hipFuncSetAttribute((const void*)attn_dec_raw_kernel<128, true>, hipFuncAttributeMaxDynamicSharedMemorySize,
-                        (int)(4 * kDecRawKeys * 8 + (kDecRawKeys + 2) * 4));
-    attn_dec_raw_kernel<128, true><<<grid, kDecWaves * 64, lds, st>>>(p, r);
-  }
+  const int maxlds = (int)(4 * kDecRawKeys * 8 + (kDecRawKeys + 2) * 4);
+#define BX_RAW_ROPE(HDV, AOV)                                                                                       \
+  do {                                                                                                           \
+    hipFuncSetAttribute((const void*)attn_dec_raw_kernel<HDV, true, AOV>, hipFuncAttributeMaxDynamicSharedMemorySize, \
+                        maxlds);                                                                                 \
+    attn_dec_raw_kernel<HDV, true, AOV><<<grid, kDecWaves * 64, lds, st>>>(p, r, ao ? *ao : AoArgs{});              \
+  } while (0)
+  if (HD == 64 && ao) BX_RAW_ROPE(64, true);
+  else if (HD == 64) BX_RAW_ROPE(64, false);
+  else if (ao) BX_RAW_ROPE(128, true);
+  else BX_RAW_ROPE(128, false);
+#undef BX_RAW_ROPE
   return check_launch("attn_dec_raw_kernel(rope)");
+}
+
+extern "C" int bx_exact_attn_paged_rope(const int64_t* y, int64_t ldy, const int64_t* pos, int64_t spos,
+                                        const int64_t* cos, const int64_t* sin, int32_t npos, int32_t H, int32_t FR,
+                                        int32_t FT, int32_t FK, int32_t FV, int32_t FZ, const int64_t* slot,
+                                        int8_t* cache, int64_t sc_nb, int64_t sc_h, int64_t sc_bs, int32_t bs,
+                                        const int32_t* bt, int64_t sbt, int32_t nblk, const int64_t* rmap,
+                                        const int64_t* lut, int64_t l2e, int64_t* num, int64_t* den, int32_t R,
+                                        int32_t HKV, int32_t HD, int32_t* err, bx_stream_t stream) {
+  return attn_rope_common(y, ldy, pos, spos, cos, sin, npos, H, FR, FT, FK, FV, FZ, slot, cache, sc_nb, sc_h, sc_bs, bs,
+                          bt, sbt, nblk, rmap, lut, l2e, num, den, R, HKV, HD, err, nullptr, (hipStream_t)stream);
+}
+
+extern "C" int64_t bx_attn_rope_out_workspace(int32_t R) {
+  if (R <= 0) return 0;
+  return (int64_t)R * 12 + 256;
+}
+
+extern "C" int64_t bx_attn_rope_out_scratch(int32_t R, int32_t H, int32_t HD) {
+  if (R <= 0 || H <= 0 || HD <= 0) return 0;
+  return (int64_t)R * H * HD * 8;
+}
+
+extern "C" int bx_exact_attn_paged_rope_out(const int64_t* y, int64_t ldy, const int64_t* pos, int64_t spos,
+                                            const int64_t* cos, const int64_t* sin, int32_t npos, int32_t H,
+                                            int32_t FR, int32_t FT, int32_t FK, int32_t FV, int32_t FZ,
+                                            const int64_t* slot, int8_t* cache, int64_t sc_nb, int64_t sc_h,
+                                            int64_t sc_bs, int32_t bs, const int32_t* bt, int64_t sbt, int32_t nblk,
+                                            const int64_t* rmap, const int64_t* lut, int64_t l2e, int32_t* q,
+                                            int64_t ldq, int64_t* sh, int32_t R, int32_t HKV, int32_t HD, int32_t* err,
+                                            void* ws, int64_t ws_bytes, void* tmp, int64_t tmp_bytes,
+                                            bx_stream_t stream) {
+  BX_REQUIRE(q && sh && ldq >= (int64_t)H * HD, "null q / sh or ldq too small");
+  BX_REQUIRE(ws && ws_bytes >= bx_attn_rope_out_workspace(R) && ((uintptr_t)ws & 7) == 0,
+             "workspace too small (%lld < %lld)", (long long)ws_bytes, (long long)bx_attn_rope_out_workspace(R));
+  BX_REQUIRE(tmp && tmp_bytes >= bx_attn_rope_out_scratch(R, H, HD) && ((uintptr_t)tmp & 7) == 0,
+             "scratch too small (%lld < %lld)", (long long)tmp_bytes, (long long)bx_attn_rope_out_scratch(R, H, HD));
+  BX_REQUIRE(FR - FV >= 0 && FR - FV <= 62, "FR - FV outside [0, 62]");
+  AoArgs ao;
+  ao.ws_p = (int64_t*)tmp;
+  ao.ws_e = (int64_t*)ws;
+  ao.cnt = (int32_t*)(ao.ws_e + R);
+  ao.q = q; ao.ldq = ldq; ao.sh = sh; ao.FR = FR; ao.FV = FV;
+  return attn_rope_common(y, ldy, pos, spos, cos, sin, npos, H, FR, FT, FK, FV, FZ, slot, cache, sc_nb, sc_h, sc_bs, bs,
+                          bt, sbt, nblk, rmap, lut, l2e, nullptr, nullptr, R, HKV, HD, err, &ao, (hipStream_t)stream);
 }
 
 extern "C" int bx_int8_attn_paged(const int64_t* q, const int64_t* qpos, int64_t sqpos_r, const int8_t* cache,

@@ -150,6 +150,21 @@ int bx_exact_attn_paged_rope(const int64_t* y, int64_t ldy, const int64_t* pos, 
                              int64_t sc_bs, int32_t bs, const int32_t* bt, int64_t sbt, int32_t nblk,
                              const int64_t* rmap, const int64_t* lut, int64_t l2e, int64_t* num, int64_t* den,
                              int32_t R, int32_t HKV, int32_t HD, int32_t* err, bx_stream_t stream);
+
+/* bx_exact_attn_paged_rope with the attention output stage fused as well (segs.attn_out, the reference's div_round +
+ * regroup + quant after the attention: src/bitexact/exact/segs.py, exact/ops.py): instead of num / den it writes
+ * q int32 [R, ldq >= H HD] and sh int64 [R], the quantized rows the wo linear reads, equal to bx_attn_out over the
+ * num / den it replaces. ws: bx_attn_rope_out_workspace(R) bytes, zero-filled (left zero); tmp:
+ * bx_attn_rope_out_scratch(R, H, HD) bytes of scratch. Each token's last block quantizes the row. */
+int64_t bx_attn_rope_out_workspace(int32_t R);
+int64_t bx_attn_rope_out_scratch(int32_t R, int32_t H, int32_t HD);
+int bx_exact_attn_paged_rope_out(const int64_t* y, int64_t ldy, const int64_t* pos, int64_t spos, const int64_t* cos,
+                                 const int64_t* sin, int32_t npos, int32_t H, int32_t FR, int32_t FT, int32_t FK,
+                                 int32_t FV, int32_t FZ, const int64_t* slot, int8_t* cache, int64_t sc_nb,
+                                 int64_t sc_h, int64_t sc_bs, int32_t bs, const int32_t* bt, int64_t sbt, int32_t nblk,
+                                 const int64_t* rmap, const int64_t* lut, int64_t l2e, int32_t* q, int64_t ldq,
+                                 int64_t* sh, int32_t R, int32_t HKV, int32_t HD, int32_t* err, void* ws,
+                                 int64_t ws_bytes, void* tmp, int64_t tmp_bytes, bx_stream_t stream);
 /* Workspace bytes of the paged attentions (exact and int8) for up to min(64, 4096 / T) key splits, T = R HKV
  * ceil(M / 4) query tiles; a call with more splits than the workspace holds is rejected. */
 int64_t bx_attn_paged_workspace(int32_t R, int32_t HKV, int32_t M, int32_t HD);

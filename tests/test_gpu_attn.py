@@ -284,7 +284,8 @@ def test_int8_paged_attention(dev, HD):
 def test_rope_attend_equals_store_then_attend(dev, HD, H, HKV):
     """The decode step's fused launch (tri_exact_attn.rope_attend: RoPE, q quantization and the K / V store as the
     attention's prologue) against the two-launch path it replaces (ops.qkv_y with the cache store, then attend
-    unsplit): the same num / den, the same cache bytes and the same flag, one token per sequence at different
+    unsplit): the same num / den, the same cache bytes and the same flag; rope_attend_out (the attention output
+    stage fused as well) against ops.attn_out of that num / den, one token per sequence at different
     context lengths, with a padding token (slot -1 keeps the cache unchanged) and the key at the token's own
     position read back from the slot the prologue just wrote."""
     from bitexact.exact import ops
@@ -321,6 +322,18 @@ def test_rope_attend_equals_store_then_attend(dev, HD, H, HKV):
     assert torch.equal(ca, cb), "cache bytes differ"
     assert torch.equal(na, nb_) and torch.equal(da, db)
     assert int(fa.item()) == int(fb.item())
+    # with the attention output stage fused too: the rows ops.attn_out makes of the same num / den (twice in a
+    # row: the exchange slots are left zero for the next call)
+    qo, sho = ops.attn_out(na.view(N * HKV, G, HD), da.view(N * HKV, G, 1), 1, HKV)
+    for _ in range(2):
+        cc = c0.clone()
+        fc = torch.zeros(1, dtype=torch.int32, device=dev)
+        qf, shf = tri_exact_attn.rope_attend_out(y.to(dev), pos.to(dev), cos, sin, (H, HKV, HD), cc, slot.to(dev),
+                                                 bt.to(dev), rmap.to(dev), lut, l2e, fc)
+        torch.cuda.synchronize()
+        assert torch.equal(cc, ca), "cache bytes differ (fused output stage)"
+        assert torch.equal(qf, qo) and torch.equal(shf, sho)
+        assert int(fc.item()) == int(fa.item())
     # a position past the rope tables flags in both forms
     pos2 = pos.clone()
     pos2[2] = 400
