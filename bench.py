@@ -550,9 +550,7 @@ def bench_engine(dev, steps, warmup, B=32, ctx=1024, bs=16):
 
     def step(i):
         x = eng.forward(kvs, ids, pos, slot, bt, rmap, one_per_seq=True)
-        ids.copy_(eng.greedy(eng.logits(x)))
-        pos.add_(1)
-        slot.copy_(bt[rmap, pos // bs].long() * bs + pos % bs)
+        eng.advance(eng.logits(x), ids, pos, slot, bt, rmap, bs)      # ids, pos, slot for the next step
 
     stream = torch.cuda.Stream(dev)
     with torch.cuda.stream(stream):

@@ -86,6 +86,7 @@ SIGNATURES = {
     "bx_int_rowop": (ctypes.c_int, [I32, I32, P, P, P, I64, I64, I64, P, P, P, P, P, I64, P, P, P]),
     "bx_stream_read": (ctypes.c_int, [P, I64, I32, I32, P, P]),
     "bx_mfma_rate": (ctypes.c_int, [I32, I32, I32, I32, P, P]),
+    "bx_decode_advance": (ctypes.c_int, [P, P, P, P, P, I64, I32, P, I32, I32, P]),
     "bx_phases_linear": (ctypes.c_int, [P]),
     "bx_phases_attn": (ctypes.c_int, [P]),
     "bx_phases_rows": (ctypes.c_int, [P]),

@@ -10,6 +10,8 @@ step can be captured in a HIP graph.
 
 import torch
 
+from bitexact import _hip
+from bitexact._ops import op
 from bitexact.exact import ops
 from bitexact.exact.consts import FR, dims
 from bitexact.exact.model import GEMMS, Lin
@@ -137,6 +139,24 @@ class ExactEngine:
         """The greedy token of each logits row: its first maximum."""
         return first_argmax(logits)
 
+    def advance(self, logits, ids, pos, slot, bt, rmap, bs=16):
+        """A greedy decode step's next inputs, in place: ids = greedy(logits), pos += 1, slot = the new position's
+        cache slot (bt[rmap, pos // bs] bs + pos % bs, bs the cache block size): the first-max kernels and one
+        launch for the rest (the reference leaves this loop to its caller)."""
+        _advance(self.greedy(logits), ids, pos, slot, bt, rmap, int(bs))
+
     def check(self):
         if bool(self.err):
             raise OverflowError("integer bound violated (exact/model.py)")
+
+
+@op("decode_advance(Tensor nxt, Tensor(a!) ids, Tensor(b!) pos, Tensor(c!) slot, Tensor bt, Tensor rmap, int bs) -> ()",
+    lambda nxt, ids, pos, slot, bt, rmap, bs: None)
+def _advance(nxt, ids, pos, slot, bt, rmap, bs):
+    _hip.require_cuda(nxt, ids, pos, slot, bt, rmap)
+    N = ids.shape[0]
+    for t in (nxt, ids, pos, slot, rmap):
+        assert t.dtype == torch.int64 and t.is_contiguous() and t.shape == (N,)
+    assert bt.dtype == torch.int32 and bt.dim() == 2 and bt.stride(1) == 1
+    _hip.call("bx_decode_advance", _hip.ptr(nxt), _hip.ptr(ids), _hip.ptr(pos), _hip.ptr(slot), _hip.ptr(bt),
+              bt.stride(0), bt.shape[1], _hip.ptr(rmap), bs, N, _hip.stream_of(ids))

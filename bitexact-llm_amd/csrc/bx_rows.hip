@@ -449,6 +449,18 @@ __global__ __launch_bounds__(64) void argmax_fin_kernel(const int64_t* slots, in
   out[m] = idx;
 }
 
+// A greedy decode step's next inputs, one thread per sequence: ids = the step's first-max tokens, pos + 1, and the
+// cache slot of the new position through the block table (slot = bt[rmap, pos / bs] bs + pos % bs).
+__global__ void decode_advance_kernel(const int64_t* next, int64_t* ids, int64_t* pos, int64_t* slot, const int32_t* bt,
+                                      int64_t sbt, const int64_t* rmap, int bs, int N) {
+  const int n = blockIdx.x * blockDim.x + threadIdx.x;
+  if (n >= N) return;
+  const int64_t p = pos[n] + 1;
+  ids[n] = next[n];
+  pos[n] = p;
+  slot[n] = (int64_t)bt[rmap[n] * sbt + p / bs] * bs + p % bs;
+}
+
 }  // namespace bx
 
 using namespace bx;
@@ -621,3 +633,13 @@ extern "C" int bx_attn_out(const int64_t* num, int64_t sn_group, int64_t sn_quer
 }
 
 BX_PHASE_DEFINE(rows)
+
+extern "C" int bx_decode_advance(const int64_t* next, int64_t* ids, int64_t* pos, int64_t* slot, const int32_t* bt,
+                                 int64_t sbt, int32_t nblk, const int64_t* rmap, int32_t bs, int32_t N,
+                                 bx_stream_t stream) {
+  BX_REQUIRE(N >= 0 && bs > 0 && nblk > 0 && sbt >= nblk, "bad sizes");
+  if (N == 0) return BX_OK;
+  BX_REQUIRE(next && ids && pos && slot && bt && rmap, "null pointer");
+  decode_advance_kernel<<<(N + 255) / 256, 256, 0, (hipStream_t)stream>>>(next, ids, pos, slot, bt, sbt, rmap, bs, N);
+  return check_launch("decode_advance_kernel");
+}

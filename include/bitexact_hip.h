@@ -358,6 +358,13 @@ int bx_int_rowop(int32_t op, int32_t nin, const void* const* ptrs, const int64_t
                  int64_t rows, int64_t D, void* out0, void* out1, void* out2, void* out3, const int64_t* lut,
                  int64_t lut_len, const int64_t* iargs, int32_t* flag, bx_stream_t stream);
 
+/* A greedy decode step's input update (the caller's loop in the reference: src/bitexact/vllm_plugin/exact_run.py
+ * decode loop / vLLM's scheduler), in one launch: ids[n] = next[n], pos[n] += 1, slot[n] = bt[rmap[n], pos[n] / bs]
+ * bs + pos[n] % bs, for N sequences (int64 next / ids / pos / slot / rmap [N], int32 bt row stride sbt, nblk
+ * columns; the new position must stay inside the table). */
+int bx_decode_advance(const int64_t* next, int64_t* ids, int64_t* pos, int64_t* slot, const int32_t* bt, int64_t sbt,
+                      int32_t nblk, const int64_t* rmap, int32_t bs, int32_t N, bx_stream_t stream);
+
 /* No counterpart in the reference: a measurement probe for the decode GEMMs' roofline. Streams `bytes` from src
  * (16-byte nontemporal loads, grid-stride over blocks x threads) and discards them: the practical read ceiling of
  * one launch at that size. sink: an int32 [1] device word (practically never written). */

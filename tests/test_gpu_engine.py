@@ -138,3 +138,24 @@ def test_constants_file_roundtrip(dev, tmp_path):
         kvs = eng.new_cache(1 + NBLK, BS)
         out.append(eng.logits(eng.forward(kvs, ids, pos, slot, bt, rmap)).cpu())
     assert torch.equal(out[0], out[1])
+
+
+def test_decode_advance(dev):
+    """ExactEngine.advance (first-max tokens, pos + 1 and the new slot through the block table, one launch after
+    the first-max kernels) against the same update in torch ops."""
+    from bitexact.vllm_plugin.exact_run import ExactEngine
+    g = torch.Generator().manual_seed(3)
+    N, nblk, bs, V = 37, 9, 16, 3000
+    logits = torch.randint(-1000, 1000, (N, V), generator=g).to(dev)
+    logits[5, 17] = logits[5, 400] = 5000                 # ties: the first maximum
+    bt = torch.randint(1, 500, (N + 3, nblk), generator=g).to(torch.int32).to(dev)
+    rmap = torch.randperm(N + 3, generator=g)[:N].to(dev)
+    pos = torch.randint(0, nblk * bs - 1, (N,), generator=g).to(dev)
+    ids = torch.zeros(N, dtype=torch.long, device=dev)
+    slot = torch.zeros(N, dtype=torch.long, device=dev)
+    want_ids = torch.argmax(logits, dim=1)               # torch returns the first maximum
+    want_pos = pos + 1
+    want_slot = bt[rmap, want_pos // bs].long() * bs + want_pos % bs
+    eng = ExactEngine.__new__(ExactEngine)               # advance uses no model state
+    eng.advance(logits, ids, pos, slot, bt, rmap, bs)
+    assert torch.equal(ids, want_ids) and torch.equal(pos, want_pos) and torch.equal(slot, want_slot)
