@@ -90,6 +90,19 @@ __device__ __forceinline__ int64_t fdiv_rcp(int64_t a, int64_t b, double binv) {
   return q;
 }
 
+// s0 + 2^8 s1 + 2^16 s2 + 2^24 s3 + 2^32 s4 (wrapping) for five int32 partial sums, formed in 32-bit halves: term
+// s_i 2^(8 i) is (s_i >> (32 - 8 i)) 2^32 + ((uint32) s_i << 8 i) with an arithmetic shift, so the low words add with
+// carries and the high words take the shifted-out parts; no 64-bit shift or add is needed.
+__device__ __forceinline__ int64_t join5(int32_t s0, int32_t s1, int32_t s2, int32_t s3, int32_t s4) {
+  unsigned c0, c1, c2;
+  uint32_t lo = __builtin_addc((uint32_t)s0, (uint32_t)s1 << 8, 0u, &c0);
+  lo = __builtin_addc(lo, (uint32_t)s2 << 16, 0u, &c1);
+  lo = __builtin_addc(lo, (uint32_t)s3 << 24, 0u, &c2);
+  const uint32_t hi = (uint32_t)(s0 >> 31) + (uint32_t)(s1 >> 24) + (uint32_t)(s2 >> 16) + (uint32_t)(s3 >> 8) +
+                      (uint32_t)s4 + c0 + c1 + c2;
+  return (int64_t)(((uint64_t)hi << 32) | lo);
+}
+
 // Signed base-256 digit and remainder (intops.split_limbs, src/bitexact/intops.py:62-70).
 __device__ __forceinline__ int32_t limb_lo(int32_t r) { return ((r + 128) & 255) - 128; }
 __device__ __forceinline__ int64_t limb_lo64(int64_t r) { return ((r + 128) & 255) - 128; }

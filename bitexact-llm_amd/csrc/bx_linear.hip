@@ -1089,71 +1089,80 @@ __global__ __launch_bounds__(WM * WN * 64) void xtile_kernel(LinArgs p) {
     shlo = imin(s_mm[0], s_mm[2]);
     shhi = imax(s_mm[1], s_mm[3]);
   }
+  // full tiles (every row < M and column < N: all of lm_head's) skip the per-output bounds tests
+  const bool full = m0 + BM <= p.M && n0 + BN <= p.N;   // block-uniform
+  auto epi = [&](auto full_t) {
+    constexpr bool FULL = decltype(full_t)::value;
 #pragma unroll
-  for (int t = 0; t < TN; ++t) {
-    const int nl = (wn * TN + t) * 32 + (lane & 31), n = n0 + nl;
-    int64_t dn = 0, gdr = 0;
-    int cs0 = 0, cs1 = 0;
-    bool colok = false;
-    if (EX) {
-      dn = s_d[nl];
-      gdr = s_gdr[nl];
-      if (E > 0 && E <= kXtEmax) {
-        cs0 = s_cs[nl];
-        cs1 = s_cs[nl + 1];
-      }
-      colok = p.K <= 8192 && shhi + gdr + dn <= 0 && shhi + gdr <= -1 && shlo + gdr >= -62;
-    }
-#pragma unroll
-    for (int a2 = 0; a2 < TM; ++a2)
-#pragma unroll
-    for (int e0 = 0; e0 < 16; e0 += 4) {
-      int64_t B[4] = {0, 0, 0, 0};
-      int rl[4];
-#pragma unroll
-      for (int u = 0; u < 4; ++u) {
-        const int e = e0 + u;
-        rl[u] = (wm * TM + a2) * 32 + (e >> 2) * 8 + (lane >> 5) * 4 + (e & 3);
-      }
-      if (EX && E > kXtEmax && n < p.N) {   // long residual lists: read from global memory
-        const int c = kcnt(p, p.cnt[n], corrupt);
-        for (int j = 0; j < c; ++j) {
-          const int col = kcol(p, p.ecol[(int64_t)n * p.R + j], corrupt);
-          const int64_t v = p.eval[(int64_t)n * p.R + j];
-#pragma unroll
-          for (int u = 0; u < 4; ++u)
-            B[u] = add_wrap(B[u], mul_wrap((int64_t)p.q[(int64_t)min(m0 + rl[u], p.M - 1) * p.ldq + col], v));
+    for (int t = 0; t < TN; ++t) {
+      const int nl = (wn * TN + t) * 32 + (lane & 31), n = n0 + nl;
+      int64_t dn = 0, gdr = 0;
+      int cs0 = 0, cs1 = 0;
+      bool colok = false;
+      if (EX) {
+        dn = s_d[nl];
+        gdr = s_gdr[nl];
+        if (E > 0 && E <= kXtEmax) {
+          cs0 = s_cs[nl];
+          cs1 = s_cs[nl + 1];
         }
-      } else if (EX) {
-        for (int x = cs0; x < cs1; ++x) {
-          const int64_t v = s_ev[x];
-#pragma unroll
-          for (int u = 0; u < 4; ++u) B[u] = add_wrap(B[u], mul_wrap((int64_t)gq[x * 128 + rl[u]], v));
-        }
+        colok = p.K <= 8192 && shhi + gdr + dn <= 0 && shhi + gdr <= -1 && shlo + gdr >= -62;
       }
 #pragma unroll
-      for (int u = 0; u < 4; ++u) {
-        const int e = e0 + u, m = m0 + rl[u];
-        int64_t v = 0;
+      for (int a2 = 0; a2 < TM; ++a2)
 #pragma unroll
-        for (int s2 = 0; s2 < 5; ++s2) v += (int64_t)acc[s2][a2][t][e] << (8 * s2);
-        int64_t y = v;
-        if (EX) {
-          const int64_t k = -(s_sh[rl[u]] + gdr);
-          const bool fast = colok && (uint64_t)(B[u] + (1LL << 60)) < (uint64_t)(1LL << 61);
-          y = (v + ((B[u] + (1LL << (k - 1))) >> dn)) >> (k - dn);
-          if (__builtin_amdgcn_ballot_w64(!fast)) {   // rare: some lane needs the full rule
-            if (!fast) {
-              bool b;
-              y = exact_round(v, B[u], dn, -k, b);
-              bad |= b && m < p.M && n < p.N;
-            }
+      for (int e0 = 0; e0 < 16; e0 += 4) {
+        int64_t B[4] = {0, 0, 0, 0};
+        int rl[4];
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+          const int e = e0 + u;
+          rl[u] = (wm * TM + a2) * 32 + (e >> 2) * 8 + (lane >> 5) * 4 + (e & 3);
+        }
+        if (EX && E > kXtEmax && n < p.N) {   // long residual lists: read from global memory
+          const int c = kcnt(p, p.cnt[n], corrupt);
+          for (int j = 0; j < c; ++j) {
+            const int col = kcol(p, p.ecol[(int64_t)n * p.R + j], corrupt);
+            const int64_t v = p.eval[(int64_t)n * p.R + j];
+#pragma unroll
+            for (int u = 0; u < 4; ++u)
+              B[u] = add_wrap(B[u], mul_wrap((int64_t)p.q[(int64_t)min(m0 + rl[u], p.M - 1) * p.ldq + col], v));
+          }
+        } else if (EX) {
+          for (int x = cs0; x < cs1; ++x) {
+            const int64_t v = s_ev[x];
+#pragma unroll
+            for (int u = 0; u < 4; ++u) B[u] = add_wrap(B[u], mul_wrap((int64_t)gq[x * 128 + rl[u]], v));
           }
         }
-        if (m < p.M && n < p.N) ((int64_t*)p.out)[(int64_t)m * p.N + n] = y;
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+          const int e = e0 + u, m = m0 + rl[u];
+          const int64_t v = join5(acc[0][a2][t][e], acc[1][a2][t][e], acc[2][a2][t][e], acc[3][a2][t][e],
+                                  acc[4][a2][t][e]);
+          const bool inb = FULL || (m < p.M && n < p.N);
+          int64_t y = v;
+          if (EX) {
+            const int64_t k = -(s_sh[rl[u]] + gdr);
+            const bool fast = colok && (uint64_t)(B[u] + (1LL << 60)) < (uint64_t)(1LL << 61);
+            y = (v + ((B[u] + (1LL << (k - 1))) >> dn)) >> (k - dn);
+            if (__builtin_amdgcn_ballot_w64(!fast)) {   // rare: some lane needs the full rule
+              if (!fast) {
+                bool b;
+                y = exact_round(v, B[u], dn, -k, b);
+                bad |= b && inb;
+              }
+            }
+          }
+          if (inb) __builtin_nontemporal_store(y, (int64_t*)p.out + (int64_t)m * p.N + n);
+        }
       }
     }
-  }
+  };
+  if (full)
+    epi(std::true_type{});
+  else
+    epi(std::false_type{});
   if (EX) write_flag(p, bad, corrupt);
   BX_PHASE(0, 5);
 }
