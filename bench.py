@@ -275,7 +275,8 @@ def bench_phases(dev):
     """Phase timestamps of the main kernels (the measurement build, BX_PHASES=1): the exact prefill tile at
     lm_head / q-o / down shapes (M = 2048), the exact decode stream kernel at the engine's gate|up shape (M = 32
     with q's limb planes), the split decode attention at config 4, the one-block decode attention at the engine's
-    shape (batch 32, context 1024), and the add + norm at the engine's shape (32 rows of 2048). Each is launched a
+    shape (batch 32, context 1024), the add + norm at the engine's shape (32 rows of 2048), and the int8 decode
+    down GEMM at M = 64 and 8 (config 2, gemv kernel). Each is launched a
     few times over rotating copies of its weights / cache (>= 400 MB, beyond the 256 MB last-level cache, so the
     timed launch reads HBM); the table holds the last launch's first 1024 blocks."""
     import torch
@@ -351,6 +352,21 @@ def bench_phases(dev):
     for _ in range(3):
         ops.add_norm_y(y, x.clone(), gm, ge, flag=flag, planes=True)
     torch.cuda.synchronize()
+    # int8 decode down GEMMs (config 2: K = 8192, N = 2048) on the gemv kernel: 256 blocks (4 K splits)
+    from bitexact.int8.gemm_skinny import int_mm_join
+    gw = torch.Generator(device=dev).manual_seed(1)
+    wc = [torch.randint(-127, 128, (2048, 8192), dtype=torch.int8, device=dev, generator=gw) for _ in range(24)]
+    for M in (64, 8):
+        xm = torch.randn(M, 8192, generator=torch.Generator().manual_seed(M), dtype=torch.float64).to(dev)
+        am = stack2(quant_rows2(torch.floor(xm * 2.0 ** 16 + 0.5).long()))
+        for i in range(len(wc)):
+            int_mm_join(am, wc[i], M, 2)
+        torch.cuda.synchronize()
+        res[f"gemv int8 down {M}x2048x8192 (config 2)"] = _phase_summary(
+            _phase_table("linear")[2], 256, ["activations to LDS", "k loop", "k-slice reduce", "split-K adds",
+                                             "last split: sums + outputs"])
+    del wc
+    torch.cuda.empty_cache()
     res["add + norm (engine: 32 rows of 2048)"] = _phase_summary(_phase_table("rows")[0], 32,
                                                                 ["row loaded", "divisor", "quotients", "quantize"])
     return res

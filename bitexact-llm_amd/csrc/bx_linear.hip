@@ -399,6 +399,7 @@ __global__ __launch_bounds__(64 * CG * KS) void gemv_kernel(LinArgs p) {
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int cg = wave % CG, kslice = wave / CG;
   int tile, part;
+  BX_PHASE(2, 0);
   gemv_block(p, tile, part);
   const int n0 = tile * BNC;
   const int m0 = part * p.mp, Ml = min(p.mp, p.M - m0);
@@ -464,6 +465,7 @@ __global__ __launch_bounds__(64 * CG * KS) void gemv_kernel(LinArgs p) {
   a_finish<RA, MODE, NT>(p, ares, asl, av, As, (int8_t*)(Cs + NB * RA * BNC), kpad);
   for (int i = tid; i < NB * RA * BNC; i += NT) Cs[i] = 0;
   lds_barrier();
+  BX_PHASE(2, 1);
 
   // later groups: one more in flight while a group is consumed (block-uniform conditions: no load is issued
   // that reads nothing)
@@ -475,6 +477,7 @@ __global__ __launch_bounds__(64 * CG * KS) void gemv_kernel(LinArgs p) {
     if (gi + 1 < ngroups) compute(b1, sb);
   }
 
+  BX_PHASE(2, 2);
   // ---- reduce the k-slices in LDS: Cs[j][row][col] += acc (row = stacked limb row, col in [0, BNC)) ----
 #pragma unroll
   for (int r = 0; r < RB; ++r)
@@ -489,6 +492,7 @@ __global__ __launch_bounds__(64 * CG * KS) void gemv_kernel(LinArgs p) {
           atomicAdd(&Cs[(j * RA + row) * BNC + col], acc[r][j][e]);
       }
   __syncthreads();
+  BX_PHASE(2, 3);
 
   bool bad = false, corrupt = false;
   const int nsplit = gridDim.y;
@@ -513,6 +517,7 @@ __global__ __launch_bounds__(64 * CG * KS) void gemv_kernel(LinArgs p) {
     else
       finalize<MODE>(p, m0 + m, n, v, bad, corrupt);
   }
+  BX_PHASE(2, 4);
   if (nsplit > 1 && splitk_last(p, blockIdx.x, nsplit, &s_last)) {
     for (int e = tid; e < Ml * BNC; e += NT) {
       const int m = e / BNC, n = n0 + (e - m * BNC);
@@ -520,6 +525,7 @@ __global__ __launch_bounds__(64 * CG * KS) void gemv_kernel(LinArgs p) {
     }
   }
   if (MODE == EXACT) write_flag(p, bad, corrupt);
+  BX_PHASE(2, 5);
 }
 
 // =====================================================================================================
