@@ -1210,6 +1210,10 @@ __global__ __launch_bounds__(64 * NWV) void stream_kernel(LinArgs p) {
   // exact: the epilogue context of the thread's column (tid % C), requested before the ring
   ColPre cpre;
   if constexpr (MODE == EXACT) cpre = col_pre(p, n0 + tid % C);
+  // exact: the row shifts too (thread m holds sh[m] until the epilogue puts them in LDS)
+  static_assert(MODE != EXACT || RP <= NT, "one row shift per thread");
+  int64_t shpre = 0;
+  if constexpr (MODE == EXACT) shpre = p.sh[min(tid, p.M - 1)];
   int voff[LPW];
 #pragma unroll
   for (int i = 0; i < LPW; ++i) {
@@ -1357,6 +1361,9 @@ __global__ __launch_bounds__(64 * NWV) void stream_kernel(LinArgs p) {
         for (int e = 0; e < 4; ++e)
           Cs[(j * RP + r * 16 + (lane >> 4) * 4 + e) * CP + wave * 16 + (lane & 15)] = acc[r][j][e];
   }
+  __shared__ int64_t s_shm[MODE == EXACT ? RP : 1];
+  if constexpr (MODE == EXACT)
+    if (tid < RP) s_shm[tid] = shpre;
   __syncthreads();
   const int nla = MODE == JOIN ? p.nl : MODE == RAW32 ? 1 : 3;
   if constexpr (MODE == EXACT || MODE == WMM_T) {
@@ -1376,7 +1383,7 @@ __global__ __launch_bounds__(64 * NWV) void stream_kernel(LinArgs p) {
       for (int e = 0; e < 8; ++e) {
         const int m = m0 + e * RG;
         if (m < Mo && n < p.N) {
-          if constexpr (MODE == EXACT) finalize_col(p, cc, m, n, p.sh[m], v[e], B[e], bad, corrupt);
+          if constexpr (MODE == EXACT) finalize_col(p, cc, m, n, s_shm[m], v[e], B[e], bad, corrupt);
           else ((int64_t*)p.out)[(int64_t)m * p.N + n] = v[e];
         }
       }
