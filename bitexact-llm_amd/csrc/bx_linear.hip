@@ -1186,21 +1186,31 @@ __global__ __launch_bounds__(WM * WN * 64) void xtile_kernel(LinArgs p) {
 // =====================================================================================================
 constexpr int kStBK = 128, kStC = 64;
 
-template <int RBM, int NB, int S, int MODE, int NWV = 4>
+// The largest wave count <= nw that divides the ring's load instructions per stage.
+constexpr int st_issuers(int lt, int nw) { return lt % nw == 0 ? nw : st_issuers(lt, nw - 1); }
+
+// WR = 2 (exact mode): 8 waves as 4 column groups x 2 row groups (wave w: columns 16 (w % 4) .., row blocks
+// (w / 4) RBM / 2 ..), two waves per SIMD over the same ring; the ring's load instructions go to the first IW waves.
+template <int RBM, int NB, int S, int MODE, int NWV = 4, int WR = 1>
 __global__ __launch_bounds__(64 * NWV) void stream_kernel(LinArgs p) {
   BX_PHASE(1, 0);
-  constexpr int RP = RBM < 2 ? 32 : 16 * RBM, BK = kStBK, C = 16 * NWV, NT = 64 * NWV;   // loaded rows: x 32
+  constexpr int CG = NWV / WR, RH = RBM / WR;                     // column groups, row blocks per wave
+  constexpr int RP = RBM < 2 ? 32 : 16 * RBM, BK = kStBK, C = 16 * CG, NT = 64 * NWV;   // loaded rows: x 32
   constexpr int SA = RP * BK, STAGE = SA + NB * C * BK;
-  constexpr int LA = RP / 8, LT = LA + NB * C / 8, LPW = LT / NWV;   // 1 KiB load instructions per stage / wave
+  constexpr int LA = RP / 8, LT = LA + NB * C / 8;                // 1 KiB load instructions per stage
+  constexpr int IW = st_issuers(LT, NWV), LPW = LT / IW;          // issuing waves, instructions per issuing wave
+  static_assert(WR == 1 || (WR == 2 && RBM % 2 == 0 && NB == 3), "row groups: exact mode, even row blocks");
   // RS: at 128 rows and one weight plane a wave owns two 16-row blocks x every column of the tile, not 16 columns x
   // every row: a k chunk's LDS operand reads per block drop from 4 x (128 + 16) rows to 4 x (32 + 64)
-  constexpr bool RS = RBM == 2 * NWV && NB == 1 && MODE != EXACT && MODE != WMM_T;
+  constexpr bool RS = RBM == 2 * NWV && NB == 1 && MODE != EXACT && MODE != WMM_T && WR == 1;
   constexpr int CB = C / 16;
   static_assert(!RS || RBM == 2 * CB, "RS layout: as many accumulators as the row-block layout");
-  static_assert(LT % NWV == 0, "load instructions per stage must split over the waves");
+  static_assert(IW * LPW == LT, "load instructions per stage must split over the issuing waves");
   extern __shared__ __align__(16) char smem[];
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int cgw = wave % CG, rgw = wave / CG;                 // the wave's column group and row group
+  const bool issuer = wave < IW;
   const int n0 = blockIdx.x * C, kb = blockIdx.y * p.ks;
   const int nks = min(p.ks, p.K - kb) / BK;
   const int rows = p.rows_a;                                  // <= 16 RBM (rows past it repeat the last row)
@@ -1217,7 +1227,7 @@ __global__ __launch_bounds__(64 * NWV) void stream_kernel(LinArgs p) {
   int voff[LPW];
 #pragma unroll
   for (int i = 0; i < LPW; ++i) {
-    const int inst = wave * LPW + i;
+    const int inst = min(wave * LPW + i, LT - 1);
     const int r8 = inst < LA ? inst : (inst - LA) % (C / 8);      // 8-row group within the A or W plane tile
     const int row = r8 * 8 + (lane >> 3);
     const int lch = ((lane & 7) ^ ((row >> 1) & 7)) << 4;
@@ -1229,6 +1239,7 @@ __global__ __launch_bounds__(64 * NWV) void stream_kernel(LinArgs p) {
     }
   }
   auto issue = [&](int it, int stage) {
+    if (!issuer) return;                                      // wave-uniform
     char* sbase = smem + stage * STAGE;
 #pragma unroll
     for (int i = 0; i < LPW; ++i) {
@@ -1237,16 +1248,16 @@ __global__ __launch_bounds__(64 * NWV) void stream_kernel(LinArgs p) {
     }
   };
 
-  v4i acc[RBM][NB];
+  v4i acc[RH][NB];
 #pragma unroll
-  for (int r = 0; r < RBM; ++r)
+  for (int r = 0; r < RH; ++r)
 #pragma unroll
     for (int j = 0; j < NB; ++j) acc[r][j] = v4i{0, 0, 0, 0};
 
 #pragma unroll
   for (int t = 0; t < S - 1; ++t)
     if (t < nks) issue(t, t);
-  const int r16 = lane & 15, wrow = wave * 16 + r16;
+  const int r16 = lane & 15, wrow = cgw * 16 + r16;
   for (int it = 0; it < nks; ++it) {
     // stage it landed (later ones may be in flight) and every wave is done with stage it - 1
     if (it + S - 2 < nks)
@@ -1283,14 +1294,14 @@ __global__ __launch_bounds__(64 * NWV) void stream_kernel(LinArgs p) {
 #pragma unroll
       for (int j = 0; j < NB; ++j)
         b[j] = *(const v4i*)(base + SA + (j * C + wrow) * BK + ((c ^ ((wrow >> 1) & 7)) << 4));
-      v4i a[RBM];
+      v4i a[RH];
 #pragma unroll
-      for (int r = 0; r < RBM; ++r) {
-        const int arow = r * 16 + r16;
+      for (int r = 0; r < RH; ++r) {
+        const int arow = (rgw * RH + r) * 16 + r16;
         a[r] = *(const v4i*)(base + arow * BK + ((c ^ ((arow >> 1) & 7)) << 4));
       }
 #pragma unroll
-      for (int r = 0; r < RBM; ++r)
+      for (int r = 0; r < RH; ++r)
 #pragma unroll
         for (int j = 0; j < NB; ++j) acc[r][j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a[r], b[j], acc[r][j], 0, 0, 0);
     }
@@ -1354,12 +1365,12 @@ __global__ __launch_bounds__(64 * NWV) void stream_kernel(LinArgs p) {
           Cs[((wave + NWV * q) * 16 + (lane >> 4) * 4 + e) * CP + cb * 16 + (lane & 15)] = acc[q * CB + cb][0][e];
   } else {
 #pragma unroll
-    for (int r = 0; r < RBM; ++r)
+    for (int r = 0; r < RH; ++r)
 #pragma unroll
       for (int j = 0; j < NB; ++j)
 #pragma unroll
         for (int e = 0; e < 4; ++e)
-          Cs[(j * RP + r * 16 + (lane >> 4) * 4 + e) * CP + wave * 16 + (lane & 15)] = acc[r][j][e];
+          Cs[(j * RP + (rgw * RH + r) * 16 + (lane >> 4) * 4 + e) * CP + cgw * 16 + (lane & 15)] = acc[r][j][e];
   }
   __shared__ int64_t s_shm[MODE == EXACT ? RP : 1];
   if constexpr (MODE == EXACT)
@@ -2050,12 +2061,12 @@ static int launch_staged(LinArgs& p, const Plan& s, hipStream_t st) {
   }
 }
 
-template <int RBM, int NB, int S, int MODE, int NWV = 4>
+template <int RBM, int NB, int S, int MODE, int NWV = 4, int WR = 1>
 static int launch_stream_cfg(LinArgs& p, const Plan& s, hipStream_t st) {
-  constexpr int RP = RBM < 2 ? 32 : 16 * RBM;
-  const size_t lds = std::max((size_t)S * kStBK * (RP + NB * 16 * NWV), (size_t)NB * RP * (16 * NWV + 1) * 4);
-  allow_lds(stream_kernel<RBM, NB, S, MODE, NWV>, lds);
-  stream_kernel<RBM, NB, S, MODE, NWV><<<dim3(s.tiles_x, s.split), 64 * NWV, lds, st>>>(p);
+  constexpr int RP = RBM < 2 ? 32 : 16 * RBM, C = 16 * NWV / WR;
+  const size_t lds = std::max((size_t)S * kStBK * (RP + NB * C), (size_t)NB * RP * (C + 1) * 4);
+  allow_lds(stream_kernel<RBM, NB, S, MODE, NWV, WR>, lds);
+  stream_kernel<RBM, NB, S, MODE, NWV, WR><<<dim3(s.tiles_x, s.split), 64 * NWV, lds, st>>>(p);
   return check_launch("stream_kernel");
 }
 
@@ -2070,10 +2081,17 @@ static int launch_stream(LinArgs& p, const Plan& s, hipStream_t st) {
   if constexpr (EX) {   // three weight planes: 4-stage rings (3 at 128 rows) within the 160 KiB of LDS
     if (s.stream == 1) return launch_stream_cfg<1, 3, 4, MODE>(p, s, st);
     if (s.stream == 2) return launch_stream_cfg<2, 3, 4, MODE>(p, s, st);
-    if (s.stream == 4) return launch_stream_cfg<4, 3, 4, MODE>(p, s, st);
+    // from 49 rows, grids of at most two rounds of blocks: 8 waves in two row groups (two waves per SIMD; measured
+    // per launch at N = 16384, K = 2048: M = 20 24.5 vs 25.4 us, M = 40 26.7 vs 29.0, M = 32 equal; lm_head's 2004
+    // blocks were 1.5 % slower, so long grids keep 4 waves over every row; BX_ST_WR=1 turns the form off)
+    static const int wr = getenv("BX_ST_WR") ? atoi(getenv("BX_ST_WR")) : 2;
+    const bool two = wr == 2 && (int64_t)s.tiles_x * s.split <= 2 * device_cus();
+    if (s.stream == 4) return two ? launch_stream_cfg<4, 3, 4, MODE, 8, 2>(p, s, st)
+                                  : launch_stream_cfg<4, 3, 4, MODE>(p, s, st);
     if (s.nwv == 2) return launch_stream_cfg<6, 3, 4, MODE, 2>(p, s, st);   // 65..96 rows (planner)
-    if (s.stream == 6) return launch_stream_cfg<6, 3, 4, MODE>(p, s, st);
-    return launch_stream_cfg<8, 3, 3, MODE>(p, s, st);
+    if (s.stream == 6) return two ? launch_stream_cfg<6, 3, 4, MODE, 8, 2>(p, s, st)
+                                  : launch_stream_cfg<6, 3, 4, MODE>(p, s, st);
+    return two ? launch_stream_cfg<8, 3, 3, MODE, 8, 2>(p, s, st) : launch_stream_cfg<8, 3, 3, MODE>(p, s, st);
   }
   // ring depth: 4 stages at 16 rows (8 measured ~0.5 us slower per launch at M = 1), 8 at 32 / 64, 6 at 128
   if (s.stream == 1) return launch_stream_cfg<1, 1, 4, MODE>(p, s, st);
