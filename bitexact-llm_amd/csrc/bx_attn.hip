@@ -1610,6 +1610,14 @@ __global__ __launch_bounds__(256) void pre_split_kernel(AttnArgs p, int8_t* kp, 
 // PV A operand as they stand (16 queries x 64 keys in Vp's order), and B = V limb plane j (64 keys x 16 dims):
 // five int32 sets per 16-dim block (exact while S 3 2^14 < 2^31), joined in int64 at the end. The table loads of
 // a tile's 16 weights go out together, before the tile's next ring stage is requested.
+// Byte k of each of four words, in order, as one word (two v_perm_b32 and an or).
+template <int k>
+__device__ __forceinline__ uint32_t gather_bytes(const uint32_t (&a)[4]) {
+  const uint32_t lo = __builtin_amdgcn_perm(a[1], a[0], 0x0c0c0400u + k * 0x101u);        // a0.k, a1.k, 0, 0
+  const uint32_t hi = __builtin_amdgcn_perm(a[3], a[2], 0x04000c0cu + k * 0x01010000u);    // 0, 0, a2.k, a3.k
+  return lo | hi;
+}
+
 template <int HD>
 struct Pre2 {
   static constexpr int KK = HD / 64, CR = HD / 16, DB = HD / 16;
@@ -1754,6 +1762,7 @@ __global__ __launch_bounds__(64 * Pre2<HD>::NW, 1) void attn_pre2_kernel(AttnArg
   // can wrap: weight_at_nn)
   const bool fast = tab2 != nullptr && __builtin_amdgcn_ballot_w64(shift < 0) == 0 && p.l2e >= 0 &&
                     p.l2e < (1LL << 31);
+  const auto rtab = buf_rsrc(tab2 != nullptr ? (const void*)tab2 : (const void*)p.lut);   // (entry, next - entry)
   int64_t den = 0;
   v4i pacc[DB][5];
 #pragma unroll
@@ -1786,8 +1795,10 @@ __global__ __launch_bounds__(64 * Pre2<HD>::NW, 1) void attn_pre2_kernel(AttnArg
           uint64_t zf = (uint64_t)((cz - raw[kb][e]) >> s62);
           zf = zf < (48ULL << kFZ) ? zf : (48ULL << kFZ);     // hidden keys (negative) clamp too: inside the table
           const uint64_t prod = (uint64_t)(uint32_t)zf * (uint64_t)(uint32_t)p.l2e + (1ULL << 27);
-          n[kb][e] = (int)(prod >> (28 + kFT2));
-          const uint32_t f = (uint32_t)(prod >> 28) & ((1u << kFT2) - 1);
+          // n = prod >> 54 and f = (prod >> 28) mod 2^26 from the product's two words
+          const uint32_t ph = (uint32_t)(prod >> 32), pl = (uint32_t)prod;
+          n[kb][e] = (int)(ph >> (28 + kFT2 - 32));
+          const uint32_t f = __builtin_amdgcn_alignbit(ph, pl, 28) & ((1u << kFT2) - 1);
           idx[kb][e] = n[kb][e] < kZeroN ? (int)(f >> (kFT2 - kExp2Bits)) : 0;
           rr[kb][e] = (int)(f & ((1u << (kFT2 - kExp2Bits)) - 1));
         }
@@ -1795,7 +1806,7 @@ __global__ __launch_bounds__(64 * Pre2<HD>::NW, 1) void attn_pre2_kernel(AttnArg
 #pragma unroll
       for (int kb = 0; kb < 4; ++kb)
 #pragma unroll
-        for (int e = 0; e < 4; ++e) tv[kb][e] = *(const v4i*)(tab2 + idx[kb][e] * 16);
+        for (int e = 0; e < 4; ++e) tv[kb][e] = buf_load16(rtab, idx[kb][e] * 16);
       if (t + NS - 1 < ntile) issue2(t + NS - 1);    // after the table loads: waiting for them leaves it in flight
 #pragma unroll
       for (int kb = 0; kb < 4; ++kb)
@@ -1835,20 +1846,20 @@ __global__ __launch_bounds__(64 * Pre2<HD>::NW, 1) void attn_pre2_kernel(AttnArg
     int32_t dt = 0;                                   // the tile's weight sum: <= 64 2^22, exact in int32
 #pragma unroll
     for (int kb = 0; kb < 4; ++kb) {
-      uint32_t wd[3] = {0, 0, 0};
+      // 0 <= x <= 2^22: signed base-256 limbs; limb_lo(x) as a byte is x & 255, the next digit is
+      // (x + 128) >> 8 and the one after it (x + 128 + 2^15) >> 16 (nested floors), so limb i's byte is byte i of
+      // x, x + 128 and x + 32896; four keys' bytes go into one word with two byte permutes and an or
+      uint32_t v0[4], v1[4], v2[4];
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
-        // 0 <= p <= 2^22: signed base-256 limbs; limb_lo(x) as a byte is x & 255 and (x - limb_lo(x)) >> 8 is
-        // (x + 128) >> 8
-        const int32_t x0 = x[kb][e];
-        dt += x0;
-        const int32_t x1 = (x0 + 128) >> 8, x2 = (x1 + 128) >> 8;
-        wd[0] |= (uint32_t)(x0 & 255) << (8 * e);
-        wd[1] |= (uint32_t)(x1 & 255) << (8 * e);
-        wd[2] |= (uint32_t)(x2 & 255) << (8 * e);
+        dt += x[kb][e];
+        v0[e] = (uint32_t)x[kb][e];
+        v1[e] = v0[e] + 128u;
+        v2[e] = v0[e] + 32896u;
       }
-#pragma unroll
-      for (int i = 0; i < 3; ++i) pa[i][kb] = (int)wd[i];
+      pa[0][kb] = (int)gather_bytes<0>(v0);
+      pa[1][kb] = (int)gather_bytes<1>(v1);
+      pa[2][kb] = (int)gather_bytes<2>(v2);
     }
     den += dt;
 #pragma unroll
