@@ -1782,14 +1782,19 @@ __global__ __launch_bounds__(64 * Pre2<HD>::NW, 1) void attn_pre2_kernel(AttnArg
     const int8_t* kbase = (const int8_t*)smem + (t % NS) * C::STAGE;
     const int8_t* vbs = kbase + C::PB;
     int64_t raw[4][4];
-#pragma unroll
-    for (int kb = 0; kb < 4; ++kb) qk(kbase, kb, raw[kb]);
-    // every score's table position, then every table load, then the next stage's request
     int32_t x[4][4];
     if constexpr (kFast) {
+      // two halves of the tile: the first half's scores, table positions and table loads, then the second half's,
+      // so the second half's MFMAs and integer work run while the first half's table rows are in flight; then the
+      // next stage's request
       int idx[4][4], n[4][4], rr[4][4];
+      v4i tv[4][4];
 #pragma unroll
-      for (int kb = 0; kb < 4; ++kb)
+      for (int hf = 0; hf < 2; ++hf) {
+#pragma unroll
+      for (int kb = 2 * hf; kb < 2 * hf + 2; ++kb) qk(kbase, kb, raw[kb]);
+#pragma unroll
+      for (int kb = 2 * hf; kb < 2 * hf + 2; ++kb)
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
           uint64_t zf = (uint64_t)((cz - raw[kb][e]) >> s62);
@@ -1802,11 +1807,12 @@ __global__ __launch_bounds__(64 * Pre2<HD>::NW, 1) void attn_pre2_kernel(AttnArg
           idx[kb][e] = n[kb][e] < kZeroN ? (int)(f >> (kFT2 - kExp2Bits)) : 0;
           rr[kb][e] = (int)(f & ((1u << (kFT2 - kExp2Bits)) - 1));
         }
-      v4i tv[4][4];
 #pragma unroll
-      for (int kb = 0; kb < 4; ++kb)
+      for (int kb = 2 * hf; kb < 2 * hf + 2; ++kb)
 #pragma unroll
         for (int e = 0; e < 4; ++e) tv[kb][e] = buf_load16(rtab, idx[kb][e] * 16);
+      __builtin_amdgcn_sched_barrier(0);
+      }
       if (t + NS - 1 < ntile) issue2(t + NS - 1);    // after the table loads: waiting for them leaves it in flight
 #pragma unroll
       for (int kb = 0; kb < 4; ++kb)
@@ -1822,6 +1828,8 @@ __global__ __launch_bounds__(64 * Pre2<HD>::NW, 1) void attn_pre2_kernel(AttnArg
           x[kb][e] = w;
         }
     } else {
+#pragma unroll
+      for (int kb = 0; kb < 4; ++kb) qk(kbase, kb, raw[kb]);
       WeightAt wa[4][4];
       int64_t ta[4][4], tb[4][4];
 #pragma unroll
