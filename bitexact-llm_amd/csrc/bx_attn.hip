@@ -990,6 +990,23 @@ __global__ __launch_bounds__(kDecWaves * 64) void attn_dec_raw_kernel(AttnArgs p
   // the block-table row (every entry the launch may reach: p.S / bs + 1), independent of the positions
   const int npg = p.S / p.bs + 1 < p.nblk ? p.S / p.bs + 1 : p.nblk;
   for (int i = threadIdx.x; i < npg; i += kDecWaves * 64) spg[i] = p.bt[brow * p.sbt + i];
+  // RP: the wave's first DR key blocks that lie wholly below the token's position (no prologue store touches
+  // them) are requested before the prologue, straight from the block table; the sweep loads the rest
+  v4i kr[DR][3][KK];
+  int npre = 0;                                             // wave-uniform: kr[0 .. npre) already requested
+  if constexpr (RP) {
+    const int64_t pos0 = r.pos[(int64_t)(group / p.hkv) * r.spb];
+    const int64_t pe = pos0 < p.S ? pos0 : p.S - 1;        // the last visible key
+#pragma unroll
+    for (int d = 0; d < DR; ++d) {
+      const int i = w + d * kDecWaves;
+      if (npre == d && pos0 >= 0 && (int64_t)(i + 1) * 16 <= pe) {   // wave-uniform
+        const int s = i * 16 + kl;
+        dec_planes<HD>(p, p.bt[brow * p.sbt + s / p.bs], h, s, 0, kr[d]);
+        npre = d + 1;
+      }
+    }
+  }
   int64_t qp[4];
   if constexpr (RP) {
     // token group / hkv, KV head h, its nq q heads h nq ..; one position for the group (the token's)
@@ -1045,10 +1062,9 @@ __global__ __launch_bounds__(kDecWaves * 64) void attn_dec_raw_kernel(AttnArgs p
 
   // ---- sweep 1: K, scores into LDS, maxima ----
   {
-    v4i kr[DR][3][KK];
 #pragma unroll
     for (int d = 0; d < DR; ++d)
-      if (w + d * kDecWaves < nb16) rows(w + d * kDecWaves, 0, kr[d]);
+      if (d >= npre && w + d * kDecWaves < nb16) rows(w + d * kDecWaves, 0, kr[d]);
     int64_t best = kNeg;
     for (int b0 = w; b0 < nb16; b0 += DR * kDecWaves) {
 #pragma unroll
