@@ -107,6 +107,22 @@ __device__ __forceinline__ void finalize(const LinArgs& p, int m, int n, int64_t
   }
 }
 
+// finalize<EXACT> with the row shift and the column's d, g and residual count already read (shm, dn, g, cnt_raw).
+__device__ __forceinline__ void finalize_pre(const LinArgs& p, int m, int n, int64_t v, int64_t shm, int64_t dn,
+                                             int64_t g, int32_t cnt_raw, bool& bad, bool& corrupt) {
+  int64_t B = 0;
+  if (p.R > 0) {
+    const int c = kcnt(p, cnt_raw, corrupt);
+    const int32_t* qr = p.q + (int64_t)m * p.ldq;
+    const int32_t* ec = p.ecol + (int64_t)n * p.R;
+    const int64_t* ev = p.eval + (int64_t)n * p.R;
+    for (int j = 0; j < c; ++j) B = add_wrap(B, mul_wrap((int64_t)qr[kcol(p, ec[j], corrupt)], ev[j]));
+  }
+  bool b;
+  ((int64_t*)p.out)[(int64_t)m * p.N + n] = exact_round_fast(v, B, dn, shm + g - dn + p.FR, b);
+  bad |= b;
+}
+
 // Per-column epilogue context, loaded once per thread when a thread keeps one output column: d, g, and the
 // first kRes residual entries of the column in registers (more entries, rare, are read from memory).
 constexpr int kRes = 4;
@@ -451,6 +467,22 @@ __global__ __launch_bounds__(64 * CG * KS) void gemv_kernel(LinArgs p) {
 
   // activations first, then the weights (the first group, and the second when there is one); the activation
   // rows are written to LDS while the weights are in flight
+  // exact: the epilogue context, requested before everything else and kept in LDS (threads < BNC: column d, g and
+  // residual count; the next Ml threads, when the block has them: the row shifts)
+  __shared__ int64_t s_cd[MODE == EXACT ? BNC : 1], s_cg[MODE == EXACT ? BNC : 1], s_csh[MODE == EXACT ? 64 : 1];
+  __shared__ int32_t s_cc[MODE == EXACT ? BNC : 1];
+  int64_t gx0 = 0, gx1 = 0;
+  int32_t gcnt = 0;
+  if constexpr (MODE == EXACT) {
+    if (tid < BNC) {
+      const int nn = min(n0 + tid, p.N - 1);
+      gx0 = p.d[nn];
+      gx1 = p.g[nn];
+      gcnt = p.R > 0 ? p.cnt[nn] : 0;
+    } else if (BNC + Ml <= NT && tid < BNC + Ml) {
+      gx0 = p.sh[m0 + tid - BNC];
+    }
+  }
   const ASlice asl = a_slice<MODE>(p, m0, Ml, k0, kend, kpad, LDA);
   const __amdgpu_buffer_rsrc_t ares = buf_rsrc(MODE == EXACT || MODE == WMM_T ? (const void*)p.q : (const void*)p.a);
   v4i av[kAB];
@@ -464,6 +496,17 @@ __global__ __launch_bounds__(64 * CG * KS) void gemv_kernel(LinArgs p) {
   for (int i = 0; i < kAB; ++i) asm volatile("" : "+v"(av[i]));
   a_finish<RA, MODE, NT>(p, ares, asl, av, As, (int8_t*)(Cs + NB * RA * BNC), kpad);
   for (int i = tid; i < NB * RA * BNC; i += NT) Cs[i] = 0;
+  if constexpr (MODE == EXACT) {
+    if (tid < BNC) {
+      s_cd[tid] = gx0;
+      s_cg[tid] = gx1;
+      s_cc[tid] = gcnt;
+    } else if (BNC + Ml <= NT && tid < BNC + Ml) {
+      s_csh[tid - BNC] = gx0;
+    }
+    if (BNC + Ml > NT)                                      // block-uniform: too few threads to hold them all
+      for (int r = tid; r < Ml; r += NT) s_csh[r] = p.sh[m0 + r];
+  }
   lds_barrier();
   BX_PHASE(2, 1);
 
@@ -514,14 +557,20 @@ __global__ __launch_bounds__(64 * CG * KS) void gemv_kernel(LinArgs p) {
     }
     if (nsplit > 1)
       ws_add(p, m0 + m, n, v);
+    else if constexpr (MODE == EXACT)
+      finalize_pre(p, m0 + m, n, v, s_csh[m], s_cd[c], s_cg[c], s_cc[c], bad, corrupt);
     else
       finalize<MODE>(p, m0 + m, n, v, bad, corrupt);
   }
   BX_PHASE(2, 4);
   if (nsplit > 1 && splitk_last(p, blockIdx.x, nsplit, &s_last)) {
     for (int e = tid; e < Ml * BNC; e += NT) {
-      const int m = e / BNC, n = n0 + (e - m * BNC);
-      if (n < p.N) finalize<MODE>(p, m0 + m, n, ws_take(p, m0 + m, n), bad, corrupt);
+      const int m = e / BNC, c = e - m * BNC, n = n0 + c;
+      if (n >= p.N) continue;
+      if constexpr (MODE == EXACT)
+        finalize_pre(p, m0 + m, n, ws_take(p, m0 + m, n), s_csh[m], s_cd[c], s_cg[c], s_cc[c], bad, corrupt);
+      else
+        finalize<MODE>(p, m0 + m, n, ws_take(p, m0 + m, n), bad, corrupt);
     }
   }
   if (MODE == EXACT) write_flag(p, bad, corrupt);
