@@ -1853,11 +1853,12 @@ static bool stream_plan(int rows_a, int M_out, int N, int K, bool exact, bool pl
     const int nch = K / kStBK;
     const int want = std::min(nch, (cus + s.tiles_x - 1) / s.tiles_x);
     const int per = (nch + want - 1) / want;
-    if (per < 8) {
-      // under 1024 k per block the split's fixed costs lose to the gemv, unless the caller brings q's limb
-      // planes (no split launch) and 65..96 limb rows: then 32-column blocks, >= 1024 k each, in one round of
-      // blocks that covers at least 3/4 of the chip (M = 32, N = 3072, K = 2048: 14.1 vs 18.8 us for the gemv;
-      // N = 2048 stays on the gemv: 12.8 us with 256 blocks of 512 k, 14.1 with 128 blocks, vs 11.9)
+    if (per < 8 || (planes && rows_a > 64 && rows_a <= 96)) {
+      // with q's limb planes from the caller (no split launch) and 65..96 limb rows: 32-column blocks, >= 1024 k
+      // each, in one round of blocks that covers at least 3/4 of the chip (M = 32, N = 3072, K = 2048: 14.1 vs
+      // 18.8 us for the gemv; N = 2048, K = 8192: 4 splits of 2048 k, 21.3 vs 22.1 us for 64-column blocks in 8
+      // splits; N = 2048, K = 2048 stays on the gemv: 12.8 us with 256 blocks of 512 k, 14.1 with 128 blocks, vs
+      // 11.9). Otherwise, under 1024 k per block the split's fixed costs lose to the gemv.
       if (!planes || rows_a <= 64 || rows_a > 96) return false;
       s.nwv = 2;
       s.tiles_x = (N + 31) / 32;

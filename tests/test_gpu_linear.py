@@ -380,25 +380,34 @@ def test_norm_quant_planes(dev):
         r = (r - lo) >> 8
 
 
-@pytest.mark.parametrize("M,N", [(32, 3072), (22, 3080), (32, 4096)])
-def test_exact_linear_narrow_planes(dev, M, N):
-    """Narrow N at K = 2048 with q's limb planes given: 32-column stream blocks with the K split over the zeroed
-    workspace (without planes the gemv serves the shape); same y and flag as the gemv, and y matches the oracle
-    (partial last column tile at N = 3080, forced residual entries, 66 and 96 limb rows). N = 2048 keeps the gemv
-    either way."""
+@pytest.mark.parametrize("M,N,K", [(32, 3072, 2048), (22, 3080, 2048), (32, 4096, 2048), (32, 2048, 8192)])
+def test_exact_linear_narrow_planes(dev, M, N, K):
+    """Narrow N with q's limb planes given: 32-column stream blocks with the K split over the zeroed workspace
+    (without planes the gemv, or at K = 8192 64-column blocks in 8 splits, serve the shape); same y and flag as
+    that path, and y matches the oracle (partial last column tile at N = 3080, forced residual entries, 66 and 96 limb rows; the
+    engine's down projection at N = 2048, K = 8192). N = 2048 at K = 2048 keeps the gemv either way."""
     from bitexact.exact import ops
     from bitexact.vllm_plugin.exact_gemm import exact_linear, needs_planes, plan
-    K = 2048
-    assert plan(32, 2048, K, planes=True)[0] == "gemv" and not needs_planes(32, 2048, K)
-    assert plan(M, N, K)[0] == "gemv"
+    assert plan(32, 2048, 2048, planes=True)[0] == "gemv" and not needs_planes(32, 2048, 2048)
+    assert plan(M, N, K)[0] == ("gemv" if K == 2048 else "stream")   # K = 8192: 64-column blocks, 8 splits
     kern, _, split, blocks = plan(M, N, K, planes=True)
     assert kern == "stream" and split > 1 and blocks == -(-N // 32), plan(M, N, K, planes=True)
     assert needs_planes(M, N, K)
     g = torch.Generator().manual_seed(M * N)
-    x = torch.randint(-(1 << 33), 1 << 33, (M, K), generator=g)
-    y = torch.randint(-(1 << 32), 1 << 32, (M, K), generator=g)
-    gm, ge = torch.randint(-255, 256, (K,), generator=g), torch.randint(-14, -6, (K,), generator=g)
-    _, (q, pl), sh, _ = ops.add_norm_y(y.to(dev), x.to(dev), gm.to(dev), ge.to(dev), planes=True)
+    if K <= 4096:                                     # the norm's row limit
+        x = torch.randint(-(1 << 33), 1 << 33, (M, K), generator=g)
+        y = torch.randint(-(1 << 32), 1 << 32, (M, K), generator=g)
+        gm, ge = torch.randint(-255, 256, (K,), generator=g), torch.randint(-14, -6, (K,), generator=g)
+        _, (q, pl), sh, _ = ops.add_norm_y(y.to(dev), x.to(dev), gm.to(dev), ge.to(dev), planes=True)
+    else:                                             # quantized rows as the SiLU stage leaves them, planes by hand
+        q = torch.randint(-(1 << 23) + 1, 1 << 23, (M, K), generator=g, dtype=torch.int32).to(dev)
+        sh = torch.randint(-40, -20, (M,), generator=g).to(dev)
+        pl = torch.empty(3, M, K, dtype=torch.int8, device=dev)
+        r = q.long()
+        for i in range(3):
+            lo = ((r + 128) & 255) - 128
+            pl[i] = lo.to(torch.int8)
+            r = (r - lo) >> 8
     dec = _dec(_bf16(N, K, 11))
     limbs = torch.from_numpy(dec["limbs"]).to(dev)
     d, gg = torch.from_numpy(dec["d"]).to(dev), torch.from_numpy(dec["g"]).to(dev)
