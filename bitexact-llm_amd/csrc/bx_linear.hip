@@ -2138,7 +2138,10 @@ static int launch_stream(LinArgs& p, const Plan& s, hipStream_t st) {
     const bool two = wr == 2 && (int64_t)s.tiles_x * s.split <= 2 * device_cus();
     if (s.stream == 4) return two ? launch_stream_cfg<4, 3, 4, MODE, 8, 2>(p, s, st)
                                   : launch_stream_cfg<4, 3, 4, MODE>(p, s, st);
-    if (s.nwv == 2) return launch_stream_cfg<6, 3, 4, MODE, 2>(p, s, st);   // 65..96 rows (planner)
+    // 32-column blocks at 65..96 rows (planner): 4 waves as 2 column groups x 2 row groups, so every SIMD has one
+    // (wqkv N = 3072: 12.2 vs 14.0 us with 2 waves over every row; down N = 2048, K = 8192: 19.4 vs 21.1)
+    if (s.nwv == 2) return wr == 2 ? launch_stream_cfg<6, 3, 4, MODE, 4, 2>(p, s, st)
+                                   : launch_stream_cfg<6, 3, 4, MODE, 2>(p, s, st);
     if (s.stream == 6) return two ? launch_stream_cfg<6, 3, 4, MODE, 8, 2>(p, s, st)
                                   : launch_stream_cfg<6, 3, 4, MODE>(p, s, st);
     return two ? launch_stream_cfg<8, 3, 3, MODE, 8, 2>(p, s, st) : launch_stream_cfg<8, 3, 3, MODE>(p, s, st);
