@@ -1229,9 +1229,10 @@ __global__ __launch_bounds__(WM * WN * 64) void xtile_kernel(LinArgs p) {
 // multiple of 32) go through an S-stage ring filled by buffer_load_dwordx4 ... lds (1 KiB = 8 rows x 128 bytes per
 // instruction; 16-byte chunks XOR-swizzled by (row / 2) % 8 so the 16 rows an MFMA operand read touches fall in 16
 // distinct bank groups), S - 1 stages ahead of the MFMAs. Each of the 4 waves owns 16 columns:
-// v_mfma_i32_16x16x64_i8 over the valid 16-row activation blocks and the NB weight planes. The int32 limb
+// v_mfma_i32_16x16x64_i8 over the valid 16-row activation blocks and the NB weight planes (exact mode may run 8
+// waves as 4 column groups x 2 row groups, WR = 2; int8 at 128 rows splits the rows instead, RS). The int32 limb
 // products meet in LDS (or, for the join of whole 16-row limb blocks, in registers) and are joined per output in
-// int64. One block walks the whole K range (the plan takes the kernel only where N / 64 tiles cover the chip).
+// int64. A block walks its K range (the whole K unless the plan splits it over the zeroed workspace).
 // =====================================================================================================
 constexpr int kStBK = 128, kStC = 64;
 
