@@ -52,6 +52,9 @@ SIGNATURES = {
     "bx_exact_attn_paged_rope_out": (ctypes.c_int, [P, I64, P, I64, P, P, I32, I32, I32, I32, I32, I32, I32, P, P, I64,
                                                     I64, I64, I32, P, I64, I32, P, P, I64, P, I64, P, I32, I32, I32,
                                                     P, P, I64, P, I64, P]),
+    "bx_exact_attn_paged_rope_out_planes": (ctypes.c_int, [P, I64, P, I64, P, P, I32, I32, I32, I32, I32, I32, I32, P,
+                                                           P, I64, I64, I64, I32, P, I64, I32, P, P, I64, P, I64, P,
+                                                           P, I32, I32, I32, P, P, I64, P, I64, P]),
     "bx_attn_paged_workspace": (I64, [I32, I32, I32, I32]),
     "bx_exact_attn_prefill": (ctypes.c_int, [P, I64, I64, P, I64, P, I64, I64, P, I64, I64, P, I64, I64, I32, P, I64,
                                              P, P, I32, I32, I32, P, I64, P]),

@@ -87,9 +87,15 @@ class ExactEngine:
                 tri_exact_attn.rope_fusable(N, HKV, self.H, bt.shape[1], kvs[0].shape[2]))
         for i in range(self.L):
             y = self.fused[i, "wqkv"](q, sh, fl, False, q_planes=pl)
+            plo = None                        # the wo linear's limb planes, when the output stage writes them
             if fuse:   # RoPE + KV store + attention + the attention output stage in one launch
-                qo, sho = tri_exact_attn.rope_attend_out(y, pos, self.cos, self.sin, (self.H, HKV, HD), kvs[i], slot,
-                                                         bt, rmap, self.exp2, self.l2e, fl)
+                if self.fused[i, "wo"].needs_planes(N):
+                    qo, sho, plo = tri_exact_attn.rope_attend_out(y, pos, self.cos, self.sin, (self.H, HKV, HD),
+                                                                  kvs[i], slot, bt, rmap, self.exp2, self.l2e, fl,
+                                                                  planes=True)
+                else:
+                    qo, sho = tri_exact_attn.rope_attend_out(y, pos, self.cos, self.sin, (self.H, HKV, HD), kvs[i],
+                                                             slot, bt, rmap, self.exp2, self.l2e, fl)
             elif kvs is None:
                 ops.qkv_y(y, pos.view(N, 1), self.cos, self.sin, N, 1, (self.H, HKV, HD), flag=fl)
                 num = torch.zeros(N, HKV, G, HD, dtype=torch.long, device=y.device)
@@ -103,11 +109,12 @@ class ExactEngine:
                 qo, sho = ops.attn_out(num.view(N * HKV, G, HD), den.view(N * HKV, G, 1), 1, HKV)
             wgu = self.fused[i, "wgu"]
             if wgu.needs_planes(N):   # the norm kernel also writes q's limb planes for the MFMA path
-                x, (q, pl), sh, _ = ops.add_norm_y(self.fused[i, "wo"](qo, sho, fl, True), x, *self.gm[i], flag=fl,
-                                                   planes=True)
+                x, (q, pl), sh, _ = ops.add_norm_y(self.fused[i, "wo"](qo, sho, fl, True, q_planes=plo), x,
+                                                   *self.gm[i], flag=fl, planes=True)
                 y = wgu(q, sh, fl, False, q_planes=pl)
             else:
-                x, q, sh, _ = ops.add_norm_y(self.fused[i, "wo"](qo, sho, fl, True), x, *self.gm[i], flag=fl)
+                x, q, sh, _ = ops.add_norm_y(self.fused[i, "wo"](qo, sho, fl, True, q_planes=plo), x, *self.gm[i],
+                                             flag=fl)
                 y = wgu(q, sh, fl, False)
             wd = self.fused[i, "wd"]
             # the column-chunked SiLU stage also writes q's limb planes for the MFMA path; measured only for the

@@ -110,6 +110,10 @@ def _rope_attend_out_fake(y, pos, cos, sin, H, HKV, HD, cache, slot, bt, rmap, l
     "Tensor slot, Tensor bt, Tensor rmap, Tensor lut, int l2e, Tensor(b!) flag) -> (Tensor, Tensor)",
     _rope_attend_out_fake)
 def _rope_attend_out(y, pos, cos, sin, H, HKV, HD, cache, slot, bt, rmap, lut, l2e, flag):
+    return _rope_out_call(y, pos, cos, sin, H, HKV, HD, cache, slot, bt, rmap, lut, l2e, flag, False)
+
+
+def _rope_out_call(y, pos, cos, sin, H, HKV, HD, cache, slot, bt, rmap, lut, l2e, flag, planes):
     from bitexact.exact.ops import FK, FR, FT, FV, FZ
     _hip.require_cuda(y, pos, cos, sin, cache, slot, bt, rmap, lut, flag)
     N = y.shape[0]
@@ -125,16 +129,35 @@ def _rope_attend_out(y, pos, cos, sin, H, HKV, HD, cache, slot, bt, rmap, lut, l
     sho = torch.empty(N, dtype=torch.long, device=y.device)
     ws, wsb = _hip.workspace(y.device, _hip.lib().bx_attn_rope_out_workspace(N))
     tmp, tmpb = _hip.scratch(y.device, _hip.lib().bx_attn_rope_out_scratch(N, H, HD))
-    _hip.call("bx_exact_attn_paged_rope_out", _hip.ptr(y), y.stride(0), _hip.ptr(pos), 1, _hip.ptr(cos),
-              _hip.ptr(sin), cos.shape[0], H, FR, FT, FK, FV, FZ, _hip.ptr(slot), _hip.ptr(cache), cache.stride(0),
-              cache.stride(1), cache.stride(2), cache.shape[2], _hip.ptr(bt), bt.stride(0), bt.shape[1],
-              _hip.ptr(rmap), _hip.ptr(lut), int(l2e), _hip.ptr(qo), qo.stride(0), _hip.ptr(sho), N, HKV, HD,
-              _hip.ptr(flag), _hip.ptr(ws), wsb, _hip.ptr(tmp), tmpb, _hip.stream_of(y))
-    return qo, sho
+    head = (_hip.ptr(y), y.stride(0), _hip.ptr(pos), 1, _hip.ptr(cos), _hip.ptr(sin), cos.shape[0], H, FR, FT, FK,
+            FV, FZ, _hip.ptr(slot), _hip.ptr(cache), cache.stride(0), cache.stride(1), cache.stride(2),
+            cache.shape[2], _hip.ptr(bt), bt.stride(0), bt.shape[1], _hip.ptr(rmap), _hip.ptr(lut), int(l2e),
+            _hip.ptr(qo), qo.stride(0), _hip.ptr(sho))
+    tail = (N, HKV, HD, _hip.ptr(flag), _hip.ptr(ws), wsb, _hip.ptr(tmp), tmpb, _hip.stream_of(y))
+    if not planes:
+        _hip.call("bx_exact_attn_paged_rope_out", *head, *tail)
+        return qo, sho
+    pl = torch.empty(3, N, H * HD, dtype=torch.int8, device=y.device)
+    _hip.call("bx_exact_attn_paged_rope_out_planes", *head, _hip.ptr(pl), *tail)
+    return qo, sho, pl
 
 
-def rope_attend_out(y, pos, cos, sin, dm, cache, slot, bt, rmap, lut, l2e, flag):
+def _rope_attend_out_planes_fake(y, pos, cos, sin, H, HKV, HD, cache, slot, bt, rmap, lut, l2e, flag):
+    N = y.shape[0]
+    return empty((N, H * HD), torch.int32, y), empty((N,), torch.long, y), empty((3, N, H * HD), torch.int8, y)
+
+
+@op("attend_exact_rope_out_planes(Tensor y, Tensor pos, Tensor cos, Tensor sin, int H, int HKV, int HD, "
+    "Tensor(a!) cache, Tensor slot, Tensor bt, Tensor rmap, Tensor lut, int l2e, Tensor(b!) flag) -> "
+    "(Tensor, Tensor, Tensor)", _rope_attend_out_planes_fake)
+def _rope_attend_out_planes(y, pos, cos, sin, H, HKV, HD, cache, slot, bt, rmap, lut, l2e, flag):
+    return _rope_out_call(y, pos, cos, sin, H, HKV, HD, cache, slot, bt, rmap, lut, l2e, flag, True)
+
+
+def rope_attend_out(y, pos, cos, sin, dm, cache, slot, bt, rmap, lut, l2e, flag, planes=False):
     """rope_attend with the attention output stage fused too (ops.attn_out over its num / den): -> (q int32
-    [N, H HD], sh int64 [N]), the wo linear's input; the same integers as rope_attend then ops.attn_out."""
+    [N, H HD], sh int64 [N]), the wo linear's input; the same integers as rope_attend then ops.attn_out.
+    planes=True also returns q's int8 limb planes [3, N, H HD] (the exact linear's q_planes)."""
     H, HKV, HD = (int(v) for v in dm)
-    return _rope_attend_out(y, pos, cos, sin, H, HKV, HD, cache, slot, bt, rmap, lut, int(l2e), flag)
+    f = _rope_attend_out_planes if planes else _rope_attend_out
+    return f(y, pos, cos, sin, H, HKV, HD, cache, slot, bt, rmap, lut, int(l2e), flag)

@@ -668,6 +668,8 @@ struct AoArgs {
   int32_t* q;
   int64_t ldq;
   int64_t* sh;
+  int8_t* planes;   // optional: q's signed int8 limb planes [3][R][H HD] (limb i of q[n][c] at i plane + n H HD + c)
+  int64_t plane;    // R H HD
   int FR, FV;
 };
 
@@ -718,7 +720,19 @@ __device__ __forceinline__ void dec_finish_ao(const AttnArgs& p, const AoArgs& a
   if (!sm.s_last) return;
   const int64_t em = (int64_t)ws_load(&ao.ws_e[n]) + kNegBig - 1;
   const int64_t shr = imax(em - kQB, kNegBig);
-  for (int64_t c = threadIdx.x; c < W; c += NT) ao.q[n * ao.ldq + c] = (int32_t)rshc(ws_load(&ao.ws_p[n * W + c]), shr + ao.FR);
+  for (int64_t c = threadIdx.x; c < W; c += NT) {
+    const int32_t qv = (int32_t)rshc(ws_load(&ao.ws_p[n * W + c]), shr + ao.FR);
+    ao.q[n * ao.ldq + c] = qv;
+    if (ao.planes != nullptr) {   // the exact linear's activation planes (split_q_kernel's limbs)
+      int32_t r = qv;
+#pragma unroll
+      for (int l = 0; l < 3; ++l) {
+        const int32_t lo = limb_lo(r);
+        ao.planes[l * ao.plane + n * W + c] = (int8_t)lo;
+        r = (r - lo) >> 8;
+      }
+    }
+  }
   if (threadIdx.x == 0) {
     ao.sh[n] = shr;
     ws_store(&ao.ws_e[n], 0);
@@ -2134,15 +2148,13 @@ extern "C" int64_t bx_attn_rope_out_scratch(int32_t R, int32_t H, int32_t HD) {
   return (int64_t)R * H * HD * 8;
 }
 
-extern "C" int bx_exact_attn_paged_rope_out(const int64_t* y, int64_t ldy, const int64_t* pos, int64_t spos,
-                                            const int64_t* cos, const int64_t* sin, int32_t npos, int32_t H,
-                                            int32_t FR, int32_t FT, int32_t FK, int32_t FV, int32_t FZ,
-                                            const int64_t* slot, int8_t* cache, int64_t sc_nb, int64_t sc_h,
-                                            int64_t sc_bs, int32_t bs, const int32_t* bt, int64_t sbt, int32_t nblk,
-                                            const int64_t* rmap, const int64_t* lut, int64_t l2e, int32_t* q,
-                                            int64_t ldq, int64_t* sh, int32_t R, int32_t HKV, int32_t HD, int32_t* err,
-                                            void* ws, int64_t ws_bytes, void* tmp, int64_t tmp_bytes,
-                                            bx_stream_t stream) {
+static int attn_rope_out(const int64_t* y, int64_t ldy, const int64_t* pos, int64_t spos, const int64_t* cos,
+                         const int64_t* sin, int32_t npos, int32_t H, int32_t FR, int32_t FT, int32_t FK, int32_t FV,
+                         int32_t FZ, const int64_t* slot, int8_t* cache, int64_t sc_nb, int64_t sc_h, int64_t sc_bs,
+                         int32_t bs, const int32_t* bt, int64_t sbt, int32_t nblk, const int64_t* rmap,
+                         const int64_t* lut, int64_t l2e, int32_t* q, int64_t ldq, int64_t* sh, int8_t* planes,
+                         int32_t R, int32_t HKV, int32_t HD, int32_t* err, void* ws, int64_t ws_bytes, void* tmp,
+                         int64_t tmp_bytes, hipStream_t stream) {
   BX_REQUIRE(q && sh && ldq >= (int64_t)H * HD, "null q / sh or ldq too small");
   BX_REQUIRE(ws && ws_bytes >= bx_attn_rope_out_workspace(R) && ((uintptr_t)ws & 7) == 0,
              "workspace too small (%lld < %lld)", (long long)ws_bytes, (long long)bx_attn_rope_out_workspace(R));
@@ -2154,8 +2166,38 @@ extern "C" int bx_exact_attn_paged_rope_out(const int64_t* y, int64_t ldy, const
   ao.ws_e = (int64_t*)ws;
   ao.cnt = (int32_t*)(ao.ws_e + R);
   ao.q = q; ao.ldq = ldq; ao.sh = sh; ao.FR = FR; ao.FV = FV;
+  ao.planes = planes; ao.plane = (int64_t)R * H * HD;
   return attn_rope_common(y, ldy, pos, spos, cos, sin, npos, H, FR, FT, FK, FV, FZ, slot, cache, sc_nb, sc_h, sc_bs, bs,
-                          bt, sbt, nblk, rmap, lut, l2e, nullptr, nullptr, R, HKV, HD, err, &ao, (hipStream_t)stream);
+                          bt, sbt, nblk, rmap, lut, l2e, nullptr, nullptr, R, HKV, HD, err, &ao, stream);
+}
+
+extern "C" int bx_exact_attn_paged_rope_out(const int64_t* y, int64_t ldy, const int64_t* pos, int64_t spos,
+                                            const int64_t* cos, const int64_t* sin, int32_t npos, int32_t H,
+                                            int32_t FR, int32_t FT, int32_t FK, int32_t FV, int32_t FZ,
+                                            const int64_t* slot, int8_t* cache, int64_t sc_nb, int64_t sc_h,
+                                            int64_t sc_bs, int32_t bs, const int32_t* bt, int64_t sbt, int32_t nblk,
+                                            const int64_t* rmap, const int64_t* lut, int64_t l2e, int32_t* q,
+                                            int64_t ldq, int64_t* sh, int32_t R, int32_t HKV, int32_t HD, int32_t* err,
+                                            void* ws, int64_t ws_bytes, void* tmp, int64_t tmp_bytes,
+                                            bx_stream_t stream) {
+  return attn_rope_out(y, ldy, pos, spos, cos, sin, npos, H, FR, FT, FK, FV, FZ, slot, cache, sc_nb, sc_h, sc_bs, bs, bt,
+                       sbt, nblk, rmap, lut, l2e, q, ldq, sh, nullptr, R, HKV, HD, err, ws, ws_bytes, tmp, tmp_bytes,
+                       (hipStream_t)stream);
+}
+
+extern "C" int bx_exact_attn_paged_rope_out_planes(const int64_t* y, int64_t ldy, const int64_t* pos, int64_t spos,
+                                                   const int64_t* cos, const int64_t* sin, int32_t npos, int32_t H,
+                                                   int32_t FR, int32_t FT, int32_t FK, int32_t FV, int32_t FZ,
+                                                   const int64_t* slot, int8_t* cache, int64_t sc_nb, int64_t sc_h,
+                                                   int64_t sc_bs, int32_t bs, const int32_t* bt, int64_t sbt,
+                                                   int32_t nblk, const int64_t* rmap, const int64_t* lut, int64_t l2e,
+                                                   int32_t* q, int64_t ldq, int64_t* sh, int8_t* planes, int32_t R,
+                                                   int32_t HKV, int32_t HD, int32_t* err, void* ws, int64_t ws_bytes,
+                                                   void* tmp, int64_t tmp_bytes, bx_stream_t stream) {
+  BX_REQUIRE(planes, "null planes");
+  return attn_rope_out(y, ldy, pos, spos, cos, sin, npos, H, FR, FT, FK, FV, FZ, slot, cache, sc_nb, sc_h, sc_bs, bs, bt,
+                       sbt, nblk, rmap, lut, l2e, q, ldq, sh, planes, R, HKV, HD, err, ws, ws_bytes, tmp, tmp_bytes,
+                       (hipStream_t)stream);
 }
 
 extern "C" int bx_int8_attn_paged(const int64_t* q, const int64_t* qpos, int64_t sqpos_r, const int8_t* cache,

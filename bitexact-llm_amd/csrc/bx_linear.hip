@@ -1856,17 +1856,19 @@ static bool stream_plan(int rows_a, int M_out, int N, int K, bool exact, bool pl
     const int per = (nch + want - 1) / want;
     if (per < 8 || (planes && rows_a > 64 && rows_a <= 96)) {
       // with q's limb planes from the caller (no split launch) and 65..96 limb rows: 32-column blocks, >= 1024 k
-      // each, in one round of blocks that covers at least 3/4 of the chip (M = 32, N = 3072, K = 2048: 14.1 vs
+      // each, in one round of blocks that covers most of the chip (M = 32, N = 3072, K = 2048: 14.1 vs
       // 18.8 us for the gemv; N = 2048, K = 8192: 4 splits of 2048 k, 21.3 vs 22.1 us for 64-column blocks in 8
-      // splits; N = 2048, K = 2048 stays on the gemv: 12.8 us with 256 blocks of 512 k, 14.1 with 128 blocks, vs
-      // 11.9). Otherwise, under 1024 k per block the split's fixed costs lose to the gemv.
+      // splits). Otherwise, under 1024 k per block the split's fixed costs lose to the gemv.
       if (!planes || rows_a <= 64 || rows_a > 96) return false;
       s.nwv = 2;
       s.tiles_x = (N + 31) / 32;
       s.split = std::max(1, std::min(cus / s.tiles_x, nch / 8));
       const int per_split = (nch + s.split - 1) / s.split;   // k chunks per block; no block left without k
       s.split = (nch + per_split - 1) / per_split;
-      if (s.tiles_x * s.split > cus || 4 * s.tiles_x * s.split < 3 * cus) return false;
+      // one round of blocks, covering at least 3/4 of the chip, or half of it with >= 1024 k a block (N = 2048,
+      // K = 2048: 128 blocks, 11.2 vs 11.8 us on the gemv)
+      const int nbk = s.tiles_x * s.split;
+      if (nbk > cus || (4 * nbk < 3 * cus && (2 * nbk < cus || per_split < 8))) return false;
     } else {
       s.split = (nch + per - 1) / per;
     }

@@ -165,6 +165,18 @@ int bx_exact_attn_paged_rope_out(const int64_t* y, int64_t ldy, const int64_t* p
                                  const int64_t* rmap, const int64_t* lut, int64_t l2e, int32_t* q, int64_t ldq,
                                  int64_t* sh, int32_t R, int32_t HKV, int32_t HD, int32_t* err, void* ws,
                                  int64_t ws_bytes, void* tmp, int64_t tmp_bytes, bx_stream_t stream);
+/* bx_exact_attn_paged_rope_out that also writes q's signed int8 limb planes, planes int8 [3][R][H HD] (limb i of
+ * q[n][c] at i R H HD + n H HD + c, the split the exact linear's activation planes use), so the wo linear that reads
+ * q needs no split launch (the reference has no counterpart; it serves the same segs.attn_out call as the entry
+ * above). */
+int bx_exact_attn_paged_rope_out_planes(const int64_t* y, int64_t ldy, const int64_t* pos, int64_t spos,
+                                        const int64_t* cos, const int64_t* sin, int32_t npos, int32_t H, int32_t FR,
+                                        int32_t FT, int32_t FK, int32_t FV, int32_t FZ, const int64_t* slot,
+                                        int8_t* cache, int64_t sc_nb, int64_t sc_h, int64_t sc_bs, int32_t bs,
+                                        const int32_t* bt, int64_t sbt, int32_t nblk, const int64_t* rmap,
+                                        const int64_t* lut, int64_t l2e, int32_t* q, int64_t ldq, int64_t* sh,
+                                        int8_t* planes, int32_t R, int32_t HKV, int32_t HD, int32_t* err, void* ws,
+                                        int64_t ws_bytes, void* tmp, int64_t tmp_bytes, bx_stream_t stream);
 /* Workspace bytes of the paged attentions (exact and int8) for up to min(64, 4096 / T) key splits, T = R HKV
  * ceil(M / 4) query tiles; a call with more splits than the workspace holds is rejected. */
 int64_t bx_attn_paged_workspace(int32_t R, int32_t HKV, int32_t M, int32_t HD);

@@ -334,6 +334,18 @@ def test_rope_attend_equals_store_then_attend(dev, HD, H, HKV):
         assert torch.equal(cc, ca), "cache bytes differ (fused output stage)"
         assert torch.equal(qf, qo) and torch.equal(shf, sho)
         assert int(fc.item()) == int(fa.item())
+    # the form that also writes q's limb planes (the wo linear's q_planes): the same rows, and the planes are their
+    # signed base-256 digits
+    cp, fp = c0.clone(), torch.zeros(1, dtype=torch.int32, device=dev)
+    qp, shp, plp = tri_exact_attn.rope_attend_out(y.to(dev), pos.to(dev), cos, sin, (H, HKV, HD), cp, slot.to(dev),
+                                                  bt.to(dev), rmap.to(dev), lut, l2e, fp, planes=True)
+    torch.cuda.synchronize()
+    assert torch.equal(cp, ca) and torch.equal(qp, qo) and torch.equal(shp, sho) and int(fp.item()) == int(fa.item())
+    r = qp.long()
+    for i in range(3):
+        lo = ((r + 128) & 255) - 128
+        assert torch.equal(plp[i].long(), lo)
+        r = (r - lo) >> 8
     # a position past the rope tables flags in both forms
     pos2 = pos.clone()
     pos2[2] = 400

@@ -380,15 +380,17 @@ def test_norm_quant_planes(dev):
         r = (r - lo) >> 8
 
 
-@pytest.mark.parametrize("M,N,K", [(32, 3072, 2048), (22, 3080, 2048), (32, 4096, 2048), (32, 2048, 8192)])
+@pytest.mark.parametrize("M,N,K", [(32, 3072, 2048), (22, 3080, 2048), (32, 4096, 2048), (32, 2048, 8192),
+                                   (32, 2048, 2048)])
 def test_exact_linear_narrow_planes(dev, M, N, K):
     """Narrow N with q's limb planes given: 32-column stream blocks with the K split over the zeroed workspace
     (without planes the gemv, or at K = 8192 64-column blocks in 8 splits, serve the shape); same y and flag as
-    that path, and y matches the oracle (partial last column tile at N = 3080, forced residual entries, 66 and 96 limb rows; the
-    engine's down projection at N = 2048, K = 8192). N = 2048 at K = 2048 keeps the gemv either way."""
+    that path, and y matches the oracle (partial last column tile at N = 3080, forced residual entries, 66 and 96
+    limb rows; the engine's down projection at N = 2048, K = 8192 and its wo at N = 2048, K = 2048, half the chip
+    in 2 splits). N = 1024 keeps the gemv either way."""
     from bitexact.exact import ops
     from bitexact.vllm_plugin.exact_gemm import exact_linear, needs_planes, plan
-    assert plan(32, 2048, 2048, planes=True)[0] == "gemv" and not needs_planes(32, 2048, 2048)
+    assert plan(32, 1024, 2048, planes=True)[0] == "gemv" and not needs_planes(32, 1024, 2048)
     assert plan(M, N, K)[0] == ("gemv" if K == 2048 else "stream")   # K = 8192: 64-column blocks, 8 splits
     kern, _, split, blocks = plan(M, N, K, planes=True)
     assert kern == "stream" and split > 1 and blocks == -(-N // 32), plan(M, N, K, planes=True)
