@@ -275,8 +275,8 @@ def bench_phases(dev):
     """Phase timestamps of the main kernels (the measurement build, BX_PHASES=1): the exact prefill tile at
     lm_head / q-o / down shapes (M = 2048), the exact decode stream kernel at the engine's gate|up shape (M = 32
     with q's limb planes), the split decode attention at config 4, the one-block decode attention at the engine's
-    shape (batch 32, context 1024), the add + norm at the engine's shape (32 rows of 2048), and the int8 decode
-    down GEMM at M = 64 and 8 (config 2, gemv kernel). Each is launched a
+    shape (batch 32, context 1024) alone and as the decode step's fused launch, the add + norm at the engine's shape
+    (32 rows of 2048), and the int8 decode down GEMM at M = 64 and 8 (config 2, gemv kernel). Each is launched a
     few times over rotating copies of its weights / cache (>= 400 MB, beyond the 256 MB last-level cache, so the
     timed launch reads HBM); the table holds the last launch's first 1024 blocks."""
     import torch
@@ -352,6 +352,29 @@ def bench_phases(dev):
     for _ in range(3):
         ops.add_norm_y(y, x.clone(), gm, ge, flag=flag, planes=True)
     torch.cuda.synchronize()
+    # the decode step's fused launch at the engine's shape (rope prologue, attention, output stage with limb planes):
+    # 32 tokens at position 1023, 8 KV heads of 4 q heads, rotating caches
+    from bitexact.exact.consts import FT, llama3_inv_freq, rope_tables
+    N, H, HKV, HD, bs, nblk = 32, 32, 8, 64, 16, 65
+    cos, sin = rope_tables(2048, FT, llama3_inv_freq(HD))
+    cos, sin = cos.to(dev), sin.to(dev)
+    gy = torch.Generator(device=dev).manual_seed(3)
+    y = torch.randint(-(1 << 30), 1 << 30, (N, (H + 2 * HKV) * HD), device=dev, generator=gy)
+    pos = torch.full((N,), 1023, dtype=torch.long, device=dev)
+    bt = torch.randperm(N * nblk, device=dev, generator=gy).to(torch.int32).view(N, nblk)
+    rmap = torch.arange(N, device=dev)
+    slot = bt[rmap, pos // bs].long() * bs + pos % bs
+    ncop = -(-(400 << 20) // (N * nblk * HKV * bs * 8 * HD))
+    caches = [torch.randint(-128, 128, (N * nblk, HKV, bs, 8 * HD), dtype=torch.int8, device=dev, generator=gy)
+              for _ in range(ncop)]
+    for i in range(max(3, ncop)):
+        tri_exact_attn.rope_attend_out(y, pos, cos, sin, (H, HKV, HD), caches[i % ncop], slot, bt, rmap, lut,
+                                       387270501, flag, planes=True)
+    torch.cuda.synchronize()
+    res["decode step attention (engine: rope + attention + output stage, 32 tokens, ctx 1024)"] = _phase_summary(
+        _phase_table("attn")[1], N * HKV, ["rope prologue", "K sweep", "V request", "V sweep", "finish + output"])
+    del caches
+    torch.cuda.empty_cache()
     # int8 decode down GEMMs (config 2: K = 8192, N = 2048) on the gemv kernel: 256 blocks (4 K splits)
     from bitexact.int8.gemm_skinny import int_mm_join
     gw = torch.Generator(device=dev).manual_seed(1)
