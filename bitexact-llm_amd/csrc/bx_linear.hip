@@ -1737,7 +1737,6 @@ static const TileShape kTileExact = {4, 2, 1, 2, 64, 2};
 struct Plan {
   int stream;                     // stream kernel: activation row blocks RBM (0: none)
   int nwv;                        // stream kernel: waves per block (16 columns each)
-  int ring3;                      // stream kernel, 32-column form: a 3-stage ring (two blocks per CU)
   int wide;                       // wide kernel configuration (0: none)
   int staged;                     // staged kernel configuration (0: none)
   bool gemv;
@@ -1874,13 +1873,12 @@ static bool stream_plan(int rows_a, int M_out, int N, int K, bool exact, bool pl
       s.split = (nch + per - 1) / per;
     }
   }
-  // long exact grids with the caller's planes at 65..96 rows (lm_head: 2004 tiles of 64): 32-column blocks on a
-  // 3-stage ring, two blocks per CU (M = 32, N = 128256: 185.7 vs 196.5 us; at N = 16384, one round of 64-column
-  // tiles, 26.4 vs 25.7, so one-round grids keep those)
+  // long exact grids with the caller's planes at 65..96 rows (lm_head: 2004 tiles of 64): 32-column blocks, two per
+  // CU (M = 32, N = 128256: 185.7 vs 196.5 us; at N = 16384, one round of 64-column tiles, 26.4 vs 25.7, so one-round
+  // grids keep those)
   if (exact && planes && rows_a > 64 && rows_a <= 96 && s.split == 1 && s.tiles_x > 2 * cus) {
     s.nwv = 2;
     s.tiles_x = (N + 31) / 32;
-    s.ring3 = 1;
   }
   s.stream = rows_a <= 16 ? 1 : rows_a <= 32 ? 2 : rows_a <= 64 ? 4 : (exact && rows_a <= 96) ? 6 : 8;
   s.kbytes = (K / kStBK + s.split - 1) / s.split * kStBK;
@@ -2152,8 +2150,8 @@ static int launch_stream(LinArgs& p, const Plan& s, hipStream_t st) {
                                   : launch_stream_cfg<4, 3, 4, MODE>(p, s, st);
     // 32-column blocks at 65..96 rows (planner): 4 waves as 2 column groups x 2 row groups, so every SIMD has one
     // (wqkv N = 3072: 12.2 vs 14.0 us with 2 waves over every row; down N = 2048, K = 8192: 19.4 vs 21.1)
-    if (s.nwv == 2 && s.ring3 && wr == 2) return launch_stream_cfg<6, 3, 3, MODE, 4, 2>(p, s, st);
-    if (s.nwv == 2) return wr == 2 ? launch_stream_cfg<6, 3, 4, MODE, 4, 2>(p, s, st)
+    // (a 3-stage ring, 72 KiB: two blocks fit a CU; lm_head 185.7 vs 196.5 us, engine +0.45 % on wqkv / wo / wd)
+    if (s.nwv == 2) return wr == 2 ? launch_stream_cfg<6, 3, 3, MODE, 4, 2>(p, s, st)
                                    : launch_stream_cfg<6, 3, 4, MODE, 2>(p, s, st);
     if (s.stream == 6) return two ? launch_stream_cfg<6, 3, 4, MODE, 8, 2>(p, s, st)
                                   : launch_stream_cfg<6, 3, 4, MODE>(p, s, st);
