@@ -1849,6 +1849,14 @@ static bool stream_plan(int rows_a, int M_out, int N, int K, bool exact, bool pl
   s.tiles_y = 1;
   s.split = 1;
   s.nwv = 4;
+  // int8 at 65..128 stacked rows with N too narrow for 64-column tiles to cover the chip but wide enough for
+  // 32-column ones: 2-wave blocks, one per CU, no K split (M = 64, N = 8192, K = 2048: 11.6 vs 12.0 us on the gemv;
+  // at M = 1 / 8 the gemv and staged kernels stay: 6.0-6.3 vs 6.6-6.9 us)
+  static const int st32 = getenv("BX_ST32") ? atoi(getenv("BX_ST32")) : 1;
+  if (!exact && st32 && rows_a > 64 && s.tiles_x < cus && (N + 31) / 32 >= cus) {
+    s.nwv = 2;
+    s.tiles_x = (N + 31) / 32;
+  }
   if (s.tiles_x < cus) {   // exact only: K split until the tiles cover the chip
     if (!exact) return false;
     const int nch = K / kStBK;
@@ -2158,6 +2166,12 @@ static int launch_stream(LinArgs& p, const Plan& s, hipStream_t st) {
     return two ? launch_stream_cfg<8, 3, 3, MODE, 8, 2>(p, s, st) : launch_stream_cfg<8, 3, 3, MODE>(p, s, st);
   }
   // ring depth: 4 stages at 16 rows (8 measured ~0.5 us slower per launch at M = 1), 8 at 32 / 64, 6 at 128
+  if (s.nwv == 2) {   // 32-column blocks (planner: int8 N with 32-column tiles covering the chip)
+    if (s.stream == 1) return launch_stream_cfg<1, 1, 4, MODE, 2>(p, s, st);
+    if (s.stream == 2) return launch_stream_cfg<2, 1, 8, MODE, 2>(p, s, st);
+    if (s.stream == 4) return launch_stream_cfg<4, 1, 8, MODE, 2>(p, s, st);
+    return launch_stream_cfg<8, 1, 6, MODE, 2>(p, s, st);
+  }
   if (s.stream == 1) return launch_stream_cfg<1, 1, 4, MODE>(p, s, st);
   if (s.stream == 2) return launch_stream_cfg<2, 1, 8, MODE>(p, s, st);
   if (s.stream == 4) return launch_stream_cfg<4, 1, 8, MODE>(p, s, st);

@@ -486,10 +486,10 @@ def test_corrupt_ell_index_sets_flag(dev, M):
             assert flag.item() == 1, (kind, checked)
 
 
-@pytest.mark.parametrize("N,K", [(16384, 2048), (16400, 1024), (32768, 512)])
+@pytest.mark.parametrize("N,K", [(16384, 2048), (16400, 1024), (32768, 512), (8192, 2048), (8200, 1024)])
 def test_int8_stream_wide(dev, N, K):
-    """int8 decode where the 64-column tiles cover the chip without a K split (the stream kernel): a partial last
-    column tile (N = 16400), join in registers (M % 16 == 0) and through LDS (other M), raw int32 rows up to 128,
+    """int8 decode where the 64-column tiles (or, at N = 8192, the 32-column tiles) cover the chip without a K split
+    (the stream kernel): a partial last column tile (N = 16400, 8200), join in registers (M % 16 == 0) and through LDS (other M), raw int32 rows up to 128,
     extreme operands, against the float64 oracle."""
     from bitexact.int8.gemm_skinny import int_mm, int_mm_join
     from bitexact import _hip
@@ -499,7 +499,9 @@ def test_int8_stream_wide(dev, N, K):
     wd = torch.from_numpy(w).to(dev)
     for M, nl in ((1, 2), (16, 2), (32, 3), (21, 3), (48, 2), (64, 2), (40, 1)):
         out = (ctypes.c_int32 * 6)()
-        assert _hip.lib().bx_int8_gemm_plan(M, N, K, nl, out) == 0 and out[0] == 5, (M, nl, list(out))
+        assert _hip.lib().bx_int8_gemm_plan(M, N, K, nl, out) == 0, (M, nl)
+        if N > 8200 or M * nl > 64:   # N = 8192: 32-column tiles from 65 stacked rows, the gemv below
+            assert out[0] == 5, (M, nl, list(out))
         z = g.integers(-(1 << 44), 1 << 44, (M, K))
         q, _, _ = R.quant_rows(z, nl)
         a = R.stack_limbs(q, nl)
