@@ -51,7 +51,7 @@ __device__ __forceinline__ void store4(int8_t* planes, int n, int row, int q, co
 
 constexpr int kNTI = 8;   // default column tiles per block, walked in sequence (the next tile's loads overlap this one's stores)
 
-template <typename TA, typename TB, int NA, int NB>
+template <typename TA, typename TB, int NA, int NB, bool A1>
 __global__ __launch_bounds__(256) void bmm_mfma_kernel(const TA* a, int64_t saz, int64_t sam, int64_t sak, const TB* b,
                                                        int64_t sbz, int64_t sbk, int64_t sbn, int64_t* c, int64_t scz,
                                                        int64_t scm, int64_t scn, int M, int N, int K, int nti) {
@@ -79,11 +79,15 @@ __global__ __launch_bounds__(256) void bmm_mfma_kernel(const TA* a, int64_t saz,
   const int ntile = min(nti, (N - nb0 + kBT - 1) / kBT);
   const int nsteps = ntile * ksteps;
   uint32_t va[4][4], vb[4][4];
+  // A1 (one k step, K <= 64, e.g. q.k over a head dimension): the A tile is the same for every column tile, so its
+  // limb planes are loaded and split once and stay in LDS
+  constexpr bool a_once = A1;
   auto fetch = [&](int st) {
     const int j = st / ksteps, k0 = (st % ksteps) * kBT;
+    const bool fa = !a_once || st == 0;   // block-uniform
 #pragma unroll
     for (int g = 0; g < 4; ++g) {
-      load4(ab, sam, sak, m0 + ar[g], M, k0 + 4 * aq[g], K, va[g]);
+      if (fa) load4(ab, sam, sak, m0 + ar[g], M, k0 + 4 * aq[g], K, va[g]);
       load4(bb, sbn, sbk, nb0 + j * kBT + br[g], N, k0 + 4 * bq[g], K, vb[g]);
     }
   };
@@ -95,9 +99,10 @@ __global__ __launch_bounds__(256) void bmm_mfma_kernel(const TA* a, int64_t saz,
   fetch(0);
   const int r16 = lane & 15, ch = lane >> 4;
   for (int st = 0; st < nsteps; ++st) {
+    const bool sa = !a_once || st == 0;   // block-uniform
 #pragma unroll
     for (int g = 0; g < 4; ++g) {
-      store4(As, NA, ar[g], aq[g], va[g]);
+      if (sa) store4(As, NA, ar[g], aq[g], va[g]);
       store4(Bs, NB, br[g], bq[g], vb[g]);
     }
     __syncthreads();
@@ -127,7 +132,9 @@ __global__ __launch_bounds__(256) void bmm_mfma_kernel(const TA* a, int64_t saz,
         int64_t v = 0;
 #pragma unroll
         for (int s = 0; s < NS; ++s) v += (int64_t)acc[s][cb][e] << (8 * s);
-        if (m < M && n < N) c[z * scz + (int64_t)m * scm + (int64_t)n * scn] = v;
+        if (m < M && n < N) {
+          c[z * scz + (int64_t)m * scm + (int64_t)n * scn] = v;
+        }
       }
 #pragma unroll
       for (int s = 0; s < NS; ++s) acc[s][cb] = v4i{0, 0, 0, 0};
@@ -135,27 +142,38 @@ __global__ __launch_bounds__(256) void bmm_mfma_kernel(const TA* a, int64_t saz,
   }
 }
 
-template <typename TA, typename TB, int NA>
+template <typename TA, typename TB, int NA, bool A1>
 static void launch_nb(int nb, dim3 grid, hipStream_t st, const TA* a, int64_t saz, int64_t sam, int64_t sak,
                       const TB* b, int64_t sbz, int64_t sbk, int64_t sbn, int64_t* c, int64_t scz, int64_t scm,
                       int64_t scn, int M, int N, int K, int nti) {
   if (nb == 1)
-    bmm_mfma_kernel<TA, TB, NA, 1><<<grid, 256, 0, st>>>(a, saz, sam, sak, b, sbz, sbk, sbn, c, scz, scm, scn, M, N, K, nti);
+    bmm_mfma_kernel<TA, TB, NA, 1, A1><<<grid, 256, 0, st>>>(a, saz, sam, sak, b, sbz, sbk, sbn, c, scz, scm, scn, M, N, K, nti);
   else if (nb == 2)
-    bmm_mfma_kernel<TA, TB, NA, 2><<<grid, 256, 0, st>>>(a, saz, sam, sak, b, sbz, sbk, sbn, c, scz, scm, scn, M, N, K, nti);
+    bmm_mfma_kernel<TA, TB, NA, 2, A1><<<grid, 256, 0, st>>>(a, saz, sam, sak, b, sbz, sbk, sbn, c, scz, scm, scn, M, N, K, nti);
   else
-    bmm_mfma_kernel<TA, TB, NA, 3><<<grid, 256, 0, st>>>(a, saz, sam, sak, b, sbz, sbk, sbn, c, scz, scm, scn, M, N, K, nti);
+    bmm_mfma_kernel<TA, TB, NA, 3, A1><<<grid, 256, 0, st>>>(a, saz, sam, sak, b, sbz, sbk, sbn, c, scz, scm, scn, M, N, K, nti);
 }
 
-template <typename TA, typename TB>
+template <typename TA, typename TB, bool A1>
 static void launch_na(int na, int nb, dim3 grid, hipStream_t st, const void* a, int64_t saz, int64_t sam, int64_t sak,
                       const void* b, int64_t sbz, int64_t sbk, int64_t sbn, int64_t* c, int64_t scz, int64_t scm,
                       int64_t scn, int M, int N, int K, int nti) {
   const TA* A = (const TA*)a;
   const TB* B = (const TB*)b;
-  if (na == 1) launch_nb<TA, TB, 1>(nb, grid, st, A, saz, sam, sak, B, sbz, sbk, sbn, c, scz, scm, scn, M, N, K, nti);
-  else if (na == 2) launch_nb<TA, TB, 2>(nb, grid, st, A, saz, sam, sak, B, sbz, sbk, sbn, c, scz, scm, scn, M, N, K, nti);
-  else launch_nb<TA, TB, 3>(nb, grid, st, A, saz, sam, sak, B, sbz, sbk, sbn, c, scz, scm, scn, M, N, K, nti);
+  if (na == 1) launch_nb<TA, TB, 1, A1>(nb, grid, st, A, saz, sam, sak, B, sbz, sbk, sbn, c, scz, scm, scn, M, N, K, nti);
+  else if (na == 2) launch_nb<TA, TB, 2, A1>(nb, grid, st, A, saz, sam, sak, B, sbz, sbk, sbn, c, scz, scm, scn, M, N, K, nti);
+  else launch_nb<TA, TB, 3, A1>(nb, grid, st, A, saz, sam, sak, B, sbz, sbk, sbn, c, scz, scm, scn, M, N, K, nti);
+}
+
+// one k step (K <= 64): the A tile's limb planes are formed once per block
+template <typename TA, typename TB>
+static void launch_k(int na, int nb, dim3 grid, hipStream_t st, const void* a, int64_t saz, int64_t sam, int64_t sak,
+                     const void* b, int64_t sbz, int64_t sbk, int64_t sbn, int64_t* c, int64_t scz, int64_t scm,
+                     int64_t scn, int M, int N, int K, int nti) {
+  if (K <= kBT)
+    launch_na<TA, TB, true>(na, nb, grid, st, a, saz, sam, sak, b, sbz, sbk, sbn, c, scz, scm, scn, M, N, K, nti);
+  else
+    launch_na<TA, TB, false>(na, nb, grid, st, a, saz, sam, sak, b, sbz, sbk, sbn, c, scz, scm, scn, M, N, K, nti);
 }
 
 }  // namespace bx
@@ -179,17 +197,17 @@ extern "C" int bx_limb_bmm(const void* a, int32_t a_bytes, int64_t saz, int64_t 
   const dim3 grid((N + kBT * nti - 1) / (kBT * nti), (M + kBT - 1) / kBT, Z);
   hipStream_t st = (hipStream_t)stream;
   if (K == 0) {   // an empty sum: zeros (one step per column tile over a zero-length K reads nothing)
-    bmm_mfma_kernel<int32_t, int32_t, 1, 1><<<grid, 256, 0, st>>>((const int32_t*)a, saz, sam, sak, (const int32_t*)b,
+    bmm_mfma_kernel<int32_t, int32_t, 1, 1, false><<<grid, 256, 0, st>>>((const int32_t*)a, saz, sam, sak, (const int32_t*)b,
                                                                   sbz, sbk, sbn, c, scz, scm, scn, M, N, 0, nti);
     return check_launch("bmm_mfma_kernel");
   }
   if (a_bytes == 4 && b_bytes == 4)
-    launch_na<int32_t, int32_t>(na, nb, grid, st, a, saz, sam, sak, b, sbz, sbk, sbn, c, scz, scm, scn, M, N, K, nti);
+    launch_k<int32_t, int32_t>(na, nb, grid, st, a, saz, sam, sak, b, sbz, sbk, sbn, c, scz, scm, scn, M, N, K, nti);
   else if (a_bytes == 4)
-    launch_na<int32_t, int64_t>(na, nb, grid, st, a, saz, sam, sak, b, sbz, sbk, sbn, c, scz, scm, scn, M, N, K, nti);
+    launch_k<int32_t, int64_t>(na, nb, grid, st, a, saz, sam, sak, b, sbz, sbk, sbn, c, scz, scm, scn, M, N, K, nti);
   else if (b_bytes == 4)
-    launch_na<int64_t, int32_t>(na, nb, grid, st, a, saz, sam, sak, b, sbz, sbk, sbn, c, scz, scm, scn, M, N, K, nti);
+    launch_k<int64_t, int32_t>(na, nb, grid, st, a, saz, sam, sak, b, sbz, sbk, sbn, c, scz, scm, scn, M, N, K, nti);
   else
-    launch_na<int64_t, int64_t>(na, nb, grid, st, a, saz, sam, sak, b, sbz, sbk, sbn, c, scz, scm, scn, M, N, K, nti);
+    launch_k<int64_t, int64_t>(na, nb, grid, st, a, saz, sam, sak, b, sbz, sbk, sbn, c, scz, scm, scn, M, N, K, nti);
   return check_launch("bmm_mfma_kernel");
 }

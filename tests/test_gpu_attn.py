@@ -198,7 +198,7 @@ def test_prefill_attention_full_size(dev, HD, T, Z):
 def test_bmm_exact(dev):
     from bitexact.bmm import bmm
     g = torch.Generator().manual_seed(0)
-    for Z, M, K, N in [(3, 5, 64, 70), (16, 4, 700, 64), (2, 130, 64, 129)]:
+    for Z, M, K, N in [(3, 5, 64, 70), (16, 4, 700, 64), (2, 130, 64, 129), (2, 70, 33, 600)]:
         a = torch.randint(-R.LIM3, R.LIM3 + 1, (Z, M, K), generator=g)
         b = torch.randint(-R.LIM3, R.LIM3 + 1, (Z, K, N), generator=g).to(torch.int32)
         ref = R.bmm(a.numpy(), b.numpy())
