@@ -198,7 +198,9 @@ def test_prefill_attention_full_size(dev, HD, T, Z):
 def test_bmm_exact(dev):
     from bitexact.bmm import bmm
     g = torch.Generator().manual_seed(0)
-    for Z, M, K, N in [(3, 5, 64, 70), (16, 4, 700, 64), (2, 130, 64, 129), (2, 70, 33, 600)]:
+    # (two 64-row tiles per block from M = 128; one k step when K <= 64)
+    for Z, M, K, N in [(3, 5, 64, 70), (16, 4, 700, 64), (2, 130, 64, 129), (2, 70, 33, 600), (2, 200, 33, 300),
+                       (2, 256, 700, 64)]:
         a = torch.randint(-R.LIM3, R.LIM3 + 1, (Z, M, K), generator=g)
         b = torch.randint(-R.LIM3, R.LIM3 + 1, (Z, K, N), generator=g).to(torch.int32)
         ref = R.bmm(a.numpy(), b.numpy())
@@ -211,7 +213,7 @@ def test_bmm_exact(dev):
     assert np.array_equal(bmm(a.to(dev), b.to(dev), na=1).cpu().numpy(), R.bmm(a.numpy(), b.numpy()))
     for na, nb in ((1, 2), (2, 3), (3, 1), (2, 2)):
         la, lb = (-128, 127) if na == 1 else (-R.LIM[na], R.LIM[na]), (-128, 127) if nb == 1 else (-R.LIM[nb], R.LIM[nb])
-        a = torch.randint(la[0], la[1] + 1, (3, 70, 150), generator=g)
+        a = torch.randint(la[0], la[1] + 1, (3, 70 if na != 2 else 150, 150), generator=g)
         b = torch.randint(lb[0], lb[1] + 1, (3, 150, 66), generator=g)
         assert np.array_equal(bmm(a.to(dev), b.to(dev), na=na, nb=nb).cpu().numpy(), R.bmm(a.numpy(), b.numpy()))
     # A transposed in memory (m contiguous), both int32
@@ -219,6 +221,11 @@ def test_bmm_exact(dev):
     b = torch.randint(-R.LIM3, R.LIM3 + 1, (2, 100, 65), generator=g).to(torch.int32)
     at = a.to(dev).transpose(1, 2).contiguous().transpose(1, 2)
     assert np.array_equal(bmm(at, b.to(dev)).cpu().numpy(), R.bmm(a.numpy(), b.numpy()))
+    for M, K in ((190, 100), (129, 40)):   # the same over two row tiles per block
+        a = torch.randint(-R.LIM3, R.LIM3 + 1, (2, M, K), generator=g).to(torch.int32)
+        b = torch.randint(-R.LIM3, R.LIM3 + 1, (2, K, 65), generator=g).to(torch.int32)
+        at = a.to(dev).transpose(1, 2).contiguous().transpose(1, 2)
+        assert np.array_equal(bmm(at, b.to(dev)).cpu().numpy(), R.bmm(a.numpy(), b.numpy()))
 
 
 def test_bmm_int32_bound(dev):
