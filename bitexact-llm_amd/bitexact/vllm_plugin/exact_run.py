@@ -76,7 +76,6 @@ class ExactEngine:
         N, G, HKV, HD = ids.shape[0], self.G, self.HKV, self.HD
         pos = pos.long().contiguous()
         slot = slot.long().clamp(min=0)    # padding (slot < 0) -> the null block 0; one launch
-        qpos = pos.view(-1, 1).expand(-1, G).contiguous()
         fl = self.fl
         pl = None                             # q's limb planes, when the norm before the layer wrote them
         if self.fused[0, "wqkv"].needs_planes(N):
@@ -85,6 +84,8 @@ class ExactEngine:
             x, q, sh, _ = ops.embed_norm(self.emb, ids, *self.ga[0], flag=fl)
         fuse = (one_per_seq and kvs is not None and
                 tri_exact_attn.rope_fusable(N, HKV, self.H, bt.shape[1], kvs[0].shape[2]))
+        # the query positions per q head of a group (the split attention's input; the fused launch reads pos)
+        qpos = None if fuse else pos.view(-1, 1).expand(-1, G).contiguous()
         for i in range(self.L):
             y = self.fused[i, "wqkv"](q, sh, fl, False, q_planes=pl)
             plo = None                        # the wo linear's limb planes, when the output stage writes them
