@@ -56,7 +56,10 @@ constexpr int kNTI = 16;
 
 // RT row tiles of 64 per block (256 RT threads; wave w computes rows 16 w .. 16 w + 15 of the 64 RT): with RT = 2
 // each B tile is loaded and split once for 128 rows.
-template <typename TA, typename TB, int NA, int NB, bool A1, int RT>
+// PF: operand steps fetched ahead into registers (2: each step's loads have two steps of MFMAs to land behind). The
+// step loop runs as PF unrolled substeps with the register set chosen at compile time; at PF = 1 this form took p.v
+// at config 4 from 1.24 to 0.90 ms over a plain step loop (same registers, same integers); PF = 2 measured 0.88-0.89.
+template <typename TA, typename TB, int NA, int NB, bool A1, int RT, int PF>
 __global__ __launch_bounds__(256 * RT) void bmm_mfma_kernel(const TA* a, int64_t saz, int64_t sam, int64_t sak,
                                                             const TB* b, int64_t sbz, int64_t sbk, int64_t sbn,
                                                             int64_t* c, int64_t scz, int64_t scm, int64_t scn, int M,
@@ -89,35 +92,41 @@ __global__ __launch_bounds__(256 * RT) void bmm_mfma_kernel(const TA* a, int64_t
   const int ksteps = max(1, (K + kBT - 1) / kBT);
   const int ntile = min(nti, (N - nb0 + kBT - 1) / kBT);
   const int nsteps = ntile * ksteps;
-  uint32_t va[4][4], vb[GB][4];
+  uint32_t va[PF][4][4], vb[PF][GB][4];
   // A1 (one k step, K <= 64, e.g. q.k over a head dimension): the A tile is the same for every column tile, so its
   // limb planes are loaded and split once and stay in LDS
   constexpr bool a_once = A1;
-  auto fetch = [&](int st) {
+  auto fetch = [&](int st, uint32_t (&fa4)[4][4], uint32_t (&fb4)[GB][4]) {
     const int j = st / ksteps, k0 = (st % ksteps) * kBT;
     const bool fa = !a_once || st == 0;   // block-uniform
 #pragma unroll
     for (int g = 0; g < 4; ++g)
-      if (fa) load4(ab, sam, sak, m0 + ar[g], M, k0 + 4 * aq[g], K, va[g]);
+      if (fa) load4(ab, sam, sak, m0 + ar[g], M, k0 + 4 * aq[g], K, fa4[g]);
 #pragma unroll
-    for (int g = 0; g < GB; ++g) load4(bb, sbn, sbk, nb0 + j * kBT + br[g], N, k0 + 4 * bq[g], K, vb[g]);
+    for (int g = 0; g < GB; ++g) load4(bb, sbn, sbk, nb0 + j * kBT + br[g], N, k0 + 4 * bq[g], K, fb4[g]);
   };
   v4i acc[NS][4];
 #pragma unroll
   for (int s = 0; s < NS; ++s)
 #pragma unroll
     for (int cb = 0; cb < 4; ++cb) acc[s][cb] = v4i{0, 0, 0, 0};
-  fetch(0);
+#pragma unroll
+  for (int h = 0; h < PF; ++h)
+    if (h < nsteps) fetch(h, va[h], vb[h]);
   const int r16 = lane & 15, ch = lane >> 4;
-  for (int st = 0; st < nsteps; ++st) {
+  for (int st0 = 0; st0 < nsteps; st0 += PF)
+#pragma unroll
+  for (int h = 0; h < PF; ++h) {
+    const int st = st0 + h;
+    if (st >= nsteps) break;              // block-uniform
     const bool sa = !a_once || st == 0;   // block-uniform
 #pragma unroll
     for (int g = 0; g < 4; ++g)
-      if (sa) store4(As, NA, AP, ar[g], aq[g], va[g]);
+      if (sa) store4(As, NA, AP, ar[g], aq[g], va[h][g]);
 #pragma unroll
-    for (int g = 0; g < GB; ++g) store4(Bs, NB, kPlane, br[g], bq[g], vb[g]);
+    for (int g = 0; g < GB; ++g) store4(Bs, NB, kPlane, br[g], bq[g], vb[h][g]);
     __syncthreads();
-    if (st + 1 < nsteps) fetch(st + 1);   // the next step's values travel while this step's MFMAs run
+    if (st + PF < nsteps) fetch(st + PF, va[h], vb[h]);   // later steps' values travel while this step's MFMAs run
     v4i af[NA];
 #pragma unroll
     for (int i = 0; i < NA; ++i) af[i] = *(const v4i*)(As + i * AP + swz(16 * wave + r16, ch));
@@ -153,27 +162,27 @@ __global__ __launch_bounds__(256 * RT) void bmm_mfma_kernel(const TA* a, int64_t
   }
 }
 
-template <typename TA, typename TB, int NA, bool A1, int RT>
+template <typename TA, typename TB, int NA, bool A1, int RT, int PF>
 static void launch_nb(int nb, dim3 grid, hipStream_t st, const TA* a, int64_t saz, int64_t sam, int64_t sak,
                       const TB* b, int64_t sbz, int64_t sbk, int64_t sbn, int64_t* c, int64_t scz, int64_t scm,
                       int64_t scn, int M, int N, int K, int nti) {
   if (nb == 1)
-    bmm_mfma_kernel<TA, TB, NA, 1, A1, RT><<<grid, 256 * RT, 0, st>>>(a, saz, sam, sak, b, sbz, sbk, sbn, c, scz, scm, scn, M, N, K, nti);
+    bmm_mfma_kernel<TA, TB, NA, 1, A1, RT, PF><<<grid, 256 * RT, 0, st>>>(a, saz, sam, sak, b, sbz, sbk, sbn, c, scz, scm, scn, M, N, K, nti);
   else if (nb == 2)
-    bmm_mfma_kernel<TA, TB, NA, 2, A1, RT><<<grid, 256 * RT, 0, st>>>(a, saz, sam, sak, b, sbz, sbk, sbn, c, scz, scm, scn, M, N, K, nti);
+    bmm_mfma_kernel<TA, TB, NA, 2, A1, RT, PF><<<grid, 256 * RT, 0, st>>>(a, saz, sam, sak, b, sbz, sbk, sbn, c, scz, scm, scn, M, N, K, nti);
   else
-    bmm_mfma_kernel<TA, TB, NA, 3, A1, RT><<<grid, 256 * RT, 0, st>>>(a, saz, sam, sak, b, sbz, sbk, sbn, c, scz, scm, scn, M, N, K, nti);
+    bmm_mfma_kernel<TA, TB, NA, 3, A1, RT, PF><<<grid, 256 * RT, 0, st>>>(a, saz, sam, sak, b, sbz, sbk, sbn, c, scz, scm, scn, M, N, K, nti);
 }
 
-template <typename TA, typename TB, bool A1, int RT>
+template <typename TA, typename TB, bool A1, int RT, int PF>
 static void launch_na(int na, int nb, dim3 grid, hipStream_t st, const void* a, int64_t saz, int64_t sam, int64_t sak,
                       const void* b, int64_t sbz, int64_t sbk, int64_t sbn, int64_t* c, int64_t scz, int64_t scm,
                       int64_t scn, int M, int N, int K, int nti) {
   const TA* A = (const TA*)a;
   const TB* B = (const TB*)b;
-  if (na == 1) launch_nb<TA, TB, 1, A1, RT>(nb, grid, st, A, saz, sam, sak, B, sbz, sbk, sbn, c, scz, scm, scn, M, N, K, nti);
-  else if (na == 2) launch_nb<TA, TB, 2, A1, RT>(nb, grid, st, A, saz, sam, sak, B, sbz, sbk, sbn, c, scz, scm, scn, M, N, K, nti);
-  else launch_nb<TA, TB, 3, A1, RT>(nb, grid, st, A, saz, sam, sak, B, sbz, sbk, sbn, c, scz, scm, scn, M, N, K, nti);
+  if (na == 1) launch_nb<TA, TB, 1, A1, RT, PF>(nb, grid, st, A, saz, sam, sak, B, sbz, sbk, sbn, c, scz, scm, scn, M, N, K, nti);
+  else if (na == 2) launch_nb<TA, TB, 2, A1, RT, PF>(nb, grid, st, A, saz, sam, sak, B, sbz, sbk, sbn, c, scz, scm, scn, M, N, K, nti);
+  else launch_nb<TA, TB, 3, A1, RT, PF>(nb, grid, st, A, saz, sam, sak, B, sbz, sbk, sbn, c, scz, scm, scn, M, N, K, nti);
 }
 
 // one k step (K <= 64): the A tile's limb planes are formed once per block; from 128 rows, blocks of two row tiles
@@ -184,11 +193,15 @@ static void launch_rt(int na, int nb, dim3 grid, hipStream_t st, const void* a, 
                       const void* b, int64_t sbz, int64_t sbk, int64_t sbn, int64_t* c, int64_t scz, int64_t scm,
                       int64_t scn, int M, int N, int K, int nti) {
   static const int rt_env = getenv("BX_BMM_RT") ? atoi(getenv("BX_BMM_RT")) : 2;
+  static const int pf_env = getenv("BX_BMM_PF") ? atoi(getenv("BX_BMM_PF")) : 1;   // 2: experiments
   if (rt_env == 2 && M >= 2 * kBT) {
     grid.y = (M + 2 * kBT - 1) / (2 * kBT);
-    launch_na<TA, TB, A1, 2>(na, nb, grid, st, a, saz, sam, sak, b, sbz, sbk, sbn, c, scz, scm, scn, M, N, K, nti);
+    if (!A1 && pf_env == 2)
+      launch_na<TA, TB, A1, 2, 2>(na, nb, grid, st, a, saz, sam, sak, b, sbz, sbk, sbn, c, scz, scm, scn, M, N, K, nti);
+    else
+      launch_na<TA, TB, A1, 2, 1>(na, nb, grid, st, a, saz, sam, sak, b, sbz, sbk, sbn, c, scz, scm, scn, M, N, K, nti);
   } else {
-    launch_na<TA, TB, A1, 1>(na, nb, grid, st, a, saz, sam, sak, b, sbz, sbk, sbn, c, scz, scm, scn, M, N, K, nti);
+    launch_na<TA, TB, A1, 1, 1>(na, nb, grid, st, a, saz, sam, sak, b, sbz, sbk, sbn, c, scz, scm, scn, M, N, K, nti);
   }
 }
 
@@ -223,7 +236,7 @@ extern "C" int bx_limb_bmm(const void* a, int32_t a_bytes, int64_t saz, int64_t 
   const dim3 grid((N + kBT * nti - 1) / (kBT * nti), (M + kBT - 1) / kBT, Z);
   hipStream_t st = (hipStream_t)stream;
   if (K == 0) {   // an empty sum: zeros (one step per column tile over a zero-length K reads nothing)
-    bmm_mfma_kernel<int32_t, int32_t, 1, 1, false, 1><<<grid, 256, 0, st>>>((const int32_t*)a, saz, sam, sak, (const int32_t*)b,
+    bmm_mfma_kernel<int32_t, int32_t, 1, 1, false, 1, 1><<<grid, 256, 0, st>>>((const int32_t*)a, saz, sam, sak, (const int32_t*)b,
                                                                   sbz, sbk, sbn, c, scz, scm, scn, M, N, 0, nti);
     return check_launch("bmm_mfma_kernel");
   }
